@@ -1,0 +1,208 @@
+"""Headline benchmark: batch-1 greedy decode tok/s, Qwen2.5-1.5B-shape q4_0, tg128.
+
+    python bench.py [--gpus 1] [--steps 128] [--warmup 8]
+
+Workload: random-init S15 GGUF (hidden 1536, 28 layers,
+12/2 heads, hd 128, FFN 8960, vocab 151936) written from a fixed seed, a 64-token
+seeded random prompt, then `--steps` decode steps (tg128 = 128). A step is one
+decode token (one pass over all weights). The timed region starts with the
+prompt's K/V and every weight resident in HBM.
+
+Prints ONE JSON line on stdout. Besides the contract keys it carries:
+  roofline      the dominant kernel (the gate/up GEMV phase: half of all bytes),
+                algorithmic bytes per launch / mean launch time from HIP events
+                on the engine stream, against MI355X's 8 TB/s HBM peak
+  step_roofline bytes/token x tok/s against the measured stream-read bandwidth
+  stream_gbps   one-launch stream read of a 4 GiB buffer (> the 256 MB MALL)
+  gemv          config 1 microbench: each S15 GEMV shape, rotated over copies
+                totalling > 512 MB so every launch reads from HBM
+  cpu_baseline  the oracle's fp32 mode (a restatement of cpu_infer.cpp whose
+                token streams equal the reference binary's) on this host's cores
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "nano-inference_amd"))
+import minfer  # noqa: E402
+
+HBM_PEAK_GBPS = 8000.0
+
+
+def log(*a):
+    print("[bench]", *a, file=sys.stderr, flush=True)
+
+
+def bytes_per_token(info, pos):
+    """Algorithmic HBM bytes of one decode token at position pos."""
+    E, L, FF = info.n_embd, info.n_layer, info.n_ff
+    kvd = info.n_head_kv * info.head_dim
+    qkv = info.n_head * info.head_dim + 2 * kvd
+    kv_row = L * 2 * kvd * 2                      # fp16 K and V of one position, all layers
+    return (info.weight_bytes + L * 2 * E * 4 + E * 4 + L * qkv * 4 + E * 4
+            + kv_row * (pos + 1) + kv_row)
+
+
+def gemv_microbench(torch, reps=40):
+    """config 1: the five S15 GEMV shapes, weights rotated over > 512 MB of copies."""
+    import numpy as np
+    out = []
+    rng = np.random.default_rng(0)
+    shapes = [("qkv", 2048, 1536, 6), ("o", 1536, 1536, 6), ("gate_up", 17920, 1536, 4),
+              ("down", 1536, 8960, 8), ("lm_head", 151936, 1536, 1)]
+    for name, rows, n_in, ks in shapes:
+        nb, cb = n_in // 32, 8
+        nbytes = minfer.packed_bytes(rows, nb, cb)
+        copies = max(2, -(-(640 << 20) // nbytes))
+        w = torch.randint(0, 256, (copies, nbytes), dtype=torch.uint8, device="cuda")
+        x = torch.randn(n_in, device="cuda")
+        xq = torch.empty(n_in, dtype=torch.int8, device="cuda")
+        xd = torch.empty(nb, device="cuda")
+        xs8 = torch.empty(nb, dtype=torch.int32, device="cuda")
+        minfer.quant_q8(x, xq, xd, xs8)
+        part = torch.empty(ks * rows, device="cuda")
+        for i in range(4):
+            minfer.gemv_q4(w[i % copies], rows, nb, cb, ks, xq, xd, xs8, part)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for i in range(reps):
+            minfer.gemv_q4(w[i % copies], rows, nb, cb, ks, xq, xd, xs8, part)
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1000 / reps
+        alg = rows * nb * 18 + n_in + nb * 4 + rows * 4
+        out.append(dict(shape=name, rows=rows, k=n_in, us=round(us, 2), gbps=round(alg / us / 1e3, 1)))
+        del w
+    torch.cuda.empty_cache()
+    _ = rng
+    return out
+
+
+def stream_bw(torch, gib=4, reps=5):
+    buf = torch.empty(gib << 30, dtype=torch.uint8, device="cuda")
+    buf.zero_()
+    sink = torch.zeros(1024, dtype=torch.int32, device="cuda")
+    minfer.stream_read(buf, buf.numel(), sink)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        minfer.stream_read(buf, buf.numel(), sink)
+    e1.record()
+    torch.cuda.synchronize()
+    gbps = buf.numel() * reps / (e0.elapsed_time(e1) * 1e-3) / 1e9
+    del buf
+    torch.cuda.empty_cache()
+    return gbps
+
+
+def cpu_baseline(path, prompt, n_prompt=6, n_gen=20):
+    """oracle fp32 (cpu_infer semantics) on the host cores, a bounded sample"""
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import oracle_lib as O
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    m = O.Model(path, O.MODE_FP32, max_seq=n_prompt + n_gen + 1, threads=threads)
+    _, _, tp, td = m.generate(prompt[:n_prompt], n_gen)
+    m.close()
+    return dict(value=round((n_gen - 1) / td, 3), unit="tok/s", cores=threads, kind="port",
+                sample="S15 greedy decode: %d-token prompt (%.1f s) then %d tokens (%d decode steps in %.1f s), "
+                       "oracle fp32 = cpu_infer.cpp semantics, OpenMP %d threads" % (n_prompt, tp, n_gen, n_gen - 1,
+                                                                                       td, threads))
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=128)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-micro", action="store_true")
+    ap.add_argument("--persistent", type=int, default=0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py: this engine runs batch-1 decode on one GPU; --gpus %d is not supported "
+              "(the multi-GPU design is described in DESIGN.md, nothing runs on a second GPU)" % args.gpus,
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    shape, mseed, pseed, n_prompt, _ = minfer.CONFIGS["config2"]
+    tmp = os.path.join(os.environ.get("TMPDIR", "/tmp"), "mi-bench")
+    os.makedirs(tmp, exist_ok=True)
+    path = os.path.join(tmp, "config2-%d.gguf" % mseed)
+    if not os.path.exists(path + ".ok"):
+        t = time.time()
+        minfer.synth_gguf(path, shape, mseed)
+        open(path + ".ok", "w").close()
+        log("wrote %s in %.1f s" % (path, time.time() - t))
+    V = minfer.SHAPES[shape]["n_vocab"]
+    prompt = minfer.prompt_ids(pseed, n_prompt, V)
+    t = time.time()
+    eng = minfer.Engine(path, max_ctx=n_prompt + args.steps + args.warmup + 16, persistent=args.persistent)
+    info = eng.info
+    log("loaded in %.1f s: plan cb=%s ks=%s, %d CUs, weights %d B" % (time.time() - t, list(info.plan_cb),
+                                                                     list(info.plan_ks), info.n_cu, info.weight_bytes))
+    # warmup: one short generation from the same prompt
+    eng.prefill(prompt)
+    eng.generate(args.warmup + 1)
+    # timed: prefill (untimed), then exactly `steps` decode steps
+    eng.prefill(prompt)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    toks, margins = eng.generate(args.steps + 1)
+    t1 = time.perf_counter()
+    st = eng.stats()
+    assert st["steps"] == args.steps
+    wall_ms = (t1 - t0) * 1000
+    ms_per_step = wall_ms / args.steps
+    tok_s = args.steps / (t1 - t0)
+    log("decode: %d steps in %.2f ms wall (%.2f ms device) = %.1f tok/s" % (args.steps, wall_ms, st["decode_ms"], tok_s))
+    mean_pos = n_prompt + (args.steps - 1) / 2.0
+    bpt = bytes_per_token(info, mean_pos)
+    # dominant kernel: the gate/up phase (weights + its prologue inputs + partial outputs)
+    E, FF = info.n_embd, info.n_ff
+    gu_ms = eng.time_phase("gate_up", layer=info.n_layer // 2, reps=50)
+    gu_bytes = 2 * FF * (E // 32) * 18 + E * 4 * (2 + info.plan_ks[1]) + info.plan_ks[2] * 2 * FF * 4
+    gu_gbps = gu_bytes / (gu_ms * 1e-3) / 1e9
+    log("gate/up phase kernel: %.2f us per launch, %.1f GB/s" % (gu_ms * 1e3, gu_gbps))
+    eng.close()
+    del eng
+    stream = stream_bw(torch)
+    log("stream read: %.1f GB/s" % stream)
+    micro = [] if args.no_micro else gemv_microbench(torch)
+    for m in micro:
+        log("gemv %-8s %6d x %5d: %8.2f us  %7.1f GB/s" % (m["shape"], m["rows"], m["k"], m["us"], m["gbps"]))
+    cpu = None if args.no_cpu else cpu_baseline(path, prompt)
+    if cpu:
+        log("cpu baseline: %s" % cpu)
+    achieved_step = bpt * tok_s / 1e9
+    rec = {
+        "metric": "batch-1 decode tok/s, Qwen2.5-1.5B q4_0 tg128; GEMV HBM GB/s vs peak",
+        "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "q4_0 weights x int8 activations, int32 dot, fp32 accumulate/softmax, fp16 KV",
+        "data": "synthetic: seeded random-init GGUF (mi_synth_gguf seed %d), seeded random prompt" % mseed,
+        "config": {"workload": "config2: Qwen2.5-1.5B-architecture q4_0 batch-1 greedy decode, 64-token prompt, tg%d"
+                   % args.steps, "shape": "S15 E1536 L28 H12/2 hd128 FF8960 V151936", "global_batch": 1,
+                   "prompt": n_prompt, "step_mode": "persistent" if info.persistent else "one launch per phase",
+                   "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "kernel": "k_gu (gate/up GEMV phase, 28 launches/token)",
+                     "achieved": round(gu_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(gu_gbps / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "bytes_per_launch": gu_bytes, "us_per_launch": round(gu_ms * 1e3, 3)},
+        "step_roofline": {"bytes_per_token": int(bpt), "achieved_gbps": round(achieved_step, 1),
+                          "stream_gbps": round(stream, 1), "frac_of_stream": round(achieved_step / stream, 4),
+                          "roofline_tok_s": round(stream * 1e9 / bpt, 1)},
+        "stream_gbps": round(stream, 1),
+        "gemv": micro,
+        "device_decode_ms": round(st["decode_ms"], 3),
+        "cpu_baseline": cpu,
+        "tokens_head": toks[:8],
+    }
+    print(json.dumps(rec), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,176 @@
+/* minfer.h -- C ABI of the MI355X (gfx950) batch-1 decode engine.
+ *
+ * The reference has no library interface: its engines are executables whose
+ * seams are internal (src/cuda_infer.cu record() :1031-1083 = one token at a
+ * device-held position, forward_batch() :990-1026 = T <= 8 tokens at pos0,
+ * src/mega.cu run<Shape>() :1005-1243 + kernel mega<M>(n_gen) :597-903 = load +
+ * whole generate). This header turns those seams into plain C entry points
+ * (int32 token IDs, plain pointers and sizes, int status codes, no exits), so
+ * the reference's host (GGUF loader, CLI, drafter) can drive this engine in place
+ * of the CUDA path. Every function is single-threaded per engine, as the
+ * reference is (one host thread, cuda_infer.cu:1170-1200).
+ *
+ * Errors: every entry point returns MI_OK (0) or a negative MI_ERR_* code and
+ * records a message readable with mi_last_error(); the reference instead prints
+ * and exits (cuda_infer.cu:20, mega.cu:46-47, gguf.h:33/79/185-192).
+ */
+#ifndef MINFER_H
+#define MINFER_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MI_OK 0
+#define MI_ERR_ARG (-1)      /* bad argument / out-of-range position or token */
+#define MI_ERR_IO (-2)       /* file cannot be opened or written */
+#define MI_ERR_FORMAT (-3)   /* not a GGUF / missing tensor / unsupported tensor type */
+#define MI_ERR_SHAPE (-4)    /* model shape the kernels do not support (mega.cu:47 REQUIRE) */
+#define MI_ERR_DEVICE (-5)   /* HIP runtime error or no gfx950 device */
+#define MI_ERR_OOM (-6)      /* device allocation failed */
+#define MI_ERR_STATE (-7)    /* call out of order (e.g. generate before prefill) */
+
+typedef struct mi_engine mi_engine;
+
+/* Engine options. Environment knobs of the reference map onto fields:
+ * TCHUNK (mega.cu:1019) -> tchunk, SPEC (mega.cu:1020) -> spec, NGMAX (:1021) -> ngmax,
+ * SPEC_SLOPE (:1022) -> spec_slope; maxseq = P + n_gen + TMAX (:1023) -> max_ctx. */
+typedef struct mi_opts {
+    int32_t max_ctx;       /* KV cache capacity in positions (0: 4096) */
+    int32_t tchunk;        /* prompt tokens per step, 1..8 */
+    int32_t spec;          /* n-gram speculative decoding inside mi_generate (0/1) */
+    int32_t ngmax;         /* longest n-gram the drafter matches (mega.cu:561-578) */
+    float spec_slope;      /* cost of each extra token in a step, relative to a 1-token step */
+    int32_t persistent;    /* 1: one persistent cooperative kernel per step; 0: one launch per phase */
+    int32_t stop_eos;      /* mi_generate stops after tokenizer.ggml.eos_token_id */
+    int32_t device;        /* HIP device ordinal */
+} mi_opts;
+
+/* reference defaults: TCHUNK 8, SPEC 1 (mega) / 0 (cuda_infer), NGMAX 3, SPEC_SLOPE 0.074 */
+void mi_default_opts(mi_opts* o);
+
+/* cuda_infer.cu:844-901 / mega.cu:1005-1113: parse the GGUF, repack every q4_0
+ * matrix into the device tile layout, upload, allocate the KV cache and state. */
+int mi_load(const char* gguf_path, const mi_opts* opts, mi_engine** out);
+void mi_free(mi_engine* e);
+/* message of the last failure on e (or of the last failed mi_load when e is NULL) */
+const char* mi_last_error(const mi_engine* e);
+
+/* Model shape and the engine's reduction plan (the fixed float summation order
+ * the kernels follow; the CPU oracle takes the same plan to match them bit for bit). */
+typedef struct mi_model_info {
+    int32_t n_layer, n_embd, n_ff, n_head, n_head_kv, head_dim, n_vocab, eos;
+    float rope_base, rms_eps;
+    int32_t max_ctx;
+    int32_t plan_cb[5];    /* blocks per chunk: qkv, o, gate/up, down, lm_head */
+    int32_t plan_ks[5];    /* K segments per row, same order */
+    int32_t attn_chunk;    /* positions per attention partial */
+    int32_t kv_f16;        /* 1: the KV cache holds fp16 */
+    int32_t n_cu;          /* compute units of the device */
+    int32_t persistent;    /* step mode in use */
+    uint64_t weight_bytes; /* q4_0 bytes streamed per token (all layers + lm_head) */
+} mi_model_info;
+int mi_info(const mi_engine* e, mi_model_info* out);
+
+/* Prefill: cuda_infer.cu:1151-1159 / mega.cu prompt steps. Runs ids[0..n) at
+ * positions 0..n-1 (from an empty cache) and returns the greedy prediction after
+ * the last one (= the first generated token) and its logit margin. */
+int mi_prefill(mi_engine* e, const int32_t* ids, int32_t n, int32_t* first, float* margin);
+
+/* One step: forward_batch(toks, T, pos0) (cuda_infer.cu:990-1026). Runs toks[0..T)
+ * at positions pos..pos+T-1 (pos <= current length: a smaller pos rewinds, which is
+ * how rejected drafts are dropped), writes their K/V, returns per token the argmax
+ * (lowest index on ties), the margin best - second, and optionally the logits
+ * [T][n_vocab] (nullable; the reference never exposes logits). T = 1 for now. */
+int mi_step(mi_engine* e, const int32_t* toks, int32_t T, int32_t pos,
+            int32_t* argmax, float* margin, float* logits);
+
+/* Token callback for mi_generate; returning nonzero stops generation. */
+typedef int (*mi_token_cb)(int32_t id, void* user);
+
+/* Greedy generation after mi_prefill (cuda_infer.cu:1170-1200, mega.cu:819-895):
+ * emits n_gen tokens, the first being mi_prefill's prediction. out[n_gen] and
+ * margins[n_gen] (nullable) receive them; *n_out the count actually emitted
+ * (fewer when stop_eos hits eos or the callback stops). */
+int mi_generate(mi_engine* e, int32_t n_gen, int32_t* out, float* margins, int32_t* n_out,
+                mi_token_cb cb, void* user);
+
+/* Timing of the last mi_generate: device time of its decode steps measured with
+ * HIP events on the engine stream (the reference prints the same figure,
+ * mega.cu:1186-1190, cuda_infer.cu:1196-1199). */
+typedef struct mi_stats {
+    int32_t steps;          /* decode steps run */
+    int32_t tokens;         /* tokens emitted by those steps */
+    double decode_ms;       /* device time of those steps */
+    double prefill_ms;      /* device time of the last mi_prefill */
+} mi_stats;
+int mi_get_stats(const mi_engine* e, mi_stats* out);
+
+/* Measurement hook, no counterpart in the reference (which profiles with nsys/ncu and
+ * in-kernel clock64 marks, mega.cu:111-119): re-launches one phase kernel of the
+ * last step `reps` times on the engine stream and returns its mean duration from
+ * HIP events. phase: 0 qkv, 1 qkv_fin, 2 attn, 3 attn_comb, 4 o, 5 gate/up, 6 act,
+ * 7 down, 8 lm_head, 9 argmax. Needs a completed step; re-running a phase rewrites
+ * the same values, so the engine state is unchanged. */
+int mi_time_phase(mi_engine* e, int32_t phase, int32_t layer, int32_t reps, double* avg_ms);
+
+/* ---------------- synthetic model files ---------------- */
+typedef struct mi_synth_shape {
+    int32_t n_layer, n_embd, n_ff, n_head, n_head_kv, n_vocab;
+    float rope_base, rms_eps;
+    int32_t emb_type;      /* 0: F32 token embedding (the configs), 2: q4_0 */
+} mi_synth_shape;
+/* Writes a seeded random-init qwen2 GGUF: q4_0 matrices (uniform nibbles, fp16
+ * |N(0,0.002)| scales), fp32 N(0,0.02) norms/biases/embedding, a token list of
+ * n_vocab entries. Same seed -> same bytes. No reference counterpart (the
+ * reference runs downloaded Qwen files, README.md:58). */
+int mi_synth_gguf(const char* path, const mi_synth_shape* shape, uint64_t seed);
+
+/* ---------------- kernel-level entry points (device pointers) ----------------
+ * For the microbenchmarks and bit-exact parity tests. `stream` is a hipStream_t
+ * (NULL = the null stream). All pointers are device pointers unless noted. */
+
+/* bytes of a rows x (nb*32) q4_0 matrix in the device tile layout: 64-row groups,
+ * chunks of cb blocks; tile (group g, chunk c) holds cb slabs of 64 x 16 quant
+ * bytes then 64 x cb fp16 scales. Replaces mega.cu pack_q4 (:966-984). */
+size_t mi_q4_packed_bytes(int32_t rows, int32_t nb, int32_t cb);
+/* host: GGUF row-major q4_0 blocks (18 B each) -> tile layout (host buffers) */
+int mi_q4_pack(const uint8_t* src, int32_t rows, int32_t nb, int32_t cb, uint8_t* dst);
+
+/* per-32 symmetric int8 quantization of x[n] (cuda_infer.cu:80-89 quant_x_q8,
+ * mega.cu:303-325 quant32): xq[n], xd[n/32] (fp16-rounded scale), xs8[n/32] = 8*sum(q) */
+int mi_quant_q8(const float* x, int32_t n, int8_t* xq, float* xd, int32_t* xs8, void* stream);
+
+/* q4_0 x int8 GEMV on a packed matrix (cuda_infer.cu:94-127 gemv_dp4a, mega.cu:178-196
+ * row_dot): part[ks][rows] = per-segment row sums, y[rows] = segments added in order
+ * (y may be NULL). */
+int mi_gemv_q4(const uint8_t* packed, int32_t rows, int32_t nb, int32_t cb, int32_t ks,
+               const int8_t* xq, const float* xd, const int32_t* xs8,
+               float* part, float* y, void* stream);
+
+/* integer block sums isum[rows][nb] = sum_j n_j * x_j of the packed matrix against xq
+ * (the exact integer part of dot_q4, mega.cu:157-165) */
+int mi_q4_block_isums(const uint8_t* packed, int32_t rows, int32_t nb, int32_t cb,
+                      const int8_t* xq, int32_t* isum, void* stream);
+
+/* single-query GQA attention over an fp16 cache (cuda_infer.cu:650-702 attn_partial +
+ * attn_combine, mega.cu:414-521): q[n_head][hd] fp32, kc/vc [n_head_kv][ctx][hd] fp16,
+ * positions 0..L-1, out[n_head][hd]. scratch holds n_head * ceil(L/64) * (hd + 2) floats. */
+int mi_attn_decode(const float* q, const uint16_t* kc, const uint16_t* vc, int32_t n_head,
+                   int32_t n_head_kv, int32_t hd, int32_t L, int32_t ctx, float scale,
+                   float* scratch, float* out, void* stream);
+
+/* stream-read roofline (bench/roofline.cu:39-71 k_gridstride): one launch reading
+ * `bytes` (multiple of 16) with several 16-byte loads in flight per thread */
+int mi_stream_read(const void* buf, size_t bytes, uint32_t* sink, void* stream);
+
+/* device-side timing helpers for callers without a HIP binding */
+int mi_stream_sync(void* stream);
+int mi_device_count(int32_t* n);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

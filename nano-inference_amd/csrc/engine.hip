@@ -1,0 +1,649 @@
+// engine.hip -- host side of the engine and the C ABI (include/minfer.h).
+//
+// Load path (reference: cuda_infer.cu:844-901, mega.cu:1005-1139): parse the GGUF,
+// repack every q4_0 matrix into the tile layout (common.hpp), fuse q|k|v rows and
+// interleave gate/up row groups, upload everything into one device arena, build
+// the RoPE table with cpu_infer's own float expressions (cpu_infer.cpp:54-55), and
+// allocate the fp16 KV cache and the step's work buffers. Steps then run on one HIP
+// stream without host round trips: the token of each position lives in device
+// memory (tokbuf), and each step's argmax writes the next token there.
+#include "common.hpp"
+#include "gguf.hpp"
+#include "kernels.hpp"
+#include "minfer.h"
+
+#include <algorithm>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <memory>
+#include <string>
+#include <vector>
+
+using namespace mi;
+
+namespace {
+
+thread_local std::string g_load_error;
+
+}  // namespace
+
+struct mi_engine {
+    mi_opts opts{};
+    GGUFFile gguf;
+    std::string err;
+    int n_cu = 0;
+    int E = 0, FF = 0, NH = 0, NKV = 0, HD = 0, G = 0, KVD = 0, QKV = 0, V = 0, NL = 0, maxseq = 0, maxch = 0, eos = 0;
+    float rope_base = 0, eps = 0;
+    int cb[5] = {0}, ks[5] = {0};
+    uint64_t weight_bytes = 0;
+    std::vector<void*> allocs;
+    DModel M{};
+    DModel M_logits{};            // same as M with the logits buffer attached
+    DLayer* d_layers = nullptr;
+    PhaseGrid pg{};
+    hipStream_t stream = nullptr;
+    hipEvent_t ev0 = nullptr, ev1 = nullptr;
+    int cur_len = 0;              // positions holding valid K/V
+    bool next_ready = false;      // tokbuf[cur_len] holds the prediction of the last step
+    mi_stats stats{};
+    ~mi_engine() {
+        if (stream) (void)hipStreamSynchronize(stream);
+        for (void* p : allocs) (void)hipFree(p);
+        if (ev0) (void)hipEventDestroy(ev0);
+        if (ev1) (void)hipEventDestroy(ev1);
+        if (stream) (void)hipStreamDestroy(stream);
+    }
+};
+
+namespace {
+
+int set_err(mi_engine* e, int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    if (e) e->err = buf; else g_load_error = buf;
+    return code;
+}
+
+#define HIPCHK(e, x)                                                                                   \
+    do {                                                                                               \
+        hipError_t st_ = (x);                                                                          \
+        if (st_ != hipSuccess) return set_err(e, MI_ERR_DEVICE, "%s: %s", #x, hipGetErrorString(st_)); \
+    } while (0)
+
+int dev_alloc(mi_engine* e, void** p, size_t bytes) {
+    if (hipMalloc(p, bytes) != hipSuccess) {
+        (void)hipGetLastError();
+        return set_err(e, MI_ERR_OOM, "hipMalloc(%zu MB) failed", bytes >> 20);
+    }
+    e->allocs.push_back(*p);
+    if (hipMemset(*p, 0, bytes) != hipSuccess) return set_err(e, MI_ERR_DEVICE, "hipMemset failed");
+    return MI_OK;
+}
+
+// mega.cu:924-936 quant_row_q4_0: any non-q4_0 weight row -> q4_0 (amax/7, +8, clamp)
+void requant_row_q4_0(const float* y, int n, uint8_t* out) {
+    for (int b = 0; b < n / 32; b++, y += 32, out += 18) {
+        float amax = 0.f;
+        for (int j = 0; j < 32; j++) amax = std::max(amax, std::fabs(y[j]));
+        const float d = amax / 7.f, inv = d > 0.f ? 1.f / d : 0.f;
+        const uint16_t hd = f32_to_f16(d);
+        memcpy(out, &hd, 2);
+        for (int j = 0; j < 16; j++) {
+            int q0 = (int)lrintf(y[j] * inv) + 8, q1 = (int)lrintf(y[j + 16] * inv) + 8;
+            q0 = std::min(15, std::max(0, q0)); q1 = std::min(15, std::max(0, q1));
+            out[2 + j] = (uint8_t)(q0 | (q1 << 4));
+        }
+    }
+}
+
+void dequant_row(const GTensor& t, int64_t r, float* out) {
+    const int64_t c = t.cols();
+    switch (t.type) {
+        case GT_F32: memcpy(out, t.data + (size_t)r * c * 4, (size_t)c * 4); break;
+        case GT_F16: {
+            const uint16_t* h = reinterpret_cast<const uint16_t*>(t.data + (size_t)r * c * 2);
+            for (int64_t i = 0; i < c; i++) out[i] = f16_to_f32(h[i]);
+            break;
+        }
+        case GT_Q4_0: {
+            const uint8_t* p = t.data + (size_t)r * (c / 32) * 18;
+            for (int64_t b = 0; b < c / 32; b++, p += 18) {
+                uint16_t hd; memcpy(&hd, p, 2);
+                const float d = f16_to_f32(hd);
+                for (int j = 0; j < 16; j++) {
+                    out[b * 32 + j] = ((p[2 + j] & 0x0F) - 8) * d;
+                    out[b * 32 + j + 16] = ((p[2 + j] >> 4) - 8) * d;
+                }
+            }
+            break;
+        }
+        case GT_Q8_0: {
+            const uint8_t* p = t.data + (size_t)r * (c / 32) * 34;
+            for (int64_t b = 0; b < c / 32; b++, p += 34) {
+                uint16_t hd; memcpy(&hd, p, 2);
+                const float d = f16_to_f32(hd);
+                for (int j = 0; j < 32; j++) out[b * 32 + j] = (int8_t)p[2 + j] * d;
+            }
+            break;
+        }
+        default: memset(out, 0, (size_t)c * 4);
+    }
+}
+
+// a weight matrix as GGUF row-major q4_0 bytes (as stored, or requantized)
+const uint8_t* q4_rows(const GTensor& t, std::vector<uint8_t>& buf) {
+    if (t.type == GT_Q4_0) return t.data;
+    const int n = (int)t.cols(), rows = (int)t.rows();
+    buf.resize((size_t)rows * (n / 32) * 18);
+    std::vector<float> row(n);
+    for (int r = 0; r < rows; r++) { dequant_row(t, r, row.data()); requant_row_q4_0(row.data(), n, buf.data() + (size_t)r * (n / 32) * 18); }
+    return buf.data();
+}
+
+int choose_ks(int groups, int nc, int cap) {
+    constexpr int kTargetTasks = 1024;   // fixed, so the plan (and the float order) is device-independent
+    const int ks = (kTargetTasks + groups - 1) / groups;
+    return std::max(1, std::min(std::min(ks, nc), cap));
+}
+
+}  // namespace
+
+extern "C" {
+
+void mi_default_opts(mi_opts* o) {
+    if (!o) return;
+    o->max_ctx = 4096;
+    o->tchunk = 8;
+    o->spec = 0;
+    o->ngmax = 3;
+    o->spec_slope = 0.074f;
+    o->persistent = 0;
+    o->stop_eos = 0;
+    o->device = 0;
+}
+
+size_t mi_q4_packed_bytes(int32_t rows, int32_t nb, int32_t cb) {
+    if (rows <= 0 || rows % 64 || nb <= 0 || (cb != 4 && cb != 8) || nb % cb) return 0;
+    return (size_t)(rows / 64) * (nb / cb) * tile_bytes(cb);
+}
+
+int mi_q4_pack(const uint8_t* src, int32_t rows, int32_t nb, int32_t cb, uint8_t* dst) {
+    if (!src || !dst || !mi_q4_packed_bytes(rows, nb, cb)) return MI_ERR_ARG;
+    const int ng = rows / 64, nc = nb / cb;
+    const size_t TB = tile_bytes(cb);
+    for (int g = 0; g < ng; g++)
+        for (int c = 0; c < nc; c++) {
+            uint8_t* t = dst + ((size_t)g * nc + c) * TB;
+            for (int r = 0; r < 64; r++) {
+                const uint8_t* row = src + (size_t)(g * 64 + r) * nb * 18;
+                for (int k = 0; k < cb; k++) {
+                    const uint8_t* blk = row + (size_t)(c * cb + k) * 18;
+                    memcpy(t + k * 1024 + r * 16, blk + 2, 16);
+                    memcpy(t + (size_t)cb * 1024 + r * cb * 2 + k * 2, blk, 2);
+                }
+            }
+        }
+    return MI_OK;
+}
+
+const char* mi_last_error(const mi_engine* e) { return e ? e->err.c_str() : g_load_error.c_str(); }
+
+}  // extern "C"
+
+static int upload_mat(mi_engine* e, const uint8_t* rows_q4, int rows, int nb, int kind, PMat* out) {
+    const int cb = e->cb[kind];
+    const size_t bytes = mi_q4_packed_bytes(rows, nb, cb);
+    if (!bytes) return set_err(e, MI_ERR_SHAPE, "matrix %dx%d blocks cannot be tiled (cb %d)", rows, nb, cb);
+    std::vector<uint8_t> host(bytes);
+    mi_q4_pack(rows_q4, rows, nb, cb, host.data());
+    void* d = nullptr;
+    int rc = dev_alloc(e, &d, bytes);
+    if (rc) return rc;
+    HIPCHK(e, hipMemcpy(d, host.data(), bytes, hipMemcpyHostToDevice));
+    *out = PMat{reinterpret_cast<const uint8_t*>(d), rows, nb, cb, nb / cb, e->ks[kind]};
+    e->weight_bytes += (uint64_t)rows * nb * 18;
+    return MI_OK;
+}
+
+static int upload_f32(mi_engine* e, const GTensor* t, int64_t n, const float** out) {
+    std::vector<float> host((size_t)n);
+    if (t->type == GT_F32) memcpy(host.data(), t->data, (size_t)n * 4);
+    else {
+        const int64_t c = t->cols();
+        for (int64_t r = 0; r < n / c; r++) dequant_row(*t, r, host.data() + r * c);
+    }
+    void* d = nullptr;
+    int rc = dev_alloc(e, &d, (size_t)n * 4);
+    if (rc) return rc;
+    HIPCHK(e, hipMemcpy(d, host.data(), (size_t)n * 4, hipMemcpyHostToDevice));
+    *out = reinterpret_cast<const float*>(d);
+    return MI_OK;
+}
+
+template <class T>
+static int alloc_buf(mi_engine* e, T** p, size_t count) {
+    void* d = nullptr;
+    int rc = dev_alloc(e, &d, std::max<size_t>(count, 1) * sizeof(T));
+    *p = reinterpret_cast<T*>(d);
+    return rc;
+}
+
+static int load_impl(mi_engine* e, const char* path) {
+    int ndev = 0;
+    if (hipGetDeviceCount(&ndev) != hipSuccess || ndev <= e->opts.device)
+        return set_err(e, MI_ERR_DEVICE, "no HIP device %d", e->opts.device);
+    HIPCHK(e, hipSetDevice(e->opts.device));
+    hipDeviceProp_t prop;
+    HIPCHK(e, hipGetDeviceProperties(&prop, e->opts.device));
+    if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+        return set_err(e, MI_ERR_DEVICE, "device %d is %s; the kernels are built for gfx950", e->opts.device, prop.gcnArchName);
+    e->n_cu = prop.multiProcessorCount;
+
+    GGUFFile& g = e->gguf;
+    if (!g.open(path)) return set_err(e, MI_ERR_FORMAT, "%s", g.error().c_str());
+    e->NL = (int)g.num("qwen2.block_count", 0);
+    e->E = (int)g.num("qwen2.embedding_length", 0);
+    e->FF = (int)g.num("qwen2.feed_forward_length", 0);
+    e->NH = (int)g.num("qwen2.attention.head_count", 0);
+    e->NKV = (int)g.num("qwen2.attention.head_count_kv", 0);
+    e->rope_base = (float)g.num("qwen2.rope.freq_base", 1e6);
+    e->eps = (float)g.num("qwen2.attention.layer_norm_rms_epsilon", 1e-6);
+    e->V = (int)g.tokens().size();
+    e->eos = (int)g.num("tokenizer.ggml.eos_token_id", 151645);
+    if (e->NL < 1 || e->E < 32 || e->NH < 1 || e->NKV < 1 || e->E % e->NH || e->NH % e->NKV)
+        return set_err(e, MI_ERR_FORMAT, "missing or inconsistent qwen2.* shape metadata");
+    e->HD = e->E / e->NH;
+    e->G = e->NH / e->NKV;
+    e->KVD = e->NKV * e->HD;
+    e->QKV = e->NH * e->HD + 2 * e->KVD;
+    if (!kernels_support(e->G, e->HD) || e->E % 64 || e->E > kMaxE || e->FF % 32 || e->FF > kMaxFF ||
+        e->QKV % 64 || e->V % 64 || e->V < 64 || (e->E / 32) % 4 || (e->FF / 32) % 4)
+        return set_err(e, MI_ERR_SHAPE, "unsupported shape E=%d FF=%d heads=%d/%d hd=%d vocab=%d", e->E, e->FF, e->NH,
+                       e->NKV, e->HD, e->V);
+    e->maxseq = e->opts.max_ctx > 0 ? e->opts.max_ctx : 4096;
+    e->maxch = (e->maxseq + kAttnChunk - 1) / kAttnChunk;
+
+    // reduction plan: chunk size by row length, K segments by row-group count
+    const int nbE = e->E / 32, nbF = e->FF / 32;
+    const int cbE = nbE % 8 == 0 ? 8 : 4, cbF = nbF % 8 == 0 ? 8 : 4;
+    e->cb[0] = e->cb[1] = e->cb[2] = e->cb[4] = cbE;
+    e->cb[3] = cbF;
+    e->ks[0] = choose_ks(e->QKV / 64, nbE / cbE, 8);
+    e->ks[1] = choose_ks(e->E / 64, nbE / cbE, 8);
+    e->ks[2] = choose_ks(e->FF / 32, nbE / cbE, 4);
+    e->ks[3] = choose_ks(e->E / 64, nbF / cbF, 8);
+    e->ks[4] = 1;
+
+    auto need = [&](const std::string& n) -> const GTensor* { return g.tensor(n); };
+    const GTensor* te = need("token_embd.weight");
+    const GTensor* tout = need("output.weight");
+    const GTensor* tnorm = need("output_norm.weight");
+    if (!te || !tnorm) return set_err(e, MI_ERR_FORMAT, "missing token_embd.weight or output_norm.weight");
+    if (!tout) tout = te;   // tied embeddings (mega.cu:1071)
+    if (te->cols() != e->E || te->rows() < e->V || tout->cols() != e->E || tout->rows() != e->V)
+        return set_err(e, MI_ERR_FORMAT, "embedding/output shapes do not match the metadata");
+
+    std::vector<DLayer> layers(e->NL);
+    std::vector<uint8_t> tmp, cat;
+    const size_t rbE = (size_t)nbE * 18, rbF = (size_t)nbF * 18;
+    for (int l = 0; l < e->NL; l++) {
+        const std::string p = "blk." + std::to_string(l) + ".";
+        const char* names[] = {"attn_norm.weight", "attn_q.weight", "attn_q.bias", "attn_k.weight", "attn_k.bias",
+                               "attn_v.weight", "attn_v.bias", "attn_output.weight", "ffn_norm.weight",
+                               "ffn_gate.weight", "ffn_up.weight", "ffn_down.weight"};
+        const GTensor* t[12];
+        for (int i = 0; i < 12; i++) {
+            t[i] = need(p + names[i]);
+            if (!t[i]) return set_err(e, MI_ERR_FORMAT, "missing tensor %s%s", p.c_str(), names[i]);
+        }
+        const int NQ = e->NH * e->HD;
+        if (t[1]->cols() != e->E || t[1]->rows() != NQ || t[3]->rows() != e->KVD || t[5]->rows() != e->KVD ||
+            t[7]->cols() != NQ || t[7]->rows() != e->E || t[9]->rows() != e->FF || t[10]->rows() != e->FF ||
+            t[11]->cols() != e->FF || t[11]->rows() != e->E)
+            return set_err(e, MI_ERR_FORMAT, "layer %d tensor shapes do not match the metadata", l);
+        // fused QKV rows [q; k; v]
+        cat.resize((size_t)e->QKV * rbE);
+        memcpy(cat.data(), q4_rows(*t[1], tmp), (size_t)NQ * rbE);
+        memcpy(cat.data() + (size_t)NQ * rbE, q4_rows(*t[3], tmp), (size_t)e->KVD * rbE);
+        memcpy(cat.data() + (size_t)(NQ + e->KVD) * rbE, q4_rows(*t[5], tmp), (size_t)e->KVD * rbE);
+        int rc = upload_mat(e, cat.data(), e->QKV, nbE, 0, &layers[l].qkv);
+        if (rc) return rc;
+        rc = upload_mat(e, q4_rows(*t[7], tmp), e->E, nbE, 1, &layers[l].o);
+        if (rc) return rc;
+        // gate/up interleaved by 32-row groups
+        {
+            std::vector<uint8_t> gb, ub;
+            const uint8_t* gr = q4_rows(*t[9], gb);
+            const uint8_t* ur = q4_rows(*t[10], ub);
+            cat.resize((size_t)2 * e->FF * rbE);
+            for (int G32 = 0; G32 < e->FF / 32; G32++) {
+                memcpy(cat.data() + (size_t)(64 * G32) * rbE, gr + (size_t)(32 * G32) * rbE, 32 * rbE);
+                memcpy(cat.data() + (size_t)(64 * G32 + 32) * rbE, ur + (size_t)(32 * G32) * rbE, 32 * rbE);
+            }
+            rc = upload_mat(e, cat.data(), 2 * e->FF, nbE, 2, &layers[l].gu);
+            if (rc) return rc;
+        }
+        rc = upload_mat(e, q4_rows(*t[11], tmp), e->E, nbF, 3, &layers[l].d);
+        if (rc) return rc;
+        (void)rbF;
+        rc = upload_f32(e, t[0], e->E, &layers[l].an);
+        if (rc) return rc;
+        rc = upload_f32(e, t[8], e->E, &layers[l].fn);
+        if (rc) return rc;
+        {
+            std::vector<float> b((size_t)e->QKV);
+            for (int i = 0; i < 3; i++) {
+                const GTensor* bt = t[2 + 2 * i];
+                const int n = i == 0 ? NQ : e->KVD, off = i == 0 ? 0 : (i == 1 ? NQ : NQ + e->KVD);
+                if (bt->cols() != n) return set_err(e, MI_ERR_FORMAT, "layer %d bias shape", l);
+                dequant_row(*bt, 0, b.data() + off);
+            }
+            void* d = nullptr;
+            rc = dev_alloc(e, &d, b.size() * 4);
+            if (rc) return rc;
+            HIPCHK(e, hipMemcpy(d, b.data(), b.size() * 4, hipMemcpyHostToDevice));
+            layers[l].bqkv = reinterpret_cast<const float*>(d);
+        }
+        for (int i : {1, 3, 5, 7, 9, 10, 11}) g.release(*t[i]);
+    }
+    DModel& M = e->M;
+    M.E = e->E; M.FF = e->FF; M.NH = e->NH; M.NKV = e->NKV; M.HD = e->HD; M.G = e->G; M.KVD = e->KVD;
+    M.QKV = e->QKV; M.V = e->V; M.NL = e->NL; M.maxseq = e->maxseq; M.maxch = e->maxch;
+    M.eps = e->eps;
+    M.scale = 1.f / sqrtf((float)e->HD);
+    int rc = upload_mat(e, q4_rows(*tout, tmp), e->V, nbE, 4, &M.lm);
+    if (rc) return rc;
+    rc = upload_f32(e, te, (int64_t)e->V * e->E, &M.emb);
+    if (rc) return rc;
+    rc = upload_f32(e, tnorm, e->E, &M.out_norm);
+    if (rc) return rc;
+    g.release(*tout);
+    g.release(*te);
+    // RoPE table: cpu_infer.cpp:54-55 evaluated with the same float expressions
+    {
+        const int half = e->HD / 2;
+        std::vector<float2> rope((size_t)e->maxseq * half);
+        for (int pos = 0; pos < e->maxseq; pos++)
+            for (int i = 0; i < half; i++) {
+                const float theta = pos * powf(e->rope_base, -2.f * i / e->HD);
+                rope[(size_t)pos * half + i] = make_float2(cosf(theta), sinf(theta));
+            }
+        float2* d = nullptr;
+        rc = alloc_buf(e, &d, rope.size());
+        if (rc) return rc;
+        HIPCHK(e, hipMemcpy(d, rope.data(), rope.size() * sizeof(float2), hipMemcpyHostToDevice));
+        M.rope = d;
+    }
+    rc = alloc_buf(e, &e->d_layers, e->NL);
+    if (rc) return rc;
+    HIPCHK(e, hipMemcpy(e->d_layers, layers.data(), layers.size() * sizeof(DLayer), hipMemcpyHostToDevice));
+    M.layers = e->d_layers;
+    const size_t kvn = (size_t)e->NL * e->NKV * e->maxseq * e->HD;
+    e->pg = plan_phase_grid(M, layers[0], e->n_cu);
+    if ((rc = alloc_buf(e, &M.kc, kvn)) || (rc = alloc_buf(e, &M.vc, kvn)) ||
+        (rc = alloc_buf(e, &M.tokbuf, (size_t)e->maxseq + 1)) ||
+        (rc = alloc_buf(e, &M.hbuf, (size_t)(2 * e->NL + 1) * e->E)) ||
+        (rc = alloc_buf(e, &M.qkv_part, (size_t)e->ks[0] * e->QKV)) ||
+        (rc = alloc_buf(e, &M.qf, (size_t)e->NH * e->HD)) ||
+        (rc = alloc_buf(e, &M.att_ml, (size_t)e->NH * e->maxch * 2)) ||
+        (rc = alloc_buf(e, &M.att_o, (size_t)e->NH * e->maxch * e->HD)) ||
+        (rc = alloc_buf(e, &M.att_out, (size_t)e->E)) ||
+        (rc = alloc_buf(e, &M.o_part, (size_t)e->ks[1] * e->E)) ||
+        (rc = alloc_buf(e, &M.gu_part, (size_t)e->ks[2] * 2 * e->FF)) ||
+        (rc = alloc_buf(e, &M.act_q, (size_t)e->FF)) ||
+        (rc = alloc_buf(e, &M.act_ds, (size_t)e->FF / 32)) ||
+        (rc = alloc_buf(e, &M.d_part, (size_t)e->ks[3] * e->E)) ||
+        (rc = alloc_buf(e, &M.cand, (size_t)std::max(e->pg.lm, 1))) ||
+        (rc = alloc_buf(e, &M.out_tok, (size_t)e->maxseq)) ||
+        (rc = alloc_buf(e, &M.out_margin, (size_t)e->maxseq)))
+        return rc;
+    M.logits = nullptr;
+    e->M_logits = M;
+    if ((rc = alloc_buf(e, &e->M_logits.logits, (size_t)e->V))) return rc;
+    HIPCHK(e, hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking));
+    HIPCHK(e, hipEventCreate(&e->ev0));
+    HIPCHK(e, hipEventCreate(&e->ev1));
+    HIPCHK(e, hipDeviceSynchronize());
+    return MI_OK;
+}
+
+extern "C" {
+
+int mi_load(const char* gguf_path, const mi_opts* opts, mi_engine** out) {
+    if (!gguf_path || !out) return set_err(nullptr, MI_ERR_ARG, "null argument");
+    *out = nullptr;
+    std::unique_ptr<mi_engine> e(new mi_engine());
+    if (opts) e->opts = *opts; else mi_default_opts(&e->opts);
+    if (e->opts.tchunk < 1 || e->opts.tchunk > 8 || e->opts.max_ctx < 0)
+        return set_err(nullptr, MI_ERR_ARG, "bad options");
+    if (e->opts.persistent) return set_err(nullptr, MI_ERR_ARG, "persistent step mode is not built yet");
+    const int rc = load_impl(e.get(), gguf_path);
+    if (rc) { g_load_error = e->err; return rc; }
+    *out = e.release();
+    return MI_OK;
+}
+
+void mi_free(mi_engine* e) { delete e; }
+
+int mi_info(const mi_engine* e, mi_model_info* o) {
+    if (!e || !o) return MI_ERR_ARG;
+    memset(o, 0, sizeof *o);
+    o->n_layer = e->NL; o->n_embd = e->E; o->n_ff = e->FF; o->n_head = e->NH; o->n_head_kv = e->NKV;
+    o->head_dim = e->HD; o->n_vocab = e->V; o->eos = e->eos; o->rope_base = e->rope_base; o->rms_eps = e->eps;
+    o->max_ctx = e->maxseq;
+    for (int i = 0; i < 5; i++) { o->plan_cb[i] = e->cb[i]; o->plan_ks[i] = e->ks[i]; }
+    o->attn_chunk = kAttnChunk;
+    o->kv_f16 = 1;
+    o->n_cu = e->n_cu;
+    o->persistent = e->opts.persistent;
+    o->weight_bytes = e->weight_bytes;
+    return MI_OK;
+}
+
+}  // extern "C"
+
+static int run_step(mi_engine* e, int pos, int gen, bool want_logits) {
+    launch_step_phases(want_logits ? e->M_logits : e->M, e->pg, pos, gen, e->stream);
+    HIPCHK(e, hipGetLastError());
+    return MI_OK;
+}
+
+extern "C" {
+
+int mi_step(mi_engine* e, const int32_t* toks, int32_t T, int32_t pos, int32_t* argmax, float* margin, float* logits) {
+    if (!e || !toks) return MI_ERR_ARG;
+    if (T != 1) return set_err(e, MI_ERR_ARG, "mi_step: T=%d; only single-token steps are built", T);
+    if (pos < 0 || pos > e->cur_len || pos + T > e->maxseq) return set_err(e, MI_ERR_ARG, "mi_step: position %d out of range (length %d, capacity %d)", pos, e->cur_len, e->maxseq);
+    for (int t = 0; t < T; t++)
+        if (toks[t] < 0 || toks[t] >= e->V) return set_err(e, MI_ERR_ARG, "mi_step: token %d out of range", toks[t]);
+    HIPCHK(e, hipMemcpyAsync(e->M.tokbuf + pos, toks, sizeof(int32_t) * T, hipMemcpyHostToDevice, e->stream));
+    int rc = run_step(e, pos, 1, logits != nullptr);
+    if (rc) return rc;
+    int32_t tok = 0;
+    float mg = 0.f;
+    HIPCHK(e, hipMemcpyAsync(&tok, e->M.out_tok + pos, 4, hipMemcpyDeviceToHost, e->stream));
+    HIPCHK(e, hipMemcpyAsync(&mg, e->M.out_margin + pos, 4, hipMemcpyDeviceToHost, e->stream));
+    if (logits) HIPCHK(e, hipMemcpyAsync(logits, e->M_logits.logits, sizeof(float) * e->V, hipMemcpyDeviceToHost, e->stream));
+    HIPCHK(e, hipStreamSynchronize(e->stream));
+    if (argmax) argmax[0] = tok;
+    if (margin) margin[0] = mg;
+    e->cur_len = pos + T;
+    e->next_ready = true;
+    return MI_OK;
+}
+
+int mi_prefill(mi_engine* e, const int32_t* ids, int32_t n, int32_t* first, float* margin) {
+    if (!e || !ids || n < 1) return MI_ERR_ARG;
+    if (n >= e->maxseq) return set_err(e, MI_ERR_ARG, "prompt of %d tokens exceeds the context capacity %d", n, e->maxseq);
+    for (int i = 0; i < n; i++)
+        if (ids[i] < 0 || ids[i] >= e->V) return set_err(e, MI_ERR_ARG, "prompt token %d out of range", ids[i]);
+    HIPCHK(e, hipMemcpyAsync(e->M.tokbuf, ids, sizeof(int32_t) * n, hipMemcpyHostToDevice, e->stream));
+    HIPCHK(e, hipEventRecord(e->ev0, e->stream));
+    for (int p = 0; p < n; p++) {
+        const int rc = run_step(e, p, p == n - 1, false);
+        if (rc) return rc;
+    }
+    HIPCHK(e, hipEventRecord(e->ev1, e->stream));
+    int32_t tok = 0;
+    float mg = 0.f;
+    HIPCHK(e, hipMemcpyAsync(&tok, e->M.out_tok + n - 1, 4, hipMemcpyDeviceToHost, e->stream));
+    HIPCHK(e, hipMemcpyAsync(&mg, e->M.out_margin + n - 1, 4, hipMemcpyDeviceToHost, e->stream));
+    HIPCHK(e, hipStreamSynchronize(e->stream));
+    float ms = 0.f;
+    HIPCHK(e, hipEventElapsedTime(&ms, e->ev0, e->ev1));
+    e->stats.prefill_ms = ms;
+    if (first) *first = tok;
+    if (margin) *margin = mg;
+    e->cur_len = n;
+    e->next_ready = true;
+    return MI_OK;
+}
+
+int mi_generate(mi_engine* e, int32_t n_gen, int32_t* out, float* margins, int32_t* n_out, mi_token_cb cb, void* user) {
+    if (!e || n_gen < 0) return MI_ERR_ARG;
+    if (!e->next_ready || e->cur_len < 1) return set_err(e, MI_ERR_STATE, "mi_generate needs mi_prefill first");
+    if (e->cur_len + n_gen > e->maxseq) return set_err(e, MI_ERR_ARG, "n_gen %d exceeds the context capacity", n_gen);
+    const int p0 = e->cur_len;                   // position of the first generated token
+    const bool sync_each = cb != nullptr || e->opts.stop_eos;
+    int emitted = 0;
+    auto fetch = [&](int pos, int32_t* t, float* m) -> int {
+        HIPCHK(e, hipMemcpyAsync(t, e->M.out_tok + pos, 4, hipMemcpyDeviceToHost, e->stream));
+        HIPCHK(e, hipMemcpyAsync(m, e->M.out_margin + pos, 4, hipMemcpyDeviceToHost, e->stream));
+        HIPCHK(e, hipStreamSynchronize(e->stream));
+        return MI_OK;
+    };
+    HIPCHK(e, hipEventRecord(e->ev0, e->stream));
+    int steps = 0;
+    if (!sync_each) {
+        for (int t = 1; t < n_gen; t++, steps++) {
+            const int rc = run_step(e, p0 + t - 1, 1, false);
+            if (rc) return rc;
+        }
+        HIPCHK(e, hipEventRecord(e->ev1, e->stream));
+        std::vector<int32_t> tk(n_gen > 0 ? n_gen : 1);
+        std::vector<float> mg(n_gen > 0 ? n_gen : 1);
+        if (n_gen > 0) {
+            HIPCHK(e, hipMemcpyAsync(tk.data(), e->M.out_tok + p0 - 1, sizeof(int32_t) * n_gen, hipMemcpyDeviceToHost, e->stream));
+            HIPCHK(e, hipMemcpyAsync(mg.data(), e->M.out_margin + p0 - 1, sizeof(float) * n_gen, hipMemcpyDeviceToHost, e->stream));
+        }
+        HIPCHK(e, hipStreamSynchronize(e->stream));
+        for (int t = 0; t < n_gen; t++) {
+            if (out) out[t] = tk[t];
+            if (margins) margins[t] = mg[t];
+        }
+        emitted = n_gen;
+    } else {
+        for (int t = 0; t < n_gen; t++) {
+            if (t > 0) {
+                const int rc = run_step(e, p0 + t - 1, 1, false);
+                if (rc) return rc;
+                steps++;
+            }
+            int32_t tok; float m;
+            const int rc = fetch(p0 + t - 1, &tok, &m);
+            if (rc) return rc;
+            if (out) out[t] = tok;
+            if (margins) margins[t] = m;
+            emitted++;
+            if ((cb && cb(tok, user)) || (e->opts.stop_eos && tok == e->eos)) break;
+        }
+        HIPCHK(e, hipEventRecord(e->ev1, e->stream));
+        HIPCHK(e, hipStreamSynchronize(e->stream));
+    }
+    float ms = 0.f;
+    HIPCHK(e, hipEventElapsedTime(&ms, e->ev0, e->ev1));
+    e->stats.decode_ms = ms;
+    e->stats.steps = steps;
+    e->stats.tokens = steps;
+    e->cur_len = p0 + steps;
+    if (n_out) *n_out = emitted;
+    return MI_OK;
+}
+
+int mi_time_phase(mi_engine* e, int32_t phase, int32_t layer, int32_t reps, double* avg_ms) {
+    if (!e || !avg_ms || phase < 0 || phase > 9 || layer < 0 || layer >= e->NL || reps < 1) return MI_ERR_ARG;
+    if (e->cur_len < 1) return set_err(e, MI_ERR_STATE, "mi_time_phase needs a completed step");
+    const int pos = e->cur_len - 1;
+    HIPCHK(e, hipEventRecord(e->ev0, e->stream));
+    for (int r = 0; r < reps; r++) launch_phase(e->M, e->pg, phase, layer, pos, 1, e->stream);
+    HIPCHK(e, hipGetLastError());
+    HIPCHK(e, hipEventRecord(e->ev1, e->stream));
+    HIPCHK(e, hipEventSynchronize(e->ev1));
+    float ms = 0.f;
+    HIPCHK(e, hipEventElapsedTime(&ms, e->ev0, e->ev1));
+    *avg_ms = ms / reps;
+    return MI_OK;
+}
+
+int mi_get_stats(const mi_engine* e, mi_stats* out) {
+    if (!e || !out) return MI_ERR_ARG;
+    *out = e->stats;
+    return MI_OK;
+}
+
+// ---------------------------------------------------------------- kernel-level entry points
+static int g_ncu = 0;
+static int ncu() {
+    if (!g_ncu) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&g_ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+            g_ncu = 256;
+    }
+    return g_ncu;
+}
+
+int mi_quant_q8(const float* x, int32_t n, int8_t* xq, float* xd, int32_t* xs8, void* stream) {
+    if (!x || !xq || !xd || !xs8 || n <= 0 || n % 32) return MI_ERR_ARG;
+    launch_quant(x, n, xq, xd, xs8, (hipStream_t)stream);
+    return hipGetLastError() == hipSuccess ? MI_OK : MI_ERR_DEVICE;
+}
+
+int mi_gemv_q4(const uint8_t* packed, int32_t rows, int32_t nb, int32_t cb, int32_t ks, const int8_t* xq,
+               const float* xd, const int32_t* xs8, float* part, float* y, void* stream) {
+    if (!packed || !xq || !xd || !xs8 || !part || !mi_q4_packed_bytes(rows, nb, cb) || ks < 1 || ks > nb / cb ||
+        nb * 32 > kMaxFF)
+        return MI_ERR_ARG;
+    const PMat W{packed, rows, nb, cb, nb / cb, ks};
+    launch_gemv(W, xq, xd, xs8, part, y, ncu(), (hipStream_t)stream);
+    return hipGetLastError() == hipSuccess ? MI_OK : MI_ERR_DEVICE;
+}
+
+int mi_q4_block_isums(const uint8_t* packed, int32_t rows, int32_t nb, int32_t cb, const int8_t* xq, int32_t* isum,
+                      void* stream) {
+    if (!packed || !xq || !isum || !mi_q4_packed_bytes(rows, nb, cb)) return MI_ERR_ARG;
+    const PMat W{packed, rows, nb, cb, nb / cb, 1};
+    launch_isums(W, xq, isum, (hipStream_t)stream);
+    return hipGetLastError() == hipSuccess ? MI_OK : MI_ERR_DEVICE;
+}
+
+int mi_attn_decode(const float* q, const uint16_t* kc, const uint16_t* vc, int32_t n_head, int32_t n_head_kv, int32_t hd,
+                   int32_t L, int32_t ctx, float scale, float* scratch, float* out, void* stream) {
+    if (!q || !kc || !vc || !scratch || !out || n_head < 1 || n_head_kv < 1 || L < 1 || L > ctx) return MI_ERR_ARG;
+    if (!launch_attn_decode(q, reinterpret_cast<const __half*>(kc), reinterpret_cast<const __half*>(vc), n_head,
+                            n_head_kv, hd, L, ctx, scale, scratch, out, (hipStream_t)stream))
+        return MI_ERR_SHAPE;
+    return hipGetLastError() == hipSuccess ? MI_OK : MI_ERR_DEVICE;
+}
+
+int mi_stream_read(const void* buf, size_t bytes, uint32_t* sink, void* stream) {
+    if (!buf || !sink || bytes % 16) return MI_ERR_ARG;
+    launch_stream(buf, bytes, sink, ncu(), (hipStream_t)stream);
+    return hipGetLastError() == hipSuccess ? MI_OK : MI_ERR_DEVICE;
+}
+
+int mi_stream_sync(void* stream) { return hipStreamSynchronize((hipStream_t)stream) == hipSuccess ? MI_OK : MI_ERR_DEVICE; }
+
+int mi_device_count(int32_t* n) {
+    int c = 0;
+    if (!n) return MI_ERR_ARG;
+    if (hipGetDeviceCount(&c) != hipSuccess) c = 0;
+    *n = c;
+    return MI_OK;
+}
+
+}  // extern "C"

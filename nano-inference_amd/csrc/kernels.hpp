@@ -1,0 +1,26 @@
+// kernels.hpp -- host-side launchers of the gfx950 kernels (kernels.hip).
+#pragma once
+#include "common.hpp"
+
+namespace mi {
+
+struct PhaseGrid { int qkv, fin, comb, o, gu, act, down, lm; };
+
+bool kernels_support(int G, int HD);
+PhaseGrid plan_phase_grid(const DModel& M, const DLayer& L0, int n_cu);
+// one decode step at position pos as one launch per phase; gen != 0 stores the
+// prediction as the token of position pos + 1
+void launch_step_phases(const DModel& M, const PhaseGrid& pg, int pos, int gen, hipStream_t s);
+
+// one phase kernel of the step at pos (the launch launch_step_phases makes)
+void launch_phase(const DModel& M, const PhaseGrid& pg, int phase, int l, int pos, int gen, hipStream_t s);
+
+void launch_quant(const float* x, int n, int8_t* xq, float* xd, int32_t* xs8, hipStream_t s);
+void launch_gemv(const PMat& W, const int8_t* xq, const float* xd, const int32_t* xs8, float* part, float* y,
+                 int n_cu, hipStream_t s);
+void launch_isums(const PMat& W, const int8_t* xq, int32_t* isum, hipStream_t s);
+bool launch_attn_decode(const float* q, const __half* kc, const __half* vc, int nh, int nkv, int hd, int L, int ctx,
+                        float scale, float* scratch, float* out, hipStream_t s);
+void launch_stream(const void* buf, size_t bytes, uint32_t* sink, int n_cu, hipStream_t s);
+
+}  // namespace mi

@@ -1,0 +1,276 @@
+"""Python host binding of the MI355X engine (ctypes over include/minfer.h).
+
+Mirrors the reference engine's interface for the batch-1 token loop: load a GGUF,
+prefill a prompt, step tokens, generate greedily (src/cuda_infer.cu:844-1200,
+src/mega.cu:1005-1243), with the same argument meaning: int32 token IDs,
+positions counted from 0, greedy argmax with the lowest index on ties. Failures
+raise MinferError carrying the engine's message instead of exiting. The library
+is the in-tree build (nano-inference_amd/_build/libminfer.so); there is no
+fallback: if it is missing, importing the engine raises.
+"""
+import ctypes as C
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.dirname(HERE)
+LIB_PATH = os.path.join(PKG, "_build", "libminfer.so")
+
+MI_OK = 0
+ERRORS = {-1: "argument", -2: "io", -3: "format", -4: "shape", -5: "device", -6: "oom", -7: "state"}
+
+
+class MinferError(RuntimeError):
+    def __init__(self, code, msg):
+        super().__init__("minfer %s error (%d): %s" % (ERRORS.get(code, "unknown"), code, msg))
+        self.code = code
+
+
+class Opts(C.Structure):
+    _fields_ = [("max_ctx", C.c_int32), ("tchunk", C.c_int32), ("spec", C.c_int32), ("ngmax", C.c_int32),
+                ("spec_slope", C.c_float), ("persistent", C.c_int32), ("stop_eos", C.c_int32), ("device", C.c_int32)]
+
+
+class ModelInfo(C.Structure):
+    _fields_ = [("n_layer", C.c_int32), ("n_embd", C.c_int32), ("n_ff", C.c_int32), ("n_head", C.c_int32),
+                ("n_head_kv", C.c_int32), ("head_dim", C.c_int32), ("n_vocab", C.c_int32), ("eos", C.c_int32),
+                ("rope_base", C.c_float), ("rms_eps", C.c_float), ("max_ctx", C.c_int32),
+                ("plan_cb", C.c_int32 * 5), ("plan_ks", C.c_int32 * 5), ("attn_chunk", C.c_int32),
+                ("kv_f16", C.c_int32), ("n_cu", C.c_int32), ("persistent", C.c_int32), ("weight_bytes", C.c_uint64)]
+
+
+class Stats(C.Structure):
+    _fields_ = [("steps", C.c_int32), ("tokens", C.c_int32), ("decode_ms", C.c_double), ("prefill_ms", C.c_double)]
+
+
+class SynthShape(C.Structure):
+    _fields_ = [("n_layer", C.c_int32), ("n_embd", C.c_int32), ("n_ff", C.c_int32), ("n_head", C.c_int32),
+                ("n_head_kv", C.c_int32), ("n_vocab", C.c_int32), ("rope_base", C.c_float), ("rms_eps", C.c_float),
+                ("emb_type", C.c_int32)]
+
+
+TOKEN_CB = C.CFUNCTYPE(C.c_int, C.c_int32, C.c_void_p)
+
+# every symbol include/minfer.h declares, with its ctypes signature
+_P = C.c_void_p
+SIGNATURES = {
+    "mi_default_opts": (None, [C.POINTER(Opts)]),
+    "mi_load": (C.c_int, [C.c_char_p, C.POINTER(Opts), C.POINTER(_P)]),
+    "mi_free": (None, [_P]),
+    "mi_last_error": (C.c_char_p, [_P]),
+    "mi_info": (C.c_int, [_P, C.POINTER(ModelInfo)]),
+    "mi_prefill": (C.c_int, [_P, C.POINTER(C.c_int32), C.c_int32, C.POINTER(C.c_int32), C.POINTER(C.c_float)]),
+    "mi_step": (C.c_int, [_P, C.POINTER(C.c_int32), C.c_int32, C.c_int32, C.POINTER(C.c_int32),
+                          C.POINTER(C.c_float), C.POINTER(C.c_float)]),
+    "mi_generate": (C.c_int, [_P, C.c_int32, C.POINTER(C.c_int32), C.POINTER(C.c_float), C.POINTER(C.c_int32),
+                              TOKEN_CB, _P]),
+    "mi_get_stats": (C.c_int, [_P, C.POINTER(Stats)]),
+    "mi_time_phase": (C.c_int, [_P, C.c_int32, C.c_int32, C.c_int32, C.POINTER(C.c_double)]),
+    "mi_synth_gguf": (C.c_int, [C.c_char_p, C.POINTER(SynthShape), C.c_uint64]),
+    "mi_q4_packed_bytes": (C.c_size_t, [C.c_int32, C.c_int32, C.c_int32]),
+    "mi_q4_pack": (C.c_int, [_P, C.c_int32, C.c_int32, C.c_int32, _P]),
+    "mi_quant_q8": (C.c_int, [_P, C.c_int32, _P, _P, _P, _P]),
+    "mi_gemv_q4": (C.c_int, [_P, C.c_int32, C.c_int32, C.c_int32, C.c_int32, _P, _P, _P, _P, _P, _P]),
+    "mi_q4_block_isums": (C.c_int, [_P, C.c_int32, C.c_int32, C.c_int32, _P, _P, _P]),
+    "mi_attn_decode": (C.c_int, [_P, _P, _P, C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_float,
+                                 _P, _P, _P]),
+    "mi_stream_read": (C.c_int, [_P, C.c_size_t, _P, _P]),
+    "mi_stream_sync": (C.c_int, [_P]),
+    "mi_device_count": (C.c_int, [C.POINTER(C.c_int32)]),
+}
+
+_lib = None
+
+
+def lib():
+    """Load libminfer.so (raises if it was not built: no fallback path exists)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise MinferError(-5, "engine library not built: %s (run __graft_entry__.build())" % LIB_PATH)
+        L = C.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = L
+    return _lib
+
+
+def _check(rc, eng=None):
+    if rc != MI_OK:
+        msg = lib().mi_last_error(eng)
+        raise MinferError(rc, msg.decode() if msg else "")
+
+
+# shapes of BASELINE.json's configs (E, layers, heads/kv, FF, vocab)
+SHAPES = {
+    "S05": dict(n_layer=24, n_embd=896, n_ff=4864, n_head=14, n_head_kv=2, n_vocab=151936),
+    "S15": dict(n_layer=28, n_embd=1536, n_ff=8960, n_head=12, n_head_kv=2, n_vocab=151936),
+    "S3": dict(n_layer=36, n_embd=2048, n_ff=11008, n_head=16, n_head_kv=2, n_vocab=151936),
+}
+
+
+def synth_gguf(path, shape, seed, rope_base=1e6, rms_eps=1e-6, emb_q4=False):
+    """Write a seeded random-init qwen2 GGUF (mi_synth_gguf). shape: name or dict."""
+    d = SHAPES[shape] if isinstance(shape, str) else shape
+    s = SynthShape(d["n_layer"], d["n_embd"], d["n_ff"], d["n_head"], d["n_head_kv"], d["n_vocab"],
+                   rope_base, rms_eps, 2 if emb_q4 else 0)
+    _check(lib().mi_synth_gguf(path.encode(), C.byref(s), C.c_uint64(seed)))
+    return path
+
+
+def default_opts(**kw):
+    o = Opts()
+    lib().mi_default_opts(C.byref(o))
+    for k, v in kw.items():
+        setattr(o, k, v)
+    return o
+
+
+def _i32(seq):
+    seq = [int(x) for x in seq]
+    return (C.c_int32 * max(len(seq), 1))(*seq)
+
+
+class Engine:
+    """One loaded model on one GPU: load / prefill / step / generate."""
+
+    def __init__(self, path, **opts):
+        self._h = C.c_void_p()
+        o = default_opts(**opts)
+        rc = lib().mi_load(path.encode(), C.byref(o), C.byref(self._h))
+        _check(rc, None)
+        self.info = ModelInfo()
+        _check(lib().mi_info(self._h, C.byref(self.info)), self._h)
+
+    def close(self):
+        if self._h:
+            lib().mi_free(self._h)
+            self._h = C.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+    @property
+    def plan(self):
+        i = self.info
+        return dict(cb=list(i.plan_cb), ks=list(i.plan_ks), attn_chunk=i.attn_chunk, kv_f16=i.kv_f16)
+
+    def prefill(self, ids):
+        first, mg = C.c_int32(), C.c_float()
+        _check(lib().mi_prefill(self._h, _i32(ids), len(ids), C.byref(first), C.byref(mg)), self._h)
+        return first.value, mg.value
+
+    def step(self, tok, pos, want_logits=False):
+        am, mg = (C.c_int32 * 1)(), (C.c_float * 1)()
+        lg = (C.c_float * self.info.n_vocab)() if want_logits else None
+        _check(lib().mi_step(self._h, _i32([tok]), 1, pos, am, mg, lg), self._h)
+        if want_logits:
+            import numpy as np
+            return am[0], mg[0], np.frombuffer(lg, dtype=np.float32).copy()
+        return am[0], mg[0]
+
+    def generate(self, n_gen, callback=None):
+        out = (C.c_int32 * max(n_gen, 1))()
+        mg = (C.c_float * max(n_gen, 1))()
+        n = C.c_int32()
+        cb = TOKEN_CB(lambda t, u: int(bool(callback(t)))) if callback else TOKEN_CB()
+        _check(lib().mi_generate(self._h, n_gen, out, mg, C.byref(n), cb, None), self._h)
+        return list(out[:n.value]), list(mg[:n.value])
+
+    PHASES = ["qkv", "qkv_fin", "attn", "attn_comb", "o", "gate_up", "act", "down", "lm_head", "argmax"]
+
+    def time_phase(self, phase, layer=0, reps=20):
+        """mean duration (ms) of one phase kernel of the last step, from HIP events"""
+        ph = self.PHASES.index(phase) if isinstance(phase, str) else phase
+        ms = C.c_double()
+        _check(lib().mi_time_phase(self._h, ph, layer, reps, C.byref(ms)), self._h)
+        return ms.value
+
+    def stats(self):
+        s = Stats()
+        _check(lib().mi_get_stats(self._h, C.byref(s)), self._h)
+        return dict(steps=s.steps, tokens=s.tokens, decode_ms=s.decode_ms, prefill_ms=s.prefill_ms)
+
+
+# ---------------------------------------------------------------- kernel-level helpers
+def packed_bytes(rows, nb, cb):
+    return lib().mi_q4_packed_bytes(rows, nb, cb)
+
+
+def pack_q4(src_bytes, rows, nb, cb):
+    """GGUF row-major q4_0 bytes (numpy uint8) -> tile layout (numpy uint8)."""
+    import numpy as np
+    src = np.ascontiguousarray(src_bytes, dtype=np.uint8)
+    n = packed_bytes(rows, nb, cb)
+    if n == 0 or src.size != rows * nb * 18:
+        raise MinferError(-1, "bad q4 matrix shape")
+    dst = np.empty(n, dtype=np.uint8)
+    _check(lib().mi_q4_pack(src.ctypes.data, rows, nb, cb, dst.ctypes.data))
+    return dst
+
+
+def _ptr(t):
+    return C.c_void_p(t.data_ptr()) if t is not None else C.c_void_p()
+
+
+def _stream(stream):
+    if stream is None:
+        import torch
+        stream = torch.cuda.current_stream()
+    return C.c_void_p(stream.cuda_stream)
+
+
+def quant_q8(x, xq, xd, xs8, stream=None):
+    _check(lib().mi_quant_q8(_ptr(x), x.numel(), _ptr(xq), _ptr(xd), _ptr(xs8), _stream(stream)))
+
+
+def gemv_q4(packed, rows, nb, cb, ks, xq, xd, xs8, part, y=None, stream=None):
+    _check(lib().mi_gemv_q4(_ptr(packed), rows, nb, cb, ks, _ptr(xq), _ptr(xd), _ptr(xs8), _ptr(part), _ptr(y),
+                            _stream(stream)))
+
+
+def q4_block_isums(packed, rows, nb, cb, xq, isum, stream=None):
+    _check(lib().mi_q4_block_isums(_ptr(packed), rows, nb, cb, _ptr(xq), _ptr(isum), _stream(stream)))
+
+
+def attn_decode(q, kc, vc, n_head, n_head_kv, hd, L, ctx, scale, scratch, out, stream=None):
+    _check(lib().mi_attn_decode(_ptr(q), _ptr(kc), _ptr(vc), n_head, n_head_kv, hd, L, ctx, C.c_float(scale),
+                                _ptr(scratch), _ptr(out), _stream(stream)))
+
+
+def stream_read(buf, nbytes, sink, stream=None):
+    _check(lib().mi_stream_read(_ptr(buf), C.c_size_t(nbytes), _ptr(sink), _stream(stream)))
+
+
+# ---------------------------------------------------------------- seeded inputs
+def prompt_ids(seed, n, n_vocab):
+    """n token IDs uniform in [0, n_vocab) from a splitmix64 stream (same on any host)."""
+    mask = (1 << 64) - 1
+    s = (seed * 0x9E3779B97F4A7C15 + 0x632BE59BD9B4E019) & mask
+    out = []
+    for _ in range(n):
+        s = (s + 0x9E3779B97F4A7C15) & mask
+        z = s
+        z = ((z ^ (z >> 30)) * 0xBF58476D1CE4E5B9) & mask
+        z = ((z ^ (z >> 27)) * 0x94D049BB133111EB) & mask
+        z ^= z >> 31
+        out.append(int((z * n_vocab) >> 64))
+    return out
+
+
+# the BASELINE configs as (shape, model seed, prompt seed, prompt length, n_gen)
+CONFIGS = {
+    "config0": ("S05", 1000, 1001, 16, 128),
+    "config2": ("S15", 2000, 2001, 64, 128),
+    "config4": ("S3", 4000, 4001, 1024, 8),
+}

@@ -1,0 +1,127 @@
+/* oracle.h -- CPU restatement of minfer's batch-1 decode path.
+ *
+ * TEST INFRASTRUCTURE ONLY. Nothing in the product (nano-inference_amd/) links,
+ * loads or calls this library; only tests/, __graft_entry__.smoke() and the
+ * cpu_baseline leg of bench.py use it, and only as the checker or the timed CPU
+ * baseline. It is plain C11 + OpenMP, built by oracle/Makefile.
+ *
+ * Two forward modes over the same GGUF file:
+ *
+ *   ORC_FP32  -- cpu_infer.cpp semantics (src/cpu_infer.cpp:16-167): every
+ *                matvec dequantizes a q4_0 row to fp32 and dots it with fp32
+ *                activations (:22-32), RMSNorm sums squares in double (:40-46),
+ *                RoPE uses powf/cosf/sinf (:49-61), fp32 KV cache, softmax with
+ *                expf (:121-140), SiLU with expf (:147), first-max argmax
+ *                (:153-154). Pinned by the token streams of the reference
+ *                cpu_infer compiled from /root/reference (tests/golden).
+ *
+ *   ORC_Q8ACT -- the GPU engine's numerics, written as a fixed sequence of
+ *                IEEE-754 binary32 operations so that a GPU implementation can
+ *                match it bit for bit. It follows the reference's int8
+ *                activation path: per-32 symmetric int8 quantization
+ *                (cuda_infer.cu:80-89, mega.cu:303-325), q4_0 x int8 block sums
+ *                with the -8 offset folded out (cuda_infer.cu:108-121,
+ *                mega.cu:157-165), and the explicitly rounded block accumulate
+ *                acc = fma(dw*dx, float(isum - 8*sum(x)), acc) (mega.cu:153-155).
+ *                Float reduction orders, which the reference leaves to its
+ *                kernels, are fixed here and parameterized by orc_plan.
+ *
+ * Parity status of each function is stated at its definition; every function
+ * below is pinned by a check in tests/test_oracle_*.py (closed forms, brute
+ * force on small inputs, libm/numpy comparisons, reference token streams).
+ */
+#ifndef MINFER_ORACLE_H
+#define MINFER_ORACLE_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---------------- GGUF v3 reader (restates src/gguf.h:19-222) ---------------- */
+enum { ORC_F32 = 0, ORC_F16 = 1, ORC_Q4_0 = 2, ORC_Q8_0 = 8 };
+
+typedef struct {
+    uint32_t type;
+    int32_t nd;
+    int64_t ne[4];          /* ne[0] = contiguous row length (gguf.h:56) */
+    const uint8_t* data;
+} orc_tensor;
+
+typedef struct orc_gguf orc_gguf;
+
+orc_gguf* orc_gguf_open(const char* path);             /* NULL on any parse error */
+void orc_gguf_close(orc_gguf* g);
+double orc_gguf_num(const orc_gguf* g, const char* key, double def);
+int64_t orc_gguf_n_tokens(const orc_gguf* g);
+const orc_tensor* orc_gguf_tensor(const orc_gguf* g, const char* name);  /* NULL if absent */
+const char* orc_gguf_error(void);
+
+/* ---------------- scalar building blocks ---------------- */
+float orc_f16_to_f32(uint16_t h);                       /* gguf.h:37-52 */
+uint16_t orc_f32_to_f16(float f);                       /* IEEE round-to-nearest-even */
+void orc_dequant_row(const orc_tensor* t, int64_t r, float* out);   /* gguf.h:85-102 (F32/F16/Q4_0/Q8_0) */
+float orc_expf(float x);                                /* the engine's exp: Cody-Waite + Taylor-7 */
+
+/* per-32 int8 quantization of n floats (n % 32 == 0): xq[n], xd[n/32], xs8[n/32] = 8*sum(q) */
+void orc_quant_q8(const float* x, int n, int8_t* xq, float* xd, int32_t* xs8);
+/* q4_0 block (18 B: fp16 d + 16 B) x 32 int8: sum_j n_j*x_j with n_j in 0..15 */
+int32_t orc_q4_block_isum(const uint8_t* blk, const int8_t* x32);
+/* one row of q4_0 blocks (row-major GGUF layout) in the canonical accumulation order:
+ * nb blocks, chunks of cb blocks, ks contiguous segments of chunks summed left to right */
+float orc_q4_row_dot(const uint8_t* row, int nb, int cb, int ks,
+                     const int8_t* xq, const float* xd, const int32_t* xs8);
+/* canonical RMSNorm (64 lane partials + xor butterfly), n % 64 == 0 */
+void orc_rmsnorm_canon(const float* x, const float* w, int n, float eps, float* out);
+/* sum of 64 values by the xor butterfly (offsets 32,16,8,4,2,1), value of lane 0 */
+float orc_butterfly64(const float* v);
+
+/* ---------------- model ---------------- */
+enum { ORC_MODE_FP32 = 0, ORC_MODE_Q8ACT = 1 };
+enum { ORC_MAT_QKV = 0, ORC_MAT_O = 1, ORC_MAT_GU = 2, ORC_MAT_DOWN = 3, ORC_MAT_LM = 4, ORC_NMAT = 5 };
+
+typedef struct {
+    int32_t cb[ORC_NMAT];   /* blocks per chunk (4 or 8) */
+    int32_t ks[ORC_NMAT];   /* contiguous K segments per row */
+    int32_t attn_chunk;     /* positions per attention partial (64) */
+    int32_t kv_f16;         /* 1: K/V rounded to fp16 before they are cached */
+} orc_plan;
+
+typedef struct {
+    int32_t n_layer, n_embd, n_ff, n_head, n_head_kv, head_dim, n_vocab;
+    float rope_base, rms_eps;
+} orc_config;
+
+typedef struct orc_model orc_model;
+
+/* mode: ORC_MODE_FP32 or ORC_MODE_Q8ACT; plan may be NULL for FP32.
+ * n_threads <= 0: OpenMP default. */
+orc_model* orc_model_new(const orc_gguf* g, int mode, const orc_plan* plan, int max_seq, int n_threads);
+void orc_model_free(orc_model* m);
+void orc_model_config(const orc_model* m, orc_config* out);
+/* one token at position pos (positions must arrive in order 0,1,2,...; a smaller pos
+ * rewinds). logits (nullable) receives n_vocab floats. Returns the argmax (lowest
+ * index on ties) and the margin best - second. Returns -1 on error. */
+int32_t orc_forward(orc_model* m, int32_t token, int32_t pos, float* logits, float* margin);
+
+/* greedy decode exactly like cpu_infer main (cpu_infer.cpp:161-167): prefill the
+ * prompt one token at a time, then n_gen tokens. out[n_gen]. Wall times in seconds. */
+int orc_generate(orc_model* m, const int32_t* prompt, int32_t n_prompt, int32_t n_gen,
+                 int32_t* out, float* margins, double* t_prefill, double* t_decode);
+
+/* ---------------- kernel-level references ---------------- */
+/* attention of one query head over cached fp32 K/V rows (already fp16-rounded values
+ * when the plan says so): q[hd], k/v rows at stride `stride` floats, positions 0..L-1 */
+void orc_attention_canon(const float* q, const float* k, const float* v, int L, int hd,
+                         int stride, float scale, int chunk, float* out);
+/* the same attention with cpu_infer's loop (cpu_infer.cpp:121-140) */
+void orc_attention_fp32(const float* q, const float* k, const float* v, int L, int hd,
+                        int stride, float scale, float* out);
+/* RoPE cos/sin for (pos, i) exactly as cpu_infer computes them (cpu_infer.cpp:54-55) */
+void orc_rope_cs(int pos, int i, int hd, float base, float* c, float* s);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

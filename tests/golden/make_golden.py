@@ -1,0 +1,65 @@
+"""Write the golden token streams of the reference cpu_infer (test fixtures).
+
+Runs in the authoring container only: it needs /root/reference (the reference
+cpu_infer is compiled from its own sources by `make -C oracle ref`) and writes
+small JSON fixtures here. The GGUF inputs are regenerated bit-identically from
+their seeds by mi_synth_gguf; the fixture records the file's xxh64 so a test can
+prove the regeneration.
+
+    python tests/golden/make_golden.py [config0] [config2] [tiny]
+"""
+import json
+import os
+import subprocess
+import sys
+import time
+
+import xxhash
+
+ROOT = os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
+sys.path.insert(0, os.path.join(ROOT, "nano-inference_amd"))
+import minfer  # noqa: E402
+
+REF = os.path.join(ROOT, "oracle", "_ref", "cpu_infer")
+TMP = os.environ.get("MI_TMP", "/tmp/mi")
+TINY = dict(n_layer=2, n_embd=256, n_ff=512, n_head=4, n_head_kv=2, n_vocab=4096)
+
+
+def file_hash(path):
+    h = xxhash.xxh64()
+    with open(path, "rb") as f:
+        while True:
+            b = f.read(1 << 24)
+            if not b:
+                break
+            h.update(b)
+    return h.hexdigest()
+
+
+def run(name, shape, mseed, pseed, n_prompt, n_gen):
+    os.makedirs(TMP, exist_ok=True)
+    path = os.path.join(TMP, "%s.gguf" % name)
+    minfer.synth_gguf(path, shape, mseed)
+    V = (minfer.SHAPES[shape] if isinstance(shape, str) else shape)["n_vocab"]
+    ids = minfer.prompt_ids(pseed, n_prompt, V)
+    t = time.time()
+    r = subprocess.run([REF, path, str(n_gen)] + [str(i) for i in ids], capture_output=True, text=True, check=True)
+    toks = [int(x) for x in r.stdout.split()]
+    fx = dict(config=name, shape=shape, model_seed=mseed, prompt_seed=pseed, prompt=ids, n_gen=n_gen,
+              tokens=toks, gguf_xxh64=file_hash(path), gguf_bytes=os.path.getsize(path),
+              source="reference src/cpu_infer.cpp built by oracle/Makefile (g++ -std=gnu++17 -O3 -march=native -fopenmp)",
+              ref_seconds=round(time.time() - t, 1))
+    out = os.path.join(os.path.dirname(os.path.abspath(__file__)), "cpu_infer_%s.json" % name)
+    with open(out, "w") as f:
+        json.dump(fx, f, indent=1)
+    print(name, "->", out, fx["ref_seconds"], "s")
+
+
+if __name__ == "__main__":
+    which = sys.argv[1:] or ["tiny", "config0", "config2"]
+    for w in which:
+        if w == "tiny":
+            run("tiny", TINY, 7, 8, 8, 64)
+        else:
+            shape, ms, ps, npr, ng = minfer.CONFIGS[w]
+            run(w, shape, ms, ps, npr, ng)

@@ -1,0 +1,126 @@
+"""GPU parity of the whole decode step (engine, through the C ABI) against the
+CPU oracle in q8act mode with the engine's own reduction plan.
+
+Bar: logits bit-identical at every position (hence within any 1e-3 tolerance),
+greedy token streams identical over 128 steps. Agreement with the fp32
+cpu_infer semantics is reported as tokens-to-first-divergence plus the margin
+there (the int8 activations make exact agreement with fp32 a matter of luck).
+"""
+import json
+import os
+import sys
+
+import numpy as np
+import pytest
+
+import minfer
+import oracle_lib as O
+from conftest import synth_cached
+
+pytestmark = pytest.mark.gpu
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+TINY = dict(n_layer=2, n_embd=256, n_ff=512, n_head=4, n_head_kv=2, n_vocab=4096)
+SMALL = dict(n_layer=3, n_embd=512, n_ff=1536, n_head=8, n_head_kv=2, n_vocab=8192)
+
+
+def say(*a):
+    print("[gpu-engine]", *a, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module", autouse=True)
+def gpu():
+    import torch
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+
+
+def plan_of(eng):
+    p = eng.plan
+    return O.Plan.make(p["cb"], p["ks"], p["attn_chunk"], p["kv_f16"])
+
+
+def golden(name):
+    with open(os.path.join(GOLDEN, "cpu_infer_%s.json" % name)) as f:
+        return json.load(f)
+
+
+@pytest.mark.parametrize("shape,seed", [(TINY, 7), (SMALL, 21)])
+def test_step_logits_bit_exact(shape, seed):
+    path = synth_cached("eng-%d" % shape["n_embd"], shape, seed)
+    say("step logits", path)
+    eng = minfer.Engine(path, max_ctx=256)
+    orc = O.Model(path, O.MODE_Q8ACT, plan=plan_of(eng), max_seq=256)
+    toks = minfer.prompt_ids(seed, 12, shape["n_vocab"])
+    nxt = None
+    for pos in range(80):
+        tok = toks[pos] if pos < len(toks) else nxt
+        a, ma, la = eng.step(tok, pos, want_logits=True)
+        b, mb, lb = orc.forward(tok, pos, True)
+        assert np.array_equal(la.view(np.uint32), lb.view(np.uint32)), "logits differ at pos %d" % pos
+        assert a == b and ma == mb
+        nxt = a
+    eng.close()
+
+
+def run_stream(path, prompt, n_gen, max_ctx=512):
+    eng = minfer.Engine(path, max_ctx=max_ctx)
+    first, _ = eng.prefill(prompt)
+    toks, margins = eng.generate(n_gen)
+    assert toks[0] == first
+    plan = plan_of(eng)
+    eng.close()
+    return toks, margins, plan
+
+
+def first_divergence(a, b):
+    for i, (x, y) in enumerate(zip(a, b)):
+        if x != y:
+            return i
+    return min(len(a), len(b))
+
+
+def test_tiny_stream_128():
+    fx = golden("tiny")
+    path = synth_cached("tiny", fx["shape"], fx["model_seed"])
+    say("tiny stream 128")
+    toks, margins, plan = run_stream(path, fx["prompt"], 128)
+    orc = O.Model(path, O.MODE_Q8ACT, plan=plan, max_seq=len(fx["prompt"]) + 130)
+    rt, rm, _, _ = orc.generate(fx["prompt"], 128)
+    assert toks == rt
+    assert np.array_equal(np.float32(margins).view(np.uint32), np.float32(rm).view(np.uint32))
+    d = first_divergence(toks, fx["tokens"])
+    say("tiny vs fp32 cpu_infer: first divergence at %d of %d" % (d, len(fx["tokens"])))
+
+
+@pytest.mark.parametrize("name", ["config0", "config2"])
+def test_config_stream_128(name):
+    fx = golden(name)
+    path = synth_cached(fx["config"], fx["shape"], fx["model_seed"])
+    say("%s stream 128 (prompt %d)" % (name, len(fx["prompt"])))
+    toks, margins, plan = run_stream(path, fx["prompt"], 128)
+    say("%s engine done; running the q8act oracle on the CPU" % name)
+    orc = O.Model(path, O.MODE_Q8ACT, plan=plan, max_seq=len(fx["prompt"]) + 130)
+    rt, rm, _, _ = orc.generate(fx["prompt"], 128)
+    assert toks == rt, "first difference at %d" % first_divergence(toks, rt)
+    assert np.array_equal(np.float32(margins).view(np.uint32), np.float32(rm).view(np.uint32))
+    d = first_divergence(toks, fx["tokens"])
+    say("%s vs fp32 cpu_infer: first divergence at %d of 128 (margin there %.4f)"
+        % (name, d, margins[d] if d < len(margins) else float("nan")))
+
+
+def test_rewind_and_restep():
+    path = synth_cached("eng-256", TINY, 7)
+    say("rewind")
+    eng = minfer.Engine(path, max_ctx=128)
+    ids = minfer.prompt_ids(5, 10, TINY["n_vocab"])
+    first, _ = eng.prefill(ids)
+    a, _, la = eng.step(first, len(ids), want_logits=True)
+    # rewind one position and step the same token again: identical logits
+    b, _, lb = eng.step(first, len(ids), want_logits=True)
+    assert a == b and np.array_equal(la, lb)
+    with pytest.raises(minfer.MinferError):
+        eng.step(first, len(ids) + 5)              # beyond the current length
+    with pytest.raises(minfer.MinferError):
+        eng.step(TINY["n_vocab"], 3)                # token out of range
+    eng.close()

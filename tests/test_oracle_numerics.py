@@ -1,0 +1,187 @@
+"""Pins the oracle's scalar building blocks against mathematics and numpy.
+
+Each check is chosen so that a plausible mistake in the oracle (wrong rounding
+mode, swapped nibble order, dropped -8 term, wrong reduction, wrong exp range
+reduction) fails it. None of these call the GPU.
+"""
+import math
+
+import numpy as np
+import pytest
+
+import oracle_lib as O
+
+RNG = np.random.default_rng(1234)
+
+
+def ulp_dist(a, b):
+    a = np.asarray(a, np.float32).view(np.int32).astype(np.int64)
+    b = np.asarray(b, np.float32).view(np.int32).astype(np.int64)
+    a = np.where(a < 0, -(a & 0x7FFFFFFF), a)
+    b = np.where(b < 0, -(b & 0x7FFFFFFF), b)
+    return np.abs(a - b)
+
+
+def test_f16_to_f32_all_patterns():
+    L = O.lib()
+    bits = np.arange(65536, dtype=np.uint16)
+    ref = bits.view(np.float16).astype(np.float32)
+    got = np.array([L.orc_f16_to_f32(int(b)) for b in bits], np.float32)
+    fin = np.isfinite(ref)
+    assert np.array_equal(got[fin].view(np.uint32), ref[fin].view(np.uint32))
+    assert np.all(np.isinf(got[np.isinf(ref)])) and np.all(np.isnan(got[np.isnan(ref)]))
+
+
+def test_f32_to_f16_round_nearest_even():
+    L = O.lib()
+    x = np.concatenate([
+        RNG.standard_normal(20000).astype(np.float32) * np.float32(2.0) ** RNG.integers(-30, 17, 20000).astype(np.float32),
+        # exact ties between two halves: midpoints of consecutive fp16 values (normal and subnormal)
+        ((np.arange(1, 2000, dtype=np.float32) + 0.5) * np.float32(2.0 ** -24)),
+        ((np.arange(1024, 2047, dtype=np.float32) + 0.5) * np.float32(2.0 ** -10)),
+        np.array([65504.0, 65519.99, 65520.0, 1e9, -1e9, 0.0, -0.0, 2.0 ** -25, 2.0 ** -26], np.float32),
+    ])
+    ref = x.astype(np.float16).view(np.uint16)
+    got = np.array([L.orc_f32_to_f16(float(v)) for v in x], np.uint16)
+    assert np.array_equal(got, ref)
+
+
+def test_expf_against_libm():
+    xs = np.concatenate([np.linspace(-87.0, 88.7, 200001, dtype=np.float32),
+                         RNG.uniform(-20, 20, 50000).astype(np.float32)])
+    got = np.array([O.expf(float(v)) for v in xs], np.float32)
+    ref = np.exp(xs.astype(np.float64)).astype(np.float32)
+    assert ulp_dist(got, ref).max() <= 2
+    assert O.expf(0.0) == 1.0
+    assert O.expf(-87.5) == 0.0 and O.expf(-1000.0) == 0.0
+    assert math.isinf(O.expf(89.0)) and O.expf(88.72) < math.inf
+    assert math.isnan(O.expf(float("nan")))
+
+
+def test_quant_q8_properties():
+    x = (RNG.standard_normal(32 * 400) * np.repeat(RNG.uniform(0.01, 10, 400), 32)).astype(np.float32)
+    x[:32] = 0.0                                     # all-zero block
+    xq, xd, xs8 = O.quant_q8(x)
+    blocks = x.reshape(-1, 32).astype(np.float64)
+    q = xq.reshape(-1, 32).astype(np.int64)
+    amax = np.abs(blocks).max(1)
+    assert np.all(np.abs(q) <= 127)
+    assert np.array_equal(xs8, 8 * q.sum(1))
+    assert np.all(q[0] == 0) and xd[0] == 0.0
+    nz = amax > 0
+    # the largest element maps to +-127, scales are fp16(amax/127) (relative 2^-11)
+    assert np.all(np.abs(q[nz]).max(1) == 127)
+    assert np.all(np.abs(xd[nz] / (amax[nz] / 127.0) - 1) <= 2.0 ** -11 + 1e-7)
+    # round to nearest: |x*127/amax - q| <= 1/2 (+ float slack)
+    frac = np.abs(blocks[nz] * (127.0 / amax[nz])[:, None] - q[nz])
+    assert frac.max() <= 0.5 + 1e-4
+
+
+def test_quant_q8_ties_to_even():
+    # amax 127 makes the scale exactly 1, so x = k + 0.5 is an exact tie
+    x = np.zeros(32, np.float32)
+    x[0] = 127.0
+    x[1:9] = [0.5, 1.5, 2.5, -0.5, -1.5, -2.5, 3.5, 4.5]
+    xq, xd, _ = O.quant_q8(x)
+    assert xq[:9].tolist() == [127, 0, 2, 2, 0, -2, -2, 4, 4]
+    assert xd[0] == 1.0
+
+
+def make_block(d, nibbles):
+    """q4_0 block bytes: fp16 d, byte j = nibble[j] | nibble[j+16] << 4 (gguf.h:94-101)."""
+    n = np.asarray(nibbles, np.uint8)
+    b = np.zeros(18, np.uint8)
+    b[:2] = np.frombuffer(np.float16(d).tobytes(), np.uint8)
+    b[2:] = n[:16] | (n[16:] << 4)
+    return b
+
+
+def test_q4_block_layout_known_answer():
+    # byte 0 = 0x9F: element 0 is the low nibble (15 -> +7), element 16 the high (9 -> +1)
+    blk = np.zeros(18, np.uint8)
+    blk[:2] = np.frombuffer(np.float16(1.0).tobytes(), np.uint8)
+    blk[2] = 0x9F
+    blk[3:] = 0x88                                   # all other elements (8 - 8) = 0
+    x = np.zeros(32, np.int8)
+    x[0], x[16] = 3, 5
+    isum = O.lib().orc_q4_block_isum(O.ptr(blk), O.ptr(x))
+    # sum n_j x_j = 15*3 + 9*5 (+ 8*x of every other element that is zero)
+    assert isum == 15 * 3 + 9 * 5
+
+
+def test_q4_block_isum_all_pairs():
+    # every nibble value against every int8 value, in every element position
+    L = O.lib()
+    xs = np.arange(-128, 128, dtype=np.int64)
+    for pos in (0, 7, 15, 16, 23, 31):
+        for nib in range(16):
+            nibbles = np.full(32, 8, np.uint8)
+            nibbles[pos] = nib
+            blk = make_block(1.0, nibbles)
+            for xv in xs[::5].tolist() + [-128, 127]:
+                x = np.zeros(32, np.int8)
+                x[pos] = xv
+                x[(pos + 1) % 32] = 1
+                got = L.orc_q4_block_isum(O.ptr(blk), O.ptr(x))
+                assert got == nib * xv + 8 * 1
+
+
+def test_q4_row_dot_matches_float64():
+    nb = 48
+    for cb, ks in [(8, 1), (8, 6), (4, 5), (8, 4)]:
+        blocks = np.stack([make_block(abs(RNG.normal(0, 0.002)), RNG.integers(0, 16, 32)) for _ in range(nb)])
+        x = RNG.standard_normal(nb * 32).astype(np.float32)
+        xq, xd, xs8 = O.quant_q8(x)
+        got = O.row_dot(blocks.reshape(-1), nb, cb, ks, xq, xd, xs8)
+        # float64 reference from the dequantized block values and the int8 activations
+        nib = np.concatenate([blocks[:, 2:] & 15, blocks[:, 2:] >> 4], axis=1).astype(np.float64)
+        d = blocks[:, :2].copy().view(np.float16).astype(np.float64).ravel()
+        terms = (d * xd.astype(np.float64))[:, None] * (nib - 8) * xq.reshape(nb, 32)
+        ref = terms.sum()
+        assert abs(got - ref) <= 1e-5 * np.abs(terms).sum(), (cb, ks, got, ref)
+
+
+def test_rmsnorm_canon_matches_float64():
+    for n in (896, 1536, 2048):
+        x = RNG.standard_normal(n).astype(np.float32) * 3
+        w = RNG.standard_normal(n).astype(np.float32) * 0.02
+        got = O.rmsnorm_canon(x, w, 1e-6)
+        xd = x.astype(np.float64)
+        ref = xd / np.sqrt((xd * xd).mean() + 1e-6) * w
+        assert np.abs(got - ref).max() <= 3e-6 * np.abs(ref).max()
+
+
+def test_butterfly64_sum():
+    v = RNG.standard_normal(64).astype(np.float32)
+    got = O.lib().orc_butterfly64(O.ptr(v))
+    assert abs(got - math.fsum(v.astype(np.float64))) <= 1e-5 * np.abs(v).sum()
+    ones = np.ones(64, np.float32)
+    assert O.lib().orc_butterfly64(O.ptr(ones)) == 64.0
+
+
+@pytest.mark.parametrize("L", [1, 5, 63, 64, 65, 200, 700])
+def test_attention_canon_matches_float64(L):
+    hd = 128
+    q = RNG.standard_normal(hd).astype(np.float32)
+    k = RNG.standard_normal((L, hd)).astype(np.float32)
+    v = RNG.standard_normal((L, hd)).astype(np.float32)
+    scale = np.float32(1 / math.sqrt(hd))
+    s = k.astype(np.float64) @ q.astype(np.float64) * float(scale)
+    p = np.exp(s - s.max())
+    ref = (p / p.sum()) @ v.astype(np.float64)
+    got = O.attention_canon(q, k.ravel(), v.ravel(), L, hd, hd, float(scale))
+    assert np.abs(got - ref).max() <= 1e-5 * max(1.0, np.abs(ref).max())
+    got32 = O.attention_fp32(q, k.ravel(), v.ravel(), L, hd, hd, float(scale))
+    assert np.abs(got32 - ref).max() <= 1e-5 * max(1.0, np.abs(ref).max())
+
+
+def test_rope_cs_float_theta():
+    import ctypes as C
+    c, s = C.c_float(), C.c_float()
+    for pos in (0, 1, 17, 4095, 32767):
+        for i in (0, 1, 31, 63):
+            O.lib().orc_rope_cs(pos, i, 128, C.c_float(1e6), C.byref(c), C.byref(s))
+            theta = np.float32(pos) * np.float32(np.float32(1e6) ** np.float32(np.float32(-2.0 * i) / np.float32(128)))
+            assert abs(c.value - math.cos(float(theta))) <= 2e-7 and abs(s.value - math.sin(float(theta))) <= 2e-7
+    O.lib().orc_rope_cs(0, 5, 128, C.c_float(1e6), C.byref(c), C.byref(s))
+    assert c.value == 1.0 and s.value == 0.0
