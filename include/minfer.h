@@ -111,10 +111,22 @@ int mi_get_stats(const mi_engine* e, mi_stats* out);
 /* Measurement hook, no counterpart in the reference (which profiles with nsys/ncu and
  * in-kernel clock64 marks, mega.cu:111-119): re-launches one phase kernel of the
  * last step `reps` times on the engine stream and returns its mean duration from
- * HIP events. phase: 0 qkv, 1 qkv_fin, 2 attn, 3 attn_comb, 4 o, 5 gate/up, 6 act,
- * 7 down, 8 lm_head, 9 argmax. Needs a completed step; re-running a phase rewrites
+ * HIP events. phase: 0 qkv, 1 attention, 2 chunk merge (launched only past 16 chunks),
+ * 3 o, 4 gate/up + SiLU + quant, 5 down, 6 lm_head, 7 argmax, 8 the whole persistent
+ * step kernel (persistent mode). Needs a completed step; re-running a phase rewrites
  * the same values, so the engine state is unchanged. */
 int mi_time_phase(mi_engine* e, int32_t phase, int32_t layer, int32_t reps, double* avg_ms);
+
+/* In-kernel phase profile of one persistent step (the reference's PROFILE=1,
+ * mega.cu:111-119, 1206-1224): reruns the last step once with workgroup 0 stamping
+ * the device wall clock (100 MHz) at every phase end and barrier exit. us[] receives
+ * n_layer*10 + 2 durations in microseconds: per layer qkv, barrier, attention,
+ * barrier, o, barrier, gate/up, barrier, down, barrier; then lm_head, barrier. */
+int mi_profile_step(mi_engine* e, double* us, int32_t n);
+
+/* Cost of a grid barrier of the persistent kernel: one cooperative launch of nwg
+ * workgroups doing n barriers and nothing else; returns microseconds per barrier. */
+int mi_barrier_cost(int32_t nwg, int32_t n, double* us_per_barrier);
 
 /* ---------------- synthetic model files ---------------- */
 typedef struct mi_synth_shape {
@@ -157,7 +169,8 @@ int mi_q4_block_isums(const uint8_t* packed, int32_t rows, int32_t nb, int32_t c
 
 /* single-query GQA attention over an fp16 cache (cuda_infer.cu:650-702 attn_partial +
  * attn_combine, mega.cu:414-521): q[n_head][hd] fp32, kc/vc [n_head_kv][ctx][hd] fp16,
- * positions 0..L-1, out[n_head][hd]. scratch holds n_head * ceil(L/64) * (hd + 2) floats. */
+ * positions 0..L-1, out[n_head][hd]. scratch holds n_head * ceil(L/64) * (hd + 32) floats
+ * (one record per head and 64-position chunk). */
 int mi_attn_decode(const float* q, const uint16_t* kc, const uint16_t* vc, int32_t n_head,
                    int32_t n_head_kv, int32_t hd, int32_t L, int32_t ctx, float scale,
                    float* scratch, float* out, void* stream);

@@ -23,9 +23,15 @@
 namespace mi {
 
 constexpr int kGroupRows = 64;     // rows per tile group = lanes per wave
-constexpr int kWaves = 4;          // waves per workgroup of every phase kernel
+constexpr int kWaves = 4;          // waves per workgroup of the per-phase kernels
 constexpr int kThreads = kGroupRows * kWaves;
+constexpr int kPWaves = 8;         // waves per workgroup of the persistent step kernel
+constexpr int kPThreads = kGroupRows * kPWaves;
+constexpr int kMaxWaves = 8;
+constexpr int kAttnWaves = 2;      // waves per workgroup that take attention items (LDS bound)
 constexpr int kAttnChunk = 64;     // positions per attention partial
+constexpr int kInlineComb = 4;     // up to this many chunks the O phase merges them itself
+constexpr int kActRec = 128;       // bytes per act block record (32 int8, scale, 8*sum, padding)
 constexpr int kMaxE = 2048;        // largest hidden size the LDS staging holds
 constexpr int kMaxFF = 11264;      // largest FFN width the LDS staging holds
 
@@ -53,18 +59,22 @@ struct DModel {
     __half* vc;
     int32_t* tokbuf;               // [maxseq+1] token at each position (prompt, then generated)
     float* hbuf;                   // [2*NL+1][E]: h_in(l) at 2l, h_mid(l) at 2l+1, lm input at 2NL
-    float* qkv_part;               // [ks_qkv][QKV]
-    float* qf;                     // [NH*HD] rotated q
-    float* att_ml;                 // [NH][maxch][2] chunk max and sum
-    float* att_o;                  // [NH][maxch][HD] chunk outputs
-    float* att_out;                // [E]
-    float* o_part;                 // [ks_o][E]
-    float* gu_part;                // [ks_gu][2*FF]
-    int8_t* act_q;                 // [FF]
-    float2* act_ds;                // [FF/32] (scale, 8*sum(q) as int bits)
-    float* d_part;                 // [ks_d][E]
+    // Values exchanged between workgroups inside one step live in per-layer buffers:
+    // every 128-byte line has a single writer and is written once per launch (with
+    // agent-coherent stores) before any workgroup reads it, so readers may use
+    // ordinary, L2-shared loads.
+    float* qkv_part;               // [NL][ks_qkv][QKV]
+    float* att;                    // [NL][NH][maxch][arec] chunk output o[HD], max, sum
+    float* att_out;                // [NL][E] merged attention (long contexts)
+    float* o_part;                 // [NL][ks_o][E]
+    uint8_t* act;                  // [NL][FF/32][kActRec] int8 block, scale, 8*sum(q)
+    float* d_part;                 // [NL][ks_d][E]
+    int32_t arec;                  // floats per attention record (HD + 32)
     float* logits;                 // [V] (written when non-null)
-    float4* cand;                  // [lm workgroups] (best, idx bits, second, 0)
+    float* cand;                   // [lm workgroups][32] (best, idx bits, second) per 128-byte line
+    uint32_t* bar;                 // grid-barrier arrival counter (persistent kernel)
+    uint64_t* prof;                // when non-null: workgroup 0 stamps every phase end (s_memrealtime)
+    int32_t* err;                  // set when a grid barrier times out
     int32_t* out_tok;              // [maxseq] prediction made at each position
     float* out_margin;             // [maxseq]
 };

@@ -45,6 +45,7 @@ struct mi_engine {
     PhaseGrid pg{};
     hipStream_t stream = nullptr;
     hipEvent_t ev0 = nullptr, ev1 = nullptr;
+    int nwg_persistent = 0;       // workgroups of the persistent step kernel (0: per-phase launches)
     int cur_len = 0;              // positions holding valid K/V
     bool next_ready = false;      // tokbuf[cur_len] holds the prediction of the last step
     mi_stats stats{};
@@ -162,7 +163,7 @@ void mi_default_opts(mi_opts* o) {
     o->spec = 0;
     o->ngmax = 3;
     o->spec_slope = 0.074f;
-    o->persistent = 0;
+    o->persistent = 1;
     o->stop_eos = 0;
     o->device = 0;
 }
@@ -273,10 +274,11 @@ static int load_impl(mi_engine* e, const char* path) {
     const int cbE = nbE % 8 == 0 ? 8 : 4, cbF = nbF % 8 == 0 ? 8 : 4;
     e->cb[0] = e->cb[1] = e->cb[2] = e->cb[4] = cbE;
     e->cb[3] = cbF;
-    e->ks[0] = choose_ks(e->QKV / 64, nbE / cbE, 8);
-    e->ks[1] = choose_ks(e->E / 64, nbE / cbE, 8);
+    const int kmax = kernels_max_ks();
+    e->ks[0] = choose_ks(e->QKV / 64, nbE / cbE, kmax);
+    e->ks[1] = choose_ks(e->E / 64, nbE / cbE, kmax);
     e->ks[2] = choose_ks(e->FF / 32, nbE / cbE, 4);
-    e->ks[3] = choose_ks(e->E / 64, nbF / cbF, 8);
+    e->ks[3] = choose_ks(e->E / 64, nbF / cbF, kmax);
     e->ks[4] = 1;
 
     auto need = [&](const std::string& n) -> const GTensor* { return g.tensor(n); };
@@ -385,24 +387,33 @@ static int load_impl(mi_engine* e, const char* path) {
     M.layers = e->d_layers;
     const size_t kvn = (size_t)e->NL * e->NKV * e->maxseq * e->HD;
     e->pg = plan_phase_grid(M, layers[0], e->n_cu);
+    if (e->opts.persistent) {
+        int coop = 0;
+        HIPCHK(e, hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, e->opts.device));
+        const int per_cu = persistent_max_grid(e->G, e->HD);
+        if (!coop || per_cu < 1)
+            return set_err(e, MI_ERR_DEVICE, "persistent step kernel cannot be co-resident (cooperative %d, %d per CU)",
+                           coop, per_cu);
+        e->nwg_persistent = e->n_cu;      // one workgroup per CU
+    }
+    M.arec = attn_record_floats(e->HD);
+    const size_t NL = (size_t)e->NL;
     if ((rc = alloc_buf(e, &M.kc, kvn)) || (rc = alloc_buf(e, &M.vc, kvn)) ||
         (rc = alloc_buf(e, &M.tokbuf, (size_t)e->maxseq + 1)) ||
         (rc = alloc_buf(e, &M.hbuf, (size_t)(2 * e->NL + 1) * e->E)) ||
-        (rc = alloc_buf(e, &M.qkv_part, (size_t)e->ks[0] * e->QKV)) ||
-        (rc = alloc_buf(e, &M.qf, (size_t)e->NH * e->HD)) ||
-        (rc = alloc_buf(e, &M.att_ml, (size_t)e->NH * e->maxch * 2)) ||
-        (rc = alloc_buf(e, &M.att_o, (size_t)e->NH * e->maxch * e->HD)) ||
-        (rc = alloc_buf(e, &M.att_out, (size_t)e->E)) ||
-        (rc = alloc_buf(e, &M.o_part, (size_t)e->ks[1] * e->E)) ||
-        (rc = alloc_buf(e, &M.gu_part, (size_t)e->ks[2] * 2 * e->FF)) ||
-        (rc = alloc_buf(e, &M.act_q, (size_t)e->FF)) ||
-        (rc = alloc_buf(e, &M.act_ds, (size_t)e->FF / 32)) ||
-        (rc = alloc_buf(e, &M.d_part, (size_t)e->ks[3] * e->E)) ||
-        (rc = alloc_buf(e, &M.cand, (size_t)std::max(e->pg.lm, 1))) ||
+        (rc = alloc_buf(e, &M.qkv_part, NL * e->ks[0] * e->QKV)) ||
+        (rc = alloc_buf(e, &M.att, NL * e->NH * e->maxch * M.arec)) ||
+        (rc = alloc_buf(e, &M.att_out, NL * e->E)) ||
+        (rc = alloc_buf(e, &M.o_part, NL * e->ks[1] * e->E)) ||
+        (rc = alloc_buf(e, &M.act, NL * (e->FF / 32) * kActRec)) ||
+        (rc = alloc_buf(e, &M.d_part, NL * e->ks[3] * e->E)) ||
+        (rc = alloc_buf(e, &M.cand, (size_t)std::max(e->pg.lm, e->nwg_persistent) * 32)) ||
+        (rc = alloc_buf(e, &M.bar, (size_t)barrier_words())) || (rc = alloc_buf(e, &M.err, 64)) ||
         (rc = alloc_buf(e, &M.out_tok, (size_t)e->maxseq)) ||
         (rc = alloc_buf(e, &M.out_margin, (size_t)e->maxseq)))
         return rc;
     M.logits = nullptr;
+    M.prof = nullptr;
     e->M_logits = M;
     if ((rc = alloc_buf(e, &e->M_logits.logits, (size_t)e->V))) return rc;
     HIPCHK(e, hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking));
@@ -421,7 +432,6 @@ int mi_load(const char* gguf_path, const mi_opts* opts, mi_engine** out) {
     if (opts) e->opts = *opts; else mi_default_opts(&e->opts);
     if (e->opts.tchunk < 1 || e->opts.tchunk > 8 || e->opts.max_ctx < 0)
         return set_err(nullptr, MI_ERR_ARG, "bad options");
-    if (e->opts.persistent) return set_err(nullptr, MI_ERR_ARG, "persistent step mode is not built yet");
     const int rc = load_impl(e.get(), gguf_path);
     if (rc) { g_load_error = e->err; return rc; }
     *out = e.release();
@@ -440,7 +450,7 @@ int mi_info(const mi_engine* e, mi_model_info* o) {
     o->attn_chunk = kAttnChunk;
     o->kv_f16 = 1;
     o->n_cu = e->n_cu;
-    o->persistent = e->opts.persistent;
+    o->persistent = e->nwg_persistent > 0;
     o->weight_bytes = e->weight_bytes;
     return MI_OK;
 }
@@ -448,8 +458,19 @@ int mi_info(const mi_engine* e, mi_model_info* o) {
 }  // extern "C"
 
 static int run_step(mi_engine* e, int pos, int gen, bool want_logits) {
-    launch_step_phases(want_logits ? e->M_logits : e->M, e->pg, pos, gen, e->stream);
+    const DModel& M = want_logits ? e->M_logits : e->M;
+    if (e->nwg_persistent) HIPCHK(e, launch_step_persistent(M, e->nwg_persistent, pos, gen, e->stream));
+    else launch_step_phases(M, e->pg, pos, gen, e->stream);
     HIPCHK(e, hipGetLastError());
+    return MI_OK;
+}
+
+// after a synchronization: a grid barrier that timed out leaves a flag
+static int check_barrier(mi_engine* e) {
+    if (!e->nwg_persistent) return MI_OK;
+    int32_t flag = 0;
+    HIPCHK(e, hipMemcpy(&flag, e->M.err, 4, hipMemcpyDeviceToHost));
+    if (flag) return set_err(e, MI_ERR_DEVICE, "grid barrier timed out (workgroups not co-resident?)");
     return MI_OK;
 }
 
@@ -470,6 +491,7 @@ int mi_step(mi_engine* e, const int32_t* toks, int32_t T, int32_t pos, int32_t* 
     HIPCHK(e, hipMemcpyAsync(&mg, e->M.out_margin + pos, 4, hipMemcpyDeviceToHost, e->stream));
     if (logits) HIPCHK(e, hipMemcpyAsync(logits, e->M_logits.logits, sizeof(float) * e->V, hipMemcpyDeviceToHost, e->stream));
     HIPCHK(e, hipStreamSynchronize(e->stream));
+    if ((rc = check_barrier(e))) return rc;
     if (argmax) argmax[0] = tok;
     if (margin) margin[0] = mg;
     e->cur_len = pos + T;
@@ -494,6 +516,7 @@ int mi_prefill(mi_engine* e, const int32_t* ids, int32_t n, int32_t* first, floa
     HIPCHK(e, hipMemcpyAsync(&tok, e->M.out_tok + n - 1, 4, hipMemcpyDeviceToHost, e->stream));
     HIPCHK(e, hipMemcpyAsync(&mg, e->M.out_margin + n - 1, 4, hipMemcpyDeviceToHost, e->stream));
     HIPCHK(e, hipStreamSynchronize(e->stream));
+    if (int rc = check_barrier(e)) return rc;
     float ms = 0.f;
     HIPCHK(e, hipEventElapsedTime(&ms, e->ev0, e->ev1));
     e->stats.prefill_ms = ms;
@@ -532,6 +555,7 @@ int mi_generate(mi_engine* e, int32_t n_gen, int32_t* out, float* margins, int32
             HIPCHK(e, hipMemcpyAsync(mg.data(), e->M.out_margin + p0 - 1, sizeof(float) * n_gen, hipMemcpyDeviceToHost, e->stream));
         }
         HIPCHK(e, hipStreamSynchronize(e->stream));
+        if (int rc = check_barrier(e)) return rc;
         for (int t = 0; t < n_gen; t++) {
             if (out) out[t] = tk[t];
             if (margins) margins[t] = mg[t];
@@ -566,17 +590,69 @@ int mi_generate(mi_engine* e, int32_t n_gen, int32_t* out, float* margins, int32
 }
 
 int mi_time_phase(mi_engine* e, int32_t phase, int32_t layer, int32_t reps, double* avg_ms) {
-    if (!e || !avg_ms || phase < 0 || phase > 9 || layer < 0 || layer >= e->NL || reps < 1) return MI_ERR_ARG;
+    if (!e || !avg_ms || phase < 0 || phase > 8 || layer < 0 || layer >= e->NL || reps < 1) return MI_ERR_ARG;
     if (e->cur_len < 1) return set_err(e, MI_ERR_STATE, "mi_time_phase needs a completed step");
+    if (phase == 8 && !e->nwg_persistent) return set_err(e, MI_ERR_STATE, "phase 8 is the persistent step kernel");
     const int pos = e->cur_len - 1;
     HIPCHK(e, hipEventRecord(e->ev0, e->stream));
-    for (int r = 0; r < reps; r++) launch_phase(e->M, e->pg, phase, layer, pos, 1, e->stream);
+    for (int r = 0; r < reps; r++) {
+        if (phase == 8) HIPCHK(e, launch_step_persistent(e->M, e->nwg_persistent, pos, 1, e->stream));
+        else launch_phase(e->M, e->pg, phase, layer, pos, 1, e->stream);
+    }
     HIPCHK(e, hipGetLastError());
     HIPCHK(e, hipEventRecord(e->ev1, e->stream));
     HIPCHK(e, hipEventSynchronize(e->ev1));
+    if (phase == 8) { int rc = check_barrier(e); if (rc) return rc; }
     float ms = 0.f;
     HIPCHK(e, hipEventElapsedTime(&ms, e->ev0, e->ev1));
     *avg_ms = ms / reps;
+    return MI_OK;
+}
+
+int mi_profile_step(mi_engine* e, double* us, int32_t n) {
+    if (!e || !us) return MI_ERR_ARG;
+    const int nslot = e->NL * kProfSlotsPerLayer + 3;
+    if (n < nslot - 1) return set_err(e, MI_ERR_ARG, "mi_profile_step needs %d entries", nslot - 1);
+    if (!e->nwg_persistent) return set_err(e, MI_ERR_STATE, "profiling needs the persistent step kernel");
+    if (e->cur_len < 1) return set_err(e, MI_ERR_STATE, "mi_profile_step needs a completed step");
+    uint64_t* prof = nullptr;
+    HIPCHK(e, hipMalloc(&prof, sizeof(uint64_t) * nslot));
+    DModel M = e->M;
+    M.prof = prof;
+    hipError_t st = launch_step_persistent(M, e->nwg_persistent, e->cur_len - 1, 1, e->stream);
+    std::vector<uint64_t> t(nslot);
+    if (st == hipSuccess) st = hipStreamSynchronize(e->stream);
+    if (st == hipSuccess) st = hipMemcpy(t.data(), prof, sizeof(uint64_t) * nslot, hipMemcpyDeviceToHost);
+    (void)hipFree(prof);
+    if (st != hipSuccess) return set_err(e, MI_ERR_DEVICE, "profile step: %s", hipGetErrorString(st));
+    for (int i = 0; i + 1 < nslot; i++) us[i] = (double)(t[i + 1] - t[i]) * 0.01;   // 100 MHz ticks
+    return check_barrier(e);
+}
+
+int mi_barrier_cost(int32_t nwg, int32_t n, double* us_per_barrier) {
+    if (nwg < 1 || n < 1 || !us_per_barrier) return MI_ERR_ARG;
+    uint32_t* bar = nullptr;
+    int32_t* err = nullptr;
+    hipEvent_t a, b;
+    if (hipMalloc(&bar, sizeof(uint32_t) * barrier_words()) != hipSuccess || hipMalloc(&err, 64) != hipSuccess) return MI_ERR_OOM;
+    (void)hipMemset(err, 0, 64);
+    (void)hipEventCreate(&a);
+    (void)hipEventCreate(&b);
+    hipError_t st = launch_barriers(bar, err, nwg, 8, nullptr);   // warm up
+    (void)hipEventRecord(a, nullptr);
+    if (st == hipSuccess) st = launch_barriers(bar, err, nwg, n, nullptr);
+    (void)hipEventRecord(b, nullptr);
+    if (st == hipSuccess) st = hipEventSynchronize(b);
+    float ms = 0.f;
+    int32_t flag = 0;
+    if (st == hipSuccess) st = hipEventElapsedTime(&ms, a, b);
+    if (st == hipSuccess) st = hipMemcpy(&flag, err, 4, hipMemcpyDeviceToHost);
+    (void)hipEventDestroy(a);
+    (void)hipEventDestroy(b);
+    (void)hipFree(bar);
+    (void)hipFree(err);
+    if (st != hipSuccess || flag) return MI_ERR_DEVICE;
+    *us_per_barrier = ms * 1000.0 / n;
     return MI_OK;
 }
 

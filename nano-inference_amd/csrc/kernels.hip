@@ -1,7 +1,7 @@
 // kernels.hip -- gfx950 kernels of the batch-1 decode step.
 //
 // Every floating-point operation below is an explicitly rounded IEEE-754 binary32
-// operation (__fadd_rn, __fmul_rn, __fmaf_rn, __fdiv_rn, __fsqrt_rn) issued in a
+// operation (__fadd_rn, __fmul_rn, __fmaf_rn, __fdiv_rn, __builtin_sqrtf) issued in a
 // fixed order, so the results do not depend on how work is split across waves
 // and workgroups, and equal the CPU restatement of the same order bit for bit.
 // The orders (the reduction plan) are:
@@ -24,6 +24,7 @@
 #include "kernels.hpp"
 
 #include <climits>
+#include <type_traits>
 
 namespace mi {
 
@@ -69,7 +70,7 @@ __device__ __forceinline__ float rms_inv(const float* xs, int n, float eps, int 
     for (int k = lane; k < n; k += 64) a = __fmaf_rn(xs[k], xs[k], a);
     a = bfly_sum64(a);
     const float mean = __fdiv_rn(a, (float)n);
-    return __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(mean, eps)));
+    return __fdiv_rn(1.0f, __builtin_sqrtf(__fadd_rn(mean, eps)));   // correctly rounded (HIP's __fsqrt_rn is the native approximation)
 }
 
 // quantize one 32-element block per half-wave; every lane runs the shuffles
@@ -91,9 +92,9 @@ __device__ __forceinline__ void quant32(float v, bool own, int8_t* xq8, int e, f
 
 // xs[0..n) (LDS) -> optional RMSNorm with w -> int8 blocks in LDS. n % 32 == 0.
 __device__ void norm_quant(const float* xs, const float* w, int n, float eps, int8_t* xq8, float2* xds, int tid) {
-    const int lane = tid & 63;
+    const int lane = tid & 63, nt = blockDim.x;
     const float sc = w ? rms_inv(xs, n, eps, lane) : 1.f;
-    for (int base = 0; base < n; base += kThreads) {
+    for (int base = 0; base < n; base += nt) {
         const int e = base + tid;
         const bool own = e < n;
         const int ec = own ? e : n - 1;
@@ -104,7 +105,7 @@ __device__ void norm_quant(const float* xs, const float* w, int n, float eps, in
 
 // xs[i] = h[i] + (part[0][i] + part[1][i] + ...), the residual add of a split-K GEMV
 __device__ void residual_into(float* xs, const float* h, const float* part, int ks, int n, float* hout, int tid) {
-    for (int i = tid; i < n; i += kThreads) {
+    for (int i = tid; i < n; i += blockDim.x) {
         float v = part[i];
         for (int s = 1; s < ks; s++) v = __fadd_rn(v, part[(size_t)s * n + i]);
         v = __fadd_rn(h[i], v);
@@ -173,28 +174,73 @@ __device__ __forceinline__ float row_segment(const PMat& W, int g, int s, const 
                      : seg_dot<4>(tile, c1 - c0, c0 * 4, xq8, xds, lane);
 }
 
+__device__ __forceinline__ int nwaves() { return blockDim.x >> 6; }
+
 // tasks (group, segment) spread over the grid's waves; part[s][row]
 __device__ void gemv_phase(const PMat& W, const int8_t* xq8, const float2* xds, float* part, int wg, int nwg, int tid) {
-    const int lane = tid & 63, wave = tid >> 6;
+    const int lane = tid & 63, wave = tid >> 6, nw = nwaves();
     const int ntask = (W.rows / 64) * W.ks;
-    for (int task = wg * kWaves + wave; task < ntask; task += nwg * kWaves) {
+    for (int task = wg * nw + wave; task < ntask; task += nwg * nw) {
         const int g = task / W.ks, s = task % W.ks;
         part[(size_t)s * W.rows + g * 64 + lane] = row_segment(W, g, s, xq8, xds, lane);
     }
 }
 
+// ------------------------------------------------------------------ cross-workgroup data
+// Inside one step, values that one workgroup writes and others read (GEMV partials,
+// attention records, the residual stream, the int8 act, argmax candidates) are
+// written once per launch into per-layer buffers whose 128-byte lines each have a
+// single writer, with agent-coherent stores (global_store sc1: written through
+// past the per-XCD L2). After the grid barrier every reader sees them with
+// ordinary loads: no reader can hold an older copy of a line that is written once
+// per launch, and the 32 workgroups of an XCD share one L2 fill. That keeps the
+// barrier free of agent-scope fences (an L2 write-back/invalidate per workgroup
+// costs ~1.7 us at 256 workgroups) and keeps the redundant prologue reads in L2.
+__device__ __forceinline__ uint32_t ldc(const uint32_t* p) {
+    return __hip_atomic_load(const_cast<uint32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void stc(float* p, float v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+__device__ __forceinline__ void stc(uint32_t* p, uint32_t v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+__device__ __forceinline__ void drain_vm() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+typedef __attribute__((address_space(3))) void* lds_ptr;
+// one wave copies `bytes` (multiple of 16, both ends 16-byte aligned) from global
+// memory straight into LDS, 1 KB per instruction (lane l moves bytes 16l..16l+15)
+__device__ __forceinline__ void dma_wave(const void* g, void* lds, int bytes, int lane) {
+    for (int off = 0; off < bytes; off += 1024)
+        if (off + lane * 16 < bytes)
+            __builtin_amdgcn_global_load_lds(static_cast<const uint8_t*>(g) + off + lane * 16,
+                                             (lds_ptr)(static_cast<uint8_t*>(lds) + off), 16, 0, 0);
+}
+// the same spread over the workgroup's waves (1 KB blocks round-robin)
+__device__ __forceinline__ void dma_wg(const void* g, void* lds, int bytes) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = nwaves();
+    for (int off = wave * 1024; off < bytes; off += nw * 1024)
+        if (off + lane * 16 < bytes)
+            __builtin_amdgcn_global_load_lds(static_cast<const uint8_t*>(g) + off + lane * 16,
+                                             (lds_ptr)(static_cast<uint8_t*>(lds) + off), 16, 0, 0);
+}
+
 // ------------------------------------------------------------------ LDS staging layout
-// [0, 8 KB)              xs: fp32 vector of the phase input (E <= 2048)
-// [8 KB, 8 KB + kMaxFF)  xq8: int8 activations
-// [.., + kMaxFF/32*8)    xds: per-block (scale, 8*sum) pairs
+// xs    fp32 vector of the phase input (E <= kMaxE)
+// xq8   int8 activations (<= kMaxFF)
+// xds   per-block (scale, 8*sum(q)) pairs
+// red   per-wave argmax candidates
+// gpart per-wave gate/up segment sums of one 64-row group
+// stg   DMA landing zone: the residual and its split-K partials, act records, or
+//       the attention records the O phase merges
 struct Stage {
-    float* xs; int8_t* xq8; float2* xds; float4* red;
+    float* xs; int8_t* xq8; float2* xds; float4* red; float* gpart; float* stg;
     __device__ explicit Stage(uint8_t* smem)
         : xs(reinterpret_cast<float*>(smem)), xq8(reinterpret_cast<int8_t*>(smem + 4 * kMaxE)),
           xds(reinterpret_cast<float2*>(smem + 4 * kMaxE + kMaxFF)),
-          red(reinterpret_cast<float4*>(smem + 4 * kMaxE + kMaxFF + kMaxFF / 4)) {}
+          red(reinterpret_cast<float4*>(smem + 4 * kMaxE + kMaxFF + kMaxFF / 4)),
+          gpart(reinterpret_cast<float*>(smem + 4 * kMaxE + kMaxFF + kMaxFF / 4 + 16 * kMaxWaves)),
+          stg(reinterpret_cast<float*>(smem + 4 * kMaxE + kMaxFF + kMaxFF / 4 + 16 * kMaxWaves + 4 * 64 * kMaxWaves)) {}
 };
-constexpr int kStageBytes = 4 * kMaxE + kMaxFF + kMaxFF / 4 + 16 * kWaves;
+constexpr int kMaxKs = 8;
+constexpr int kStgBytes = 4 * (kMaxKs + 1) * kMaxE;           // >= act records (kMaxFF/32*128) and merge records
+constexpr int kStageBytes = 4 * kMaxE + kMaxFF + kMaxFF / 4 + 16 * kMaxWaves + 4 * 64 * kMaxWaves + kStgBytes;
 
 // ------------------------------------------------------------------ argmax candidates
 struct Top2 { float best; int idx; float second; };
@@ -213,285 +259,461 @@ __device__ __forceinline__ void top2_wave(Top2& t) {
         top2_merge(t, __shfl_xor(t.best, off), __shfl_xor(t.idx, off), __shfl_xor(t.second, off));
 }
 
+// ------------------------------------------------------------------ grid barrier
+// Two-level arrival tree: workgroup w arrives on counter w % 16 (16 counters on
+// separate 256-byte lines, so arrivals do not serialize on one address); the last
+// arrival of each counter bumps the top counter, whose last arrival publishes the
+// epoch every workgroup polls. Arrival first waits for the workgroup's own
+// (write-through) stores to complete. A poll that outlives kSpinLimit sets *err and
+// returns, so no wave can wait forever. bar[]: counter k at 64*k, top at 64*16,
+// epoch at 64*17 (zeroed by the host before each launch).
+constexpr unsigned kSpinLimit = 1u << 26;
+constexpr int kBarGroups = 16;
+constexpr int kBarWords = 64 * 18;
+__device__ __forceinline__ void grid_barrier(uint32_t* bar, int32_t* err, unsigned& epoch) {
+    drain_vm();
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        epoch++;
+        const int ng = min(kBarGroups, (int)gridDim.x), g = blockIdx.x % ng;
+        const unsigned gsize = gridDim.x / ng + ((int)(gridDim.x % ng) > g ? 1u : 0u);
+        const unsigned old = __hip_atomic_fetch_add(bar + 64 * g, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (old + 1 == gsize * epoch) {
+            const unsigned t = __hip_atomic_fetch_add(bar + 64 * kBarGroups, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (t + 1 == (unsigned)ng * epoch) stc(bar + 64 * (kBarGroups + 1), epoch);
+        }
+        unsigned spins = 0;
+        while ((int)(ldc(bar + 64 * (kBarGroups + 1)) - epoch) < 0) {
+            if (++spins > kSpinLimit) { stc(reinterpret_cast<uint32_t*>(err), 1u); break; }
+        }
+    }
+    __syncthreads();
+}
+
+// ------------------------------------------------------------------ GEMV first-tile prefetch
+// The weights a wave reads first do not depend on the activations, so before the
+// phase's prologue (residual loads, norm, quant) each wave touches every 128-byte
+// line of its first tile with one dword load; the tile then comes from L2 once the
+// activations are ready. The loaded words only feed a never-taken store, so the
+// prefetch holds one register instead of the tile.
+struct Touch { uint32_t acc; };
+__device__ __forceinline__ void touch_lines(const uint8_t* p, int bytes, Touch& t) {
+    const int lane = threadIdx.x & 63;
+    for (int off = lane * 128; off < bytes; off += 64 * 128) t.acc ^= *reinterpret_cast<const uint32_t*>(p + off);
+}
+__device__ __forceinline__ Touch prefetch_first(const PMat& W, int wg) {
+    const int wave = threadIdx.x >> 6, nw = nwaves();
+    Touch t{0};
+    const int task = wg * nw + wave, ntask = (W.rows / 64) * W.ks;
+    if (task < ntask) {
+        const int g = task / W.ks, s = task % W.ks, c0 = s * W.nc / W.ks;
+        touch_lines(W.base + ((size_t)g * W.nc + c0) * tile_bytes(W.cb), (int)tile_bytes(W.cb), t);
+    }
+    return t;
+}
+__device__ __forceinline__ void retire(const Touch& t, int32_t* err) {
+    if (t.acc == 0x9E3779B9u && threadIdx.x == 1023) *err = 2;   // never true: keeps the loads
+}
+
+// tasks (group, segment) over the grid's waves; part[s][row], one 256-byte line pair per task
+__device__ void gemv_tasks(const PMat& W, const int8_t* xq8, const float2* xds, float* part, int wg, int nwg) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = nwaves();
+    const int ntask = (W.rows / 64) * W.ks;
+    for (int task = wg * nw + wave; task < ntask; task += nwg * nw) {
+        const int g = task / W.ks, s = task % W.ks;
+        stc(part + (size_t)s * W.rows + g * 64 + lane, row_segment(W, g, s, xq8, xds, lane));
+    }
+}
+
 // ------------------------------------------------------------------ phases
 __device__ __forceinline__ size_t hin(int l, int E) { return (size_t)(2 * l) * E; }
 __device__ __forceinline__ size_t hmid(int l, int E) { return (size_t)(2 * l + 1) * E; }
+__device__ __forceinline__ float* qkv_part(const DModel& M, int l) { return M.qkv_part + (size_t)l * M.layers[0].qkv.ks * M.QKV; }
+__device__ __forceinline__ float* o_part(const DModel& M, int l) { return M.o_part + (size_t)l * M.layers[0].o.ks * M.E; }
+__device__ __forceinline__ float* d_part(const DModel& M, int l) { return M.d_part + (size_t)l * M.layers[0].d.ks * M.E; }
+__device__ __forceinline__ float* att_rec(const DModel& M, int l) { return M.att + (size_t)l * M.NH * M.maxch * M.arec; }
+__device__ __forceinline__ uint8_t* act_rec(const DModel& M, int l) { return M.act + (size_t)l * (M.FF / 32) * kActRec; }
 
-// P1: residual (or embedding row) -> RMSNorm -> int8 -> fused QKV rows
+// xs = h + (part[0] + ... + part[ks-1]) (the residual add of a split-K GEMV): h and
+// the partials arrive in LDS in one DMA batch; hout (workgroup 0) keeps the result
+__device__ void residual_dma(const Stage& S, const float* h, const float* part, int ks, int n, float* hout) {
+    dma_wg(h, S.stg, n * 4);
+    dma_wg(part, S.stg + n, ks * n * 4);
+    drain_vm();
+    __syncthreads();
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        float v = S.stg[n + i];
+        for (int s = 1; s < ks; s++) v = __fadd_rn(v, S.stg[n + s * n + i]);
+        v = __fadd_rn(S.stg[i], v);
+        S.xs[i] = v;
+        if (hout) stc(hout + i, v);
+    }
+}
+
+// P1: residual (or embedding row) -> RMSNorm -> int8 -> fused QKV rows (split-K partials)
 __device__ void phase_qkv(const DModel& M, int l, int pos, int wg, int nwg, uint8_t* smem) {
     const int tid = threadIdx.x;
     Stage S(smem);
     const DLayer& L = M.layers[l];
+    const Touch pre = prefetch_first(L.qkv, wg);
     if (l == 0) {
-        const int tok = M.tokbuf[pos];
-        const float* er = M.emb + (size_t)tok * M.E;
-        for (int i = tid; i < M.E; i += kThreads) {
+        const float* er = M.emb + (size_t)M.tokbuf[pos] * M.E;
+        for (int i = tid; i < M.E; i += blockDim.x) {
             const float v = er[i];
             S.xs[i] = v;
-            if (wg == 0) M.hbuf[hin(0, M.E) + i] = v;
+            if (wg == 0) stc(M.hbuf + hin(0, M.E) + i, v);
         }
     } else {
-        residual_into(S.xs, M.hbuf + hmid(l - 1, M.E), M.d_part, M.layers[l - 1].d.ks, M.E,
-                      wg == 0 ? M.hbuf + hin(l, M.E) : nullptr, tid);
+        residual_dma(S, M.hbuf + hmid(l - 1, M.E), d_part(M, l - 1), M.layers[l - 1].d.ks, M.E,
+                     wg == 0 ? M.hbuf + hin(l, M.E) : nullptr);
     }
     __syncthreads();
     norm_quant(S.xs, L.an, M.E, M.eps, S.xq8, S.xds, tid);
     __syncthreads();
-    gemv_phase(L.qkv, S.xq8, S.xds, M.qkv_part, wg, nwg, tid);
+    gemv_tasks(L.qkv, S.xq8, S.xds, qkv_part(M, l), wg, nwg);
+    retire(pre, M.err);
 }
 
-// P1 epilogue: sum the QKV segments + bias, NEOX RoPE on q and k (pairs i, i+HD/2,
-// cpu_infer.cpp:49-61), q -> qf, k/v -> fp16 cache slot pos
-__device__ void phase_qkv_fin(const DModel& M, int l, int pos, int wg, int nwg) {
-    const DLayer& L = M.layers[l];
-    const int half = M.HD / 2, nq = M.NH * half, nk = M.NKV * half, nv = M.KVD;
-    const int ks = L.qkv.ks;
-    auto val = [&](int r) {
-        float v = M.qkv_part[r];
-        for (int s = 1; s < ks; s++) v = __fadd_rn(v, M.qkv_part[(size_t)s * M.QKV + r]);
-        return __fadd_rn(v, L.bqkv[r]);
-    };
-    const float2* cs = M.rope + (size_t)pos * half;
-    for (int it = wg * kThreads + threadIdx.x; it < nq + nk + nv; it += nwg * kThreads) {
-        if (it < nq + nk) {
-            const bool isq = it < nq;
-            const int j = isq ? it : it - nq, h = j / half, i = j % half;
-            const int r0 = (isq ? 0 : M.NH * M.HD) + h * M.HD + i;
-            const float x0 = val(r0), x1 = val(r0 + half);
-            const float2 c = cs[i];
-            const float y0 = __fsub_rn(__fmul_rn(x0, c.x), __fmul_rn(x1, c.y));
-            const float y1 = __fadd_rn(__fmul_rn(x0, c.y), __fmul_rn(x1, c.x));
-            if (isq) {
-                M.qf[h * M.HD + i] = y0;
-                M.qf[h * M.HD + i + half] = y1;
-            } else {
-                __half* kr = M.kc + (((size_t)l * M.NKV + h) * M.maxseq + pos) * M.HD;
-                kr[i] = __float2half(y0);
-                kr[i + half] = __float2half(y1);
-            }
-        } else {
-            const int j = it - nq - nk, h = j / M.HD, d = j % M.HD;
-            M.vc[(((size_t)l * M.NKV + h) * M.maxseq + pos) * M.HD + d] = __float2half(val(M.NH * M.HD + M.KVD + j));
-        }
-    }
-}
+// ------------------------------------------------------------------ attention
+// per-wave LDS: K [HD/8][64] 16-byte vectors (vector j of position t at j*64 + t, so
+// a lane-per-position read is conflict-free) | V [64][HD] | q partials [8][HD] |
+// k, v partials [2][8][HD] | q [HD] | k(pos) [HD] | p [64]
+template <int HD>
+constexpr int attn_wave_lds() { return 2 * 64 * HD * 2 + 3 * 4 * kMaxKs * HD + 4 * HD * 2 + 4 * 64; }
 
-// P2: one wave per (kv head, 64-position chunk) of positions 0..L-1. q: G heads x HD
-// (the kv head's query group), krow/vrow: rows of this kv head (stride HD halves).
-// Writes the chunk's (max, sum) and unnormalized output for each of the G heads.
-template <int G, int HD>
-__device__ void attn_chunk(const float* q, const __half* krow, const __half* vrow, int L, int c, float scale,
-                           float* ml, float* o, int maxch, int h0, uint8_t* lds, int lane) {
-    constexpr int KS = HD + 8;                 // padded LDS row (halves)
-    float* qs = reinterpret_cast<float*>(lds);                       // [G][HD]
-    __half* kv = reinterpret_cast<__half*>(lds + 4 * G * HD);        // [64][KS] K, then V
-    float* ps = reinterpret_cast<float*>(lds + 4 * G * HD + 2 * 64 * KS);   // [G][64]
-    const int t0 = c * kAttnChunk, n = min(kAttnChunk, L - t0);
-    for (int i = lane; i < G * HD; i += 64) qs[i] = q[i];
-    constexpr int VPR = HD / 8;                // 16-byte vectors per row
-    for (int v = lane; v < n * VPR; v += 64) {
-        const int row = v / VPR, col = (v % VPR) * 8;
-        *reinterpret_cast<uint4*>(kv + row * KS + col) = *reinterpret_cast<const uint4*>(krow + (size_t)(t0 + row) * HD + col);
-    }
-    wave_lds_sync();
-    // scores, lane = position
-    float a[G][4];
+// DMA the chunk's K rows (swizzled) and V rows; rows past n repeat row n-1
+template <int HD>
+__device__ __forceinline__ void attn_issue_kv(const __half* krows, const __half* vrows, int t0, int n, uint4* kls,
+                                              __half* vls, int lane) {
+    constexpr int NV = HD / 8, RPI = 64 / NV;
+    const __half* kr = krows + (size_t)(t0 + min(lane, n - 1)) * HD;
 #pragma unroll
-    for (int j = 0; j < G; j++) a[j][0] = a[j][1] = a[j][2] = a[j][3] = 0.f;
-    const bool valid = lane < n;
-    const __half* kr = kv + (valid ? lane : 0) * KS;
+    for (int j = 0; j < NV; j++)
+        __builtin_amdgcn_global_load_lds(kr + 8 * j, (lds_ptr)(kls + j * 64), 16, 0, 0);
+    const int r = lane / NV, col = (lane % NV) * 8;
+#pragma unroll
+    for (int i = 0; i < 64 / RPI; i++) {
+        const int row = min(i * RPI + r, n - 1);
+        __builtin_amdgcn_global_load_lds(vrows + (size_t)(t0 + row) * HD + col, (lds_ptr)(vls + i * RPI * HD), 16, 0, 0);
+    }
+}
+
+// scores (lane = position; lane `cur` takes its K row from kcur), chunk softmax, p.v
+// (lane = dims). The chunk max and sum end on every lane, the lane's outputs in acc.
+template <int HD>
+__device__ __forceinline__ void attn_core(const uint4* kls, const float* qs, const float* kcur, int cur, const __half* vls,
+                                          float* ps, int n, float scale, int lane, float& m, float& lsum,
+                                          float (&acc)[HD / 64]) {
+    constexpr int NV = HD / 8, DPL = HD / 64;
+    float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+    const bool mine = lane == cur;
 #pragma unroll 4
-    for (int d = 0; d < HD; d += 4) {
-        const uint2 kw = *reinterpret_cast<const uint2*>(kr + d);
-        const float k0 = h2f_lo(kw.x), k1 = h2f_hi(kw.x), k2 = h2f_lo(kw.y), k3 = h2f_hi(kw.y);
+    for (int j = 0; j < NV; j++) {
+        const uint4 w = kls[j * 64 + lane];
+        float kf[8] = {h2f_lo(w.x), h2f_hi(w.x), h2f_lo(w.y), h2f_hi(w.y), h2f_lo(w.z), h2f_hi(w.z), h2f_lo(w.w), h2f_hi(w.w)};
+        if (mine) {
 #pragma unroll
-        for (int j = 0; j < G; j++) {
-            const float4 qv = *reinterpret_cast<const float4*>(qs + j * HD + d);
-            a[j][0] = __fmaf_rn(qv.x, k0, a[j][0]);
-            a[j][1] = __fmaf_rn(qv.y, k1, a[j][1]);
-            a[j][2] = __fmaf_rn(qv.z, k2, a[j][2]);
-            a[j][3] = __fmaf_rn(qv.w, k3, a[j][3]);
+            for (int e = 0; e < 8; e++) kf[e] = kcur[8 * j + e];
         }
+        const float4 q0 = *reinterpret_cast<const float4*>(qs + 8 * j);
+        const float4 q1 = *reinterpret_cast<const float4*>(qs + 8 * j + 4);
+        a0 = __fmaf_rn(q0.x, kf[0], a0); a1 = __fmaf_rn(q0.y, kf[1], a1);
+        a2 = __fmaf_rn(q0.z, kf[2], a2); a3 = __fmaf_rn(q0.w, kf[3], a3);
+        a0 = __fmaf_rn(q1.x, kf[4], a0); a1 = __fmaf_rn(q1.y, kf[5], a1);
+        a2 = __fmaf_rn(q1.z, kf[6], a2); a3 = __fmaf_rn(q1.w, kf[7], a3);
     }
-    float m[G], lsum[G];
-#pragma unroll
-    for (int j = 0; j < G; j++) {
-        const float sc = __fmul_rn(__fadd_rn(__fadd_rn(a[j][0], a[j][1]), __fadd_rn(a[j][2], a[j][3])), scale);
-        const float s = valid ? sc : -__builtin_inff();
-        m[j] = wave_max(s);
-        const float p = valid ? mi_expf(__fsub_rn(s, m[j])) : 0.f;
-        lsum[j] = bfly_sum64(p);
-        ps[j * 64 + lane] = p;
-    }
+    const bool valid = lane < n;
+    const float sc = __fmul_rn(__fadd_rn(__fadd_rn(a0, a1), __fadd_rn(a2, a3)), scale);
+    const float s = valid ? sc : -__builtin_inff();
+    m = wave_max(s);
+    const float p = valid ? mi_expf(__fsub_rn(s, m)) : 0.f;
+    lsum = bfly_sum64(p);
+    ps[lane] = p;
     wave_lds_sync();
-    // V rows replace K rows in LDS
-    for (int v = lane; v < n * VPR; v += 64) {
-        const int row = v / VPR, col = (v % VPR) * 8;
-        *reinterpret_cast<uint4*>(kv + row * KS + col) = *reinterpret_cast<const uint4*>(vrow + (size_t)(t0 + row) * HD + col);
-    }
-    wave_lds_sync();
-    // p.v, lane = dims
-    constexpr int DPL = HD / 64;
-    float acc[G][DPL];
 #pragma unroll
-    for (int j = 0; j < G; j++)
-#pragma unroll
-        for (int e = 0; e < DPL; e++) acc[j][e] = 0.f;
+    for (int e = 0; e < DPL; e++) acc[e] = 0.f;
     for (int t = 0; t < n; t++) {
-        float vv[DPL];
+        const float pt = ps[t];
         if constexpr (DPL == 2) {
-            const uint32_t w2 = *reinterpret_cast<const uint32_t*>(kv + t * KS + 2 * lane);
-            vv[0] = h2f_lo(w2); vv[1] = h2f_hi(w2);
+            const uint32_t w2 = *reinterpret_cast<const uint32_t*>(vls + t * HD + 2 * lane);
+            acc[0] = __fmaf_rn(pt, h2f_lo(w2), acc[0]);
+            acc[1] = __fmaf_rn(pt, h2f_hi(w2), acc[1]);
         } else {
-            vv[0] = __half2float(kv[t * KS + lane]);
-        }
-#pragma unroll
-        for (int j = 0; j < G; j++) {
-            const float p = ps[j * 64 + t];
-#pragma unroll
-            for (int e = 0; e < DPL; e++) acc[j][e] = __fmaf_rn(p, vv[e], acc[j][e]);
+            acc[0] = __fmaf_rn(pt, __half2float(vls[t * HD + lane]), acc[0]);
         }
     }
-#pragma unroll
-    for (int j = 0; j < G; j++) {
-        const size_t hc = (size_t)(h0 + j) * maxch + c;
-#pragma unroll
-        for (int e = 0; e < DPL; e++) o[hc * HD + DPL * lane + e] = acc[j][e];
-        if (lane == 0) { ml[hc * 2] = m[j]; ml[hc * 2 + 1] = lsum[j]; }
+}
+
+// P2 item: one wave = one query head x one 64-position chunk of positions 0..L-1.
+// One DMA batch brings the chunk's K and V rows, the QKV partials of the head's q
+// rows and, in the chunk that holds position pos, of its kv head's k and v rows.
+// Then q = segments + bias + NEOX RoPE (cpu_infer.cpp:49-61); the last chunk
+// finishes k/v of pos, rounds them to fp16, appends them to the cache and uses them
+// for its own row.
+template <int HD>
+__device__ void attn_item(const DModel& M, int l, int pos, int h, int c, uint8_t* lds, int lane) {
+    constexpr int half = HD / 2, DPL = HD / 64;
+    uint4* kls = reinterpret_cast<uint4*>(lds);
+    __half* vls = reinterpret_cast<__half*>(lds + 64 * HD * 2);
+    float* qp = reinterpret_cast<float*>(lds + 2 * 64 * HD * 2);                 // [ks][HD]
+    float* kvp = qp + kMaxKs * HD;                                               // [ks][HD] k then [ks][HD] v
+    float* qs = qp + 3 * kMaxKs * HD;
+    float* kcur = qs + HD;
+    float* ps = kcur + HD;
+    const DLayer& Ly = M.layers[l];
+    const int ks = Ly.qkv.ks, kvh = h / M.G;
+    const int L = pos + 1, nch = (L + kAttnChunk - 1) / kAttnChunk, t0 = c * kAttnChunk;
+    const int n = min(kAttnChunk, L - t0);
+    const bool last = c == nch - 1;
+    const int cur = last ? pos - t0 : -1;
+    const size_t rowbase = ((size_t)l * M.NKV + kvh) * M.maxseq;
+    attn_issue_kv<HD>(M.kc + rowbase * HD, M.vc + rowbase * HD, t0, n, kls, vls, lane);
+    const float* part = qkv_part(M, l);
+    const int rq = h * HD, rk = M.NH * HD + kvh * HD, rv = M.NH * HD + M.KVD + kvh * HD;
+    for (int s = 0; s < ks; s++) {
+        dma_wave(part + (size_t)s * M.QKV + rq, qp + s * HD, HD * 4, lane);
+        if (last) {
+            dma_wave(part + (size_t)s * M.QKV + rk, kvp + s * HD, HD * 4, lane);
+            dma_wave(part + (size_t)s * M.QKV + rv, kvp + (kMaxKs + s) * HD, HD * 4, lane);
+        }
     }
+    drain_vm();
+    wave_lds_sync();
+    auto fin = [&](const float* p, int i, float bias) {
+        float v = p[i];
+        for (int s = 1; s < ks; s++) v = __fadd_rn(v, p[s * HD + i]);
+        return __fadd_rn(v, bias);
+    };
+    const int ip = lane % half;
+    const float2 cz = M.rope[(size_t)pos * half + ip];
+    if (lane < half) {
+        const float x0 = fin(qp, ip, Ly.bqkv[rq + ip]), x1 = fin(qp, ip + half, Ly.bqkv[rq + ip + half]);
+        qs[ip] = __fsub_rn(__fmul_rn(x0, cz.x), __fmul_rn(x1, cz.y));
+        qs[ip + half] = __fadd_rn(__fmul_rn(x0, cz.y), __fmul_rn(x1, cz.x));
+        if (last) {
+            const float k0 = fin(kvp, ip, Ly.bqkv[rk + ip]), k1 = fin(kvp, ip + half, Ly.bqkv[rk + ip + half]);
+            const __half y0 = __float2half(__fsub_rn(__fmul_rn(k0, cz.x), __fmul_rn(k1, cz.y)));
+            const __half y1 = __float2half(__fadd_rn(__fmul_rn(k0, cz.y), __fmul_rn(k1, cz.x)));
+            const __half v0 = __float2half(fin(kvp + kMaxKs * HD, ip, Ly.bqkv[rv + ip]));
+            const __half v1 = __float2half(fin(kvp + kMaxKs * HD, ip + half, Ly.bqkv[rv + ip + half]));
+            kcur[ip] = __half2float(y0);
+            kcur[ip + half] = __half2float(y1);
+            vls[cur * HD + ip] = v0;
+            vls[cur * HD + ip + half] = v1;
+            if (h % M.G == 0) {                    // one of the kv head's G query heads appends to the cache
+                __half* kd = M.kc + (rowbase + pos) * HD;
+                __half* vd = M.vc + (rowbase + pos) * HD;
+                kd[ip] = y0; kd[ip + half] = y1;
+                vd[ip] = v0; vd[ip + half] = v1;
+            }
+        }
+    }
+    wave_lds_sync();
+    float m, lsum, acc[DPL];
+    attn_core<HD>(kls, qs, kcur, cur, vls, ps, n, M.scale, lane, m, lsum, acc);
+    float* rec = att_rec(M, l) + ((size_t)h * M.maxch + c) * M.arec;
+#pragma unroll
+    for (int e = 0; e < DPL; e++) stc(rec + DPL * lane + e, acc[e]);
+    if (lane == 0) { stc(rec + HD, m); stc(rec + HD + 1, lsum); }
     wave_lds_sync();                           // LDS is reused by the wave's next item
 }
 
-template <int G, int HD>
-constexpr int attn_lds_bytes() { return 4 * G * HD + 2 * 64 * (HD + 8) + 4 * G * 64; }
-
-template <int G, int HD>
-__device__ void phase_attn_t(const DModel& M, int l, int pos, int wg, int nwg, uint8_t* smem) {
+template <int HD>
+__device__ void phase_attn(const DModel& M, int l, int pos, int wg, int nwg, uint8_t* smem) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int L = pos + 1, nch = (L + kAttnChunk - 1) / kAttnChunk, items = M.NKV * nch;
-    uint8_t* lds = smem + wave * attn_lds_bytes<G, HD>();
-    for (int it = wg * kWaves + wave; it < items; it += nwg * kWaves) {
-        const int kvh = it / nch, c = it % nch;
-        const size_t rows = ((size_t)l * M.NKV + kvh) * M.maxseq * HD;
-        attn_chunk<G, HD>(M.qf + kvh * G * HD, M.kc + rows, M.vc + rows, L, c, M.scale, M.att_ml, M.att_o,
-                          M.maxch, kvh * G, lds, lane);
-    }
+    if (wave >= kAttnWaves) return;
+    const int nch = (pos + 1 + kAttnChunk - 1) / kAttnChunk, items = M.NH * nch;
+    uint8_t* lds = smem + wave * attn_wave_lds<HD>();
+    for (int it = wg * kAttnWaves + wave; it < items; it += nwg * kAttnWaves)
+        attn_item<HD>(M, l, pos, it / nch, it % nch, lds, lane);
 }
 
-// P2 merge: per (head, dim) the chunk partials in chunk order
-__device__ void attn_combine(const float* ml, const float* o, int nh, int hd, int nch, int maxch, float* out,
-                             int wg, int nwg) {
-    for (int it = wg * kThreads + threadIdx.x; it < nh * hd; it += nwg * kThreads) {
-        const int h = it / hd, d = it % hd;
-        const float* mh = ml + (size_t)h * maxch * 2;
-        float Mx = -__builtin_inff();
-        for (int c = 0; c < nch; c++) Mx = fmaxf(Mx, mh[2 * c]);
-        float den = 0.f, acc = 0.f;
-        for (int c = 0; c < nch; c++) {
-            const float w = mi_expf(__fsub_rn(mh[2 * c], Mx));
-            den = __fmaf_rn(mh[2 * c + 1], w, den);
-            acc = __fmaf_rn(o[((size_t)h * maxch + c) * hd + d], w, acc);
-        }
-        out[it] = __fdiv_rn(acc, den);
+// merge of one (head, dim) from the chunk records in chunk order (cuda_infer.cu:688-702)
+__device__ __forceinline__ float combine_one(const float* recs, int rec, int hd, int d, int nch) {
+    float Mx = -__builtin_inff();
+    for (int c = 0; c < nch; c++) Mx = fmaxf(Mx, recs[c * rec + hd]);
+    float den = 0.f, acc = 0.f;
+    for (int c = 0; c < nch; c++) {
+        const float w = mi_expf(__fsub_rn(recs[c * rec + hd], Mx));
+        den = __fmaf_rn(recs[c * rec + hd + 1], w, den);
+        acc = __fmaf_rn(recs[c * rec + d], w, acc);
     }
+    return __fdiv_rn(acc, den);
 }
 
-// P3: attention output -> int8 -> O rows
-__device__ void phase_o(const DModel& M, int l, int wg, int nwg, uint8_t* smem) {
+// P2 merge as its own phase (more than kInlineComb chunks): one thread per (head, dim)
+__device__ void phase_comb(const DModel& M, int l, int pos, int wg, int nwg) {
+    const int nch = (pos + 1 + kAttnChunk - 1) / kAttnChunk;
+    const float* att = att_rec(M, l);
+    float* out = M.att_out + (size_t)l * M.E;
+    for (int it = wg * blockDim.x + threadIdx.x; it < M.E; it += nwg * blockDim.x)
+        stc(out + it, combine_one(att + (size_t)(it / M.HD) * M.maxch * M.arec, M.arec, M.HD, it % M.HD, nch));
+}
+
+// P3: attention output (chunk records merged here up to kInlineComb chunks) -> int8 -> O rows
+__device__ void phase_o(const DModel& M, int l, int pos, int wg, int nwg, uint8_t* smem) {
     const int tid = threadIdx.x;
     Stage S(smem);
-    for (int i = tid; i < M.E; i += kThreads) S.xs[i] = M.att_out[i];
+    const Touch pre = prefetch_first(M.layers[l].o, wg);
+    const int nch = (pos + 1 + kAttnChunk - 1) / kAttnChunk;
+    if (nch <= kInlineComb) {
+        const float* att = att_rec(M, l);
+        const int hb = nch * M.arec * 4;                 // bytes of one head's records
+        for (int h = 0; h < M.NH; h++) dma_wg(att + (size_t)h * M.maxch * M.arec, S.stg + h * nch * M.arec, hb);
+        drain_vm();
+        __syncthreads();
+        for (int i = tid; i < M.E; i += blockDim.x)
+            S.xs[i] = combine_one(S.stg + (i / M.HD) * nch * M.arec, M.arec, M.HD, i % M.HD, nch);
+    } else {
+        dma_wg(M.att_out + (size_t)l * M.E, S.xs, M.E * 4);
+        drain_vm();
+    }
     __syncthreads();
     norm_quant(S.xs, nullptr, M.E, 0.f, S.xq8, S.xds, tid);
     __syncthreads();
-    gemv_phase(M.layers[l].o, S.xq8, S.xds, M.o_part, wg, nwg, tid);
+    gemv_tasks(M.layers[l].o, S.xq8, S.xds, o_part(M, l), wg, nwg);
+    retire(pre, M.err);
 }
 
-// P4: residual (h_mid = h_in + O) -> RMSNorm -> int8 -> gate/up rows
+// quantize one 32-element block per half-wave and return the lane's code, the block
+// scale and 8*sum(q) on every lane (cuda_infer.cu:80-89)
+__device__ __forceinline__ void quant32_vals(float v, int& q, float& d, int& s8) {
+    float a = fabsf(v);
+#pragma unroll
+    for (int off = 16; off >= 1; off >>= 1) a = fmaxf(a, __shfl_xor(a, off));
+    const float inv = a > 0.f ? __fdiv_rn(127.f, a) : 0.f;
+    q = __float2int_rn(__fmul_rn(v, inv));
+    int s = q;
+#pragma unroll
+    for (int off = 16; off >= 1; off >>= 1) s += __shfl_xor(s, off);
+    d = __half2float(__float2half(__fdiv_rn(a, 127.f)));
+    s8 = 8 * s;
+}
+
+// P4: residual (h_mid = h_in + O) -> RMSNorm -> int8 -> gate/up rows -> silu(gate)*up
+// (cpu_infer.cpp:144-147) -> int8 act block records. A workgroup owns whole 64-row
+// groups (32 gate rows + their 32 up rows = one 32-element act block): its waves
+// compute the ks K segments, which are added in order from LDS.
 __device__ void phase_gu(const DModel& M, int l, int wg, int nwg, uint8_t* smem) {
-    const int tid = threadIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = nwaves();
     Stage S(smem);
     const DLayer& L = M.layers[l];
-    residual_into(S.xs, M.hbuf + hin(l, M.E), M.o_part, L.o.ks, M.E, wg == 0 ? M.hbuf + hmid(l, M.E) : nullptr, tid);
+    const PMat& W = L.gu;
+    const int ks = W.ks, slots = nw / ks, ng = W.rows / 64;
+    const int slot = wave / ks, seg = wave % ks;
+    Touch pre{0};
+    if (slot < slots && wg * slots + slot < ng) {
+        const int g = wg * slots + slot, c0 = seg * W.nc / ks;
+        touch_lines(W.base + ((size_t)g * W.nc + c0) * tile_bytes(W.cb), (int)tile_bytes(W.cb), pre);
+    }
+    residual_dma(S, M.hbuf + hin(l, M.E), o_part(M, l), L.o.ks, M.E, wg == 0 ? M.hbuf + hmid(l, M.E) : nullptr);
     __syncthreads();
     norm_quant(S.xs, L.fn, M.E, M.eps, S.xq8, S.xds, tid);
     __syncthreads();
-    gemv_phase(L.gu, S.xq8, S.xds, M.gu_part, wg, nwg, tid);
-}
-
-// P4 epilogue: silu(gate) * up (cpu_infer.cpp:147) -> int8 blocks of the down input
-__device__ void phase_act(const DModel& M, int l, int wg, int nwg) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const PMat& W = M.layers[l].gu;
-    const int nblk = M.FF / 32, rows = 2 * M.FF;
-    for (int it = wg * kWaves + wave; 2 * it < nblk; it += nwg * kWaves) {
-        const int b = 2 * it + (lane >> 5), j = lane & 31;
-        const bool own = b < nblk;
-        const int bc = own ? b : nblk - 1;
-        const float* pg = M.gu_part + bc * 64 + j;
-        float g = pg[0], u = pg[32];
-        for (int s = 1; s < W.ks; s++) {
-            g = __fadd_rn(g, pg[(size_t)s * rows]);
-            u = __fadd_rn(u, pg[(size_t)s * rows + 32]);
+    uint8_t* act = act_rec(M, l);
+    for (int base = wg * slots; base < ng; base += nwg * slots) {
+        const int g = base + slot;
+        if (slot < slots && g < ng)
+            S.gpart[wave * 64 + lane] = row_segment(W, g, seg, S.xq8, S.xds, lane);
+        __syncthreads();
+        if (wave < slots) {
+            const int gg = base + wave;
+            float v = S.gpart[(wave * ks) * 64 + lane];
+            for (int s = 1; s < ks; s++) v = __fadd_rn(v, S.gpart[(wave * ks + s) * 64 + lane]);
+            const float u = __shfl(v, (lane & 31) + 32);
+            const float t = mi_expf(-v);
+            const float a = __fmul_rn(__fdiv_rn(v, __fadd_rn(1.0f, t)), u);
+            int q, s8;
+            float d;
+            quant32_vals(a, q, d, s8);
+            const uint32_t b = (uint32_t)(q & 0xFF);
+            const uint32_t w = b | (__shfl_down(b, 1) << 8) | (__shfl_down(b, 2) << 16) | (__shfl_down(b, 3) << 24);
+            if (gg < ng && lane < 32) {
+                uint32_t* r = reinterpret_cast<uint32_t*>(act + (size_t)gg * kActRec);
+                if ((lane & 3) == 0) stc(r + lane / 4, w);
+                if (lane == 0) { stc(r + 8, __float_as_uint(d)); stc(r + 9, (uint32_t)s8); }
+            }
         }
-        const float t = mi_expf(-g);
-        const float a = __fmul_rn(__fdiv_rn(g, __fadd_rn(1.0f, t)), u);
-        quant32(a, own, M.act_q, bc * 32 + j, M.act_ds, lane);
+        __syncthreads();
     }
+    retire(pre, M.err);
 }
 
-// P5: int8 act -> down rows
+// P5: int8 act records -> LDS -> down rows
 __device__ void phase_down(const DModel& M, int l, int wg, int nwg, uint8_t* smem) {
     const int tid = threadIdx.x;
     Stage S(smem);
-    const int nw = M.FF / 16;                   // 16-byte vectors of act_q
-    for (int i = tid; i < nw; i += kThreads)
-        reinterpret_cast<uint4*>(S.xq8)[i] = reinterpret_cast<const uint4*>(M.act_q)[i];
-    for (int i = tid; i < M.FF / 32; i += kThreads) S.xds[i] = M.act_ds[i];
+    const Touch pre = prefetch_first(M.layers[l].d, wg);
+    const int nblk = M.FF / 32;
+    dma_wg(act_rec(M, l), S.stg, nblk * kActRec);
+    drain_vm();
     __syncthreads();
-    gemv_phase(M.layers[l].d, S.xq8, S.xds, M.d_part, wg, nwg, tid);
+    const uint8_t* rec = reinterpret_cast<const uint8_t*>(S.stg);
+    for (int i = tid; i < nblk * 8; i += blockDim.x)
+        reinterpret_cast<uint32_t*>(S.xq8)[i] = reinterpret_cast<const uint32_t*>(rec + (i / 8) * kActRec)[i % 8];
+    for (int i = tid; i < nblk; i += blockDim.x) {
+        const uint32_t* r = reinterpret_cast<const uint32_t*>(rec + i * kActRec);
+        S.xds[i] = make_float2(__uint_as_float(r[8]), __uint_as_float(r[9]));
+    }
+    __syncthreads();
+    gemv_tasks(M.layers[l].d, S.xq8, S.xds, d_part(M, l), wg, nwg);
+    retire(pre, M.err);
 }
 
 // lm_head: final residual -> RMSNorm -> int8 -> vocab rows, per-workgroup top-2
 __device__ void phase_lm(const DModel& M, int wg, int nwg, uint8_t* smem) {
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = nwaves();
     Stage S(smem);
-    residual_into(S.xs, M.hbuf + hmid(M.NL - 1, M.E), M.d_part, M.layers[M.NL - 1].d.ks, M.E,
-                  wg == 0 ? M.hbuf + (size_t)2 * M.NL * M.E : nullptr, tid);
+    const int ng = M.lm.rows / 64;
+    const Touch pre = prefetch_first(M.lm, wg);
+    residual_dma(S, M.hbuf + hmid(M.NL - 1, M.E), d_part(M, M.NL - 1), M.layers[M.NL - 1].d.ks, M.E,
+                 wg == 0 ? M.hbuf + (size_t)2 * M.NL * M.E : nullptr);
     __syncthreads();
     norm_quant(S.xs, M.out_norm, M.E, M.eps, S.xq8, S.xds, tid);
     __syncthreads();
     Top2 t{-__builtin_inff(), INT_MAX, -__builtin_inff()};
-    const int ng = M.lm.rows / 64;
-    for (int g = wg * kWaves + wave; g < ng; g += nwg * kWaves) {
+    for (int g = wg * nw + wave; g < ng; g += nwg * nw) {
         const float v = row_segment(M.lm, g, 0, S.xq8, S.xds, lane);
         const int row = g * 64 + lane;
         if (M.logits) M.logits[row] = v;
         top2_push(t, v, row);
     }
     top2_wave(t);
+    retire(pre, M.err);
     if (lane == 0) S.red[wave] = make_float4(t.best, __int_as_float(t.idx), t.second, 0.f);
     __syncthreads();
     if (tid == 0) {
         Top2 a{S.red[0].x, __float_as_int(S.red[0].y), S.red[0].z};
-        for (int w = 1; w < kWaves; w++) top2_merge(a, S.red[w].x, __float_as_int(S.red[w].y), S.red[w].z);
-        M.cand[wg] = make_float4(a.best, __int_as_float(a.idx), a.second, 0.f);
+        for (int w = 1; w < nw; w++) top2_merge(a, S.red[w].x, __float_as_int(S.red[w].y), S.red[w].z);
+        float* cd = M.cand + (size_t)wg * 32;
+        stc(cd, a.best);
+        stc(reinterpret_cast<uint32_t*>(cd + 1), (uint32_t)a.idx);
+        stc(cd + 2, a.second);
     }
 }
 
 // merge the lm workgroups' candidates (top-2 merging is associative and commutative,
-// so any order gives the same token and margin)
-__device__ Top2 merge_cands(const float4* cand, int n, float4* red) {
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+// so any order gives the same token and margin); the result is on every thread
+__device__ Top2 merge_cands(const float* cand, int n, float4* red) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = nwaves();
     Top2 t{-__builtin_inff(), INT_MAX, -__builtin_inff()};
-    for (int i = tid; i < n; i += kThreads) { const float4 c = cand[i]; top2_merge(t, c.x, __float_as_int(c.y), c.z); }
+    for (int i = tid; i < n; i += blockDim.x) {
+        const float* cd = cand + (size_t)i * 32;
+        top2_merge(t, cd[0], __float_as_int(cd[1]), cd[2]);
+    }
     top2_wave(t);
     __syncthreads();
     if (lane == 0) red[wave] = make_float4(t.best, __int_as_float(t.idx), t.second, 0.f);
     __syncthreads();
     Top2 a{red[0].x, __float_as_int(red[0].y), red[0].z};
-    for (int w = 1; w < kWaves; w++) top2_merge(a, red[w].x, __float_as_int(red[w].y), red[w].z);
+    for (int w = 1; w < nw; w++) top2_merge(a, red[w].x, __float_as_int(red[w].y), red[w].z);
     return a;
+}
+
+__device__ __forceinline__ void emit_token(const DModel& M, const Top2& a, int pos, int gen) {
+    M.out_tok[pos] = a.idx;
+    M.out_margin[pos] = __fsub_rn(a.best, a.second);
+    if (gen) M.tokbuf[pos + 1] = a.idx;
 }
 
 // ------------------------------------------------------------------ per-phase kernels
@@ -499,27 +721,22 @@ __global__ __launch_bounds__(kThreads) void k_qkv(DModel M, int l, int pos) {
     __shared__ __align__(16) uint8_t smem[kStageBytes];
     phase_qkv(M, l, pos, blockIdx.x, gridDim.x, smem);
 }
-__global__ __launch_bounds__(kThreads) void k_qkv_fin(DModel M, int l, int pos) {
-    phase_qkv_fin(M, l, pos, blockIdx.x, gridDim.x);
-}
-template <int G, int HD>
+template <int HD>
 __global__ __launch_bounds__(kThreads) void k_attn(DModel M, int l, int pos) {
-    __shared__ __align__(16) uint8_t smem[kWaves * attn_lds_bytes<G, HD>()];
-    phase_attn_t<G, HD>(M, l, pos, blockIdx.x, gridDim.x, smem);
+    __shared__ __align__(16) uint8_t smem[kAttnWaves * attn_wave_lds<HD>()];
+    phase_attn<HD>(M, l, pos, blockIdx.x, gridDim.x, smem);
 }
-__global__ __launch_bounds__(kThreads) void k_attn_comb(DModel M, int pos) {
-    const int nch = (pos + 1 + kAttnChunk - 1) / kAttnChunk;
-    attn_combine(M.att_ml, M.att_o, M.NH, M.HD, nch, M.maxch, M.att_out, blockIdx.x, gridDim.x);
+__global__ __launch_bounds__(kThreads) void k_attn_comb(DModel M, int l, int pos) {
+    phase_comb(M, l, pos, blockIdx.x, gridDim.x);
 }
-__global__ __launch_bounds__(kThreads) void k_o(DModel M, int l) {
+__global__ __launch_bounds__(kThreads) void k_o(DModel M, int l, int pos) {
     __shared__ __align__(16) uint8_t smem[kStageBytes];
-    phase_o(M, l, blockIdx.x, gridDim.x, smem);
+    phase_o(M, l, pos, blockIdx.x, gridDim.x, smem);
 }
 __global__ __launch_bounds__(kThreads) void k_gu(DModel M, int l) {
     __shared__ __align__(16) uint8_t smem[kStageBytes];
     phase_gu(M, l, blockIdx.x, gridDim.x, smem);
 }
-__global__ __launch_bounds__(kThreads) void k_act(DModel M, int l) { phase_act(M, l, blockIdx.x, gridDim.x); }
 __global__ __launch_bounds__(kThreads) void k_down(DModel M, int l) {
     __shared__ __align__(16) uint8_t smem[kStageBytes];
     phase_down(M, l, blockIdx.x, gridDim.x, smem);
@@ -529,13 +746,72 @@ __global__ __launch_bounds__(kThreads) void k_lm(DModel M) {
     phase_lm(M, blockIdx.x, gridDim.x, smem);
 }
 __global__ __launch_bounds__(kThreads) void k_argmax(DModel M, int ncand, int pos, int gen) {
-    __shared__ float4 red[kWaves];
+    __shared__ float4 red[kMaxWaves];
     const Top2 a = merge_cands(M.cand, ncand, red);
-    if (threadIdx.x == 0) {
-        M.out_tok[pos] = a.idx;
-        M.out_margin[pos] = __fsub_rn(a.best, a.second);
-        if (gen) M.tokbuf[pos + 1] = a.idx;
+    if (threadIdx.x == 0) emit_token(M, a, pos, gen);
+}
+
+// ------------------------------------------------------------------ persistent step kernel
+// The whole decode step of position pos in one cooperative launch (one workgroup per
+// CU): the phases above separated by grid barriers, 5 per layer + 1 before the
+// argmax (the reference's mega kernel has the same count, mega.cu:695-833). Every
+// workgroup merges the lm_head candidates itself, so the token needs no barrier.
+// Profile slots per layer: end of qkv, its barrier, attention, barrier, o, barrier,
+// gate/up, barrier, down, barrier; then lm, barrier.
+constexpr int kProfPerLayer = 10;
+__device__ __forceinline__ void stamp(const DModel& M, int slot) {
+    if (M.prof && blockIdx.x == 0 && threadIdx.x == 0) M.prof[slot] = __builtin_amdgcn_s_memrealtime();
+}
+
+template <int HD>
+constexpr int step_lds() { return kAttnWaves * attn_wave_lds<HD>() > kStageBytes ? kAttnWaves * attn_wave_lds<HD>() : kStageBytes; }
+
+template <int HD>
+__global__ __launch_bounds__(kPThreads) void k_step(DModel M, int pos, int gen) {
+    __shared__ __align__(16) uint8_t smem[step_lds<HD>()];
+    const int wg = blockIdx.x, nwg = gridDim.x;
+    const int nch = (pos + 1 + kAttnChunk - 1) / kAttnChunk;
+    unsigned epoch = 0;
+    stamp(M, 0);
+    for (int l = 0; l < M.NL; l++) {
+        const int p0 = 1 + l * kProfPerLayer;
+        phase_qkv(M, l, pos, wg, nwg, smem);
+        stamp(M, p0 + 0);
+        grid_barrier(M.bar, M.err, epoch);
+        stamp(M, p0 + 1);
+        phase_attn<HD>(M, l, pos, wg, nwg, smem);
+        stamp(M, p0 + 2);
+        grid_barrier(M.bar, M.err, epoch);
+        if (nch > kInlineComb) {
+            phase_comb(M, l, pos, wg, nwg);
+            grid_barrier(M.bar, M.err, epoch);
+        }
+        stamp(M, p0 + 3);
+        phase_o(M, l, pos, wg, nwg, smem);
+        stamp(M, p0 + 4);
+        grid_barrier(M.bar, M.err, epoch);
+        stamp(M, p0 + 5);
+        phase_gu(M, l, wg, nwg, smem);
+        stamp(M, p0 + 6);
+        grid_barrier(M.bar, M.err, epoch);
+        stamp(M, p0 + 7);
+        phase_down(M, l, wg, nwg, smem);
+        stamp(M, p0 + 8);
+        grid_barrier(M.bar, M.err, epoch);
+        stamp(M, p0 + 9);
     }
+    phase_lm(M, wg, nwg, smem);
+    stamp(M, 1 + M.NL * kProfPerLayer);
+    grid_barrier(M.bar, M.err, epoch);
+    stamp(M, 2 + M.NL * kProfPerLayer);
+    const Top2 a = merge_cands(M.cand, nwg, Stage(smem).red);
+    if (wg == 0 && threadIdx.x == 0) emit_token(M, a, pos, gen);
+}
+
+// barrier cost: n grid barriers and nothing else
+__global__ __launch_bounds__(kPThreads) void k_barriers(uint32_t* bar, int32_t* err, int n) {
+    unsigned epoch = 0;
+    for (int i = 0; i < n; i++) grid_barrier(bar, err, epoch);
 }
 
 // ------------------------------------------------------------------ standalone kernels
@@ -543,30 +819,29 @@ __global__ __launch_bounds__(kThreads) void k_quant(const float* x, int n, int8_
     const int lane = threadIdx.x & 63;
     const int e = blockIdx.x * kThreads + threadIdx.x;
     const bool own = e < n;
-    const float v = own ? x[e] : 0.f;
-    float a = fabsf(v);
-#pragma unroll
-    for (int off = 16; off >= 1; off >>= 1) a = fmaxf(a, __shfl_xor(a, off));
-    const float inv = a > 0.f ? __fdiv_rn(127.f, a) : 0.f;
-    const int q = __float2int_rn(__fmul_rn(v, inv));
-    int s = q;
-#pragma unroll
-    for (int off = 16; off >= 1; off >>= 1) s += __shfl_xor(s, off);
+    int q, s8;
+    float d;
+    quant32_vals(own ? x[e] : 0.f, q, d, s8);
     if (own) {
         xq[e] = (int8_t)q;
-        if ((lane & 31) == 0) { xd[e >> 5] = __half2float(__float2half(__fdiv_rn(a, 127.f))); xs8[e >> 5] = 8 * s; }
+        if ((lane & 31) == 0) { xd[e >> 5] = d; xs8[e >> 5] = s8; }
     }
 }
 
 __global__ __launch_bounds__(kThreads) void k_gemv(PMat W, const int8_t* xq, const float* xd, const int32_t* xs8, float* part) {
-    __shared__ __align__(16) uint8_t smem[kStageBytes];
-    Stage S(smem);
+    __shared__ __align__(16) uint8_t smem[4 * kMaxE + kMaxFF + kMaxFF / 4];
+    int8_t* xq8 = reinterpret_cast<int8_t*>(smem + 4 * kMaxE);
+    float2* xds = reinterpret_cast<float2*>(smem + 4 * kMaxE + kMaxFF);
     const int n = W.nb * 32;
-    for (int i = threadIdx.x; i < n / 16; i += kThreads)
-        reinterpret_cast<uint4*>(S.xq8)[i] = reinterpret_cast<const uint4*>(xq)[i];
-    for (int i = threadIdx.x; i < W.nb; i += kThreads) S.xds[i] = make_float2(xd[i], __int_as_float(xs8[i]));
+    for (int i = threadIdx.x; i < n / 16; i += kThreads) reinterpret_cast<uint4*>(xq8)[i] = reinterpret_cast<const uint4*>(xq)[i];
+    for (int i = threadIdx.x; i < W.nb; i += kThreads) xds[i] = make_float2(xd[i], __int_as_float(xs8[i]));
     __syncthreads();
-    gemv_phase(W, S.xq8, S.xds, part, blockIdx.x, gridDim.x, threadIdx.x);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int ntask = (W.rows / 64) * W.ks;
+    for (int task = blockIdx.x * kWaves + wave; task < ntask; task += gridDim.x * kWaves) {
+        const int g = task / W.ks, s = task % W.ks;
+        part[(size_t)s * W.rows + g * 64 + lane] = row_segment(W, g, s, xq8, xds, lane);
+    }
 }
 
 __global__ void k_seg_sum(const float* part, int rows, int ks, float* y) {
@@ -587,22 +862,38 @@ __global__ __launch_bounds__(64) void k_isums(PMat W, const int8_t* xq, int32_t*
     isum[(size_t)(g * 64 + lane) * W.nb + b] = dot_q4(w, xp[0], xp[1]);
 }
 
-template <int G, int HD>
-__global__ __launch_bounds__(kThreads) void k_attn_standalone(const float* q, const __half* kc, const __half* vc, int nkv,
-                                                               int L, int ctx, float scale, float* ml, float* o, int maxch) {
-    __shared__ __align__(16) uint8_t smem[kWaves * attn_lds_bytes<G, HD>()];
+// standalone attention: q[nh][hd] and an fp16 cache [nkv][ctx][hd]; records [nh][nch][hd+32]
+template <int HD>
+__global__ __launch_bounds__(kThreads) void k_attn_standalone(const float* q, const __half* kc, const __half* vc, int nh,
+                                                               int nkv, int L, int ctx, float scale, float* recs) {
+    constexpr int DPL = HD / 64, REC = HD + 32;
+    __shared__ __align__(16) uint8_t smem[kAttnWaves * attn_wave_lds<HD>()];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int nch = (L + kAttnChunk - 1) / kAttnChunk, items = nkv * nch;
-    uint8_t* lds = smem + wave * attn_lds_bytes<G, HD>();
-    for (int it = blockIdx.x * kWaves + wave; it < items; it += gridDim.x * kWaves) {
-        const int kvh = it / nch, c = it % nch;
-        attn_chunk<G, HD>(q + kvh * G * HD, kc + (size_t)kvh * ctx * HD, vc + (size_t)kvh * ctx * HD, L, c, scale,
-                          ml, o, maxch, kvh * G, lds, lane);
+    if (wave >= kAttnWaves) return;
+    const int nch = (L + kAttnChunk - 1) / kAttnChunk, items = nh * nch, G = nh / nkv;
+    uint8_t* lds = smem + wave * attn_wave_lds<HD>();
+    uint4* kls = reinterpret_cast<uint4*>(lds);
+    __half* vls = reinterpret_cast<__half*>(lds + 64 * HD * 2);
+    float* qs = reinterpret_cast<float*>(lds + 2 * 64 * HD * 2) + 3 * kMaxKs * HD;
+    float* ps = qs + 2 * HD;
+    for (int it = blockIdx.x * kAttnWaves + wave; it < items; it += gridDim.x * kAttnWaves) {
+        const int h = it / nch, c = it % nch, kvh = h / G, t0 = c * kAttnChunk, n = min(kAttnChunk, L - t0);
+        attn_issue_kv<HD>(kc + (size_t)kvh * ctx * HD, vc + (size_t)kvh * ctx * HD, t0, n, kls, vls, lane);
+        for (int i = lane; i < HD; i += 64) qs[i] = q[(size_t)h * HD + i];
+        drain_vm();
+        wave_lds_sync();
+        float m, lsum, acc[DPL];
+        attn_core<HD>(kls, qs, qs, -1, vls, ps, n, scale, lane, m, lsum, acc);
+        float* rec = recs + ((size_t)h * nch + c) * REC;
+#pragma unroll
+        for (int e = 0; e < DPL; e++) rec[DPL * lane + e] = acc[e];
+        if (lane == 0) { rec[HD] = m; rec[HD + 1] = lsum; }
+        wave_lds_sync();
     }
 }
-__global__ __launch_bounds__(kThreads) void k_comb_standalone(const float* ml, const float* o, int nh, int hd, int nch,
-                                                               float* out) {
-    attn_combine(ml, o, nh, hd, nch, nch, out, blockIdx.x, gridDim.x);
+__global__ __launch_bounds__(kThreads) void k_comb_standalone(const float* recs, int nh, int hd, int nch, float* out) {
+    for (int it = blockIdx.x * blockDim.x + threadIdx.x; it < nh * hd; it += gridDim.x * blockDim.x)
+        out[it] = combine_one(recs + (size_t)(it / hd) * nch * (hd + 32), hd + 32, hd, it % hd, nch);
 }
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
@@ -625,62 +916,83 @@ __global__ __launch_bounds__(kThreads) void k_stream(const u32x4* __restrict__ p
 // ------------------------------------------------------------------ host launchers
 #define LAUNCH(kern, grid, block, stream, ...) hipLaunchKernelGGL(kern, dim3(grid), dim3(block), 0, stream, __VA_ARGS__)
 
-static bool attn_supported(int G, int HD) {
-    return (HD == 64 || HD == 128) && (G == 1 || G == 2 || G == 4 || G == 6 || G == 7 || G == 8);
-}
-bool kernels_support(int G, int HD) { return attn_supported(G, HD); }
-
-template <int HD>
-static void launch_attn_hd(int G, const DModel& M, int l, int pos, int grid, hipStream_t s) {
-    switch (G) {
-        case 1: LAUNCH((k_attn<1, HD>), grid, kThreads, s, M, l, pos); break;
-        case 2: LAUNCH((k_attn<2, HD>), grid, kThreads, s, M, l, pos); break;
-        case 4: LAUNCH((k_attn<4, HD>), grid, kThreads, s, M, l, pos); break;
-        case 6: LAUNCH((k_attn<6, HD>), grid, kThreads, s, M, l, pos); break;
-        case 7: LAUNCH((k_attn<7, HD>), grid, kThreads, s, M, l, pos); break;
-        default: LAUNCH((k_attn<8, HD>), grid, kThreads, s, M, l, pos); break;
-    }
-}
+bool kernels_support(int G, int HD) { return (HD == 64 || HD == 128) && G >= 1; }
+int kernels_max_ks() { return kMaxKs; }
+int attn_record_floats(int HD) { return HD + 32; }
 
 static int waves_grid(int tasks, int cap) { return std::max(1, std::min(cap, (tasks + kWaves - 1) / kWaves)); }
 
+template <class F>
+static void with_hd(int HD, F f) {
+    if (HD == 64) f(std::integral_constant<int, 64>());
+    else f(std::integral_constant<int, 128>());
+}
+
 void launch_phase(const DModel& M, const PhaseGrid& pg, int phase, int l, int pos, int gen, hipStream_t s) {
+    const int nch = (pos + 1 + kAttnChunk - 1) / kAttnChunk;
     switch (phase) {
         case 0: LAUNCH(k_qkv, pg.qkv, kThreads, s, M, l, pos); break;
-        case 1: LAUNCH(k_qkv_fin, pg.fin, kThreads, s, M, l, pos); break;
-        case 2: {
-            const int nch = (pos + 1 + kAttnChunk - 1) / kAttnChunk;
-            const int ag = waves_grid(M.NKV * nch, 1 << 16);
-            if (M.HD == 64) launch_attn_hd<64>(M.G, M, l, pos, ag, s);
-            else launch_attn_hd<128>(M.G, M, l, pos, ag, s);
+        case 1: {
+            const int ag = std::max(1, std::min(1 << 16, (M.NH * nch + kAttnWaves - 1) / kAttnWaves));
+            with_hd(M.HD, [&](auto hd) { LAUNCH((k_attn<decltype(hd)::value>), ag, kThreads, s, M, l, pos); });
             break;
         }
-        case 3: LAUNCH(k_attn_comb, pg.comb, kThreads, s, M, pos); break;
-        case 4: LAUNCH(k_o, pg.o, kThreads, s, M, l); break;
-        case 5: LAUNCH(k_gu, pg.gu, kThreads, s, M, l); break;
-        case 6: LAUNCH(k_act, pg.act, kThreads, s, M, l); break;
-        case 7: LAUNCH(k_down, pg.down, kThreads, s, M, l); break;
-        case 8: LAUNCH(k_lm, pg.lm, kThreads, s, M); break;
+        case 2: if (nch > kInlineComb) LAUNCH(k_attn_comb, pg.comb, kThreads, s, M, l, pos); break;
+        case 3: LAUNCH(k_o, pg.o, kThreads, s, M, l, pos); break;
+        case 4: LAUNCH(k_gu, pg.gu, kThreads, s, M, l); break;
+        case 5: LAUNCH(k_down, pg.down, kThreads, s, M, l); break;
+        case 6: LAUNCH(k_lm, pg.lm, kThreads, s, M); break;
         default: LAUNCH(k_argmax, 1, kThreads, s, M, pg.lm, pos, gen); break;
     }
 }
 
 void launch_step_phases(const DModel& M, const PhaseGrid& pg, int pos, int gen, hipStream_t s) {
     for (int l = 0; l < M.NL; l++)
-        for (int ph = 0; ph < 8; ph++) launch_phase(M, pg, ph, l, pos, gen, s);
-    launch_phase(M, pg, 8, 0, pos, gen, s);
-    launch_phase(M, pg, 9, 0, pos, gen, s);
+        for (int ph = 0; ph < 6; ph++) launch_phase(M, pg, ph, l, pos, gen, s);
+    launch_phase(M, pg, 6, 0, pos, gen, s);
+    launch_phase(M, pg, 7, 0, pos, gen, s);
+}
+
+hipError_t launch_step_persistent(const DModel& M, int nwg, int pos, int gen, hipStream_t s) {
+    hipError_t err = hipMemsetAsync(M.bar, 0, sizeof(uint32_t) * kBarWords, s);
+    if (err != hipSuccess) return err;
+    with_hd(M.HD, [&](auto hd) {
+        DModel m = M;
+        void* args[] = {&m, &pos, &gen};
+        err = hipLaunchCooperativeKernel(reinterpret_cast<const void*>(&k_step<decltype(hd)::value>), dim3(nwg),
+                                         dim3(kPThreads), args, 0, s);
+    });
+    return err;
+}
+
+hipError_t launch_barriers(uint32_t* bar, int32_t* err, int nwg, int n, hipStream_t s) {
+    hipError_t e = hipMemsetAsync(bar, 0, sizeof(uint32_t) * kBarWords, s);
+    if (e != hipSuccess) return e;
+    void* args[] = {&bar, &err, &n};
+    return hipLaunchCooperativeKernel(reinterpret_cast<const void*>(&k_barriers), dim3(nwg), dim3(kPThreads), args, 0, s);
+}
+int barrier_words() { return kBarWords; }
+
+int persistent_max_grid(int G, int HD) {
+    (void)G;
+    int per_cu = 0;
+    with_hd(HD, [&](auto hd) {
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(&k_step<decltype(hd)::value>),
+                                                         kPThreads, 0) != hipSuccess)
+            per_cu = 0;
+    });
+    return per_cu;
 }
 
 PhaseGrid plan_phase_grid(const DModel& M, const DLayer& L0, int n_cu) {
     PhaseGrid g;
     const int cap = 4 * n_cu;
     g.qkv = waves_grid((L0.qkv.rows / 64) * L0.qkv.ks, cap);
-    g.fin = std::max(1, std::min(cap, (M.NH * M.HD / 2 + M.KVD / 2 + M.KVD + kThreads - 1) / kThreads));
-    g.comb = std::max(1, (M.NH * M.HD + kThreads - 1) / kThreads);
+    g.fin = 0;
+    g.comb = std::max(1, (M.E + kThreads - 1) / kThreads);
     g.o = waves_grid((L0.o.rows / 64) * L0.o.ks, cap);
-    g.gu = waves_grid((L0.gu.rows / 64) * L0.gu.ks, cap);
-    g.act = waves_grid((M.FF / 32 + 1) / 2, cap);
+    g.gu = std::max(1, std::min(cap, (L0.gu.rows / 64) / std::max(1, kWaves / L0.gu.ks)));
+    g.act = 0;
     g.down = waves_grid((L0.d.rows / 64) * L0.d.ks, cap);
     g.lm = waves_grid(M.lm.rows / 64, cap);
     return g;
@@ -697,29 +1009,15 @@ void launch_gemv(const PMat& W, const int8_t* xq, const float* xd, const int32_t
 void launch_isums(const PMat& W, const int8_t* xq, int32_t* isum, hipStream_t s) {
     hipLaunchKernelGGL(k_isums, dim3(W.rows / 64, W.nb), dim3(64), 0, s, W, xq, isum);
 }
-template <int HD>
-static void launch_attn_sa_hd(int G, const float* q, const __half* kc, const __half* vc, int nkv, int L, int ctx,
-                              float scale, float* ml, float* o, int maxch, int grid, hipStream_t s) {
-    switch (G) {
-        case 1: LAUNCH((k_attn_standalone<1, HD>), grid, kThreads, s, q, kc, vc, nkv, L, ctx, scale, ml, o, maxch); break;
-        case 2: LAUNCH((k_attn_standalone<2, HD>), grid, kThreads, s, q, kc, vc, nkv, L, ctx, scale, ml, o, maxch); break;
-        case 4: LAUNCH((k_attn_standalone<4, HD>), grid, kThreads, s, q, kc, vc, nkv, L, ctx, scale, ml, o, maxch); break;
-        case 6: LAUNCH((k_attn_standalone<6, HD>), grid, kThreads, s, q, kc, vc, nkv, L, ctx, scale, ml, o, maxch); break;
-        case 7: LAUNCH((k_attn_standalone<7, HD>), grid, kThreads, s, q, kc, vc, nkv, L, ctx, scale, ml, o, maxch); break;
-        default: LAUNCH((k_attn_standalone<8, HD>), grid, kThreads, s, q, kc, vc, nkv, L, ctx, scale, ml, o, maxch); break;
-    }
-}
 bool launch_attn_decode(const float* q, const __half* kc, const __half* vc, int nh, int nkv, int hd, int L, int ctx,
                         float scale, float* scratch, float* out, hipStream_t s) {
-    const int G = nh / nkv;
-    if (nh % nkv || !attn_supported(G, hd)) return false;
+    if (nh % nkv || !kernels_support(nh / nkv, hd)) return false;
     const int nch = (L + kAttnChunk - 1) / kAttnChunk;
-    float* ml = scratch;
-    float* o = scratch + (size_t)nh * nch * 2;
-    const int grid = waves_grid(nkv * nch, 1 << 16);
-    if (hd == 64) launch_attn_sa_hd<64>(G, q, kc, vc, nkv, L, ctx, scale, ml, o, nch, grid, s);
-    else launch_attn_sa_hd<128>(G, q, kc, vc, nkv, L, ctx, scale, ml, o, nch, grid, s);
-    LAUNCH(k_comb_standalone, (nh * hd + kThreads - 1) / kThreads, kThreads, s, ml, o, nh, hd, nch, out);
+    const int grid = std::max(1, std::min(1 << 16, (nh * nch + kAttnWaves - 1) / kAttnWaves));
+    with_hd(hd, [&](auto h) {
+        LAUNCH((k_attn_standalone<decltype(h)::value>), grid, kThreads, s, q, kc, vc, nh, nkv, L, ctx, scale, scratch);
+    });
+    LAUNCH(k_comb_standalone, (nh * hd + kThreads - 1) / kThreads, kThreads, s, scratch, nh, hd, nch, out);
     return true;
 }
 void launch_stream(const void* buf, size_t bytes, uint32_t* sink, int n_cu, hipStream_t s) {

@@ -65,6 +65,8 @@ SIGNATURES = {
                               TOKEN_CB, _P]),
     "mi_get_stats": (C.c_int, [_P, C.POINTER(Stats)]),
     "mi_time_phase": (C.c_int, [_P, C.c_int32, C.c_int32, C.c_int32, C.POINTER(C.c_double)]),
+    "mi_profile_step": (C.c_int, [_P, C.POINTER(C.c_double), C.c_int32]),
+    "mi_barrier_cost": (C.c_int, [C.c_int32, C.c_int32, C.POINTER(C.c_double)]),
     "mi_synth_gguf": (C.c_int, [C.c_char_p, C.POINTER(SynthShape), C.c_uint64]),
     "mi_q4_packed_bytes": (C.c_size_t, [C.c_int32, C.c_int32, C.c_int32]),
     "mi_q4_pack": (C.c_int, [_P, C.c_int32, C.c_int32, C.c_int32, _P]),
@@ -187,7 +189,7 @@ class Engine:
         _check(lib().mi_generate(self._h, n_gen, out, mg, C.byref(n), cb, None), self._h)
         return list(out[:n.value]), list(mg[:n.value])
 
-    PHASES = ["qkv", "qkv_fin", "attn", "attn_comb", "o", "gate_up", "act", "down", "lm_head", "argmax"]
+    PHASES = ["qkv", "attn", "attn_comb", "o", "gate_up", "down", "lm_head", "argmax", "step"]
 
     def time_phase(self, phase, layer=0, reps=20):
         """mean duration (ms) of one phase kernel of the last step, from HIP events"""
@@ -195,6 +197,23 @@ class Engine:
         ms = C.c_double()
         _check(lib().mi_time_phase(self._h, ph, layer, reps, C.byref(ms)), self._h)
         return ms.value
+
+    PROFILE_NAMES = ["qkv", "bar_qkv", "attn", "bar_attn", "o", "bar_o", "gate_up", "bar_gu", "down", "bar_down"]
+
+    def profile_step(self):
+        """per-phase microseconds of one persistent step (workgroup 0's view)"""
+        n = self.info.n_layer * 10 + 2
+        buf = (C.c_double * n)()
+        _check(lib().mi_profile_step(self._h, buf, n), self._h)
+        v = list(buf)
+        out = {k: 0.0 for k in self.PROFILE_NAMES}
+        for l in range(self.info.n_layer):
+            for i, k in enumerate(self.PROFILE_NAMES):
+                out[k] += v[l * 10 + i]
+        out["lm_head"] = v[self.info.n_layer * 10]
+        out["bar_lm"] = v[self.info.n_layer * 10 + 1]
+        out["total"] = sum(v)
+        return out
 
     def stats(self):
         s = Stats()
@@ -246,6 +265,12 @@ def q4_block_isums(packed, rows, nb, cb, xq, isum, stream=None):
 def attn_decode(q, kc, vc, n_head, n_head_kv, hd, L, ctx, scale, scratch, out, stream=None):
     _check(lib().mi_attn_decode(_ptr(q), _ptr(kc), _ptr(vc), n_head, n_head_kv, hd, L, ctx, C.c_float(scale),
                                 _ptr(scratch), _ptr(out), _stream(stream)))
+
+
+def barrier_cost(nwg, n=1000):
+    us = C.c_double()
+    _check(lib().mi_barrier_cost(nwg, n, C.byref(us)))
+    return us.value
 
 
 def stream_read(buf, nbytes, sink, stream=None):

@@ -45,11 +45,16 @@ def golden(name):
         return json.load(f)
 
 
+MODES = [pytest.param(1, id="persistent"), pytest.param(0, id="per-phase")]
+
+
+@pytest.mark.parametrize("persistent", MODES)
 @pytest.mark.parametrize("shape,seed", [(TINY, 7), (SMALL, 21)])
-def test_step_logits_bit_exact(shape, seed):
+def test_step_logits_bit_exact(shape, seed, persistent):
     path = synth_cached("eng-%d" % shape["n_embd"], shape, seed)
-    say("step logits", path)
-    eng = minfer.Engine(path, max_ctx=256)
+    say("step logits", path, "persistent" if persistent else "per-phase")
+    eng = minfer.Engine(path, max_ctx=256, persistent=persistent)
+    assert eng.info.persistent == persistent
     orc = O.Model(path, O.MODE_Q8ACT, plan=plan_of(eng), max_seq=256)
     toks = minfer.prompt_ids(seed, 12, shape["n_vocab"])
     nxt = None
@@ -63,8 +68,8 @@ def test_step_logits_bit_exact(shape, seed):
     eng.close()
 
 
-def run_stream(path, prompt, n_gen, max_ctx=512):
-    eng = minfer.Engine(path, max_ctx=max_ctx)
+def run_stream(path, prompt, n_gen, max_ctx=512, persistent=1):
+    eng = minfer.Engine(path, max_ctx=max_ctx, persistent=persistent)
     first, _ = eng.prefill(prompt)
     toks, margins = eng.generate(n_gen)
     assert toks[0] == first
@@ -93,12 +98,13 @@ def test_tiny_stream_128():
     say("tiny vs fp32 cpu_infer: first divergence at %d of %d" % (d, len(fx["tokens"])))
 
 
+@pytest.mark.parametrize("persistent", MODES)
 @pytest.mark.parametrize("name", ["config0", "config2"])
-def test_config_stream_128(name):
+def test_config_stream_128(name, persistent):
     fx = golden(name)
     path = synth_cached(fx["config"], fx["shape"], fx["model_seed"])
-    say("%s stream 128 (prompt %d)" % (name, len(fx["prompt"])))
-    toks, margins, plan = run_stream(path, fx["prompt"], 128)
+    say("%s stream 128 (prompt %d, %s)" % (name, len(fx["prompt"]), "persistent" if persistent else "per-phase"))
+    toks, margins, plan = run_stream(path, fx["prompt"], 128, persistent=persistent)
     say("%s engine done; running the q8act oracle on the CPU" % name)
     orc = O.Model(path, O.MODE_Q8ACT, plan=plan, max_seq=len(fx["prompt"]) + 130)
     rt, rm, _, _ = orc.generate(fx["prompt"], 128)
@@ -107,6 +113,23 @@ def test_config_stream_128(name):
     d = first_divergence(toks, fx["tokens"])
     say("%s vs fp32 cpu_infer: first divergence at %d of 128 (margin there %.4f)"
         % (name, d, margins[d] if d < len(margins) else float("nan")))
+
+
+def test_long_context_chunk_merge_phase():
+    """past 16 chunks the merge runs as its own phase: positions 0..1100 (18 chunks)"""
+    path = synth_cached("eng-256", TINY, 7)
+    say("long context 1100 positions")
+    ids = minfer.prompt_ids(9, 1090, TINY["n_vocab"])
+    res = {}
+    for persistent in (1, 0):
+        eng = minfer.Engine(path, max_ctx=1200, persistent=persistent)
+        eng.prefill(ids)
+        toks, _ = eng.generate(12)
+        res[persistent] = toks
+        eng.close()
+    orc = O.Model(path, O.MODE_Q8ACT, plan=plan_of(minfer.Engine(path, max_ctx=1200)), max_seq=1200)
+    rt, _, _, _ = orc.generate(ids, 12)
+    assert res[1] == rt and res[0] == rt
 
 
 def test_rewind_and_restep():
