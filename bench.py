@@ -9,9 +9,15 @@ decode token (one pass over all weights). The timed region starts with the
 prompt's K/V and every weight resident in HBM.
 
 Prints ONE JSON line on stdout. Besides the contract keys it carries:
-  roofline      the dominant kernel (the gate/up GEMV phase: half of all bytes),
-                algorithmic bytes per launch / mean launch time from HIP events
-                on the engine stream, against MI355X's 8 TB/s HBM peak
+  roofline      the dominant kernel: the persistent step kernel k_step, one
+                launch per token. achieved = algorithmic bytes of one token at
+                the mean timed position / the mean launch time, from HIP events
+                recorded on the engine's stream around the timed steps; peak =
+                MI355X's 8 TB/s HBM. traffic = HBM bytes per launch measured with
+                the rocprofv3 FETCH_SIZE and WRITE_SIZE counters (each scaled by
+                what it reads for a plain copy of known size), read from the
+                committed summary profiles/k_step_config2.md.
+                With --persistent 0 the dominant kernel is the gate/up phase.
   step_roofline bytes/token x tok/s against the measured stream-read bandwidth
   stream_gbps   one-launch stream read of a 4 GiB buffer (> the 256 MB MALL)
   gemv          config 1 microbench: each S15 GEMV shape, rotated over copies
@@ -37,7 +43,9 @@ def log(*a):
 
 
 def bytes_per_token(info, pos):
-    """Algorithmic HBM bytes of one decode token at position pos."""
+    """Algorithmic HBM bytes of one decode token at position pos: every weight
+    once, the residual stream in/out and the QKV vector per layer, the final norm
+    input, the fp16 K/V rows of positions 0..pos read plus the new row written."""
     E, L, FF = info.n_embd, info.n_layer, info.n_ff
     kvd = info.n_head_kv * info.head_dim
     qkv = info.n_head * info.head_dim + 2 * kvd
@@ -81,6 +89,18 @@ def gemv_microbench(torch, reps=40):
     return out
 
 
+def traffic_bytes():
+    """HBM bytes per k_step launch from the committed rocprofv3 counter summary"""
+    try:
+        with open(os.path.join(ROOT, "profiles", "k_step_config2.md")) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":")[1])
+    except OSError:
+        pass
+    return None
+
+
 def stream_bw(torch, gib=4, reps=5):
     buf = torch.empty(gib << 30, dtype=torch.uint8, device="cuda")
     buf.zero_()
@@ -98,8 +118,9 @@ def stream_bw(torch, gib=4, reps=5):
     return gbps
 
 
-def cpu_baseline(path, prompt, n_prompt=6, n_gen=20):
-    """oracle fp32 (cpu_infer semantics) on the host cores, a bounded sample"""
+def cpu_baseline(path, prompt, n_prompt=64, n_gen=129):
+    """oracle fp32 (cpu_infer semantics) on the host cores: the whole config2
+    workload (64-token prompt, 128 decode steps), about 15 s on 16 threads"""
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     import oracle_lib as O
     threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
@@ -119,12 +140,23 @@ def main():
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-micro", action="store_true")
-    ap.add_argument("--persistent", type=int, default=0)
+    ap.add_argument("--persistent", type=int, default=1)
+    ap.add_argument("--copy-calib", type=int, default=0, metavar="MIB",
+                    help="only run a plain device copy of MIB MiB three times (calibrates the "
+                         "rocprofv3 FETCH_SIZE/WRITE_SIZE counters) and exit")
     args = ap.parse_args()
+    if args.copy_calib:
+        import torch
+        src = torch.ones(args.copy_calib << 20, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calib_bytes": src.numel(), "reps": 3}), flush=True)
+        return
     if args.gpus != 1:
-        print("bench.py: this engine runs batch-1 decode on one GPU; --gpus %d is not supported "
-              "(the multi-GPU design is described in DESIGN.md, nothing runs on a second GPU)" % args.gpus,
-              file=sys.stderr)
+        print("bench.py: batch-1 decode runs on one GPU; --gpus %d is not supported here "
+              "(no collective or second-GPU path is built)" % args.gpus, file=sys.stderr)
         sys.exit(2)
     import torch
     assert torch.cuda.is_available(), "bench.py needs a GPU"
@@ -161,12 +193,19 @@ def main():
     log("decode: %d steps in %.2f ms wall (%.2f ms device) = %.1f tok/s" % (args.steps, wall_ms, st["decode_ms"], tok_s))
     mean_pos = n_prompt + (args.steps - 1) / 2.0
     bpt = bytes_per_token(info, mean_pos)
-    # dominant kernel: the gate/up phase (weights + its prologue inputs + partial outputs)
-    E, FF = info.n_embd, info.n_ff
-    gu_ms = eng.time_phase("gate_up", layer=info.n_layer // 2, reps=50)
-    gu_bytes = 2 * FF * (E // 32) * 18 + E * 4 * (2 + info.plan_ks[1]) + info.plan_ks[2] * 2 * FF * 4
-    gu_gbps = gu_bytes / (gu_ms * 1e-3) / 1e9
-    log("gate/up phase kernel: %.2f us per launch, %.1f GB/s" % (gu_ms * 1e3, gu_gbps))
+    if info.persistent:
+        # dominant kernel: k_step, one launch per token; its mean duration comes
+        # from the engine's HIP events around the timed launches on its stream
+        k_us = st["decode_ms"] * 1e3 / args.steps
+        k_bytes = int(bpt)
+        kname = "k_step (persistent decode step, 1 launch/token, %d workgroups)" % info.n_cu
+    else:
+        E, FF = info.n_embd, info.n_ff
+        k_us = eng.time_phase("gate_up", layer=info.n_layer // 2, reps=50) * 1e3
+        k_bytes = 2 * FF * (E // 32) * 18 + E * 4 * (2 + info.plan_ks[1]) + info.plan_ks[2] * 2 * FF * 4
+        kname = "k_gu (gate/up GEMV phase, %d launches/token)" % info.n_layer
+    k_gbps = k_bytes / (k_us * 1e-6) / 1e9
+    log("%s: %.2f us per launch, %.1f GB/s" % (kname, k_us, k_gbps))
     eng.close()
     del eng
     stream = stream_bw(torch)
@@ -188,10 +227,11 @@ def main():
                    % args.steps, "shape": "S15 E1536 L28 H12/2 hd128 FF8960 V151936", "global_batch": 1,
                    "prompt": n_prompt, "step_mode": "persistent" if info.persistent else "one launch per phase",
                    "parallelism": "single GPU"},
-        "roofline": {"bound": "hbm", "kernel": "k_gu (gate/up GEMV phase, 28 launches/token)",
-                     "achieved": round(gu_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(gu_gbps / HBM_PEAK_GBPS, 4), "traffic": None,
-                     "bytes_per_launch": gu_bytes, "us_per_launch": round(gu_ms * 1e3, 3)},
+        "roofline": {"bound": "hbm", "kernel": kname,
+                     "achieved": round(k_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(k_gbps / HBM_PEAK_GBPS, 4),
+                     "traffic": traffic_bytes() if info.persistent else None,
+                     "bytes_per_launch": k_bytes, "us_per_launch": round(k_us, 3)},
         "step_roofline": {"bytes_per_token": int(bpt), "achieved_gbps": round(achieved_step, 1),
                           "stream_gbps": round(stream, 1), "frac_of_stream": round(achieved_step / stream, 4),
                           "roofline_tok_s": round(stream * 1e9 / bpt, 1)},

@@ -118,10 +118,13 @@ int mi_get_stats(const mi_engine* e, mi_stats* out);
 int mi_time_phase(mi_engine* e, int32_t phase, int32_t layer, int32_t reps, double* avg_ms);
 
 /* In-kernel phase profile of one persistent step (the reference's PROFILE=1,
- * mega.cu:111-119, 1206-1224): reruns the last step once with workgroup 0 stamping
- * the device wall clock (100 MHz) at every phase end and barrier exit. us[] receives
- * n_layer*10 + 2 durations in microseconds: per layer qkv, barrier, attention,
- * barrier, o, barrier, gate/up, barrier, down, barrier; then lm_head, barrier. */
+ * mega.cu:111-119, 1206-1224): reruns the last step once with every workgroup
+ * stamping the device wall clock (100 MHz). With S = n_layer*15 + 4 slots and W =
+ * the persistent grid (mi_model_info.n_cu workgroups), us[w*S + s] receives slot s
+ * of workgroup w in microseconds since the earliest start, n >= W*S. Slots: 0 start;
+ * then per layer, for qkv, attention, o, gate/up and down in turn: prologue end
+ * (inputs loaded, normalised and quantised), phase end, barrier exit; then the
+ * lm_head prologue end, lm_head end, last barrier exit. */
 int mi_profile_step(mi_engine* e, double* us, int32_t n);
 
 /* Cost of a grid barrier of the persistent kernel: one cooperative launch of nwg

@@ -73,7 +73,7 @@ struct DModel {
     float* logits;                 // [V] (written when non-null)
     float* cand;                   // [lm workgroups][32] (best, idx bits, second) per 128-byte line
     uint32_t* bar;                 // grid-barrier arrival counter (persistent kernel)
-    uint64_t* prof;                // when non-null: workgroup 0 stamps every phase end (s_memrealtime)
+    uint64_t* prof;                // when non-null: [workgroup][prof_slots] s_memrealtime stamps
     int32_t* err;                  // set when a grid barrier times out
     int32_t* out_tok;              // [maxseq] prediction made at each position
     float* out_margin;             // [maxseq]

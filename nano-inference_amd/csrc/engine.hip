@@ -611,21 +611,24 @@ int mi_time_phase(mi_engine* e, int32_t phase, int32_t layer, int32_t reps, doub
 
 int mi_profile_step(mi_engine* e, double* us, int32_t n) {
     if (!e || !us) return MI_ERR_ARG;
-    const int nslot = e->NL * kProfSlotsPerLayer + 3;
-    if (n < nslot - 1) return set_err(e, MI_ERR_ARG, "mi_profile_step needs %d entries", nslot - 1);
     if (!e->nwg_persistent) return set_err(e, MI_ERR_STATE, "profiling needs the persistent step kernel");
     if (e->cur_len < 1) return set_err(e, MI_ERR_STATE, "mi_profile_step needs a completed step");
+    const int nslot = prof_slots(e->NL), nwg = e->nwg_persistent;
+    const size_t total = (size_t)nslot * nwg;
+    if ((size_t)n < total) return set_err(e, MI_ERR_ARG, "mi_profile_step needs %zu entries", total);
     uint64_t* prof = nullptr;
-    HIPCHK(e, hipMalloc(&prof, sizeof(uint64_t) * nslot));
+    HIPCHK(e, hipMalloc(&prof, sizeof(uint64_t) * total));
     DModel M = e->M;
     M.prof = prof;
-    hipError_t st = launch_step_persistent(M, e->nwg_persistent, e->cur_len - 1, 1, e->stream);
-    std::vector<uint64_t> t(nslot);
+    hipError_t st = launch_step_persistent(M, nwg, e->cur_len - 1, 1, e->stream);
+    std::vector<uint64_t> t(total);
     if (st == hipSuccess) st = hipStreamSynchronize(e->stream);
-    if (st == hipSuccess) st = hipMemcpy(t.data(), prof, sizeof(uint64_t) * nslot, hipMemcpyDeviceToHost);
+    if (st == hipSuccess) st = hipMemcpy(t.data(), prof, sizeof(uint64_t) * total, hipMemcpyDeviceToHost);
     (void)hipFree(prof);
     if (st != hipSuccess) return set_err(e, MI_ERR_DEVICE, "profile step: %s", hipGetErrorString(st));
-    for (int i = 0; i + 1 < nslot; i++) us[i] = (double)(t[i + 1] - t[i]) * 0.01;   // 100 MHz ticks
+    uint64_t t0 = t[0];
+    for (int w = 1; w < nwg; w++) t0 = std::min(t0, t[(size_t)w * nslot]);
+    for (size_t i = 0; i < total; i++) us[i] = (double)(int64_t)(t[i] - t0) * 0.01;   // 100 MHz ticks
     return check_barrier(e);
 }
 

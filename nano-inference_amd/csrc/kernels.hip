@@ -186,6 +186,12 @@ __device__ void gemv_phase(const PMat& W, const int8_t* xq8, const float2* xds, 
     }
 }
 
+// device wall clock (100 MHz) of one profile slot, one row per workgroup
+__device__ __forceinline__ void stamp(const DModel& M, int slot) {
+    if (M.prof && slot >= 0 && threadIdx.x == 0)
+        M.prof[(size_t)blockIdx.x * prof_slots(M.NL) + slot] = __builtin_amdgcn_s_memrealtime();
+}
+
 // ------------------------------------------------------------------ cross-workgroup data
 // Inside one step, values that one workgroup writes and others read (GEMV partials,
 // attention records, the residual stream, the int8 act, argmax candidates) are
@@ -351,7 +357,7 @@ __device__ void residual_dma(const Stage& S, const float* h, const float* part, 
 }
 
 // P1: residual (or embedding row) -> RMSNorm -> int8 -> fused QKV rows (split-K partials)
-__device__ void phase_qkv(const DModel& M, int l, int pos, int wg, int nwg, uint8_t* smem) {
+__device__ void phase_qkv(const DModel& M, int l, int pos, int wg, int nwg, uint8_t* smem, int ps = -1) {
     const int tid = threadIdx.x;
     Stage S(smem);
     const DLayer& L = M.layers[l];
@@ -370,6 +376,7 @@ __device__ void phase_qkv(const DModel& M, int l, int pos, int wg, int nwg, uint
     __syncthreads();
     norm_quant(S.xs, L.an, M.E, M.eps, S.xq8, S.xds, tid);
     __syncthreads();
+    stamp(M, ps);
     gemv_tasks(L.qkv, S.xq8, S.xds, qkv_part(M, l), wg, nwg);
     retire(pre, M.err);
 }
@@ -551,7 +558,7 @@ __device__ void phase_comb(const DModel& M, int l, int pos, int wg, int nwg) {
 }
 
 // P3: attention output (chunk records merged here up to kInlineComb chunks) -> int8 -> O rows
-__device__ void phase_o(const DModel& M, int l, int pos, int wg, int nwg, uint8_t* smem) {
+__device__ void phase_o(const DModel& M, int l, int pos, int wg, int nwg, uint8_t* smem, int ps = -1) {
     const int tid = threadIdx.x;
     Stage S(smem);
     const Touch pre = prefetch_first(M.layers[l].o, wg);
@@ -571,6 +578,7 @@ __device__ void phase_o(const DModel& M, int l, int pos, int wg, int nwg, uint8_
     __syncthreads();
     norm_quant(S.xs, nullptr, M.E, 0.f, S.xq8, S.xds, tid);
     __syncthreads();
+    stamp(M, ps);
     gemv_tasks(M.layers[l].o, S.xq8, S.xds, o_part(M, l), wg, nwg);
     retire(pre, M.err);
 }
@@ -594,7 +602,7 @@ __device__ __forceinline__ void quant32_vals(float v, int& q, float& d, int& s8)
 // (cpu_infer.cpp:144-147) -> int8 act block records. A workgroup owns whole 64-row
 // groups (32 gate rows + their 32 up rows = one 32-element act block): its waves
 // compute the ks K segments, which are added in order from LDS.
-__device__ void phase_gu(const DModel& M, int l, int wg, int nwg, uint8_t* smem) {
+__device__ void phase_gu(const DModel& M, int l, int wg, int nwg, uint8_t* smem, int ps = -1) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = nwaves();
     Stage S(smem);
     const DLayer& L = M.layers[l];
@@ -610,6 +618,7 @@ __device__ void phase_gu(const DModel& M, int l, int wg, int nwg, uint8_t* smem)
     __syncthreads();
     norm_quant(S.xs, L.fn, M.E, M.eps, S.xq8, S.xds, tid);
     __syncthreads();
+    stamp(M, ps);
     uint8_t* act = act_rec(M, l);
     for (int base = wg * slots; base < ng; base += nwg * slots) {
         const int g = base + slot;
@@ -640,7 +649,7 @@ __device__ void phase_gu(const DModel& M, int l, int wg, int nwg, uint8_t* smem)
 }
 
 // P5: int8 act records -> LDS -> down rows
-__device__ void phase_down(const DModel& M, int l, int wg, int nwg, uint8_t* smem) {
+__device__ void phase_down(const DModel& M, int l, int wg, int nwg, uint8_t* smem, int ps = -1) {
     const int tid = threadIdx.x;
     Stage S(smem);
     const Touch pre = prefetch_first(M.layers[l].d, wg);
@@ -656,12 +665,13 @@ __device__ void phase_down(const DModel& M, int l, int wg, int nwg, uint8_t* sme
         S.xds[i] = make_float2(__uint_as_float(r[8]), __uint_as_float(r[9]));
     }
     __syncthreads();
+    stamp(M, ps);
     gemv_tasks(M.layers[l].d, S.xq8, S.xds, d_part(M, l), wg, nwg);
     retire(pre, M.err);
 }
 
 // lm_head: final residual -> RMSNorm -> int8 -> vocab rows, per-workgroup top-2
-__device__ void phase_lm(const DModel& M, int wg, int nwg, uint8_t* smem) {
+__device__ void phase_lm(const DModel& M, int wg, int nwg, uint8_t* smem, int ps = -1) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = nwaves();
     Stage S(smem);
     const int ng = M.lm.rows / 64;
@@ -671,6 +681,7 @@ __device__ void phase_lm(const DModel& M, int wg, int nwg, uint8_t* smem) {
     __syncthreads();
     norm_quant(S.xs, M.out_norm, M.E, M.eps, S.xq8, S.xds, tid);
     __syncthreads();
+    stamp(M, ps);
     Top2 t{-__builtin_inff(), INT_MAX, -__builtin_inff()};
     for (int g = wg * nw + wave; g < ng; g += nwg * nw) {
         const float v = row_segment(M.lm, g, 0, S.xq8, S.xds, lane);
@@ -756,12 +767,9 @@ __global__ __launch_bounds__(kThreads) void k_argmax(DModel M, int ncand, int po
 // CU): the phases above separated by grid barriers, 5 per layer + 1 before the
 // argmax (the reference's mega kernel has the same count, mega.cu:695-833). Every
 // workgroup merges the lm_head candidates itself, so the token needs no barrier.
-// Profile slots per layer: end of qkv, its barrier, attention, barrier, o, barrier,
-// gate/up, barrier, down, barrier; then lm, barrier.
-constexpr int kProfPerLayer = 10;
-__device__ __forceinline__ void stamp(const DModel& M, int slot) {
-    if (M.prof && blockIdx.x == 0 && threadIdx.x == 0) M.prof[slot] = __builtin_amdgcn_s_memrealtime();
-}
+// Profile slots (every workgroup stamps its own row): 0 = start; per layer and
+// phase (qkv, attention, o, gate/up, down) the end of the prologue, the end of the
+// phase and the barrier exit; then lm prologue, lm end, last barrier exit.
 
 template <int HD>
 constexpr int step_lds() { return kAttnWaves * attn_wave_lds<HD>() > kStageBytes ? kAttnWaves * attn_wave_lds<HD>() : kStageBytes; }
@@ -774,36 +782,38 @@ __global__ __launch_bounds__(kPThreads) void k_step(DModel M, int pos, int gen) 
     unsigned epoch = 0;
     stamp(M, 0);
     for (int l = 0; l < M.NL; l++) {
-        const int p0 = 1 + l * kProfPerLayer;
-        phase_qkv(M, l, pos, wg, nwg, smem);
-        stamp(M, p0 + 0);
-        grid_barrier(M.bar, M.err, epoch);
+        const int p0 = 1 + l * kProfSlotsPerLayer;
+        phase_qkv(M, l, pos, wg, nwg, smem, p0);
         stamp(M, p0 + 1);
-        phase_attn<HD>(M, l, pos, wg, nwg, smem);
+        grid_barrier(M.bar, M.err, epoch);
         stamp(M, p0 + 2);
+        stamp(M, p0 + 3);
+        phase_attn<HD>(M, l, pos, wg, nwg, smem);
+        stamp(M, p0 + 4);
         grid_barrier(M.bar, M.err, epoch);
         if (nch > kInlineComb) {
             phase_comb(M, l, pos, wg, nwg);
             grid_barrier(M.bar, M.err, epoch);
         }
-        stamp(M, p0 + 3);
-        phase_o(M, l, pos, wg, nwg, smem);
-        stamp(M, p0 + 4);
-        grid_barrier(M.bar, M.err, epoch);
         stamp(M, p0 + 5);
-        phase_gu(M, l, wg, nwg, smem);
-        stamp(M, p0 + 6);
-        grid_barrier(M.bar, M.err, epoch);
+        phase_o(M, l, pos, wg, nwg, smem, p0 + 6);
         stamp(M, p0 + 7);
-        phase_down(M, l, wg, nwg, smem);
-        stamp(M, p0 + 8);
         grid_barrier(M.bar, M.err, epoch);
-        stamp(M, p0 + 9);
+        stamp(M, p0 + 8);
+        phase_gu(M, l, wg, nwg, smem, p0 + 9);
+        stamp(M, p0 + 10);
+        grid_barrier(M.bar, M.err, epoch);
+        stamp(M, p0 + 11);
+        phase_down(M, l, wg, nwg, smem, p0 + 12);
+        stamp(M, p0 + 13);
+        grid_barrier(M.bar, M.err, epoch);
+        stamp(M, p0 + 14);
     }
-    phase_lm(M, wg, nwg, smem);
-    stamp(M, 1 + M.NL * kProfPerLayer);
+    const int pl = 1 + M.NL * kProfSlotsPerLayer;
+    phase_lm(M, wg, nwg, smem, pl);
+    stamp(M, pl + 1);
     grid_barrier(M.bar, M.err, epoch);
-    stamp(M, 2 + M.NL * kProfPerLayer);
+    stamp(M, pl + 2);
     const Top2 a = merge_cands(M.cand, nwg, Stage(smem).red);
     if (wg == 0 && threadIdx.x == 0) emit_token(M, a, pos, gen);
 }

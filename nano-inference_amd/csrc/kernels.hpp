@@ -19,7 +19,9 @@ hipError_t launch_barriers(uint32_t* bar, int32_t* err, int nwg, int n, hipStrea
 int barrier_words();        // uint32 words the grid barrier uses
 int kernels_max_ks();       // largest K-segment count the phases stage in LDS
 int attn_record_floats(int HD);   // floats per attention chunk record
-constexpr int kProfSlotsPerLayer = 10;
+constexpr int kProfSlotsPerLayer = 15;
+// profile slots of one workgroup: start, 15 per layer, lm prologue, lm end, last barrier
+constexpr int prof_slots(int n_layer) { return n_layer * kProfSlotsPerLayer + 4; }
 
 // one phase kernel of the step at pos: 0 qkv, 1 attention, 2 chunk merge (only
 // launched past kInlineComb chunks), 3 o, 4 gate/up+act, 5 down, 6 lm_head, 7 argmax

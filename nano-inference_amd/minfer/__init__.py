@@ -198,21 +198,39 @@ class Engine:
         _check(lib().mi_time_phase(self._h, ph, layer, reps, C.byref(ms)), self._h)
         return ms.value
 
-    PROFILE_NAMES = ["qkv", "bar_qkv", "attn", "bar_attn", "o", "bar_o", "gate_up", "bar_gu", "down", "bar_down"]
+    PROFILE_PHASES = ["qkv", "attn", "o", "gate_up", "down"]
 
     def profile_step(self):
-        """per-phase microseconds of one persistent step (workgroup 0's view)"""
-        n = self.info.n_layer * 10 + 2
+        """Stamps of one persistent step: an array [workgroups][n_layer*15 + 4] of
+        microseconds since the earliest start (slot layout in mi_profile_step)."""
+        import numpy as np
+        nslot = self.info.n_layer * 15 + 4
+        n = nslot * self.info.n_cu
         buf = (C.c_double * n)()
         _check(lib().mi_profile_step(self._h, buf, n), self._h)
-        v = list(buf)
-        out = {k: 0.0 for k in self.PROFILE_NAMES}
-        for l in range(self.info.n_layer):
-            for i, k in enumerate(self.PROFILE_NAMES):
-                out[k] += v[l * 10 + i]
-        out["lm_head"] = v[self.info.n_layer * 10]
-        out["bar_lm"] = v[self.info.n_layer * 10 + 1]
-        out["total"] = sum(v)
+        return np.frombuffer(buf, dtype=np.float64).reshape(self.info.n_cu, nslot).copy()
+
+    def profile_summary(self):
+        """Per phase, summed over layers (microseconds): the prologue, work and
+        barrier-wait time averaged over workgroups and of the slowest workgroup,
+        plus the barrier latency proper (earliest exit minus latest arrival)."""
+        import numpy as np
+        t = self.profile_step()
+        L = self.info.n_layer
+        d = np.diff(t, axis=1)                        # d[:, s-1] = slot s - slot s-1
+        out = {}
+        for k, ph in enumerate(self.PROFILE_PHASES):
+            for j, part in enumerate(("prep", "work", "wait")):
+                cols = [l * 15 + 3 * k + j for l in range(L)]
+                v = d[:, cols].sum(axis=1)
+                out[ph + "_" + part] = (round(float(v.mean()), 1), round(float(v.max()), 1))
+            ends = [1 + l * 15 + 3 * k + 1 for l in range(L)]
+            out[ph + "_barrier"] = round(float(sum(t[:, e + 1].min() - t[:, e].max() for e in ends)), 1)
+        s0 = 1 + L * 15
+        for j, part in enumerate(("lm_prep", "lm_work", "lm_wait")):
+            v = d[:, s0 - 1 + j]
+            out[part] = (round(float(v.mean()), 1), round(float(v.max()), 1))
+        out["total"] = round(float(t[:, -1].max()), 1)
         return out
 
     def stats(self):
