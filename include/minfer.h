@@ -119,12 +119,14 @@ int mi_time_phase(mi_engine* e, int32_t phase, int32_t layer, int32_t reps, doub
 
 /* In-kernel phase profile of one persistent step (the reference's PROFILE=1,
  * mega.cu:111-119, 1206-1224): reruns the last step once with every workgroup
- * stamping the device wall clock (100 MHz). With S = n_layer*15 + 4 slots and W =
+ * stamping the device wall clock (100 MHz). With S = n_layer*25 + 6 slots and W =
  * the persistent grid (mi_model_info.n_cu workgroups), us[w*S + s] receives slot s
  * of workgroup w in microseconds since the earliest start, n >= W*S. Slots: 0 start;
- * then per layer, for qkv, attention, o, gate/up and down in turn: prologue end
- * (inputs loaded, normalised and quantised), phase end, barrier exit; then the
- * lm_head prologue end, lm_head end, last barrier exit. */
+ * then five per phase, for qkv, attention, o, gate/up and down of every layer and
+ * finally lm_head: prologue end (inputs loaded, normalised and quantised), the
+ * first worker wave's tiles done, its stores drained (lm_head: the workgroup's
+ * argmax candidate written), phase end, barrier exit. Slots never stamped read as
+ * 0 - earliest start. */
 int mi_profile_step(mi_engine* e, double* us, int32_t n);
 
 /* Cost of a grid barrier of the persistent kernel: one cooperative launch of nwg

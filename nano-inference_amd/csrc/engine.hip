@@ -41,8 +41,8 @@ struct mi_engine {
     std::vector<void*> allocs;
     DModel M{};
     DModel M_logits{};            // same as M with the logits buffer attached
+    DModel* dM = nullptr;         // device copies the kernels read: [0] M, [1] M_logits, [2] profiling
     DLayer* d_layers = nullptr;
-    PhaseGrid pg{};
     hipStream_t stream = nullptr;
     hipEvent_t ev0 = nullptr, ev1 = nullptr;
     int nwg_persistent = 0;       // workgroups of the persistent step kernel (0: per-phase launches)
@@ -144,12 +144,6 @@ const uint8_t* q4_rows(const GTensor& t, std::vector<uint8_t>& buf) {
     std::vector<float> row(n);
     for (int r = 0; r < rows; r++) { dequant_row(t, r, row.data()); requant_row_q4_0(row.data(), n, buf.data() + (size_t)r * (n / 32) * 18); }
     return buf.data();
-}
-
-int choose_ks(int groups, int nc, int cap) {
-    constexpr int kTargetTasks = 1024;   // fixed, so the plan (and the float order) is device-independent
-    const int ks = (kTargetTasks + groups - 1) / groups;
-    return std::max(1, std::min(std::min(ks, nc), cap));
 }
 
 }  // namespace
@@ -269,17 +263,18 @@ static int load_impl(mi_engine* e, const char* path) {
     e->maxseq = e->opts.max_ctx > 0 ? e->opts.max_ctx : 4096;
     e->maxch = (e->maxseq + kAttnChunk - 1) / kAttnChunk;
 
-    // reduction plan: chunk size by row length, K segments by row-group count
+    // reduction plan (the float summation order; depends on the shape only)
     const int nbE = e->E / 32, nbF = e->FF / 32;
-    const int cbE = nbE % 8 == 0 ? 8 : 4, cbF = nbF % 8 == 0 ? 8 : 4;
-    e->cb[0] = e->cb[1] = e->cb[2] = e->cb[4] = cbE;
-    e->cb[3] = cbF;
-    const int kmax = kernels_max_ks();
-    e->ks[0] = choose_ks(e->QKV / 64, nbE / cbE, kmax);
-    e->ks[1] = choose_ks(e->E / 64, nbE / cbE, kmax);
-    e->ks[2] = choose_ks(e->FF / 32, nbE / cbE, 4);
-    e->ks[3] = choose_ks(e->E / 64, nbF / cbF, kmax);
-    e->ks[4] = 1;
+    if (!kernels_plan(e->E, e->FF, e->cb, e->ks))
+        return set_err(e, MI_ERR_SHAPE, "E=%d FF=%d do not fit the kernels' staging", e->E, e->FF);
+    {
+        const int rows[5] = {e->QKV, e->E, 2 * e->FF, e->E, e->V}, nbs[5] = {nbE, nbE, nbE, nbF, nbE};
+        for (int i = 0; i < 5; i++)
+            if (kernels_tiles_per_wg(rows[i], nbs[i], e->cb[i], e->ks[i], e->n_cu) > kernels_max_tiles_per_wg())
+                return set_err(e, MI_ERR_SHAPE, "matrix %d needs %d tiles per workgroup on %d CUs (limit %d)", i,
+                               kernels_tiles_per_wg(rows[i], nbs[i], e->cb[i], e->ks[i], e->n_cu), e->n_cu,
+                               kernels_max_tiles_per_wg());
+    }
 
     auto need = [&](const std::string& n) -> const GTensor* { return g.tensor(n); };
     const GTensor* te = need("token_embd.weight");
@@ -386,7 +381,6 @@ static int load_impl(mi_engine* e, const char* path) {
     HIPCHK(e, hipMemcpy(e->d_layers, layers.data(), layers.size() * sizeof(DLayer), hipMemcpyHostToDevice));
     M.layers = e->d_layers;
     const size_t kvn = (size_t)e->NL * e->NKV * e->maxseq * e->HD;
-    e->pg = plan_phase_grid(M, layers[0], e->n_cu);
     if (e->opts.persistent) {
         int coop = 0;
         HIPCHK(e, hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, e->opts.device));
@@ -407,7 +401,7 @@ static int load_impl(mi_engine* e, const char* path) {
         (rc = alloc_buf(e, &M.o_part, NL * e->ks[1] * e->E)) ||
         (rc = alloc_buf(e, &M.act, NL * (e->FF / 32) * kActRec)) ||
         (rc = alloc_buf(e, &M.d_part, NL * e->ks[3] * e->E)) ||
-        (rc = alloc_buf(e, &M.cand, (size_t)std::max(e->pg.lm, e->nwg_persistent) * 32)) ||
+        (rc = alloc_buf(e, &M.cand, (size_t)e->n_cu * 32)) ||
         (rc = alloc_buf(e, &M.bar, (size_t)barrier_words())) || (rc = alloc_buf(e, &M.err, 64)) ||
         (rc = alloc_buf(e, &M.out_tok, (size_t)e->maxseq)) ||
         (rc = alloc_buf(e, &M.out_margin, (size_t)e->maxseq)))
@@ -416,6 +410,9 @@ static int load_impl(mi_engine* e, const char* path) {
     M.prof = nullptr;
     e->M_logits = M;
     if ((rc = alloc_buf(e, &e->M_logits.logits, (size_t)e->V))) return rc;
+    if ((rc = alloc_buf(e, &e->dM, 3))) return rc;
+    HIPCHK(e, hipMemcpy(e->dM, &e->M, sizeof(DModel), hipMemcpyHostToDevice));
+    HIPCHK(e, hipMemcpy(e->dM + 1, &e->M_logits, sizeof(DModel), hipMemcpyHostToDevice));
     HIPCHK(e, hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking));
     HIPCHK(e, hipEventCreate(&e->ev0));
     HIPCHK(e, hipEventCreate(&e->ev1));
@@ -459,8 +456,9 @@ int mi_info(const mi_engine* e, mi_model_info* o) {
 
 static int run_step(mi_engine* e, int pos, int gen, bool want_logits) {
     const DModel& M = want_logits ? e->M_logits : e->M;
-    if (e->nwg_persistent) HIPCHK(e, launch_step_persistent(M, e->nwg_persistent, pos, gen, e->stream));
-    else launch_step_phases(M, e->pg, pos, gen, e->stream);
+    const DModel* dM = e->dM + (want_logits ? 1 : 0);
+    if (e->nwg_persistent) HIPCHK(e, launch_step_persistent(M, dM, e->nwg_persistent, pos, gen, e->stream));
+    else launch_step_phases(M, dM, e->n_cu, pos, gen, e->stream);
     HIPCHK(e, hipGetLastError());
     return MI_OK;
 }
@@ -596,8 +594,8 @@ int mi_time_phase(mi_engine* e, int32_t phase, int32_t layer, int32_t reps, doub
     const int pos = e->cur_len - 1;
     HIPCHK(e, hipEventRecord(e->ev0, e->stream));
     for (int r = 0; r < reps; r++) {
-        if (phase == 8) HIPCHK(e, launch_step_persistent(e->M, e->nwg_persistent, pos, 1, e->stream));
-        else launch_phase(e->M, e->pg, phase, layer, pos, 1, e->stream);
+        if (phase == 8) HIPCHK(e, launch_step_persistent(e->M, e->dM, e->nwg_persistent, pos, 1, e->stream));
+        else launch_phase(e->M, e->dM, e->n_cu, phase, layer, pos, 1, e->stream);
     }
     HIPCHK(e, hipGetLastError());
     HIPCHK(e, hipEventRecord(e->ev1, e->stream));
@@ -620,7 +618,8 @@ int mi_profile_step(mi_engine* e, double* us, int32_t n) {
     HIPCHK(e, hipMalloc(&prof, sizeof(uint64_t) * total));
     DModel M = e->M;
     M.prof = prof;
-    hipError_t st = launch_step_persistent(M, nwg, e->cur_len - 1, 1, e->stream);
+    hipError_t st = hipMemcpy(e->dM + 2, &M, sizeof(DModel), hipMemcpyHostToDevice);
+    if (st == hipSuccess) st = launch_step_persistent(M, e->dM + 2, nwg, e->cur_len - 1, 1, e->stream);
     std::vector<uint64_t> t(total);
     if (st == hipSuccess) st = hipStreamSynchronize(e->stream);
     if (st == hipSuccess) st = hipMemcpy(t.data(), prof, sizeof(uint64_t) * total, hipMemcpyDeviceToHost);

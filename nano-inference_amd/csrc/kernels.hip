@@ -7,11 +7,12 @@
 // The orders (the reduction plan) are:
 //   q4_0 x int8 row   per block isum = sum(nibble * x) via v_dot4_i32_i8, minus
 //                     8*sum(x); acc = fma(dw*dx, float(isum - 8 sum x), acc) over the
-//                     blocks of a K segment in order (mega.cu:153-155); the ks
-//                     segments of a row are added left to right (mega.cu:665-673)
-//   RMSNorm           64 lane partials (lane j: elements j, j+64, ...) by fma, then
-//                     xor butterfly 32..1; x * (1/sqrt(mean+eps)) * w
-//                     (cpu_infer.cpp:40-46, mega.cu:336-347)
+//                     cb blocks of a chunk, from 0 (mega.cu:153-155); the chunk sums
+//                     of a K segment are added left to right, then the ks segments
+//                     of the row left to right (mega.cu:665-673)
+//   RMSNorm           64 lane partials (lane l: elements 256j + 4l + i, i < 4, in
+//                     order) by fma, then xor butterfly 32..1; x * (1/sqrt(mean+eps))
+//                     * w (cpu_infer.cpp:40-46, mega.cu:336-347)
 //   int8 quant        per 32 elements: amax, 127/amax, round half even, fp16(amax/127),
 //                     8*sum(q) (cuda_infer.cu:80-89, mega.cu:303-325)
 //   attention         64-position chunks: lane = position for q.k (4 fma chains over
@@ -20,13 +21,42 @@
 //                     chunk order (cuda_infer.cu:650-702)
 //   exp               mi_expf: Cody-Waite by ln2 + Taylor-7 Horner (no libm)
 // Compile with -ffp-contract=off (nothing else gets fused) and without packed fp32.
+//
+// Work split of a step workgroup (512 threads = 8 waves, one workgroup per CU):
+//   wave 0, "control"      the grid barrier, then the phase prologue: it gathers the
+//                          phase input (split-K partials, attention records, act
+//                          records) into LDS by DMA, adds the residual, normalises
+//                          and quantises it into int8 block records in LDS
+//   waves 1..7, "workers"  the phase's q4_0 weight tiles. A worker loads its tiles
+//                          of the NEXT phase into registers as soon as its part of
+//                          the current phase is stored, so the weight stream runs
+//                          during the grid barrier and the control wave's prologue.
+// A wave's vector memory reads complete in issue order, so a prefetch issued by a
+// wave delays every later load of that same wave; keeping the barrier polls and the
+// prologue loads in a wave that never prefetches is what lets them overlap.
 #include "common.hpp"
 #include "kernels.hpp"
 
+#include <algorithm>
 #include <climits>
 #include <type_traits>
 
 namespace mi {
+
+// The model description is read through constant-address-space pointers: a read of
+// a generic pointer compiles to a vector load (the compiler cannot prove that the
+// kernel's own stores leave it unchanged), which would queue behind a wave's weight
+// prefetch; constant-space reads are scalar loads on their own counter, and the
+// compiler reloads them instead of keeping every field live in registers.
+#define AS4 __attribute__((address_space(4)))
+typedef const AS4 DModel* MPtr;
+typedef const AS4 DLayer* LPtr;
+__device__ __forceinline__ LPtr LY(MPtr M, int l) { return (LPtr)M->layers + l; }
+__device__ __forceinline__ PMat ldmat(const AS4 PMat* m) {
+    PMat r;
+    r.base = m->base; r.rows = m->rows; r.nb = m->nb; r.cb = m->cb; r.nc = m->nc; r.ks = m->ks;
+    return r;
+}
 
 // ------------------------------------------------------------------ scalar helpers
 __device__ __forceinline__ float mi_expf(float x) {
@@ -57,64 +87,65 @@ __device__ __forceinline__ float wave_max(float v) {
     for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
     return v;
 }
-// LDS hand-off between lanes of one wave: waves process attention items
-// independently (non-uniform trip counts), so a workgroup barrier cannot be used;
-// DS operations of one wave complete in order once lgkmcnt drains
-__device__ __forceinline__ void wave_lds_sync() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+// LDS hand-off between lanes of one wave (waves run independently, so a workgroup
+// barrier cannot be used): DS operations of one wave complete in order
+// (the s_waitcnt builtin, unlike inline asm, is seen by the compiler's own wait
+// insertion, which then knows nothing is outstanding afterwards; gfx9 encoding:
+// vmcnt in bits 3:0 + 15:14, expcnt 6:4, lgkmcnt 11:8)
+__device__ __forceinline__ void wave_lds_sync() { __builtin_amdgcn_s_waitcnt(0xC07F); }   // lgkmcnt(0)
 __device__ __forceinline__ float h2f_lo(uint32_t u) { return __half2float(__ushort_as_half((unsigned short)(u & 0xFFFFu))); }
 __device__ __forceinline__ float h2f_hi(uint32_t u) { return __half2float(__ushort_as_half((unsigned short)(u >> 16))); }
+__device__ __forceinline__ float fp16_round(float v) { return __half2float(__float2half(v)); }
 
-// 1/sqrt(mean(x^2) + eps) for x[0..n) in LDS, the same value on every lane of every wave
-__device__ __forceinline__ float rms_inv(const float* xs, int n, float eps, int lane) {
-    float a = 0.f;
-    for (int k = lane; k < n; k += 64) a = __fmaf_rn(xs[k], xs[k], a);
-    a = bfly_sum64(a);
-    const float mean = __fdiv_rn(a, (float)n);
-    return __fdiv_rn(1.0f, __builtin_sqrtf(__fadd_rn(mean, eps)));   // correctly rounded (HIP's __fsqrt_rn is the native approximation)
-}
-
-// quantize one 32-element block per half-wave; every lane runs the shuffles
-__device__ __forceinline__ void quant32(float v, bool own, int8_t* xq8, int e, float2* xds, int lane) {
+// quantize one 32-element block per half-wave: the lane's code, the block scale and
+// 8*sum(q) on every lane (cuda_infer.cu:80-89, mega.cu:303-325)
+__device__ __forceinline__ void quant32_vals(float v, int& q, float& d, int& s8) {
     float a = fabsf(v);
 #pragma unroll
     for (int off = 16; off >= 1; off >>= 1) a = fmaxf(a, __shfl_xor(a, off));
     const float inv = a > 0.f ? __fdiv_rn(127.f, a) : 0.f;
-    const int q = __float2int_rn(__fmul_rn(v, inv));
+    q = __float2int_rn(__fmul_rn(v, inv));
     int s = q;
 #pragma unroll
     for (int off = 16; off >= 1; off >>= 1) s += __shfl_xor(s, off);
-    if (own) {
-        xq8[e] = (int8_t)q;
-        if ((lane & 31) == 0)
-            xds[e >> 5] = make_float2(__half2float(__float2half(__fdiv_rn(a, 127.f))), __int_as_float(8 * s));
-    }
+    d = fp16_round(__fdiv_rn(a, 127.f));
+    s8 = 8 * s;
 }
 
-// xs[0..n) (LDS) -> optional RMSNorm with w -> int8 blocks in LDS. n % 32 == 0.
-__device__ void norm_quant(const float* xs, const float* w, int n, float eps, int8_t* xq8, float2* xds, int tid) {
-    const int lane = tid & 63, nt = blockDim.x;
-    const float sc = w ? rms_inv(xs, n, eps, lane) : 1.f;
-    for (int base = 0; base < n; base += nt) {
-        const int e = base + tid;
-        const bool own = e < n;
-        const int ec = own ? e : n - 1;
-        const float y = w ? __fmul_rn(__fmul_rn(xs[ec], sc), w[ec]) : xs[ec];
-        quant32(y, own, xq8, e, xds, lane);
-    }
+// ------------------------------------------------------------------ memory helpers
+// Inside one step, values that one workgroup writes and others read (GEMV partials,
+// attention records, the int8 act, argmax candidates) are written once per launch
+// into per-layer buffers whose 128-byte lines each have a single writer, with
+// agent-coherent stores (global_store sc1: written through past the per-XCD L2).
+// After the grid barrier every reader sees them with ordinary loads: no reader can
+// hold an older copy of a line that is written once per launch, and the 32
+// workgroups of an XCD share one L2 fill. That keeps the barrier free of agent-scope
+// fences (an L2 write-back/invalidate per workgroup costs ~1.7 us at 256 workgroups).
+__device__ __forceinline__ uint32_t ldc(const uint32_t* p) {
+    return __hip_atomic_load(const_cast<uint32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void stc(float* p, float v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+__device__ __forceinline__ void stc(uint32_t* p, uint32_t v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+__device__ __forceinline__ void drain_vm() { __builtin_amdgcn_s_waitcnt(0x0F70); }      // vmcnt(0)
+
+typedef __attribute__((address_space(3))) void* lds_ptr;
+// one wave copies `bytes` (multiple of 16, both ends 16-byte aligned) from global
+// memory straight into LDS, 1 KB per instruction (lane l moves bytes 16l..16l+15)
+__device__ __forceinline__ void dma_wave(const void* g, void* lds, int bytes, int lane) {
+    for (int off = 0; off < bytes; off += 1024)
+        if (off + lane * 16 < bytes)
+            __builtin_amdgcn_global_load_lds(static_cast<const uint8_t*>(g) + off + lane * 16,
+                                             (lds_ptr)(static_cast<uint8_t*>(lds) + off), 16, 0, 0);
 }
 
-// xs[i] = h[i] + (part[0][i] + part[1][i] + ...), the residual add of a split-K GEMV
-__device__ void residual_into(float* xs, const float* h, const float* part, int ks, int n, float* hout, int tid) {
-    for (int i = tid; i < n; i += blockDim.x) {
-        float v = part[i];
-        for (int s = 1; s < ks; s++) v = __fadd_rn(v, part[(size_t)s * n + i]);
-        v = __fadd_rn(h[i], v);
-        xs[i] = v;
-        if (hout) hout[i] = v;
-    }
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+// weights are read once per token (868 MB > the 256 MB MALL): streaming loads
+__device__ __forceinline__ uint4 ntload16(const uint8_t* p) {
+    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
 }
 
-// ------------------------------------------------------------------ q4_0 x int8 GEMV
+// ------------------------------------------------------------------ q4_0 x int8
 // q4_0 block (16 bytes: byte j = element j low nibble, element j+16 high nibble)
 // against 32 int8: the nibbles stay 0..15 (the -8 is folded into 8*sum(x))
 __device__ __forceinline__ int dot_q4(uint4 w, int4 x0, int4 x1) {
@@ -130,123 +161,166 @@ __device__ __forceinline__ int dot_q4(uint4 w, int4 x0, int4 x1) {
     return s;
 }
 
-template <int CB>
-__device__ __forceinline__ void load_tile(const uint8_t* t, int lane, uint4 (&w)[CB], uint32_t (&s)[CB / 2]) {
+// One lane's row of one tile (64-row group x cb blocks): cb x 16 quant bytes and cb
+// fp16 scales. Int8 activations are "block records" in LDS: block b at x + b*rs holds
+// 32 int8 codes, then the fp32 scale and 8*sum(q) as int32.
+struct Tile { uint4 q[8]; uint4 s; };
+constexpr int kXRec = 48;          // record stride of a quantised E vector (act records use kActRec)
+
+__device__ __forceinline__ void tile_load(Tile& t, const uint8_t* p, int cb, int lane) {
+    if (cb == 8) {
 #pragma unroll
-    for (int k = 0; k < CB; k++) w[k] = *reinterpret_cast<const uint4*>(t + k * 1024 + lane * 16);
-    if constexpr (CB == 8) {
-        const uint4 v = *reinterpret_cast<const uint4*>(t + 8192 + lane * 16);
-        s[0] = v.x; s[1] = v.y; s[2] = v.z; s[3] = v.w;
+        for (int k = 0; k < 8; k++) t.q[k] = ntload16(p + k * 1024 + lane * 16);
+        t.s = ntload16(p + 8192 + lane * 16);
     } else {
-        const uint2 v = *reinterpret_cast<const uint2*>(t + 4096 + lane * 8);
-        s[0] = v.x; s[1] = v.y;
+#pragma unroll
+        for (int k = 0; k < 4; k++) t.q[k] = ntload16(p + k * 1024 + lane * 16);
+        const uint2 v = *reinterpret_cast<const uint2*>(p + 4096 + lane * 8);
+        t.s = make_uint4(v.x, v.y, 0u, 0u);
     }
 }
+__device__ __forceinline__ uint32_t u4_at(const uint4& v, int i) { return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w; }
 
-// one lane's row over nch consecutive chunks starting at block b0. One chunk's
-// loads (cb x 1 KB of quants + the scales) are in flight per wave; a double-buffered
-// variant needed 280 VGPRs and spilled.
+// sum of one chunk: an fma chain over its CB blocks, from 0
 template <int CB>
-__device__ __forceinline__ float seg_dot(const uint8_t* tile, int nch, int b0, const int8_t* xq8, const float2* xds, int lane) {
-    constexpr size_t TB = (size_t)CB * 1152;
+__device__ __forceinline__ float chunk_dot(const Tile& t, const uint8_t* x, int rs, int b0) {
     float acc = 0.f;
-    for (int c = 0; c < nch; c++) {
-        uint4 w[CB];
-        uint32_t s[CB / 2];
-        load_tile<CB>(tile + (size_t)c * TB, lane, w, s);
 #pragma unroll
-        for (int k = 0; k < CB; k++) {
-            const int b = b0 + c * CB + k;
-            const int4* xp = reinterpret_cast<const int4*>(xq8 + 32 * b);
-            const int isum = dot_q4(w[k], xp[0], xp[1]);
-            const float2 ds = xds[b];
-            const float dw = (k & 1) ? h2f_hi(s[k >> 1]) : h2f_lo(s[k >> 1]);
-            acc = __fmaf_rn(__fmul_rn(dw, ds.x), __int2float_rn(isum - __float_as_int(ds.y)), acc);
-        }
+    for (int k = 0; k < CB; k++) {
+        const uint8_t* xb = x + (b0 + k) * rs;
+        const int4 x0 = *reinterpret_cast<const int4*>(xb);
+        const int4 x1 = *reinterpret_cast<const int4*>(xb + 16);
+        const float2 ds = *reinterpret_cast<const float2*>(xb + 32);
+        const int isum = dot_q4(t.q[k], x0, x1);
+        const uint32_t sw = u4_at(t.s, k >> 1);
+        const float dw = (k & 1) ? h2f_hi(sw) : h2f_lo(sw);
+        acc = __fmaf_rn(__fmul_rn(dw, ds.x), __int2float_rn(isum - __float_as_int(ds.y)), acc);
     }
     return acc;
 }
+__device__ __forceinline__ float chunk_dot(const Tile& t, int cb, const uint8_t* x, int rs, int b0) {
+    return cb == 8 ? chunk_dot<8>(t, x, rs, b0) : chunk_dot<4>(t, x, rs, b0);
+}
+__device__ __forceinline__ const uint8_t* tile_ptr(const PMat W, int g, int c) {
+    return W.base + ((size_t)g * W.nc + c) * tile_bytes(W.cb);
+}
+__device__ __forceinline__ int seg_c0(const PMat W, int s) { return s * W.nc / W.ks; }
 
-__device__ __forceinline__ float row_segment(const PMat& W, int g, int s, const int8_t* xq8, const float2* xds, int lane) {
-    const int c0 = s * W.nc / W.ks, c1 = (s + 1) * W.nc / W.ks;
-    const uint8_t* tile = W.base + ((size_t)g * W.nc + c0) * tile_bytes(W.cb);
-    return W.cb == 8 ? seg_dot<8>(tile, c1 - c0, c0 * 8, xq8, xds, lane)
-                     : seg_dot<4>(tile, c1 - c0, c0 * 4, xq8, xds, lane);
+// ------------------------------------------------------------------ workgroup work split
+constexpr int kWorkers = kPWaves - 1;      // waves 1..7
+constexpr int kPartTiles = 96;             // chunk sums a workgroup stages per phase
+constexpr int kCtlBytes = 64 * 1024;       // control-wave DMA staging
+constexpr int kMaxKsQkv = 2;               // q/k/v partials an attention item stages
+constexpr int kMaxKsRes = 8;               // split-K partials a residual add takes
+
+// Segments (64-row group g, K segment s; t = g*ks + s) go round-robin to
+// workgroups, t -> workgroup t % nwg. A workgroup's tiles are its segments'
+// chunks in order; tile k belongs to worker k % kWorkers, which holds it in
+// register slot (k / kWorkers) % 2.
+struct TileRef { const uint8_t* p; int b0; };
+__device__ __forceinline__ bool wg_tile(const PMat W, int wg, int nwg, int k, TileRef& r) {
+    const int nseg = (W.rows >> 6) * W.ks;
+    int t, c;
+    if (W.ks == 1) {
+        const int round = k / W.nc;
+        t = wg + round * nwg;
+        c = k - round * W.nc;
+        if (t >= nseg) return false;
+    } else {
+        t = wg;
+        for (;;) {
+            if (t >= nseg) return false;
+            const int s = t % W.ks, c0 = seg_c0(W, s), len = seg_c0(W, s + 1) - c0;
+            if (k < len) { c = c0 + k; break; }
+            k -= len;
+            t += nwg;
+        }
+    }
+    r.p = tile_ptr(W, t / W.ks, c);
+    r.b0 = c * W.cb;
+    return true;
 }
 
-__device__ __forceinline__ int nwaves() { return blockDim.x >> 6; }
-
-// tasks (group, segment) spread over the grid's waves; part[s][row]
-__device__ void gemv_phase(const PMat& W, const int8_t* xq8, const float2* xds, float* part, int wg, int nwg, int tid) {
-    const int lane = tid & 63, wave = tid >> 6, nw = nwaves();
-    const int ntask = (W.rows / 64) * W.ks;
-    for (int task = wg * nw + wave; task < ntask; task += nwg * nw) {
-        const int g = task / W.ks, s = task % W.ks;
-        part[(size_t)s * W.rows + g * 64 + lane] = row_segment(W, g, s, xq8, xds, lane);
+// calls f(g, s, k0, k1) for the workgroup's segments that worker kw finishes
+// (segment r of the workgroup -> worker r % kWorkers); tiles k0..k1-1 are its chunks
+template <class F>
+__device__ __forceinline__ void wg_segments(const PMat W, int wg, int nwg, int kw, F f) {
+    const int nseg = (W.rows >> 6) * W.ks;
+    int k0 = 0, r = 0;
+    for (int t = wg; t < nseg; t += nwg, r++) {
+        const int s = t % W.ks, len = seg_c0(W, s + 1) - seg_c0(W, s);
+        if (r % kWorkers == kw) f(t / W.ks, s, k0, k0 + len);
+        k0 += len;
     }
 }
-
-// device wall clock (100 MHz) of one profile slot, one row per workgroup
-__device__ __forceinline__ void stamp(const DModel& M, int slot) {
-    if (M.prof && slot >= 0 && threadIdx.x == 0)
-        M.prof[(size_t)blockIdx.x * prof_slots(M.NL) + slot] = __builtin_amdgcn_s_memrealtime();
+__device__ __forceinline__ float seg_sum(const float* P, int k0, int k1, int lane) {
+    float v = P[k0 * 64 + lane];
+    for (int k = k0 + 1; k < k1; k++) v = __fadd_rn(v, P[k * 64 + lane]);
+    return v;
 }
 
-// ------------------------------------------------------------------ cross-workgroup data
-// Inside one step, values that one workgroup writes and others read (GEMV partials,
-// attention records, the residual stream, the int8 act, argmax candidates) are
-// written once per launch into per-layer buffers whose 128-byte lines each have a
-// single writer, with agent-coherent stores (global_store sc1: written through
-// past the per-XCD L2). After the grid barrier every reader sees them with
-// ordinary loads: no reader can hold an older copy of a line that is written once
-// per launch, and the 32 workgroups of an XCD share one L2 fill. That keeps the
-// barrier free of agent-scope fences (an L2 write-back/invalidate per workgroup
-// costs ~1.7 us at 256 workgroups) and keeps the redundant prologue reads in L2.
-__device__ __forceinline__ uint32_t ldc(const uint32_t* p) {
-    return __hip_atomic_load(const_cast<uint32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void stc(float* p, float v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
-__device__ __forceinline__ void stc(uint32_t* p, uint32_t v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
-__device__ __forceinline__ void drain_vm() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
-
-typedef __attribute__((address_space(3))) void* lds_ptr;
-// one wave copies `bytes` (multiple of 16, both ends 16-byte aligned) from global
-// memory straight into LDS, 1 KB per instruction (lane l moves bytes 16l..16l+15)
-__device__ __forceinline__ void dma_wave(const void* g, void* lds, int bytes, int lane) {
-    for (int off = 0; off < bytes; off += 1024)
-        if (off + lane * 16 < bytes)
-            __builtin_amdgcn_global_load_lds(static_cast<const uint8_t*>(g) + off + lane * 16,
-                                             (lds_ptr)(static_cast<uint8_t*>(lds) + off), 16, 0, 0);
-}
-// the same spread over the workgroup's waves (1 KB blocks round-robin)
-__device__ __forceinline__ void dma_wg(const void* g, void* lds, int bytes) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = nwaves();
-    for (int off = wave * 1024; off < bytes; off += nw * 1024)
-        if (off + lane * 16 < bytes)
-            __builtin_amdgcn_global_load_lds(static_cast<const uint8_t*>(g) + off + lane * 16,
-                                             (lds_ptr)(static_cast<uint8_t*>(lds) + off), 16, 0, 0);
+// the worker's first two tiles of W into registers. Both slots are written either
+// way, so no older tile stays live (in registers) across the phases in between.
+__device__ __forceinline__ void prefetch(const PMat W, int wg, int nwg, int kw, Tile (&tl)[2], int lane) {
+    TileRef r;
+    tl[0] = Tile{};
+    tl[1] = Tile{};
+    if (wg_tile(W, wg, nwg, kw, r)) tile_load(tl[0], r.p, W.cb, lane);
+    if (wg_tile(W, wg, nwg, kw + kWorkers, r)) tile_load(tl[1], r.p, W.cb, lane);
 }
 
-// ------------------------------------------------------------------ LDS staging layout
-// xs    fp32 vector of the phase input (E <= kMaxE)
-// xq8   int8 activations (<= kMaxFF)
-// xds   per-block (scale, 8*sum(q)) pairs
-// red   per-wave argmax candidates
-// gpart per-wave gate/up segment sums of one 64-row group
-// stg   DMA landing zone: the residual and its split-K partials, act records, or
-//       the attention records the O phase merges
-struct Stage {
-    float* xs; int8_t* xq8; float2* xds; float4* red; float* gpart; float* stg;
-    __device__ explicit Stage(uint8_t* smem)
-        : xs(reinterpret_cast<float*>(smem)), xq8(reinterpret_cast<int8_t*>(smem + 4 * kMaxE)),
-          xds(reinterpret_cast<float2*>(smem + 4 * kMaxE + kMaxFF)),
-          red(reinterpret_cast<float4*>(smem + 4 * kMaxE + kMaxFF + kMaxFF / 4)),
-          gpart(reinterpret_cast<float*>(smem + 4 * kMaxE + kMaxFF + kMaxFF / 4 + 16 * kMaxWaves)),
-          stg(reinterpret_cast<float*>(smem + 4 * kMaxE + kMaxFF + kMaxFF / 4 + 16 * kMaxWaves + 4 * 64 * kMaxWaves)) {}
+// chunk sums of the worker's tiles into P[k][64]: the two prefetched tiles, then any
+// further ones loaded one at a time (only lm_head has more than two per worker; its
+// 1792 workers keep ~16 MB in flight, enough to stay bandwidth-bound)
+template <int CB>
+__device__ __forceinline__ void gemv_tiles_cb(const PMat W, int wg, int nwg, int kw, Tile (&tl)[2], const uint8_t* x,
+                                              int rs, float* P, int lane) {
+    TileRef r;
+    if (!wg_tile(W, wg, nwg, kw, r)) return;
+    P[kw * 64 + lane] = chunk_dot<CB>(tl[0], x, rs, r.b0);
+    if (!wg_tile(W, wg, nwg, kw + kWorkers, r)) return;
+    P[(kw + kWorkers) * 64 + lane] = chunk_dot<CB>(tl[1], x, rs, r.b0);
+    for (int k = kw + 2 * kWorkers; wg_tile(W, wg, nwg, k, r); k += kWorkers) {
+        tile_load(tl[0], r.p, CB, lane);
+        P[k * 64 + lane] = chunk_dot<CB>(tl[0], x, rs, r.b0);
+    }
+}
+__device__ __forceinline__ void gemv_tiles(const PMat W, int wg, int nwg, int kw, Tile (&tl)[2], const uint8_t* x, int rs,
+                                           float* P, int lane) {
+    if (W.cb == 8) gemv_tiles_cb<8>(W, wg, nwg, kw, tl, x, rs, P, lane);
+    else gemv_tiles_cb<4>(W, wg, nwg, kw, tl, x, rs, P, lane);
+}
+
+// worker epilogue: segment sums stored as split-K partials part[s][row]
+__device__ __forceinline__ void seg_store(const PMat W, int wg, int nwg, int kw, const float* P, float* part, int lane) {
+    wg_segments(W, wg, nwg, kw, [&](int g, int s, int k0, int k1) {
+        stc(part + (size_t)s * W.rows + g * 64 + lane, seg_sum(P, k0, k1, lane));
+    });
+}
+
+// ------------------------------------------------------------------ LDS layout
+template <int HD>
+constexpr int attn_wave_lds() { return 2 * 64 * HD * 2 + 3 * kMaxKsQkv * HD * 4 + 2 * HD * 4 + 64 * 4; }
+template <int HD>
+constexpr int union_bytes() { return kAttnWaves * attn_wave_lds<HD>() > kCtlBytes ? kAttnWaves * attn_wave_lds<HD>() : kCtlBytes; }
+constexpr int kFixedLds = 8 * kMaxE + (kMaxE / 32) * kXRec + kPartTiles * 256 + 1024;
+template <int HD>
+constexpr int step_lds() { return kFixedLds + union_bytes<HD>(); }
+
+// R     the residual stream h [kMaxE] (the persistent kernel keeps it resident)
+// T     the vector the control wave normalises / quantises [kMaxE]
+// X     int8 block records of the phase input [kMaxE/32][kXRec]
+// P     chunk sums [kPartTiles][64]
+// misc  256 floats: per-wave argmax candidates, per-head merge weights
+// U     control-wave DMA staging, or the attention waves' K/V (never both at once)
+struct Lds {
+    float* R; float* T; uint8_t* X; float* P; float* misc; uint8_t* U;
+    __device__ explicit Lds(uint8_t* s)
+        : R(reinterpret_cast<float*>(s)), T(reinterpret_cast<float*>(s + 4 * kMaxE)), X(s + 8 * kMaxE),
+          P(reinterpret_cast<float*>(s + 8 * kMaxE + (kMaxE / 32) * kXRec)),
+          misc(reinterpret_cast<float*>(s + 8 * kMaxE + (kMaxE / 32) * kXRec + kPartTiles * 256)),
+          U(s + kFixedLds) {}
 };
-constexpr int kMaxKs = 8;
-constexpr int kStgBytes = 4 * (kMaxKs + 1) * kMaxE;           // >= act records (kMaxFF/32*128) and merge records
-constexpr int kStageBytes = 4 * kMaxE + kMaxFF + kMaxFF / 4 + 16 * kMaxWaves + 4 * 64 * kMaxWaves + kStgBytes;
 
 // ------------------------------------------------------------------ argmax candidates
 struct Top2 { float best; int idx; float second; };
@@ -269,16 +343,15 @@ __device__ __forceinline__ void top2_wave(Top2& t) {
 // Two-level arrival tree: workgroup w arrives on counter w % 16 (16 counters on
 // separate 256-byte lines, so arrivals do not serialize on one address); the last
 // arrival of each counter bumps the top counter, whose last arrival publishes the
-// epoch every workgroup polls. Arrival first waits for the workgroup's own
-// (write-through) stores to complete. A poll that outlives kSpinLimit sets *err and
-// returns, so no wave can wait forever. bar[]: counter k at 64*k, top at 64*16,
-// epoch at 64*17 (zeroed by the host before each launch).
+// epoch every workgroup polls. Run by the control wave after the workgroup barrier
+// that follows every worker's own store drain; it drains its own stores first. A
+// poll that outlives kSpinLimit sets *err and returns, so no wave can wait forever.
+// bar[]: counter k at 64*k, top at 64*16, epoch at 64*17 (zeroed before each launch).
 constexpr unsigned kSpinLimit = 1u << 26;
 constexpr int kBarGroups = 16;
 constexpr int kBarWords = 64 * 18;
-__device__ __forceinline__ void grid_barrier(uint32_t* bar, int32_t* err, unsigned& epoch) {
+__device__ __forceinline__ void ctl_barrier(uint32_t* bar, int32_t* err, unsigned& epoch) {
     drain_vm();
-    __syncthreads();
     if (threadIdx.x == 0) {
         epoch++;
         const int ng = min(kBarGroups, (int)gridDim.x), g = blockIdx.x % ng;
@@ -293,100 +366,271 @@ __device__ __forceinline__ void grid_barrier(uint32_t* bar, int32_t* err, unsign
             if (++spins > kSpinLimit) { stc(reinterpret_cast<uint32_t*>(err), 1u); break; }
         }
     }
-    __syncthreads();
 }
 
-// ------------------------------------------------------------------ GEMV first-tile prefetch
-// The weights a wave reads first do not depend on the activations, so before the
-// phase's prologue (residual loads, norm, quant) each wave touches every 128-byte
-// line of its first tile with one dword load; the tile then comes from L2 once the
-// activations are ready. The loaded words only feed a never-taken store, so the
-// prefetch holds one register instead of the tile.
-struct Touch { uint32_t acc; };
-__device__ __forceinline__ void touch_lines(const uint8_t* p, int bytes, Touch& t) {
-    const int lane = threadIdx.x & 63;
-    for (int off = lane * 128; off < bytes; off += 64 * 128) t.acc ^= *reinterpret_cast<const uint32_t*>(p + off);
-}
-__device__ __forceinline__ Touch prefetch_first(const PMat& W, int wg) {
-    const int wave = threadIdx.x >> 6, nw = nwaves();
-    Touch t{0};
-    const int task = wg * nw + wave, ntask = (W.rows / 64) * W.ks;
-    if (task < ntask) {
-        const int g = task / W.ks, s = task % W.ks, c0 = s * W.nc / W.ks;
-        touch_lines(W.base + ((size_t)g * W.nc + c0) * tile_bytes(W.cb), (int)tile_bytes(W.cb), t);
-    }
-    return t;
-}
-__device__ __forceinline__ void retire(const Touch& t, int32_t* err) {
-    if (t.acc == 0x9E3779B9u && threadIdx.x == 1023) *err = 2;   // never true: keeps the loads
-}
-
-// tasks (group, segment) over the grid's waves; part[s][row], one 256-byte line pair per task
-__device__ void gemv_tasks(const PMat& W, const int8_t* xq8, const float2* xds, float* part, int wg, int nwg) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = nwaves();
-    const int ntask = (W.rows / 64) * W.ks;
-    for (int task = wg * nw + wave; task < ntask; task += nwg * nw) {
-        const int g = task / W.ks, s = task % W.ks;
-        stc(part + (size_t)s * W.rows + g * 64 + lane, row_segment(W, g, s, xq8, xds, lane));
-    }
-}
-
-// ------------------------------------------------------------------ phases
+// ------------------------------------------------------------------ per-layer buffers
 __device__ __forceinline__ size_t hin(int l, int E) { return (size_t)(2 * l) * E; }
 __device__ __forceinline__ size_t hmid(int l, int E) { return (size_t)(2 * l + 1) * E; }
-__device__ __forceinline__ float* qkv_part(const DModel& M, int l) { return M.qkv_part + (size_t)l * M.layers[0].qkv.ks * M.QKV; }
-__device__ __forceinline__ float* o_part(const DModel& M, int l) { return M.o_part + (size_t)l * M.layers[0].o.ks * M.E; }
-__device__ __forceinline__ float* d_part(const DModel& M, int l) { return M.d_part + (size_t)l * M.layers[0].d.ks * M.E; }
-__device__ __forceinline__ float* att_rec(const DModel& M, int l) { return M.att + (size_t)l * M.NH * M.maxch * M.arec; }
-__device__ __forceinline__ uint8_t* act_rec(const DModel& M, int l) { return M.act + (size_t)l * (M.FF / 32) * kActRec; }
+__device__ __forceinline__ float* qkv_part(MPtr M, int l) { return M->qkv_part + (size_t)l * LY(M, 0)->qkv.ks * M->QKV; }
+__device__ __forceinline__ float* o_part(MPtr M, int l) { return M->o_part + (size_t)l * LY(M, 0)->o.ks * M->E; }
+__device__ __forceinline__ float* d_part(MPtr M, int l) { return M->d_part + (size_t)l * LY(M, 0)->d.ks * M->E; }
+__device__ __forceinline__ float* att_rec(MPtr M, int l) { return M->att + (size_t)l * M->NH * M->maxch * M->arec; }
+__device__ __forceinline__ uint8_t* act_rec(MPtr M, int l) { return M->act + (size_t)l * (M->FF / 32) * kActRec; }
 
-// xs = h + (part[0] + ... + part[ks-1]) (the residual add of a split-K GEMV): h and
-// the partials arrive in LDS in one DMA batch; hout (workgroup 0) keeps the result
-__device__ void residual_dma(const Stage& S, const float* h, const float* part, int ks, int n, float* hout) {
-    dma_wg(h, S.stg, n * 4);
-    dma_wg(part, S.stg + n, ks * n * 4);
-    drain_vm();
-    __syncthreads();
-    for (int i = threadIdx.x; i < n; i += blockDim.x) {
-        float v = S.stg[n + i];
-        for (int s = 1; s < ks; s++) v = __fadd_rn(v, S.stg[n + s * n + i]);
-        v = __fadd_rn(S.stg[i], v);
-        S.xs[i] = v;
-        if (hout) stc(hout + i, v);
+// device wall clock (100 MHz) of one profile slot, one row per workgroup, written by
+// thread `who` (0: the control wave, 64: the first worker)
+__device__ __forceinline__ void stamp(MPtr M, int slot, int who = 0) {
+    if (threadIdx.x == who && M->prof)
+        M->prof[(size_t)blockIdx.x * prof_slots(M->NL) + slot] = __builtin_amdgcn_s_memrealtime();
+}
+
+// ------------------------------------------------------------------ control-wave prologues
+// the phases of a layer, then lm_head
+enum { PH_QKV = 0, PH_ATTN = 1, PH_O = 2, PH_GU = 3, PH_DOWN = 4, PH_LM = 5 };
+// Vectors live in LDS; a lane handles the float4 at element 256j + 4*lane for
+// j = 0, 1, ... (loops are not unrolled: the control wave's registers are shared
+// with the workers' tiles in one kernel, so it keeps little in registers).
+__device__ __forceinline__ float4 f4add(float4 a, float4 b) {
+    return make_float4(__fadd_rn(a.x, b.x), __fadd_rn(a.y, b.y), __fadd_rn(a.z, b.z), __fadd_rn(a.w, b.w));
+}
+__device__ __forceinline__ float4 ld4(const float* p) { return *reinterpret_cast<const float4*>(p); }
+__device__ __forceinline__ void st4(float* p, float4 v) { *reinterpret_cast<float4*>(p) = v; }
+__device__ __forceinline__ void st4(float* p, int i, float4 v) { *reinterpret_cast<float4*>(p + i) = v; }
+
+// Phase prologue, in two steps. ctl_stage (control wave, right after the grid
+// barrier): one DMA batch brings the phase's inputs into LDS. wg_prologue (all
+// eight waves): wave j handles the 256-element slice j of the input vector (the
+// float4 at 256j + 4*lane), so the residual add, RMSNorm and int8 quantisation run
+// on all four SIMDs; a single wave64 needs ~4 cycles per instruction and ~2.5 us
+// for the same work.
+//
+// U staging of the norm phases: [w: n][h: n, when not resident][part: ks*n]
+
+// quantise slice j (already scaled) into block records X; a 32-element block is
+// 8 lanes x 4 elements
+__device__ __forceinline__ void quant_slice(float4 y, bool own, int e0, uint8_t* X, int lane) {
+    if (!own) y = make_float4(0.f, 0.f, 0.f, 0.f);
+    float a = fmaxf(fmaxf(fabsf(y.x), fabsf(y.y)), fmaxf(fabsf(y.z), fabsf(y.w)));
+    a = fmaxf(a, __shfl_xor(a, 1));
+    a = fmaxf(a, __shfl_xor(a, 2));
+    a = fmaxf(a, __shfl_xor(a, 4));
+    const float inv = a > 0.f ? __fdiv_rn(127.f, a) : 0.f;
+    const int q0 = __float2int_rn(__fmul_rn(y.x, inv)), q1 = __float2int_rn(__fmul_rn(y.y, inv));
+    const int q2 = __float2int_rn(__fmul_rn(y.z, inv)), q3 = __float2int_rn(__fmul_rn(y.w, inv));
+    int s = q0 + q1 + q2 + q3;
+    s += __shfl_xor(s, 1);
+    s += __shfl_xor(s, 2);
+    s += __shfl_xor(s, 4);
+    if (own) {
+        uint8_t* rec = X + (e0 >> 5) * kXRec;
+        *reinterpret_cast<uint32_t*>(rec + (e0 & 31)) =
+            (uint32_t)(q0 & 0xFF) | ((uint32_t)(q1 & 0xFF) << 8) | ((uint32_t)(q2 & 0xFF) << 16) | ((uint32_t)q3 << 24);
+        if ((lane & 7) == 0) {
+            *reinterpret_cast<float*>(rec + 32) = fp16_round(__fdiv_rn(a, 127.f));
+            *reinterpret_cast<int*>(rec + 36) = 8 * s;
+        }
     }
 }
 
-// P1: residual (or embedding row) -> RMSNorm -> int8 -> fused QKV rows (split-K partials)
-__device__ void phase_qkv(const DModel& M, int l, int pos, int wg, int nwg, uint8_t* smem, int ps = -1) {
-    const int tid = threadIdx.x;
-    Stage S(smem);
-    const DLayer& L = M.layers[l];
-    const Touch pre = prefetch_first(L.qkv, wg);
-    if (l == 0) {
-        const float* er = M.emb + (size_t)M.tokbuf[pos] * M.E;
-        for (int i = tid; i < M.E; i += blockDim.x) {
-            const float v = er[i];
-            S.xs[i] = v;
-            if (wg == 0) stc(M.hbuf + hin(0, M.E) + i, v);
+// 1/sqrt(mean(x^2) + eps) of the n-vector x in LDS, the same on every lane of every
+// wave: lane l sums x[256j + 4l + i]^2 over j, then i, by fma; xor butterfly
+__device__ __forceinline__ float rms_scale(const float* x, int n, float eps, int lane) {
+    float a = 0.f;
+#pragma unroll 8
+    for (int e0 = 4 * lane; e0 < n; e0 += 256) {
+        const float4 v = ld4(x + e0);
+        a = __fmaf_rn(v.x, v.x, a);
+        a = __fmaf_rn(v.y, v.y, a);
+        a = __fmaf_rn(v.z, v.z, a);
+        a = __fmaf_rn(v.w, v.w, a);
+    }
+    a = bfly_sum64(a);
+    return __fdiv_rn(1.0f, __builtin_sqrtf(__fadd_rn(__fdiv_rn(a, (float)n), eps)));   // correctly rounded sqrt
+}
+
+// the previous GEMV of a norm phase: down of layer l-1 (qkv), o of layer l
+// (gate/up), down of the last layer (lm_head)
+__device__ __forceinline__ int norm_src_layer(MPtr M, int l, int kind) {
+    return kind == PH_QKV ? l - 1 : kind == PH_LM ? M->NL - 1 : l;
+}
+
+// control wave: DMA the inputs of phase (l, kind) into LDS and wait for them
+__device__ __forceinline__ void ctl_stage(MPtr M, int l, int kind, int pos, const Lds& S, int lane, bool resident) {
+    const int n = M->E;
+    if (kind == PH_DOWN) {
+        dma_wave(act_rec(M, l), S.U, (M->FF / 32) * kActRec, lane);
+    } else if (kind == PH_O) {
+        const int nch = (pos + 1 + kAttnChunk - 1) / kAttnChunk, arec = M->arec;
+        if (nch <= kInlineComb) {
+            const float* att = att_rec(M, l);
+            const int hb = nch * arec;
+            for (int h = 0; h < M->NH; h++)
+                dma_wave(att + (size_t)h * M->maxch * arec, reinterpret_cast<float*>(S.U) + h * hb, hb * 4, lane);
+        } else {
+            dma_wave(M->att_out + (size_t)l * n, S.T, n * 4, lane);
         }
-    } else {
-        residual_dma(S, M.hbuf + hmid(l - 1, M.E), d_part(M, l - 1), M.layers[l - 1].d.ks, M.E,
-                     wg == 0 ? M.hbuf + hin(l, M.E) : nullptr);
+    } else if (kind != PH_ATTN) {
+        float* w = reinterpret_cast<float*>(S.U);
+        dma_wave(kind == PH_LM ? M->out_norm : kind == PH_QKV ? LY(M, l)->an : LY(M, l)->fn, w, n * 4, lane);
+        if (kind == PH_QKV && l == 0) {
+            dma_wave(M->emb + (size_t)M->tokbuf[pos] * n, resident ? S.R : S.T, n * 4, lane);
+        } else {
+            const int pl = norm_src_layer(M, l, kind);
+            const bool dsrc = kind != PH_GU;
+            if (!resident) dma_wave(M->hbuf + (dsrc ? hmid(pl, n) : hin(l, n)), w + n, n * 4, lane);
+            dma_wave(dsrc ? d_part(M, pl) : o_part(M, pl), w + (resident ? n : 2 * n),
+                     (dsrc ? LY(M, pl)->d.ks : LY(M, pl)->o.ks) * n * 4, lane);
+        }
+    }
+    drain_vm();
+}
+
+// all waves: the phase input records X from the staged data (see ctl_stage)
+__device__ __forceinline__ void wg_prologue(MPtr M, int l, int kind, int pos, int wg, const Lds& S, int wave,
+                                            int lane, bool resident) {
+    const int n = M->E, e0 = 256 * wave + 4 * lane;
+    const bool has = 256 * wave < n, own = e0 < n;
+    if (kind == PH_O) {
+        const int nch = (pos + 1 + kAttnChunk - 1) / kAttnChunk;
+        if (!has) return;
+        float4 y = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (own && nch <= kInlineComb) {
+            // merge of the head's chunk records by max rescaling in chunk order
+            // (cuda_infer.cu:688-702), the per-chunk weights computed per lane
+            const int HD = M->HD, arec = M->arec, hb = nch * arec;
+            const int hh = e0 / HD, d = e0 - hh * HD;        // 4 | HD: one head
+            const float* r = reinterpret_cast<const float*>(S.U) + hh * hb;
+            float mx = -__builtin_inff();
+            for (int c = 0; c < nch; c++) mx = fmaxf(mx, r[c * arec + HD]);
+            float den = 0.f;
+            float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+            for (int c = 0; c < nch; c++) {
+                const float wc = mi_expf(__fsub_rn(r[c * arec + HD], mx));
+                den = __fmaf_rn(r[c * arec + HD + 1], wc, den);
+                const float4 o = ld4(r + c * arec + d);
+                acc = make_float4(__fmaf_rn(o.x, wc, acc.x), __fmaf_rn(o.y, wc, acc.y), __fmaf_rn(o.z, wc, acc.z),
+                                  __fmaf_rn(o.w, wc, acc.w));
+            }
+            y = make_float4(__fdiv_rn(acc.x, den), __fdiv_rn(acc.y, den), __fdiv_rn(acc.z, den), __fdiv_rn(acc.w, den));
+        } else if (own) {
+            y = ld4(S.T + e0);
+        }
+        quant_slice(y, own, e0, S.X, lane);
+        return;
+    }
+    if (kind == PH_DOWN || kind == PH_ATTN) return;
+    // norm phases: residual add of slice `wave`, then RMSNorm + int8 of it
+    const float* w = reinterpret_cast<const float*>(S.U);
+    float* h = resident && kind != PH_LM ? S.R : S.T;
+    if (has && own && !(kind == PH_QKV && l == 0)) {
+        const int pl = norm_src_layer(M, l, kind);
+        const int ks = kind != PH_GU ? LY(M, pl)->d.ks : LY(M, pl)->o.ks;
+        const float* hs = resident ? S.R : w + n;
+        const float* ps = w + (resident ? n : 2 * n);
+        float4 p[kMaxKsRes];
+#pragma unroll
+        for (int s = 0; s < kMaxKsRes; s++)
+            if (s < ks) p[s] = ld4(ps + s * n + e0);
+        float4 v = p[0];
+#pragma unroll
+        for (int s = 1; s < kMaxKsRes; s++)
+            if (s < ks) v = f4add(v, p[s]);
+        const float4 x = f4add(ld4(hs + e0), v);
+        st4(h, e0, x);
+        if (!resident && wg == 0 && kind != PH_LM) {
+            float* dst = M->hbuf + (kind == PH_QKV ? hin(l, n) : hmid(l, n)) + e0;
+            stc(dst, x.x); stc(dst + 1, x.y); stc(dst + 2, x.z); stc(dst + 3, x.w);
+        }
+    } else if (has && own && kind == PH_QKV && l == 0 && !resident && wg == 0) {
+        const float4 x = ld4(h + e0);
+        float* dst = M->hbuf + hin(0, n) + e0;
+        stc(dst, x.x); stc(dst + 1, x.y); stc(dst + 2, x.z); stc(dst + 3, x.w);
     }
     __syncthreads();
-    norm_quant(S.xs, L.an, M.E, M.eps, S.xq8, S.xds, tid);
+    const float sc = rms_scale(h, n, M->eps, lane);
+    if (!has) return;
+    float4 y = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (own) {
+        const float4 x = ld4(h + e0), wv = ld4(w + e0);
+        y = make_float4(__fmul_rn(__fmul_rn(x.x, sc), wv.x), __fmul_rn(__fmul_rn(x.y, sc), wv.y),
+                        __fmul_rn(__fmul_rn(x.z, sc), wv.z), __fmul_rn(__fmul_rn(x.w, sc), wv.w));
+    }
+    quant_slice(y, own, e0, S.X, lane);
+}
+
+// ------------------------------------------------------------------ gate/up epilogue
+// A 64-row group = 32 gate rows + their 32 up rows (ks = 1: the segment is the whole
+// row): silu(g)*u = g/(1+exp(-g))*u (cpu_infer.cpp:144-147) on lanes 0..31, quantized
+// to one int8 act block record (32 codes, scale, 8*sum) on its own 128-byte line.
+__device__ __forceinline__ void gu_store(const PMat W, int wg, int nwg, int kw, const float* P, uint8_t* act, int lane) {
+    wg_segments(W, wg, nwg, kw, [&](int g, int s, int k0, int k1) {
+        (void)s;
+        const float v = seg_sum(P, k0, k1, lane);
+        const float u = __shfl(v, (lane & 31) + 32);
+        const float t = mi_expf(-v);
+        const float a = __fmul_rn(__fdiv_rn(v, __fadd_rn(1.0f, t)), u);
+        int q, s8;
+        float d;
+        quant32_vals(a, q, d, s8);
+        const uint32_t b = (uint32_t)(q & 0xFF);
+        const uint32_t wd = b | (__shfl_down(b, 1) << 8) | (__shfl_down(b, 2) << 16) | (__shfl_down(b, 3) << 24);
+        if (lane < 32) {
+            uint32_t* r = reinterpret_cast<uint32_t*>(act + (size_t)g * kActRec);
+            if ((lane & 3) == 0) stc(r + lane / 4, wd);
+            if (lane == 0) { stc(r + 8, __float_as_uint(d)); stc(r + 9, (uint32_t)s8); }
+        }
+    });
+}
+
+// ------------------------------------------------------------------ lm_head epilogue
+// workers: row values of the workgroup's vocab groups (logits when requested),
+// per-lane top-2, wave top-2 -> misc; control wave: the workgroup's candidate
+__device__ __forceinline__ void lm_epilogue(MPtr M, int wg, int nwg, const Lds& S, int wave, int lane) {
+    if (wave > 0) {
+        Top2 t{-__builtin_inff(), INT_MAX, -__builtin_inff()};
+        wg_segments(ldmat(&M->lm), wg, nwg, wave - 1, [&](int g, int s, int k0, int k1) {
+            (void)s;
+            const float v = seg_sum(S.P, k0, k1, lane);
+            const int row = g * 64 + lane;
+            if (M->logits) M->logits[row] = v;
+            top2_push(t, v, row);
+        });
+        top2_wave(t);
+        if (lane == 0) reinterpret_cast<float4*>(S.misc)[wave] = make_float4(t.best, __int_as_float(t.idx), t.second, 0.f);
+    }
     __syncthreads();
-    stamp(M, ps);
-    gemv_tasks(L.qkv, S.xq8, S.xds, qkv_part(M, l), wg, nwg);
-    retire(pre, M.err);
+    if (threadIdx.x == 0) {
+        const float4* red = reinterpret_cast<const float4*>(S.misc);
+        Top2 a{red[1].x, __float_as_int(red[1].y), red[1].z};
+        for (int w = 2; w <= kWorkers; w++) top2_merge(a, red[w].x, __float_as_int(red[w].y), red[w].z);
+        float* cd = M->cand + (size_t)wg * 32;
+        stc(cd, a.best);
+        stc(reinterpret_cast<uint32_t*>(cd + 1), (uint32_t)a.idx);
+        stc(cd + 2, a.second);
+    }
+}
+
+// merge of the workgroups' candidates by one wave (top-2 merging is associative and
+// commutative, so any order gives the same token and margin); result on every lane
+__device__ __forceinline__ Top2 wave_merge_cands(const float* cand, int n, int lane) {
+    Top2 t{-__builtin_inff(), INT_MAX, -__builtin_inff()};
+    for (int i = lane; i < n; i += 64) {
+        const float* cd = cand + (size_t)i * 32;
+        top2_merge(t, cd[0], __float_as_int(cd[1]), cd[2]);
+    }
+    top2_wave(t);
+    return t;
+}
+__device__ __forceinline__ void emit_token(MPtr M, const Top2& a, int pos, int gen) {
+    M->out_tok[pos] = a.idx;
+    M->out_margin[pos] = __fsub_rn(a.best, a.second);
+    if (gen) M->tokbuf[pos + 1] = a.idx;
 }
 
 // ------------------------------------------------------------------ attention
 // per-wave LDS: K [HD/8][64] 16-byte vectors (vector j of position t at j*64 + t, so
-// a lane-per-position read is conflict-free) | V [64][HD] | q partials [8][HD] |
-// k, v partials [2][8][HD] | q [HD] | k(pos) [HD] | p [64]
-template <int HD>
-constexpr int attn_wave_lds() { return 2 * 64 * HD * 2 + 3 * 4 * kMaxKs * HD + 4 * HD * 2 + 4 * 64; }
+// a lane-per-position read is conflict-free) | V [64][HD] | q partials [2][HD] |
+// k, v partials [2][2][HD] | q [HD] | k(pos) [HD] | p [64]
 
 // DMA the chunk's K rows (swizzled) and V rows; rows past n repeat row n-1
 template <int HD>
@@ -439,6 +683,7 @@ __device__ __forceinline__ void attn_core(const uint4* kls, const float* qs, con
     wave_lds_sync();
 #pragma unroll
     for (int e = 0; e < DPL; e++) acc[e] = 0.f;
+#pragma unroll 8
     for (int t = 0; t < n; t++) {
         const float pt = ps[t];
         if constexpr (DPL == 2) {
@@ -451,37 +696,71 @@ __device__ __forceinline__ void attn_core(const uint4* kls, const float* qs, con
     }
 }
 
-// P2 item: one wave = one query head x one 64-position chunk of positions 0..L-1.
-// One DMA batch brings the chunk's K and V rows, the QKV partials of the head's q
-// rows and, in the chunk that holds position pos, of its kv head's k and v rows.
-// Then q = segments + bias + NEOX RoPE (cpu_infer.cpp:49-61); the last chunk
-// finishes k/v of pos, rounds them to fp16, appends them to the cache and uses them
-// for its own row.
+// Attention items (query head h, 64-position chunk c) of positions 0..pos. The G
+// query heads of one (kv head, chunk) read the same K/V rows, so they are placed on
+// one XCD (workgroups w = x + 8k share XCD x): unit u = kvh*nch + c, item index
+// iv = (u % 8) + 8*(hh + G*(u / 8)) for the unit's hh-th head; iv -> workgroup
+// iv % nwg, attention wave (iv / nwg) % kAttnWaves. Index values with u out of range
+// are skipped.
+struct AttnItem { int h, c; };
+__device__ __forceinline__ int attn_nvi(MPtr M, int nch) {
+    const int units = M->NKV * nch;
+    return 8 * M->G * ((units + 7) / 8);
+}
+__device__ __forceinline__ bool attn_decode(MPtr M, int nch, int iv, AttnItem& it) {
+    const int ux = iv % 8, rest = iv / 8, hh = rest % M->G, u = (rest / M->G) * 8 + ux;
+    if (u >= M->NKV * nch) return false;
+    it.h = (u / nch) * M->G + hh;
+    it.c = u % nch;
+    return true;
+}
+// the wave's first valid item index at or after iv (stride nwg * kAttnWaves); -1 if none
+__device__ __forceinline__ int attn_next(MPtr M, int nch, int iv, int nwg) {
+    const int nvi = attn_nvi(M, nch);
+    AttnItem it;
+    for (; iv < nvi; iv += nwg * kAttnWaves)
+        if (attn_decode(M, nch, iv, it)) return iv;
+    return -1;
+}
+
 template <int HD>
-__device__ void attn_item(const DModel& M, int l, int pos, int h, int c, uint8_t* lds, int lane) {
+__device__ __forceinline__ void attn_issue_item(MPtr M, int l, int pos, const AttnItem& it, uint8_t* lds, int lane) {
+    const int kvh = it.h / M->G, t0 = it.c * kAttnChunk, n = min(kAttnChunk, pos + 1 - t0);
+    const size_t rowbase = ((size_t)l * M->NKV + kvh) * M->maxseq;
+    attn_issue_kv<HD>(M->kc + rowbase * HD, M->vc + rowbase * HD, t0, n, reinterpret_cast<uint4*>(lds),
+                      reinterpret_cast<__half*>(lds + 64 * HD * 2), lane);
+}
+
+// One item after its K/V DMA was issued: the QKV partials of the head's q rows and,
+// in the chunk that holds position pos, of its kv head's k and v rows; q = segments
+// + bias + NEOX RoPE (cpu_infer.cpp:49-61); the last chunk finishes k/v of pos,
+// rounds them to fp16, appends them to the cache and uses them for its own row.
+// The record o[HD], max, sum goes to att[l][h][c] (agent-coherent stores).
+template <int HD>
+__device__ __forceinline__ void attn_finish(MPtr M, int l, int pos, const AttnItem& it, uint8_t* lds, int lane) {
     constexpr int half = HD / 2, DPL = HD / 64;
     uint4* kls = reinterpret_cast<uint4*>(lds);
     __half* vls = reinterpret_cast<__half*>(lds + 64 * HD * 2);
     float* qp = reinterpret_cast<float*>(lds + 2 * 64 * HD * 2);                 // [ks][HD]
-    float* kvp = qp + kMaxKs * HD;                                               // [ks][HD] k then [ks][HD] v
-    float* qs = qp + 3 * kMaxKs * HD;
+    float* kvp = qp + kMaxKsQkv * HD;                                            // [ks][HD] k then [ks][HD] v
+    float* qs = qp + 3 * kMaxKsQkv * HD;
     float* kcur = qs + HD;
     float* ps = kcur + HD;
-    const DLayer& Ly = M.layers[l];
-    const int ks = Ly.qkv.ks, kvh = h / M.G;
+    const LPtr Ly = LY(M, l);
+    const int h = it.h, c = it.c;
+    const int ks = Ly->qkv.ks, kvh = h / M->G;
     const int L = pos + 1, nch = (L + kAttnChunk - 1) / kAttnChunk, t0 = c * kAttnChunk;
     const int n = min(kAttnChunk, L - t0);
     const bool last = c == nch - 1;
     const int cur = last ? pos - t0 : -1;
-    const size_t rowbase = ((size_t)l * M.NKV + kvh) * M.maxseq;
-    attn_issue_kv<HD>(M.kc + rowbase * HD, M.vc + rowbase * HD, t0, n, kls, vls, lane);
+    const size_t rowbase = ((size_t)l * M->NKV + kvh) * M->maxseq;
     const float* part = qkv_part(M, l);
-    const int rq = h * HD, rk = M.NH * HD + kvh * HD, rv = M.NH * HD + M.KVD + kvh * HD;
+    const int rq = h * HD, rk = M->NH * HD + kvh * HD, rv = M->NH * HD + M->KVD + kvh * HD;
     for (int s = 0; s < ks; s++) {
-        dma_wave(part + (size_t)s * M.QKV + rq, qp + s * HD, HD * 4, lane);
+        dma_wave(part + (size_t)s * M->QKV + rq, qp + s * HD, HD * 4, lane);
         if (last) {
-            dma_wave(part + (size_t)s * M.QKV + rk, kvp + s * HD, HD * 4, lane);
-            dma_wave(part + (size_t)s * M.QKV + rv, kvp + (kMaxKs + s) * HD, HD * 4, lane);
+            dma_wave(part + (size_t)s * M->QKV + rk, kvp + s * HD, HD * 4, lane);
+            dma_wave(part + (size_t)s * M->QKV + rv, kvp + (kMaxKsQkv + s) * HD, HD * 4, lane);
         }
     }
     drain_vm();
@@ -492,24 +771,24 @@ __device__ void attn_item(const DModel& M, int l, int pos, int h, int c, uint8_t
         return __fadd_rn(v, bias);
     };
     const int ip = lane % half;
-    const float2 cz = M.rope[(size_t)pos * half + ip];
+    const float2 cz = M->rope[(size_t)pos * half + ip];
     if (lane < half) {
-        const float x0 = fin(qp, ip, Ly.bqkv[rq + ip]), x1 = fin(qp, ip + half, Ly.bqkv[rq + ip + half]);
+        const float x0 = fin(qp, ip, Ly->bqkv[rq + ip]), x1 = fin(qp, ip + half, Ly->bqkv[rq + ip + half]);
         qs[ip] = __fsub_rn(__fmul_rn(x0, cz.x), __fmul_rn(x1, cz.y));
         qs[ip + half] = __fadd_rn(__fmul_rn(x0, cz.y), __fmul_rn(x1, cz.x));
         if (last) {
-            const float k0 = fin(kvp, ip, Ly.bqkv[rk + ip]), k1 = fin(kvp, ip + half, Ly.bqkv[rk + ip + half]);
+            const float k0 = fin(kvp, ip, Ly->bqkv[rk + ip]), k1 = fin(kvp, ip + half, Ly->bqkv[rk + ip + half]);
             const __half y0 = __float2half(__fsub_rn(__fmul_rn(k0, cz.x), __fmul_rn(k1, cz.y)));
             const __half y1 = __float2half(__fadd_rn(__fmul_rn(k0, cz.y), __fmul_rn(k1, cz.x)));
-            const __half v0 = __float2half(fin(kvp + kMaxKs * HD, ip, Ly.bqkv[rv + ip]));
-            const __half v1 = __float2half(fin(kvp + kMaxKs * HD, ip + half, Ly.bqkv[rv + ip + half]));
+            const __half v0 = __float2half(fin(kvp + kMaxKsQkv * HD, ip, Ly->bqkv[rv + ip]));
+            const __half v1 = __float2half(fin(kvp + kMaxKsQkv * HD, ip + half, Ly->bqkv[rv + ip + half]));
             kcur[ip] = __half2float(y0);
             kcur[ip + half] = __half2float(y1);
             vls[cur * HD + ip] = v0;
             vls[cur * HD + ip + half] = v1;
-            if (h % M.G == 0) {                    // one of the kv head's G query heads appends to the cache
-                __half* kd = M.kc + (rowbase + pos) * HD;
-                __half* vd = M.vc + (rowbase + pos) * HD;
+            if (h % M->G == 0) {                    // one of the kv head's G query heads appends to the cache
+                __half* kd = M->kc + (rowbase + pos) * HD;
+                __half* vd = M->vc + (rowbase + pos) * HD;
                 kd[ip] = y0; kd[ip + half] = y1;
                 vd[ip] = v0; vd[ip + half] = v1;
             }
@@ -517,22 +796,37 @@ __device__ void attn_item(const DModel& M, int l, int pos, int h, int c, uint8_t
     }
     wave_lds_sync();
     float m, lsum, acc[DPL];
-    attn_core<HD>(kls, qs, kcur, cur, vls, ps, n, M.scale, lane, m, lsum, acc);
-    float* rec = att_rec(M, l) + ((size_t)h * M.maxch + c) * M.arec;
+    attn_core<HD>(kls, qs, kcur, cur, vls, ps, n, M->scale, lane, m, lsum, acc);
+    float* rec = att_rec(M, l) + ((size_t)h * M->maxch + c) * M->arec;
 #pragma unroll
     for (int e = 0; e < DPL; e++) stc(rec + DPL * lane + e, acc[e]);
     if (lane == 0) { stc(rec + HD, m); stc(rec + HD + 1, lsum); }
     wave_lds_sync();                           // LDS is reused by the wave's next item
 }
 
+// the attention wave kw's first item: K/V DMA only (issued before the grid barrier)
 template <int HD>
-__device__ void phase_attn(const DModel& M, int l, int pos, int wg, int nwg, uint8_t* smem) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    if (wave >= kAttnWaves) return;
-    const int nch = (pos + 1 + kAttnChunk - 1) / kAttnChunk, items = M.NH * nch;
-    uint8_t* lds = smem + wave * attn_wave_lds<HD>();
-    for (int it = wg * kAttnWaves + wave; it < items; it += nwg * kAttnWaves)
-        attn_item<HD>(M, l, pos, it / nch, it % nch, lds, lane);
+__device__ __forceinline__ void attn_prefetch(MPtr M, int l, int pos, int wg, int nwg, uint8_t* U, int kw, int lane) {
+    if (kw >= kAttnWaves) return;
+    const int nch = (pos + 1 + kAttnChunk - 1) / kAttnChunk;
+    const int iv = attn_next(M, nch, wg + nwg * kw, nwg);
+    AttnItem it;
+    if (iv >= 0 && attn_decode(M, nch, iv, it)) attn_issue_item<HD>(M, l, pos, it, U + kw * attn_wave_lds<HD>(), lane);
+}
+// all of the wave's items; the first one's K/V are already in flight
+template <int HD>
+__device__ __forceinline__ void attn_run(MPtr M, int l, int pos, int wg, int nwg, uint8_t* U, int kw, int lane) {
+    if (kw >= kAttnWaves) return;
+    const int nch = (pos + 1 + kAttnChunk - 1) / kAttnChunk;
+    uint8_t* lds = U + kw * attn_wave_lds<HD>();
+    bool first = true;
+    for (int iv = attn_next(M, nch, wg + nwg * kw, nwg); iv >= 0; iv = attn_next(M, nch, iv + nwg * kAttnWaves, nwg)) {
+        AttnItem it;
+        attn_decode(M, nch, iv, it);
+        if (!first) attn_issue_item<HD>(M, l, pos, it, lds, lane);
+        first = false;
+        attn_finish<HD>(M, l, pos, it, lds, lane);
+    }
 }
 
 // merge of one (head, dim) from the chunk records in chunk order (cuda_infer.cu:688-702)
@@ -548,280 +842,251 @@ __device__ __forceinline__ float combine_one(const float* recs, int rec, int hd,
     return __fdiv_rn(acc, den);
 }
 
-// P2 merge as its own phase (more than kInlineComb chunks): one thread per (head, dim)
-__device__ void phase_comb(const DModel& M, int l, int pos, int wg, int nwg) {
+// chunk merge as its own phase (more than kInlineComb chunks): one thread per (head, dim)
+__device__ __forceinline__ void phase_comb(MPtr M, int l, int pos, int wg, int nwg) {
     const int nch = (pos + 1 + kAttnChunk - 1) / kAttnChunk;
     const float* att = att_rec(M, l);
-    float* out = M.att_out + (size_t)l * M.E;
-    for (int it = wg * blockDim.x + threadIdx.x; it < M.E; it += nwg * blockDim.x)
-        stc(out + it, combine_one(att + (size_t)(it / M.HD) * M.maxch * M.arec, M.arec, M.HD, it % M.HD, nch));
+    float* out = M->att_out + (size_t)l * M->E;
+    for (int it = wg * blockDim.x + threadIdx.x; it < M->E; it += nwg * blockDim.x)
+        stc(out + it, combine_one(att + (size_t)(it / M->HD) * M->maxch * M->arec, M->arec, M->HD, it % M->HD, nch));
 }
 
-// P3: attention output (chunk records merged here up to kInlineComb chunks) -> int8 -> O rows
-__device__ void phase_o(const DModel& M, int l, int pos, int wg, int nwg, uint8_t* smem, int ps = -1) {
-    const int tid = threadIdx.x;
-    Stage S(smem);
-    const Touch pre = prefetch_first(M.layers[l].o, wg);
-    const int nch = (pos + 1 + kAttnChunk - 1) / kAttnChunk;
-    if (nch <= kInlineComb) {
-        const float* att = att_rec(M, l);
-        const int hb = nch * M.arec * 4;                 // bytes of one head's records
-        for (int h = 0; h < M.NH; h++) dma_wg(att + (size_t)h * M.maxch * M.arec, S.stg + h * nch * M.arec, hb);
-        drain_vm();
-        __syncthreads();
-        for (int i = tid; i < M.E; i += blockDim.x)
-            S.xs[i] = combine_one(S.stg + (i / M.HD) * nch * M.arec, M.arec, M.HD, i % M.HD, nch);
+// ------------------------------------------------------------------ the persistent step
+// One cooperative launch of one 512-thread workgroup per CU runs the whole token:
+// five phases per layer separated by grid barriers (the reference's mega kernel has
+// the same count, mega.cu:695-833) + one for the chunk merge past kInlineComb
+// chunks, then lm_head, one barrier and workgroup 0 merges the candidates.
+// The phases run as one loop over the flattened sequence (layer, kind), so each
+// piece of code exists once: the whole kernel stays within the instruction cache
+// (an unrolled body of ~115 KB missed it on every layer).
+// Per phase: [control: barrier, prologue] sync [workers: tiles] sync [workers:
+// segment sums, stores, store drain, next phase's prefetch] sync.
+// Profile slots (every workgroup): 0 = start; then five per phase in the sequence
+// (qkv, attention, o, gate/up, down per layer, then lm_head): prologue end, first
+// worker's tiles done, its stores drained (its next-phase prefetch follows; lm:
+// the control wave's candidate written), phase end, barrier exit.
+__device__ __forceinline__ PMat phase_mat(MPtr M, int l, int kind) {
+    if (kind == PH_LM) return ldmat(&M->lm);
+    const LPtr L = LY(M, l);
+    return ldmat(kind == PH_QKV ? &L->qkv : kind == PH_O ? &L->o : kind == PH_GU ? &L->gu : &L->d);
+}
+// the phase after (l, kind)
+__device__ __forceinline__ void phase_next(MPtr M, int l, int kind, int& nl, int& nk) {
+    if (kind == PH_DOWN) { nl = l + 1; nk = nl < M->NL ? PH_QKV : PH_LM; }
+    else { nl = l; nk = kind + 1; }
+}
+// workers: the tiles of phase (l, kind), or its attention items
+template <int HD>
+__device__ __forceinline__ void phase_work(MPtr M, int l, int kind, int pos, int wg, int nwg, const Lds& S,
+                                           int kw, Tile (&tl)[2], int lane) {
+    if (kind == PH_ATTN) {
+        attn_run<HD>(M, l, pos, wg, nwg, S.U, kw, lane);
     } else {
-        dma_wg(M.att_out + (size_t)l * M.E, S.xs, M.E * 4);
-        drain_vm();
-    }
-    __syncthreads();
-    norm_quant(S.xs, nullptr, M.E, 0.f, S.xq8, S.xds, tid);
-    __syncthreads();
-    stamp(M, ps);
-    gemv_tasks(M.layers[l].o, S.xq8, S.xds, o_part(M, l), wg, nwg);
-    retire(pre, M.err);
-}
-
-// quantize one 32-element block per half-wave and return the lane's code, the block
-// scale and 8*sum(q) on every lane (cuda_infer.cu:80-89)
-__device__ __forceinline__ void quant32_vals(float v, int& q, float& d, int& s8) {
-    float a = fabsf(v);
-#pragma unroll
-    for (int off = 16; off >= 1; off >>= 1) a = fmaxf(a, __shfl_xor(a, off));
-    const float inv = a > 0.f ? __fdiv_rn(127.f, a) : 0.f;
-    q = __float2int_rn(__fmul_rn(v, inv));
-    int s = q;
-#pragma unroll
-    for (int off = 16; off >= 1; off >>= 1) s += __shfl_xor(s, off);
-    d = __half2float(__float2half(__fdiv_rn(a, 127.f)));
-    s8 = 8 * s;
-}
-
-// P4: residual (h_mid = h_in + O) -> RMSNorm -> int8 -> gate/up rows -> silu(gate)*up
-// (cpu_infer.cpp:144-147) -> int8 act block records. A workgroup owns whole 64-row
-// groups (32 gate rows + their 32 up rows = one 32-element act block): its waves
-// compute the ks K segments, which are added in order from LDS.
-__device__ void phase_gu(const DModel& M, int l, int wg, int nwg, uint8_t* smem, int ps = -1) {
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = nwaves();
-    Stage S(smem);
-    const DLayer& L = M.layers[l];
-    const PMat& W = L.gu;
-    const int ks = W.ks, slots = nw / ks, ng = W.rows / 64;
-    const int slot = wave / ks, seg = wave % ks;
-    Touch pre{0};
-    if (slot < slots && wg * slots + slot < ng) {
-        const int g = wg * slots + slot, c0 = seg * W.nc / ks;
-        touch_lines(W.base + ((size_t)g * W.nc + c0) * tile_bytes(W.cb), (int)tile_bytes(W.cb), pre);
-    }
-    residual_dma(S, M.hbuf + hin(l, M.E), o_part(M, l), L.o.ks, M.E, wg == 0 ? M.hbuf + hmid(l, M.E) : nullptr);
-    __syncthreads();
-    norm_quant(S.xs, L.fn, M.E, M.eps, S.xq8, S.xds, tid);
-    __syncthreads();
-    stamp(M, ps);
-    uint8_t* act = act_rec(M, l);
-    for (int base = wg * slots; base < ng; base += nwg * slots) {
-        const int g = base + slot;
-        if (slot < slots && g < ng)
-            S.gpart[wave * 64 + lane] = row_segment(W, g, seg, S.xq8, S.xds, lane);
-        __syncthreads();
-        if (wave < slots) {
-            const int gg = base + wave;
-            float v = S.gpart[(wave * ks) * 64 + lane];
-            for (int s = 1; s < ks; s++) v = __fadd_rn(v, S.gpart[(wave * ks + s) * 64 + lane]);
-            const float u = __shfl(v, (lane & 31) + 32);
-            const float t = mi_expf(-v);
-            const float a = __fmul_rn(__fdiv_rn(v, __fadd_rn(1.0f, t)), u);
-            int q, s8;
-            float d;
-            quant32_vals(a, q, d, s8);
-            const uint32_t b = (uint32_t)(q & 0xFF);
-            const uint32_t w = b | (__shfl_down(b, 1) << 8) | (__shfl_down(b, 2) << 16) | (__shfl_down(b, 3) << 24);
-            if (gg < ng && lane < 32) {
-                uint32_t* r = reinterpret_cast<uint32_t*>(act + (size_t)gg * kActRec);
-                if ((lane & 3) == 0) stc(r + lane / 4, w);
-                if (lane == 0) { stc(r + 8, __float_as_uint(d)); stc(r + 9, (uint32_t)s8); }
-            }
-        }
-        __syncthreads();
-    }
-    retire(pre, M.err);
-}
-
-// P5: int8 act records -> LDS -> down rows
-__device__ void phase_down(const DModel& M, int l, int wg, int nwg, uint8_t* smem, int ps = -1) {
-    const int tid = threadIdx.x;
-    Stage S(smem);
-    const Touch pre = prefetch_first(M.layers[l].d, wg);
-    const int nblk = M.FF / 32;
-    dma_wg(act_rec(M, l), S.stg, nblk * kActRec);
-    drain_vm();
-    __syncthreads();
-    const uint8_t* rec = reinterpret_cast<const uint8_t*>(S.stg);
-    for (int i = tid; i < nblk * 8; i += blockDim.x)
-        reinterpret_cast<uint32_t*>(S.xq8)[i] = reinterpret_cast<const uint32_t*>(rec + (i / 8) * kActRec)[i % 8];
-    for (int i = tid; i < nblk; i += blockDim.x) {
-        const uint32_t* r = reinterpret_cast<const uint32_t*>(rec + i * kActRec);
-        S.xds[i] = make_float2(__uint_as_float(r[8]), __uint_as_float(r[9]));
-    }
-    __syncthreads();
-    stamp(M, ps);
-    gemv_tasks(M.layers[l].d, S.xq8, S.xds, d_part(M, l), wg, nwg);
-    retire(pre, M.err);
-}
-
-// lm_head: final residual -> RMSNorm -> int8 -> vocab rows, per-workgroup top-2
-__device__ void phase_lm(const DModel& M, int wg, int nwg, uint8_t* smem, int ps = -1) {
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = nwaves();
-    Stage S(smem);
-    const int ng = M.lm.rows / 64;
-    const Touch pre = prefetch_first(M.lm, wg);
-    residual_dma(S, M.hbuf + hmid(M.NL - 1, M.E), d_part(M, M.NL - 1), M.layers[M.NL - 1].d.ks, M.E,
-                 wg == 0 ? M.hbuf + (size_t)2 * M.NL * M.E : nullptr);
-    __syncthreads();
-    norm_quant(S.xs, M.out_norm, M.E, M.eps, S.xq8, S.xds, tid);
-    __syncthreads();
-    stamp(M, ps);
-    Top2 t{-__builtin_inff(), INT_MAX, -__builtin_inff()};
-    for (int g = wg * nw + wave; g < ng; g += nwg * nw) {
-        const float v = row_segment(M.lm, g, 0, S.xq8, S.xds, lane);
-        const int row = g * 64 + lane;
-        if (M.logits) M.logits[row] = v;
-        top2_push(t, v, row);
-    }
-    top2_wave(t);
-    retire(pre, M.err);
-    if (lane == 0) S.red[wave] = make_float4(t.best, __int_as_float(t.idx), t.second, 0.f);
-    __syncthreads();
-    if (tid == 0) {
-        Top2 a{S.red[0].x, __float_as_int(S.red[0].y), S.red[0].z};
-        for (int w = 1; w < nw; w++) top2_merge(a, S.red[w].x, __float_as_int(S.red[w].y), S.red[w].z);
-        float* cd = M.cand + (size_t)wg * 32;
-        stc(cd, a.best);
-        stc(reinterpret_cast<uint32_t*>(cd + 1), (uint32_t)a.idx);
-        stc(cd + 2, a.second);
+        const bool down = kind == PH_DOWN;
+        gemv_tiles(phase_mat(M, l, kind), wg, nwg, kw, tl, down ? S.U : S.X, down ? kActRec : kXRec, S.P, lane);
     }
 }
-
-// merge the lm workgroups' candidates (top-2 merging is associative and commutative,
-// so any order gives the same token and margin); the result is on every thread
-__device__ Top2 merge_cands(const float* cand, int n, float4* red) {
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = nwaves();
-    Top2 t{-__builtin_inff(), INT_MAX, -__builtin_inff()};
-    for (int i = tid; i < n; i += blockDim.x) {
-        const float* cd = cand + (size_t)i * 32;
-        top2_merge(t, cd[0], __float_as_int(cd[1]), cd[2]);
+// workers: the stores of phase (l, kind) (lm_head has its own epilogue)
+__device__ __forceinline__ void phase_store(MPtr M, int l, int kind, int wg, int nwg, const Lds& S, int kw, int lane) {
+    if (kind == PH_ATTN) return;
+    const PMat W = phase_mat(M, l, kind);
+    if (kind == PH_GU) {
+        gu_store(W, wg, nwg, kw, S.P, act_rec(M, l), lane);
+    } else {
+        float* part = kind == PH_QKV ? qkv_part(M, l) : kind == PH_O ? o_part(M, l) : d_part(M, l);
+        seg_store(W, wg, nwg, kw, S.P, part, lane);
     }
-    top2_wave(t);
-    __syncthreads();
-    if (lane == 0) red[wave] = make_float4(t.best, __int_as_float(t.idx), t.second, 0.f);
-    __syncthreads();
-    Top2 a{red[0].x, __float_as_int(red[0].y), red[0].z};
-    for (int w = 1; w < nw; w++) top2_merge(a, red[w].x, __float_as_int(red[w].y), red[w].z);
-    return a;
 }
-
-__device__ __forceinline__ void emit_token(const DModel& M, const Top2& a, int pos, int gen) {
-    M.out_tok[pos] = a.idx;
-    M.out_margin[pos] = __fsub_rn(a.best, a.second);
-    if (gen) M.tokbuf[pos + 1] = a.idx;
+// workers: the prefetch of phase (l, kind)'s first tiles (the attention K/V of the
+// first items are brought in by the control wave during the QKV phase)
+__device__ __forceinline__ void phase_prefetch(MPtr M, int l, int kind, int wg, int nwg, int kw, Tile (&tl)[2], int lane) {
+    if (kind != PH_ATTN) {
+        prefetch(phase_mat(M, l, kind), wg, nwg, kw, tl, lane);
+    } else {
+        tl[0] = Tile{};        // written on every path: the tiles are never live across the attention phase
+        tl[1] = Tile{};
+    }
 }
-
-// ------------------------------------------------------------------ per-phase kernels
-__global__ __launch_bounds__(kThreads) void k_qkv(DModel M, int l, int pos) {
-    __shared__ __align__(16) uint8_t smem[kStageBytes];
-    phase_qkv(M, l, pos, blockIdx.x, gridDim.x, smem);
-}
-template <int HD>
-__global__ __launch_bounds__(kThreads) void k_attn(DModel M, int l, int pos) {
-    __shared__ __align__(16) uint8_t smem[kAttnWaves * attn_wave_lds<HD>()];
-    phase_attn<HD>(M, l, pos, blockIdx.x, gridDim.x, smem);
-}
-__global__ __launch_bounds__(kThreads) void k_attn_comb(DModel M, int l, int pos) {
-    phase_comb(M, l, pos, blockIdx.x, gridDim.x);
-}
-__global__ __launch_bounds__(kThreads) void k_o(DModel M, int l, int pos) {
-    __shared__ __align__(16) uint8_t smem[kStageBytes];
-    phase_o(M, l, pos, blockIdx.x, gridDim.x, smem);
-}
-__global__ __launch_bounds__(kThreads) void k_gu(DModel M, int l) {
-    __shared__ __align__(16) uint8_t smem[kStageBytes];
-    phase_gu(M, l, blockIdx.x, gridDim.x, smem);
-}
-__global__ __launch_bounds__(kThreads) void k_down(DModel M, int l) {
-    __shared__ __align__(16) uint8_t smem[kStageBytes];
-    phase_down(M, l, blockIdx.x, gridDim.x, smem);
-}
-__global__ __launch_bounds__(kThreads) void k_lm(DModel M) {
-    __shared__ __align__(16) uint8_t smem[kStageBytes];
-    phase_lm(M, blockIdx.x, gridDim.x, smem);
-}
-__global__ __launch_bounds__(kThreads) void k_argmax(DModel M, int ncand, int pos, int gen) {
-    __shared__ float4 red[kMaxWaves];
-    const Top2 a = merge_cands(M.cand, ncand, red);
-    if (threadIdx.x == 0) emit_token(M, a, pos, gen);
-}
-
-// ------------------------------------------------------------------ persistent step kernel
-// The whole decode step of position pos in one cooperative launch (one workgroup per
-// CU): the phases above separated by grid barriers, 5 per layer + 1 before the
-// argmax (the reference's mega kernel has the same count, mega.cu:695-833). Every
-// workgroup merges the lm_head candidates itself, so the token needs no barrier.
-// Profile slots (every workgroup stamps its own row): 0 = start; per layer and
-// phase (qkv, attention, o, gate/up, down) the end of the prologue, the end of the
-// phase and the barrier exit; then lm prologue, lm end, last barrier exit.
 
 template <int HD>
-constexpr int step_lds() { return kAttnWaves * attn_wave_lds<HD>() > kStageBytes ? kAttnWaves * attn_wave_lds<HD>() : kStageBytes; }
-
-template <int HD>
-__global__ __launch_bounds__(kPThreads) void k_step(DModel M, int pos, int gen) {
+__global__ __launch_bounds__(kPThreads) void k_step(const DModel* Mp, int pos, int gen) {
+    const MPtr M = (MPtr)Mp;
     __shared__ __align__(16) uint8_t smem[step_lds<HD>()];
-    const int wg = blockIdx.x, nwg = gridDim.x;
+    const Lds S(smem);
+    const int wg = blockIdx.x, nwg = gridDim.x, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const bool ctl = wave == 0;
+    const int kw = wave - 1;
     const int nch = (pos + 1 + kAttnChunk - 1) / kAttnChunk;
     unsigned epoch = 0;
+    Tile tl[2];
     stamp(M, 0);
-    for (int l = 0; l < M.NL; l++) {
-        const int p0 = 1 + l * kProfSlotsPerLayer;
-        phase_qkv(M, l, pos, wg, nwg, smem, p0);
-        stamp(M, p0 + 1);
-        grid_barrier(M.bar, M.err, epoch);
-        stamp(M, p0 + 2);
-        stamp(M, p0 + 3);
-        phase_attn<HD>(M, l, pos, wg, nwg, smem);
-        stamp(M, p0 + 4);
-        grid_barrier(M.bar, M.err, epoch);
-        if (nch > kInlineComb) {
-            phase_comb(M, l, pos, wg, nwg);
-            grid_barrier(M.bar, M.err, epoch);
+    if (ctl) ctl_stage(M, 0, PH_QKV, pos, S, lane, true);
+    else phase_prefetch(M, 0, PH_QKV, wg, nwg, kw, tl, lane);
+    int l = 0, kind = PH_QKV;
+    for (int sb = 1;; sb += 5) {
+        __syncthreads();
+        wg_prologue(M, l, kind, pos, wg, S, wave, lane, true);
+        __syncthreads();
+        stamp(M, sb);
+        if (!ctl) {
+            phase_work<HD>(M, l, kind, pos, wg, nwg, S, kw, tl, lane);
+            tl[0] = Tile{};        // consumed: dead (and not in registers) until the next prefetch
+            tl[1] = Tile{};
+        } else if (kind == PH_QKV) {
+            // U is free while the QKV tiles run: the K/V rows of the attention waves'
+            // first items, drained before the control wave leaves this branch
+            for (int a = 0; a < kAttnWaves; a++) attn_prefetch<HD>(M, l, pos, wg, nwg, S.U, a, lane);
+            drain_vm();
         }
-        stamp(M, p0 + 5);
-        phase_o(M, l, pos, wg, nwg, smem, p0 + 6);
-        stamp(M, p0 + 7);
-        grid_barrier(M.bar, M.err, epoch);
-        stamp(M, p0 + 8);
-        phase_gu(M, l, wg, nwg, smem, p0 + 9);
-        stamp(M, p0 + 10);
-        grid_barrier(M.bar, M.err, epoch);
-        stamp(M, p0 + 11);
-        phase_down(M, l, wg, nwg, smem, p0 + 12);
-        stamp(M, p0 + 13);
-        grid_barrier(M.bar, M.err, epoch);
-        stamp(M, p0 + 14);
+        if (kind == PH_ATTN && nch > kInlineComb) {           // the chunk merge as a phase of its own
+            drain_vm();
+            __syncthreads();
+            if (ctl) ctl_barrier(M->bar, M->err, epoch);
+            __syncthreads();
+            phase_comb(M, l, pos, wg, nwg);
+        }
+        __syncthreads();
+        stamp(M, sb + 1, 64);
+        if (kind == PH_LM) {
+            lm_epilogue(M, wg, nwg, S, wave, lane);
+            stamp(M, sb + 2);
+            __syncthreads();
+            stamp(M, sb + 3);
+            if (ctl) {
+                ctl_barrier(M->bar, M->err, epoch);
+                stamp(M, sb + 4);
+                if (wg == 0) {
+                    const Top2 a = wave_merge_cands(M->cand, nwg, lane);
+                    if (lane == 0) emit_token(M, a, pos, gen);
+                }
+            }
+            return;
+        }
+        int nl, nk;
+        phase_next(M, l, kind, nl, nk);
+        if (!ctl) {
+            phase_store(M, l, kind, wg, nwg, S, kw, lane);
+            drain_vm();
+            stamp(M, sb + 2, 64);
+            phase_prefetch(M, nl, nk, wg, nwg, kw, tl, lane);
+        } else {
+            drain_vm();
+            tl[0] = Tile{};
+            tl[1] = Tile{};
+        }
+        __syncthreads();
+        stamp(M, sb + 3);
+        if (ctl) {
+            ctl_barrier(M->bar, M->err, epoch);
+            stamp(M, sb + 4);
+            ctl_stage(M, nl, nk, pos, S, lane, true);
+        }
+        l = nl;
+        kind = nk;
     }
-    const int pl = 1 + M.NL * kProfSlotsPerLayer;
-    phase_lm(M, wg, nwg, smem, pl);
-    stamp(M, pl + 1);
-    grid_barrier(M.bar, M.err, epoch);
-    stamp(M, pl + 2);
-    const Top2 a = merge_cands(M.cand, nwg, Stage(smem).red);
-    if (wg == 0 && threadIdx.x == 0) emit_token(M, a, pos, gen);
 }
 
 // barrier cost: n grid barriers and nothing else
 __global__ __launch_bounds__(kPThreads) void k_barriers(uint32_t* bar, int32_t* err, int n) {
     unsigned epoch = 0;
-    for (int i = 0; i < n; i++) grid_barrier(bar, err, epoch);
+    for (int i = 0; i < n; i++) {
+        __syncthreads();
+        if (threadIdx.x < 64) ctl_barrier(bar, err, epoch);
+    }
+}
+
+// ------------------------------------------------------------------ per-phase kernels
+// The same phases as one launch each (same grid and roles; the residual stream goes
+// through hbuf, workgroup 0 writes it): the non-persistent reference path.
+constexpr int kPhaseLds = step_lds<128>();
+#define PHASE_PRELUDE                                                                        \
+    __shared__ __align__(16) uint8_t smem[kPhaseLds];                                        \
+    const Lds S(smem);                                                                       \
+    const int wg = blockIdx.x, nwg = gridDim.x, wave = threadIdx.x >> 6, lane = threadIdx.x & 63; \
+    const bool ctl = wave == 0;                                                              \
+    const int kw = wave - 1;                                                                 \
+    Tile tl[2];
+
+__global__ __launch_bounds__(kPThreads) void k_qkv(const DModel* Mp, int l, int pos) {
+    const MPtr M = (MPtr)Mp;
+    PHASE_PRELUDE
+    const PMat W = ldmat(&LY(M, l)->qkv);
+    if (ctl) ctl_stage(M, l, PH_QKV, pos, S, lane, false);
+    else prefetch(W, wg, nwg, kw, tl, lane);
+    __syncthreads();
+    wg_prologue(M, l, PH_QKV, pos, wg, S, wave, lane, false);
+    __syncthreads();
+    if (!ctl) gemv_tiles(W, wg, nwg, kw, tl, S.X, kXRec, S.P, lane);
+    __syncthreads();
+    if (!ctl) seg_store(W, wg, nwg, kw, S.P, qkv_part(M, l), lane);
+}
+template <int HD>
+__global__ __launch_bounds__(kPThreads) void k_attn(const DModel* Mp, int l, int pos) {
+    const MPtr M = (MPtr)Mp;
+    __shared__ __align__(16) uint8_t smem[step_lds<HD>()];
+    const Lds S(smem);
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    if (wave == 0) return;
+    attn_prefetch<HD>(M, l, pos, blockIdx.x, gridDim.x, S.U, wave - 1, lane);
+    attn_run<HD>(M, l, pos, blockIdx.x, gridDim.x, S.U, wave - 1, lane);
+}
+__global__ __launch_bounds__(kPThreads) void k_attn_comb(const DModel* Mp, int l, int pos) {
+    const MPtr M = (MPtr)Mp;
+    phase_comb(M, l, pos, blockIdx.x, gridDim.x);
+}
+__global__ __launch_bounds__(kPThreads) void k_o(const DModel* Mp, int l, int pos) {
+    const MPtr M = (MPtr)Mp;
+    PHASE_PRELUDE
+    const PMat W = ldmat(&LY(M, l)->o);
+    if (ctl) ctl_stage(M, l, PH_O, pos, S, lane, false);
+    else prefetch(W, wg, nwg, kw, tl, lane);
+    __syncthreads();
+    wg_prologue(M, l, PH_O, pos, wg, S, wave, lane, false);
+    __syncthreads();
+    if (!ctl) gemv_tiles(W, wg, nwg, kw, tl, S.X, kXRec, S.P, lane);
+    __syncthreads();
+    if (!ctl) seg_store(W, wg, nwg, kw, S.P, o_part(M, l), lane);
+}
+__global__ __launch_bounds__(kPThreads) void k_gu(const DModel* Mp, int l) {
+    const MPtr M = (MPtr)Mp;
+    PHASE_PRELUDE
+    const PMat W = ldmat(&LY(M, l)->gu);
+    if (ctl) ctl_stage(M, l, PH_GU, 0, S, lane, false);
+    else prefetch(W, wg, nwg, kw, tl, lane);
+    __syncthreads();
+    wg_prologue(M, l, PH_GU, 0, wg, S, wave, lane, false);
+    __syncthreads();
+    if (!ctl) gemv_tiles(W, wg, nwg, kw, tl, S.X, kXRec, S.P, lane);
+    __syncthreads();
+    if (!ctl) gu_store(W, wg, nwg, kw, S.P, act_rec(M, l), lane);
+}
+__global__ __launch_bounds__(kPThreads) void k_down(const DModel* Mp, int l) {
+    const MPtr M = (MPtr)Mp;
+    PHASE_PRELUDE
+    const PMat W = ldmat(&LY(M, l)->d);
+    if (ctl) ctl_stage(M, l, PH_DOWN, 0, S, lane, false);
+    else prefetch(W, wg, nwg, kw, tl, lane);
+    __syncthreads();
+    if (!ctl) gemv_tiles(W, wg, nwg, kw, tl, S.U, kActRec, S.P, lane);
+    __syncthreads();
+    if (!ctl) seg_store(W, wg, nwg, kw, S.P, d_part(M, l), lane);
+}
+__global__ __launch_bounds__(kPThreads) void k_lm(const DModel* Mp) {
+    const MPtr M = (MPtr)Mp;
+    PHASE_PRELUDE
+    if (ctl) ctl_stage(M, M->NL - 1, PH_LM, 0, S, lane, false);
+    else prefetch(ldmat(&M->lm), wg, nwg, kw, tl, lane);
+    __syncthreads();
+    wg_prologue(M, M->NL - 1, PH_LM, 0, wg, S, wave, lane, false);
+    __syncthreads();
+    if (!ctl) gemv_tiles(ldmat(&M->lm), wg, nwg, kw, tl, S.X, kXRec, S.P, lane);
+    __syncthreads();
+    lm_epilogue(M, wg, nwg, S, wave, lane);
+}
+__global__ __launch_bounds__(64) void k_argmax(const DModel* Mp, int ncand, int pos, int gen) {
+    const MPtr M = (MPtr)Mp;
+    const Top2 a = wave_merge_cands(M->cand, ncand, threadIdx.x);
+    if (threadIdx.x == 0) emit_token(M, a, pos, gen);
 }
 
 // ------------------------------------------------------------------ standalone kernels
@@ -838,19 +1103,31 @@ __global__ __launch_bounds__(kThreads) void k_quant(const float* x, int n, int8_
     }
 }
 
+// split-K partials part[s][row] of a packed matrix: one wave per (group, segment),
+// its chunks in order (chunk sums added left to right)
 __global__ __launch_bounds__(kThreads) void k_gemv(PMat W, const int8_t* xq, const float* xd, const int32_t* xs8, float* part) {
-    __shared__ __align__(16) uint8_t smem[4 * kMaxE + kMaxFF + kMaxFF / 4];
-    int8_t* xq8 = reinterpret_cast<int8_t*>(smem + 4 * kMaxE);
-    float2* xds = reinterpret_cast<float2*>(smem + 4 * kMaxE + kMaxFF);
-    const int n = W.nb * 32;
-    for (int i = threadIdx.x; i < n / 16; i += kThreads) reinterpret_cast<uint4*>(xq8)[i] = reinterpret_cast<const uint4*>(xq)[i];
-    for (int i = threadIdx.x; i < W.nb; i += kThreads) xds[i] = make_float2(xd[i], __int_as_float(xs8[i]));
+    __shared__ __align__(16) uint8_t X[(kMaxFF / 32) * kXRec];
+    for (int b = threadIdx.x; b < W.nb; b += kThreads) {
+        uint8_t* r = X + b * kXRec;
+        const uint4* src = reinterpret_cast<const uint4*>(xq + 32 * b);
+        reinterpret_cast<uint4*>(r)[0] = src[0];
+        reinterpret_cast<uint4*>(r)[1] = src[1];
+        *reinterpret_cast<float*>(r + 32) = xd[b];
+        *reinterpret_cast<int32_t*>(r + 36) = xs8[b];
+    }
     __syncthreads();
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int ntask = (W.rows / 64) * W.ks;
     for (int task = blockIdx.x * kWaves + wave; task < ntask; task += gridDim.x * kWaves) {
-        const int g = task / W.ks, s = task % W.ks;
-        part[(size_t)s * W.rows + g * 64 + lane] = row_segment(W, g, s, xq8, xds, lane);
+        const int g = task / W.ks, s = task % W.ks, c0 = seg_c0(W, s), c1 = seg_c0(W, s + 1);
+        float seg = 0.f;
+        for (int c = c0; c < c1; c++) {
+            Tile t;
+            tile_load(t, tile_ptr(W, g, c), W.cb, lane);
+            const float p = chunk_dot(t, W.cb, X, kXRec, c * W.cb);
+            seg = c == c0 ? p : __fadd_rn(seg, p);
+        }
+        part[(size_t)s * W.rows + g * 64 + lane] = seg;
     }
 }
 
@@ -866,7 +1143,7 @@ __global__ void k_seg_sum(const float* part, int rows, int ks, float* y) {
 __global__ __launch_bounds__(64) void k_isums(PMat W, const int8_t* xq, int32_t* isum) {
     const int g = blockIdx.x, b = blockIdx.y, lane = threadIdx.x;
     const int c = b / W.cb, k = b % W.cb;
-    const uint8_t* t = W.base + ((size_t)g * W.nc + c) * tile_bytes(W.cb);
+    const uint8_t* t = tile_ptr(W, g, c);
     const uint4 w = *reinterpret_cast<const uint4*>(t + k * 1024 + lane * 16);
     const int4* xp = reinterpret_cast<const int4*>(xq + 32 * b);
     isum[(size_t)(g * 64 + lane) * W.nb + b] = dot_q4(w, xp[0], xp[1]);
@@ -884,7 +1161,7 @@ __global__ __launch_bounds__(kThreads) void k_attn_standalone(const float* q, co
     uint8_t* lds = smem + wave * attn_wave_lds<HD>();
     uint4* kls = reinterpret_cast<uint4*>(lds);
     __half* vls = reinterpret_cast<__half*>(lds + 64 * HD * 2);
-    float* qs = reinterpret_cast<float*>(lds + 2 * 64 * HD * 2) + 3 * kMaxKs * HD;
+    float* qs = reinterpret_cast<float*>(lds + 2 * 64 * HD * 2) + 3 * kMaxKsQkv * HD;
     float* ps = qs + 2 * HD;
     for (int it = blockIdx.x * kAttnWaves + wave; it < items; it += gridDim.x * kAttnWaves) {
         const int h = it / nch, c = it % nch, kvh = h / G, t0 = c * kAttnChunk, n = min(kAttnChunk, L - t0);
@@ -906,7 +1183,6 @@ __global__ __launch_bounds__(kThreads) void k_comb_standalone(const float* recs,
         out[it] = combine_one(recs + (size_t)(it / hd) * nch * (hd + 32), hd + 32, hd, it % hd, nch);
 }
 
-typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 __global__ __launch_bounds__(kThreads) void k_stream(const u32x4* __restrict__ p, size_t n4, uint32_t* sink) {
     const size_t nth = (size_t)gridDim.x * blockDim.x;
     size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -923,14 +1199,11 @@ __global__ __launch_bounds__(kThreads) void k_stream(const u32x4* __restrict__ p
     if (acc == 0x9E3779B9u) sink[threadIdx.x] = acc;   // never true in practice; keeps the loads
 }
 
-// ------------------------------------------------------------------ host launchers
+// ------------------------------------------------------------------ host side
 #define LAUNCH(kern, grid, block, stream, ...) hipLaunchKernelGGL(kern, dim3(grid), dim3(block), 0, stream, __VA_ARGS__)
 
 bool kernels_support(int G, int HD) { return (HD == 64 || HD == 128) && G >= 1; }
-int kernels_max_ks() { return kMaxKs; }
 int attn_record_floats(int HD) { return HD + 32; }
-
-static int waves_grid(int tasks, int cap) { return std::max(1, std::min(cap, (tasks + kWaves - 1) / kWaves)); }
 
 template <class F>
 static void with_hd(int HD, F f) {
@@ -938,36 +1211,56 @@ static void with_hd(int HD, F f) {
     else f(std::integral_constant<int, 128>());
 }
 
-void launch_phase(const DModel& M, const PhaseGrid& pg, int phase, int l, int pos, int gen, hipStream_t s) {
+// Reduction plan: chunk size by row length (8 blocks, 4 when the block count is not
+// a multiple of 8); one K segment per row except the down matrix, whose rows are
+// split so a workgroup's segment has at most 5 chunks, within what the control
+// wave stages (the norm weights, the h vector and ks partials in kCtlBytes). The
+// plan depends only on the shape, so the float order is device-independent.
+bool kernels_plan(int E, int FF, int cb[5], int ks[5]) {
+    const int nbE = E / 32, nbF = FF / 32;
+    const int cbE = nbE % 8 == 0 ? 8 : 4, cbF = nbF % 8 == 0 ? 8 : 4;
+    cb[0] = cb[1] = cb[2] = cb[4] = cbE;
+    cb[3] = cbF;
+    ks[0] = ks[1] = ks[2] = ks[4] = 1;
+    const int ncF = nbF / cbF, cap = std::min(kMaxKsRes, kCtlBytes / (4 * E) - 2);
+    if (cap < 1) return false;
+    ks[3] = std::max(1, std::min(std::min(cap, ncF), (ncF + 4) / 5));
+    return (FF / 32) * kActRec <= kCtlBytes;
+}
+
+// chunk sums a workgroup stages for one matrix (rows x nb blocks, plan cb/ks) over nwg workgroups
+int kernels_tiles_per_wg(int rows, int nb, int cb, int ks, int nwg) {
+    const int nseg = (rows / 64) * ks, nc = nb / cb;
+    return ((nseg + nwg - 1) / nwg) * ((nc + ks - 1) / ks);
+}
+int kernels_max_tiles_per_wg() { return kPartTiles; }
+
+void launch_phase(const DModel& M, const DModel* dM, int nwg, int phase, int l, int pos, int gen, hipStream_t s) {
     const int nch = (pos + 1 + kAttnChunk - 1) / kAttnChunk;
     switch (phase) {
-        case 0: LAUNCH(k_qkv, pg.qkv, kThreads, s, M, l, pos); break;
-        case 1: {
-            const int ag = std::max(1, std::min(1 << 16, (M.NH * nch + kAttnWaves - 1) / kAttnWaves));
-            with_hd(M.HD, [&](auto hd) { LAUNCH((k_attn<decltype(hd)::value>), ag, kThreads, s, M, l, pos); });
-            break;
-        }
-        case 2: if (nch > kInlineComb) LAUNCH(k_attn_comb, pg.comb, kThreads, s, M, l, pos); break;
-        case 3: LAUNCH(k_o, pg.o, kThreads, s, M, l, pos); break;
-        case 4: LAUNCH(k_gu, pg.gu, kThreads, s, M, l); break;
-        case 5: LAUNCH(k_down, pg.down, kThreads, s, M, l); break;
-        case 6: LAUNCH(k_lm, pg.lm, kThreads, s, M); break;
-        default: LAUNCH(k_argmax, 1, kThreads, s, M, pg.lm, pos, gen); break;
+        case 0: LAUNCH(k_qkv, nwg, kPThreads, s, dM, l, pos); break;
+        case 1: with_hd(M.HD, [&](auto hd) { LAUNCH((k_attn<decltype(hd)::value>), nwg, kPThreads, s, dM, l, pos); }); break;
+        case 2: if (nch > kInlineComb) LAUNCH(k_attn_comb, nwg, kPThreads, s, dM, l, pos); break;
+        case 3: LAUNCH(k_o, nwg, kPThreads, s, dM, l, pos); break;
+        case 4: LAUNCH(k_gu, nwg, kPThreads, s, dM, l); break;
+        case 5: LAUNCH(k_down, nwg, kPThreads, s, dM, l); break;
+        case 6: LAUNCH(k_lm, nwg, kPThreads, s, dM); break;
+        default: LAUNCH(k_argmax, 1, 64, s, dM, nwg, pos, gen); break;
     }
 }
 
-void launch_step_phases(const DModel& M, const PhaseGrid& pg, int pos, int gen, hipStream_t s) {
+void launch_step_phases(const DModel& M, const DModel* dM, int nwg, int pos, int gen, hipStream_t s) {
     for (int l = 0; l < M.NL; l++)
-        for (int ph = 0; ph < 6; ph++) launch_phase(M, pg, ph, l, pos, gen, s);
-    launch_phase(M, pg, 6, 0, pos, gen, s);
-    launch_phase(M, pg, 7, 0, pos, gen, s);
+        for (int ph = 0; ph < 6; ph++) launch_phase(M, dM, nwg, ph, l, pos, gen, s);
+    launch_phase(M, dM, nwg, 6, 0, pos, gen, s);
+    launch_phase(M, dM, nwg, 7, 0, pos, gen, s);
 }
 
-hipError_t launch_step_persistent(const DModel& M, int nwg, int pos, int gen, hipStream_t s) {
+hipError_t launch_step_persistent(const DModel& M, const DModel* dM, int nwg, int pos, int gen, hipStream_t s) {
     hipError_t err = hipMemsetAsync(M.bar, 0, sizeof(uint32_t) * kBarWords, s);
     if (err != hipSuccess) return err;
     with_hd(M.HD, [&](auto hd) {
-        DModel m = M;
+        const DModel* m = dM;
         void* args[] = {&m, &pos, &gen};
         err = hipLaunchCooperativeKernel(reinterpret_cast<const void*>(&k_step<decltype(hd)::value>), dim3(nwg),
                                          dim3(kPThreads), args, 0, s);
@@ -994,26 +1287,14 @@ int persistent_max_grid(int G, int HD) {
     return per_cu;
 }
 
-PhaseGrid plan_phase_grid(const DModel& M, const DLayer& L0, int n_cu) {
-    PhaseGrid g;
-    const int cap = 4 * n_cu;
-    g.qkv = waves_grid((L0.qkv.rows / 64) * L0.qkv.ks, cap);
-    g.fin = 0;
-    g.comb = std::max(1, (M.E + kThreads - 1) / kThreads);
-    g.o = waves_grid((L0.o.rows / 64) * L0.o.ks, cap);
-    g.gu = std::max(1, std::min(cap, (L0.gu.rows / 64) / std::max(1, kWaves / L0.gu.ks)));
-    g.act = 0;
-    g.down = waves_grid((L0.d.rows / 64) * L0.d.ks, cap);
-    g.lm = waves_grid(M.lm.rows / 64, cap);
-    return g;
-}
-
 void launch_quant(const float* x, int n, int8_t* xq, float* xd, int32_t* xs8, hipStream_t s) {
     LAUNCH(k_quant, (n + kThreads - 1) / kThreads, kThreads, s, x, n, xq, xd, xs8);
 }
 void launch_gemv(const PMat& W, const int8_t* xq, const float* xd, const int32_t* xs8, float* part, float* y,
                  int n_cu, hipStream_t s) {
-    LAUNCH(k_gemv, waves_grid((W.rows / 64) * W.ks, 4 * n_cu), kThreads, s, W, xq, xd, xs8, part);
+    const int tasks = (W.rows / 64) * W.ks;
+    const int grid = std::max(1, std::min(4 * n_cu, (tasks + kWaves - 1) / kWaves));
+    LAUNCH(k_gemv, grid, kThreads, s, W, xq, xd, xs8, part);
     if (y) LAUNCH(k_seg_sum, (W.rows + 255) / 256, 256, s, part, W.rows, W.ks, y);
 }
 void launch_isums(const PMat& W, const int8_t* xq, int32_t* isum, hipStream_t s) {

@@ -4,28 +4,33 @@
 
 namespace mi {
 
-struct PhaseGrid { int qkv, fin, comb, o, gu, act, down, lm; };
-
+// Kernels read the model description through a pointer to a device copy (dM) of the
+// host DModel M: a kernel-argument struct would be treated as invariant and kept in
+// scalar registers for the whole persistent step, which runs out of them.
 bool kernels_support(int G, int HD);
-PhaseGrid plan_phase_grid(const DModel& M, const DLayer& L0, int n_cu);
-// one decode step at position pos as one launch per phase; gen != 0 stores the
-// prediction as the token of position pos + 1
-void launch_step_phases(const DModel& M, const PhaseGrid& pg, int pos, int gen, hipStream_t s);
+// reduction plan (blocks per chunk, K segments) of qkv, o, gate/up, down, lm_head;
+// false when the shape does not fit the kernels' LDS staging
+bool kernels_plan(int E, int FF, int cb[5], int ks[5]);
+// chunk sums one workgroup stages for a matrix under the plan, and the limit
+int kernels_tiles_per_wg(int rows, int nb, int cb, int ks, int nwg);
+int kernels_max_tiles_per_wg();
+// one decode step at position pos as one launch per phase (nwg workgroups each);
+// gen != 0 stores the prediction as the token of position pos + 1
+void launch_step_phases(const DModel& M, const DModel* dM, int nwg, int pos, int gen, hipStream_t s);
 // the same step as one cooperative launch of nwg workgroups (zeroes the barrier counter first)
-hipError_t launch_step_persistent(const DModel& M, int nwg, int pos, int gen, hipStream_t s);
+hipError_t launch_step_persistent(const DModel& M, const DModel* dM, int nwg, int pos, int gen, hipStream_t s);
 // co-resident workgroups per CU of the persistent kernel (0: cannot launch)
 int persistent_max_grid(int G, int HD);
 hipError_t launch_barriers(uint32_t* bar, int32_t* err, int nwg, int n, hipStream_t s);
 int barrier_words();        // uint32 words the grid barrier uses
-int kernels_max_ks();       // largest K-segment count the phases stage in LDS
 int attn_record_floats(int HD);   // floats per attention chunk record
-constexpr int kProfSlotsPerLayer = 15;
-// profile slots of one workgroup: start, 15 per layer, lm prologue, lm end, last barrier
-constexpr int prof_slots(int n_layer) { return n_layer * kProfSlotsPerLayer + 4; }
+constexpr int kProfSlotsPerLayer = 25;
+// profile slots of one workgroup: start, 5 per phase (5 phases per layer, then lm_head)
+constexpr int prof_slots(int n_layer) { return n_layer * kProfSlotsPerLayer + 6; }
 
 // one phase kernel of the step at pos: 0 qkv, 1 attention, 2 chunk merge (only
 // launched past kInlineComb chunks), 3 o, 4 gate/up+act, 5 down, 6 lm_head, 7 argmax
-void launch_phase(const DModel& M, const PhaseGrid& pg, int phase, int l, int pos, int gen, hipStream_t s);
+void launch_phase(const DModel& M, const DModel* dM, int nwg, int phase, int l, int pos, int gen, hipStream_t s);
 
 void launch_quant(const float* x, int n, int8_t* xq, float* xd, int32_t* xs8, hipStream_t s);
 void launch_gemv(const PMat& W, const int8_t* xq, const float* xd, const int32_t* xs8, float* part, float* y,

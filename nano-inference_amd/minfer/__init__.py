@@ -201,34 +201,37 @@ class Engine:
     PROFILE_PHASES = ["qkv", "attn", "o", "gate_up", "down"]
 
     def profile_step(self):
-        """Stamps of one persistent step: an array [workgroups][n_layer*15 + 4] of
+        """Stamps of one persistent step: an array [workgroups][n_layer*25 + 6] of
         microseconds since the earliest start (slot layout in mi_profile_step)."""
         import numpy as np
-        nslot = self.info.n_layer * 15 + 4
+        nslot = self.info.n_layer * 25 + 6
         n = nslot * self.info.n_cu
         buf = (C.c_double * n)()
         _check(lib().mi_profile_step(self._h, buf, n), self._h)
         return np.frombuffer(buf, dtype=np.float64).reshape(self.info.n_cu, nslot).copy()
 
     def profile_summary(self):
-        """Per phase, summed over layers (microseconds): the prologue, work and
-        barrier-wait time averaged over workgroups and of the slowest workgroup,
-        plus the barrier latency proper (earliest exit minus latest arrival)."""
+        """Per phase, summed over layers (microseconds, (mean, max) over workgroups):
+        prep = barrier exit -> prologue end, tiles = -> first worker's tiles done,
+        store = -> its stores drained, sync = -> phase end, wait = -> barrier exit;
+        barrier = earliest exit minus latest phase end."""
         import numpy as np
         t = self.profile_step()
         L = self.info.n_layer
-        d = np.diff(t, axis=1)                        # d[:, s-1] = slot s - slot s-1
         out = {}
+        parts = ("prep", "tiles", "store", "sync", "wait")
         for k, ph in enumerate(self.PROFILE_PHASES):
-            for j, part in enumerate(("prep", "work", "wait")):
-                cols = [l * 15 + 3 * k + j for l in range(L)]
-                v = d[:, cols].sum(axis=1)
-                out[ph + "_" + part] = (round(float(v.mean()), 1), round(float(v.max()), 1))
-            ends = [1 + l * 15 + 3 * k + 1 for l in range(L)]
+            for j, part in enumerate(parts):
+                acc = np.zeros(t.shape[0])
+                for l in range(L):
+                    s = 1 + l * 25 + 5 * k + j
+                    acc += t[:, s] - t[:, s - 1]
+                out[ph + "_" + part] = (round(float(acc.mean()), 1), round(float(acc.max()), 1))
+            ends = [1 + l * 25 + 5 * k + 3 for l in range(L)]
             out[ph + "_barrier"] = round(float(sum(t[:, e + 1].min() - t[:, e].max() for e in ends)), 1)
-        s0 = 1 + L * 15
-        for j, part in enumerate(("lm_prep", "lm_work", "lm_wait")):
-            v = d[:, s0 - 1 + j]
+        s0 = 1 + L * 25
+        for j, part in enumerate(("lm_prep", "lm_tiles", "lm_cand", "lm_sync", "lm_wait")):
+            v = t[:, s0 + j] - t[:, s0 + j - 1]
             out[part] = (round(float(v.mean()), 1), round(float(v.max()), 1))
         out["total"] = round(float(t[:, -1].max()), 1)
         return out

@@ -4,7 +4,7 @@
  * cpu_infer as gnu++17 -O3 -march=native), so GCC contracts the same
  * multiply-adds it contracts in cpu_infer. Each function keeps the expression
  * shape of the line it restates. Parity: the greedy token streams of the
- * reference cpu_infer compiled from /root/reference (tests/golden/*.json,
+ * reference cpu_infer compiled from /root/reference (tests/golden/cpu_infer_*.json fixtures,
  * tests/test_oracle_golden.py).
  */
 #include "internal.h"

@@ -69,10 +69,11 @@ void orc_quant_q8(const float* x, int n, int8_t* xq, float* xd, int32_t* xs8);
 /* q4_0 block (18 B: fp16 d + 16 B) x 32 int8: sum_j n_j*x_j with n_j in 0..15 */
 int32_t orc_q4_block_isum(const uint8_t* blk, const int8_t* x32);
 /* one row of q4_0 blocks (row-major GGUF layout) in the canonical accumulation order:
- * nb blocks, chunks of cb blocks, ks contiguous segments of chunks summed left to right */
+ * nb blocks in chunks of cb (each an fma chain from 0), ks contiguous segments of
+ * chunks (chunk sums added left to right), segments added left to right */
 float orc_q4_row_dot(const uint8_t* row, int nb, int cb, int ks,
                      const int8_t* xq, const float* xd, const int32_t* xs8);
-/* canonical RMSNorm (64 lane partials + xor butterfly), n % 64 == 0 */
+/* canonical RMSNorm (lane l of 64 sums x[256j+4l+i]^2 in order, xor butterfly), n % 64 == 0 */
 void orc_rmsnorm_canon(const float* x, const float* w, int n, float eps, float* out);
 /* sum of 64 values by the xor butterfly (offsets 32,16,8,4,2,1), value of lane 0 */
 float orc_butterfly64(const float* v);

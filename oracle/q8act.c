@@ -9,11 +9,13 @@
  *   q4 x int8 block   cuda_infer.cu:108-121, mega.cu:157-165 (nibble n in 0..15
  *                     times x, minus 8*sum(x))
  *   block accumulate  mega.cu:153-155: acc = fma(dw*dx, float(isum - 8*sum x), acc)
- *   row order         fixed here: cb-block chunks, ks contiguous segments of chunks,
- *                     each summed in block order, segments added left to right
- *                     (the reference's mega sums splits in order, :665-673)
+ *   row order         fixed here: cb-block chunks, each an fma chain from 0; ks
+ *                     contiguous segments of chunks, chunk sums added left to
+ *                     right; segments added left to right (the reference's mega
+ *                     sums splits in order, :665-673)
  *   RMSNorm           cpu_infer.cpp:40-46 formula; the sum of squares is a fixed
- *                     64-lane fma partial + xor butterfly instead of a double loop
+ *                     64-lane fma partial (lane l: elements 256j+4l+i) + xor
+ *                     butterfly instead of a double loop
  *   RoPE              cpu_infer.cpp:49-61 pairs (i, i+hd/2), cos/sin from the same
  *                     float powf/cosf/sinf values; products rounded separately
  *   attention         cpu_infer.cpp:121-140 softmax(q.k/sqrt(hd)) v, computed as
@@ -79,23 +81,29 @@ int32_t orc_q4_block_isum(const uint8_t* blk, const int8_t* x) {
     return s;
 }
 
-/* mega.cu:153-155 accumulate, mega.cu:178-196 + 665-673 order (segments in order).
+/* mega.cu:153-155 accumulate; the order is fixed here (the reference's mega adds its
+ * splits in order, :665-673): every chunk of cb blocks is an fma chain from 0, the
+ * chunks of a segment are added left to right, then the segments left to right.
  * Parity: closed form (exact int) + float tolerance vs fp64 dot of dequantized rows. */
 float orc_q4_row_dot(const uint8_t* row, int nb, int cb, int ks,
                      const int8_t* xq, const float* xd, const int32_t* xs8) {
     const int nc = nb / cb;
     float tot = 0.f;
     for (int s = 0; s < ks; s++) {
-        const int b0 = (s * nc / ks) * cb, b1 = ((s + 1) * nc / ks) * cb;
-        float acc = 0.f;
-        for (int b = b0; b < b1; b++) {
-            const uint8_t* blk = row + (size_t)b * 18;
-            uint16_t hd; memcpy(&hd, blk, 2);
-            const float dw = orc_f16_to_f32(hd);
-            const int32_t isum = orc_q4_block_isum(blk, xq + 32 * b);
-            acc = fmaf(dw * xd[b], (float)(isum - xs8[b]), acc);
+        const int c0 = s * nc / ks, c1 = (s + 1) * nc / ks;
+        float seg = 0.f;
+        for (int c = c0; c < c1; c++) {
+            float acc = 0.f;
+            for (int b = c * cb; b < (c + 1) * cb; b++) {
+                const uint8_t* blk = row + (size_t)b * 18;
+                uint16_t hd; memcpy(&hd, blk, 2);
+                const float dw = orc_f16_to_f32(hd);
+                const int32_t isum = orc_q4_block_isum(blk, xq + 32 * b);
+                acc = fmaf(dw * xd[b], (float)(isum - xs8[b]), acc);
+            }
+            seg = c == c0 ? acc : seg + acc;
         }
-        tot = s == 0 ? acc : tot + acc;
+        tot = s == 0 ? seg : tot + seg;
     }
     return tot;
 }
@@ -110,15 +118,20 @@ float orc_butterfly64(const float* v) {
     return a[0];
 }
 
-/* cpu_infer.cpp:40-46 with the sum of squares as 64 lane partials (lane j takes
- * elements j, j+64, ...) folded by the xor butterfly. Parity: tolerance vs the
+/* cpu_infer.cpp:40-46 with the sum of squares as 64 lane partials folded by the xor
+ * butterfly: lane l takes the elements 256j + 4l + i (i = 0..3) for j = 0, 1, ... in
+ * that order (one float4 per lane per 256 elements). Parity: tolerance vs the
  * double-accumulated cpu_infer form (tests/test_oracle_numerics.py). */
 void orc_rmsnorm_canon(const float* x, const float* w, int n, float eps, float* out) {
     float p[64];
-    for (int j = 0; j < 64; j++) {
+    for (int l = 0; l < 64; l++) {
         float a = 0.f;
-        for (int k = j; k < n; k += 64) a = fmaf(x[k], x[k], a);
-        p[j] = a;
+        for (int j = 0; 256 * j < n; j++)
+            for (int i = 0; i < 4; i++) {
+                const int e = 256 * j + 4 * l + i;
+                if (e < n) a = fmaf(x[e], x[e], a);
+            }
+        p[l] = a;
     }
     const float ss = orc_butterfly64(p);
     const float mean = ss / (float)n;
