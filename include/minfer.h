@@ -83,7 +83,10 @@ int mi_prefill(mi_engine* e, const int32_t* ids, int32_t n, int32_t* first, floa
  * at positions pos..pos+T-1 (pos <= current length: a smaller pos rewinds, which is
  * how rejected drafts are dropped), writes their K/V, returns per token the argmax
  * (lowest index on ties), the margin best - second, and optionally the logits
- * [T][n_vocab] (nullable; the reference never exposes logits). T = 1 for now. */
+ * [T][n_vocab] (nullable; the reference never exposes logits). 1 <= T <= 8 (TMAX,
+ * mega.cu:50). T > 1 is the verify step of speculative decoding: one pass over the
+ * weights with int8 MFMA tiles; every token's logits are bit-identical to running
+ * the tokens one at a time with T = 1. */
 int mi_step(mi_engine* e, const int32_t* toks, int32_t T, int32_t pos,
             int32_t* argmax, float* margin, float* logits);
 

@@ -34,6 +34,7 @@ constexpr int kInlineComb = 4;     // up to this many chunks the O phase merges 
 constexpr int kActRec = 128;       // bytes per act block record (32 int8, scale, 8*sum, padding)
 constexpr int kMaxE = 2048;        // largest hidden size the LDS staging holds
 constexpr int kMaxFF = 11264;      // largest FFN width the LDS staging holds
+constexpr int kMaxT = 8;           // tokens of one multi-token step (mega.cu:50 TMAX)
 
 struct PMat {                      // one q4_0 matrix in the tile layout
     const uint8_t* base;
@@ -77,6 +78,17 @@ struct DModel {
     int32_t* err;                  // set when a grid barrier times out
     int32_t* out_tok;              // [maxseq] prediction made at each position
     float* out_margin;             // [maxseq]
+    // multi-token steps (T <= kMaxT tokens at positions pos..pos+T-1, one launch per
+    // phase): per-token copies of the exchange buffers, token index after the segment
+    float* hT;                     // [2*NL+1][kMaxT][E]
+    float* qkvT;                   // [NL][ks_qkv][kMaxT][QKV]
+    float* attT;                   // [NL][kMaxT][NH][maxch][arec]
+    float* att_outT;               // [NL][kMaxT][E]
+    float* oT;                     // [NL][ks_o][kMaxT][E]
+    uint8_t* actT;                 // [NL][kMaxT][FF/32][kActRec]
+    float* dT;                     // [NL][ks_d][kMaxT][E]
+    float* candT;                  // [workgroups][kMaxT][4]
+    float* logitsT;                // [kMaxT][V] (written when non-null)
 };
 
 inline __host__ __device__ size_t tile_bytes(int cb) { return (size_t)cb * 1152; }

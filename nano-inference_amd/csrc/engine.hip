@@ -270,7 +270,8 @@ static int load_impl(mi_engine* e, const char* path) {
     {
         const int rows[5] = {e->QKV, e->E, 2 * e->FF, e->E, e->V}, nbs[5] = {nbE, nbE, nbE, nbF, nbE};
         for (int i = 0; i < 5; i++)
-            if (kernels_tiles_per_wg(rows[i], nbs[i], e->cb[i], e->ks[i], e->n_cu) > kernels_max_tiles_per_wg())
+            if (kernels_tiles_per_wg(rows[i], nbs[i], e->cb[i], e->ks[i], e->n_cu) > kernels_max_tiles_per_wg() ||
+                (nbs[i] / e->cb[i] + e->ks[i] - 1) / e->ks[i] > kernels_max_chunks_multi())
                 return set_err(e, MI_ERR_SHAPE, "matrix %d needs %d tiles per workgroup on %d CUs (limit %d)", i,
                                kernels_tiles_per_wg(rows[i], nbs[i], e->cb[i], e->ks[i], e->n_cu), e->n_cu,
                                kernels_max_tiles_per_wg());
@@ -406,10 +407,23 @@ static int load_impl(mi_engine* e, const char* path) {
         (rc = alloc_buf(e, &M.out_tok, (size_t)e->maxseq)) ||
         (rc = alloc_buf(e, &M.out_margin, (size_t)e->maxseq)))
         return rc;
+    // multi-token step buffers (mi_step with T > 1)
+    const size_t TM = kMaxT;
+    if ((rc = alloc_buf(e, &M.hT, (size_t)(2 * e->NL + 1) * TM * e->E)) ||
+        (rc = alloc_buf(e, &M.qkvT, NL * e->ks[0] * TM * e->QKV)) ||
+        (rc = alloc_buf(e, &M.attT, NL * TM * e->NH * e->maxch * M.arec)) ||
+        (rc = alloc_buf(e, &M.att_outT, NL * TM * e->E)) ||
+        (rc = alloc_buf(e, &M.oT, NL * e->ks[1] * TM * e->E)) ||
+        (rc = alloc_buf(e, &M.actT, NL * TM * (e->FF / 32) * kActRec)) ||
+        (rc = alloc_buf(e, &M.dT, NL * e->ks[3] * TM * e->E)) ||
+        (rc = alloc_buf(e, &M.candT, (size_t)e->n_cu * TM * 4)))
+        return rc;
     M.logits = nullptr;
+    M.logitsT = nullptr;
     M.prof = nullptr;
     e->M_logits = M;
     if ((rc = alloc_buf(e, &e->M_logits.logits, (size_t)e->V))) return rc;
+    if ((rc = alloc_buf(e, &e->M_logits.logitsT, TM * e->V))) return rc;
     if ((rc = alloc_buf(e, &e->dM, 3))) return rc;
     HIPCHK(e, hipMemcpy(e->dM, &e->M, sizeof(DModel), hipMemcpyHostToDevice));
     HIPCHK(e, hipMemcpy(e->dM + 1, &e->M_logits, sizeof(DModel), hipMemcpyHostToDevice));
@@ -476,22 +490,38 @@ extern "C" {
 
 int mi_step(mi_engine* e, const int32_t* toks, int32_t T, int32_t pos, int32_t* argmax, float* margin, float* logits) {
     if (!e || !toks) return MI_ERR_ARG;
-    if (T != 1) return set_err(e, MI_ERR_ARG, "mi_step: T=%d; only single-token steps are built", T);
+    if (T < 1 || T > kernels_max_tokens())
+        return set_err(e, MI_ERR_ARG, "mi_step: T=%d outside 1..%d", T, kernels_max_tokens());
     if (pos < 0 || pos > e->cur_len || pos + T > e->maxseq) return set_err(e, MI_ERR_ARG, "mi_step: position %d out of range (length %d, capacity %d)", pos, e->cur_len, e->maxseq);
     for (int t = 0; t < T; t++)
         if (toks[t] < 0 || toks[t] >= e->V) return set_err(e, MI_ERR_ARG, "mi_step: token %d out of range", toks[t]);
     HIPCHK(e, hipMemcpyAsync(e->M.tokbuf + pos, toks, sizeof(int32_t) * T, hipMemcpyHostToDevice, e->stream));
-    int rc = run_step(e, pos, 1, logits != nullptr);
+    int rc;
+    if (T == 1) {
+        rc = run_step(e, pos, 1, logits != nullptr);
+    } else {
+        const DModel& M = logits ? e->M_logits : e->M;
+        launch_step_multi(M, e->dM + (logits ? 1 : 0), e->n_cu, pos, T, e->stream);
+        rc = MI_OK;
+        HIPCHK(e, hipGetLastError());
+    }
     if (rc) return rc;
-    int32_t tok = 0;
-    float mg = 0.f;
-    HIPCHK(e, hipMemcpyAsync(&tok, e->M.out_tok + pos, 4, hipMemcpyDeviceToHost, e->stream));
-    HIPCHK(e, hipMemcpyAsync(&mg, e->M.out_margin + pos, 4, hipMemcpyDeviceToHost, e->stream));
-    if (logits) HIPCHK(e, hipMemcpyAsync(logits, e->M_logits.logits, sizeof(float) * e->V, hipMemcpyDeviceToHost, e->stream));
+    std::vector<int32_t> tok(T);
+    std::vector<float> mg(T);
+    HIPCHK(e, hipMemcpyAsync(tok.data(), e->M.out_tok + pos, 4 * T, hipMemcpyDeviceToHost, e->stream));
+    HIPCHK(e, hipMemcpyAsync(mg.data(), e->M.out_margin + pos, 4 * T, hipMemcpyDeviceToHost, e->stream));
+    if (logits)
+        HIPCHK(e, hipMemcpyAsync(logits, T == 1 ? e->M_logits.logits : e->M_logits.logitsT, sizeof(float) * e->V * T,
+                                 hipMemcpyDeviceToHost, e->stream));
     HIPCHK(e, hipStreamSynchronize(e->stream));
-    if ((rc = check_barrier(e))) return rc;
-    if (argmax) argmax[0] = tok;
-    if (margin) margin[0] = mg;
+    if (T == 1 && (rc = check_barrier(e))) return rc;
+    for (int t = 0; t < T; t++) {
+        if (argmax) argmax[t] = tok[t];
+        if (margin) margin[t] = mg[t];
+    }
+    // the next position's token is the last prediction (mi_generate continues from it)
+    HIPCHK(e, hipMemcpyAsync(e->M.tokbuf + pos + T, &tok[T - 1], 4, hipMemcpyHostToDevice, e->stream));
+    HIPCHK(e, hipStreamSynchronize(e->stream));
     e->cur_len = pos + T;
     e->next_ready = true;
     return MI_OK;

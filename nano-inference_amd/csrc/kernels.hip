@@ -408,7 +408,7 @@ __device__ __forceinline__ void st4(float* p, int i, float4 v) { *reinterpret_ca
 
 // quantise slice j (already scaled) into block records X; a 32-element block is
 // 8 lanes x 4 elements
-__device__ __forceinline__ void quant_slice(float4 y, bool own, int e0, uint8_t* X, int lane) {
+__device__ __forceinline__ void quant_slice(float4 y, bool own, int e0, uint8_t* X, int lane, int rs = kXRec) {
     if (!own) y = make_float4(0.f, 0.f, 0.f, 0.f);
     float a = fmaxf(fmaxf(fabsf(y.x), fabsf(y.y)), fmaxf(fabsf(y.z), fabsf(y.w)));
     a = fmaxf(a, __shfl_xor(a, 1));
@@ -422,7 +422,7 @@ __device__ __forceinline__ void quant_slice(float4 y, bool own, int e0, uint8_t*
     s += __shfl_xor(s, 2);
     s += __shfl_xor(s, 4);
     if (own) {
-        uint8_t* rec = X + (e0 >> 5) * kXRec;
+        uint8_t* rec = X + (e0 >> 5) * rs;
         *reinterpret_cast<uint32_t*>(rec + (e0 & 31)) =
             (uint32_t)(q0 & 0xFF) | ((uint32_t)(q1 & 0xFF) << 8) | ((uint32_t)(q2 & 0xFF) << 16) | ((uint32_t)q3 << 24);
         if ((lane & 7) == 0) {
@@ -630,7 +630,7 @@ __device__ __forceinline__ void emit_token(MPtr M, const Top2& a, int pos, int g
 // ------------------------------------------------------------------ attention
 // per-wave LDS: K [HD/8][64] 16-byte vectors (vector j of position t at j*64 + t, so
 // a lane-per-position read is conflict-free) | V [64][HD] | q partials [2][HD] |
-// k, v partials [2][2][HD] | q [HD] | k(pos) [HD] | p [64]
+// k, v partials [2][2][HD] | q [HD] (+ spare)
 
 // DMA the chunk's K rows (swizzled) and V rows; rows past n repeat row n-1
 template <int HD>
@@ -649,29 +649,23 @@ __device__ __forceinline__ void attn_issue_kv(const __half* krows, const __half*
     }
 }
 
-// scores (lane = position; lane `cur` takes its K row from kcur), chunk softmax, p.v
-// (lane = dims). The chunk max and sum end on every lane, the lane's outputs in acc.
+// scores (lane = position), chunk softmax, p.v (lane = dims; p of position t
+// broadcast from lane t by readlane). The chunk max and sum end on every lane, the
+// lane's outputs in acc.
 template <int HD>
-__device__ __forceinline__ void attn_core(const uint4* kls, const float* qs, const float* kcur, int cur, const __half* vls,
-                                          float* ps, int n, float scale, int lane, float& m, float& lsum,
-                                          float (&acc)[HD / 64]) {
+__device__ __forceinline__ void attn_core(const uint4* kls, const float* qs, const __half* vls, int n, float scale, int lane,
+                                          float& m, float& lsum, float (&acc)[HD / 64]) {
     constexpr int NV = HD / 8, DPL = HD / 64;
     float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
-    const bool mine = lane == cur;
 #pragma unroll 4
     for (int j = 0; j < NV; j++) {
         const uint4 w = kls[j * 64 + lane];
-        float kf[8] = {h2f_lo(w.x), h2f_hi(w.x), h2f_lo(w.y), h2f_hi(w.y), h2f_lo(w.z), h2f_hi(w.z), h2f_lo(w.w), h2f_hi(w.w)};
-        if (mine) {
-#pragma unroll
-            for (int e = 0; e < 8; e++) kf[e] = kcur[8 * j + e];
-        }
         const float4 q0 = *reinterpret_cast<const float4*>(qs + 8 * j);
         const float4 q1 = *reinterpret_cast<const float4*>(qs + 8 * j + 4);
-        a0 = __fmaf_rn(q0.x, kf[0], a0); a1 = __fmaf_rn(q0.y, kf[1], a1);
-        a2 = __fmaf_rn(q0.z, kf[2], a2); a3 = __fmaf_rn(q0.w, kf[3], a3);
-        a0 = __fmaf_rn(q1.x, kf[4], a0); a1 = __fmaf_rn(q1.y, kf[5], a1);
-        a2 = __fmaf_rn(q1.z, kf[6], a2); a3 = __fmaf_rn(q1.w, kf[7], a3);
+        a0 = __fmaf_rn(q0.x, h2f_lo(w.x), a0); a1 = __fmaf_rn(q0.y, h2f_hi(w.x), a1);
+        a2 = __fmaf_rn(q0.z, h2f_lo(w.y), a2); a3 = __fmaf_rn(q0.w, h2f_hi(w.y), a3);
+        a0 = __fmaf_rn(q1.x, h2f_lo(w.z), a0); a1 = __fmaf_rn(q1.y, h2f_hi(w.z), a1);
+        a2 = __fmaf_rn(q1.z, h2f_lo(w.w), a2); a3 = __fmaf_rn(q1.w, h2f_hi(w.w), a3);
     }
     const bool valid = lane < n;
     const float sc = __fmul_rn(__fadd_rn(__fadd_rn(a0, a1), __fadd_rn(a2, a3)), scale);
@@ -679,13 +673,12 @@ __device__ __forceinline__ void attn_core(const uint4* kls, const float* qs, con
     m = wave_max(s);
     const float p = valid ? mi_expf(__fsub_rn(s, m)) : 0.f;
     lsum = bfly_sum64(p);
-    ps[lane] = p;
-    wave_lds_sync();
 #pragma unroll
     for (int e = 0; e < DPL; e++) acc[e] = 0.f;
+    const int pb = __float_as_int(p);
 #pragma unroll 8
     for (int t = 0; t < n; t++) {
-        const float pt = ps[t];
+        const float pt = __int_as_float(__builtin_amdgcn_readlane(pb, t));
         if constexpr (DPL == 2) {
             const uint32_t w2 = *reinterpret_cast<const uint32_t*>(vls + t * HD + 2 * lane);
             acc[0] = __fmaf_rn(pt, h2f_lo(w2), acc[0]);
@@ -744,8 +737,6 @@ __device__ __forceinline__ void attn_finish(MPtr M, int l, int pos, const AttnIt
     float* qp = reinterpret_cast<float*>(lds + 2 * 64 * HD * 2);                 // [ks][HD]
     float* kvp = qp + kMaxKsQkv * HD;                                            // [ks][HD] k then [ks][HD] v
     float* qs = qp + 3 * kMaxKsQkv * HD;
-    float* kcur = qs + HD;
-    float* ps = kcur + HD;
     const LPtr Ly = LY(M, l);
     const int h = it.h, c = it.c;
     const int ks = Ly->qkv.ks, kvh = h / M->G;
@@ -756,6 +747,13 @@ __device__ __forceinline__ void attn_finish(MPtr M, int l, int pos, const AttnIt
     const size_t rowbase = ((size_t)l * M->NKV + kvh) * M->maxseq;
     const float* part = qkv_part(M, l);
     const int rq = h * HD, rk = M->NH * HD + kvh * HD, rv = M->NH * HD + M->KVD + kvh * HD;
+    // bias and RoPE table values are loaded in the same batch as the partials
+    const int ip = lane % half;
+    const float* bq = Ly->bqkv;
+    const float2 cz = M->rope[(size_t)pos * half + ip];
+    const float bq0 = bq[rq + ip], bq1 = bq[rq + ip + half];
+    float bk0 = 0.f, bk1 = 0.f, bv0 = 0.f, bv1 = 0.f;
+    if (last) { bk0 = bq[rk + ip]; bk1 = bq[rk + ip + half]; bv0 = bq[rv + ip]; bv1 = bq[rv + ip + half]; }
     for (int s = 0; s < ks; s++) {
         dma_wave(part + (size_t)s * M->QKV + rq, qp + s * HD, HD * 4, lane);
         if (last) {
@@ -770,20 +768,19 @@ __device__ __forceinline__ void attn_finish(MPtr M, int l, int pos, const AttnIt
         for (int s = 1; s < ks; s++) v = __fadd_rn(v, p[s * HD + i]);
         return __fadd_rn(v, bias);
     };
-    const int ip = lane % half;
-    const float2 cz = M->rope[(size_t)pos * half + ip];
     if (lane < half) {
-        const float x0 = fin(qp, ip, Ly->bqkv[rq + ip]), x1 = fin(qp, ip + half, Ly->bqkv[rq + ip + half]);
+        const float x0 = fin(qp, ip, bq0), x1 = fin(qp, ip + half, bq1);
         qs[ip] = __fsub_rn(__fmul_rn(x0, cz.x), __fmul_rn(x1, cz.y));
         qs[ip + half] = __fadd_rn(__fmul_rn(x0, cz.y), __fmul_rn(x1, cz.x));
         if (last) {
-            const float k0 = fin(kvp, ip, Ly->bqkv[rk + ip]), k1 = fin(kvp, ip + half, Ly->bqkv[rk + ip + half]);
+            const float k0 = fin(kvp, ip, bk0), k1 = fin(kvp, ip + half, bk1);
             const __half y0 = __float2half(__fsub_rn(__fmul_rn(k0, cz.x), __fmul_rn(k1, cz.y)));
             const __half y1 = __float2half(__fadd_rn(__fmul_rn(k0, cz.y), __fmul_rn(k1, cz.x)));
-            const __half v0 = __float2half(fin(kvp + kMaxKsQkv * HD, ip, Ly->bqkv[rv + ip]));
-            const __half v1 = __float2half(fin(kvp + kMaxKsQkv * HD, ip + half, Ly->bqkv[rv + ip + half]));
-            kcur[ip] = __half2float(y0);
-            kcur[ip + half] = __half2float(y1);
+            const __half v0 = __float2half(fin(kvp + kMaxKsQkv * HD, ip, bv0));
+            const __half v1 = __float2half(fin(kvp + kMaxKsQkv * HD, ip + half, bv1));
+            __half* kh = reinterpret_cast<__half*>(kls);      // position cur's K row into the swizzled tile
+            kh[((ip >> 3) * 64 + cur) * 8 + (ip & 7)] = y0;
+            kh[(((ip + half) >> 3) * 64 + cur) * 8 + ((ip + half) & 7)] = y1;
             vls[cur * HD + ip] = v0;
             vls[cur * HD + ip + half] = v1;
             if (h % M->G == 0) {                    // one of the kv head's G query heads appends to the cache
@@ -796,7 +793,7 @@ __device__ __forceinline__ void attn_finish(MPtr M, int l, int pos, const AttnIt
     }
     wave_lds_sync();
     float m, lsum, acc[DPL];
-    attn_core<HD>(kls, qs, kcur, cur, vls, ps, n, M->scale, lane, m, lsum, acc);
+    attn_core<HD>(kls, qs, vls, n, M->scale, lane, m, lsum, acc);
     float* rec = att_rec(M, l) + ((size_t)h * M->maxch + c) * M->arec;
 #pragma unroll
     for (int e = 0; e < DPL; e++) stc(rec + DPL * lane + e, acc[e]);
@@ -1089,6 +1086,435 @@ __global__ __launch_bounds__(64) void k_argmax(const DModel* Mp, int ncand, int 
     if (threadIdx.x == 0) emit_token(M, a, pos, gen);
 }
 
+// ================================================================== multi-token steps
+// T <= kMaxT tokens at positions pos..pos+T-1 in one pass over the weights: the
+// verify step of speculative decoding (forward_batch, cuda_infer.cu:990-1026; mega.cu
+// gemv_part T>1 :259-265, tile_dot :197-244). One launch per phase, one 512-thread
+// workgroup per CU, all eight waves work. Every value equals the single-token
+// step's bit for bit: the per-block integer dot of q4 nibbles and int8 activations
+// comes from int8 MFMA (exact), and the float work keeps the same plan (block fma
+// chain per chunk, chunk sums left to right, segment sums left to right), the same
+// prologue arithmetic and the same attention items.
+constexpr int kTRec = 40;          // block record stride in the multi-token kernels: 32 codes, scale, 8*sum
+constexpr int kTChunks = 16;       // chunks of one segment staged in LDS
+constexpr int kTAttnWaves = 4;     // attention waves per workgroup (LDS bound)
+constexpr int kTxsBytes = kMaxT * kMaxE * 4;
+constexpr int kTXeBytes = kMaxT * (kMaxE / 32) * kTRec;
+constexpr int kTXfBytes = kMaxT * (kMaxFF / 32) * kTRec;
+constexpr int kTPBytes = kTChunks * kMaxT * 64 * 4;
+constexpr int kTNormLds = kTxsBytes + kTXeBytes + kTPBytes;   // qkv, o, gate/up, lm_head
+constexpr int kTDownLds = kTXfBytes + kTPBytes;               // down
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ size_t hT_at(MPtr M, int slot, int t) { return ((size_t)slot * kMaxT + t) * M->E; }
+__device__ __forceinline__ float4 ldg4(const float* p) { return *reinterpret_cast<const float4*>(p); }
+
+// chunk sums of one tile (64 rows x CB blocks) for T tokens. MFMA 16x16x32 i8 per
+// block and 16-row subgroup q: lane l feeds A[row q*16 + l%16][k = 8*(l/16) ..+7]
+// (the q4 nibbles of block elements 8*(l/16)..: low nibbles of bytes 0-7 / 8-15,
+// then high nibbles) and B[k][token l%16]; D[4*(l/16) + i][l%16] lands in d[i]. The
+// float epilogue per (row, token) is the single-token chain in block order.
+// acc[q*4 + i]: row q*16 + 4*(l/16) + i, token l%16.
+template <int CB>
+__device__ __forceinline__ void chunk_mfma(const uint8_t* tile, const uint8_t* XT, int nblk, int b0, int T, float (&acc)[16],
+                                           int lane) {
+    const int col = lane & 15, kg = lane >> 4;
+    const bool tok = col < T;
+    const uint8_t* xt = XT + (size_t)(tok ? col : 0) * nblk * kTRec;
+    long bv[CB];
+    float dx[CB];
+    int xs[CB];
+#pragma unroll
+    for (int k = 0; k < CB; k++) {
+        const uint8_t* xb = xt + (b0 + k) * kTRec;
+        bv[k] = tok ? *reinterpret_cast<const long*>(xb + 8 * kg) : 0;
+        dx[k] = tok ? *reinterpret_cast<const float*>(xb + 32) : 0.f;
+        xs[k] = tok ? *reinterpret_cast<const int*>(xb + 36) : 0;
+    }
+    const uint32_t sh = (kg >> 1) * 4;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        uint2 wa[CB];
+#pragma unroll
+        for (int k = 0; k < CB; k++)
+            wa[k] = *reinterpret_cast<const uint2*>(tile + k * 1024 + (q * 16 + col) * 16 + 8 * (kg & 1));
+        uint32_t sc[4][CB / 2];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint8_t* sp = tile + CB * 1024 + (q * 16 + 4 * kg + i) * CB * 2;
+            if constexpr (CB == 8) {
+                const uint4 v = *reinterpret_cast<const uint4*>(sp);
+                sc[i][0] = v.x; sc[i][1] = v.y; sc[i][2] = v.z; sc[i][3] = v.w;
+            } else {
+                const uint2 v = *reinterpret_cast<const uint2*>(sp);
+                sc[i][0] = v.x; sc[i][1] = v.y;
+            }
+        }
+        float a[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int k = 0; k < CB; k++) {
+            const uint32_t lo = (wa[k].x >> sh) & 0x0F0F0F0Fu, hi = (wa[k].y >> sh) & 0x0F0F0F0Fu;
+            const long av = (long)((unsigned long)lo | ((unsigned long)hi << 32));
+            const v4i d = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, bv[k], v4i{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const uint32_t sw = sc[i][k >> 1];
+                const float dw = (k & 1) ? h2f_hi(sw) : h2f_lo(sw);
+                a[i] = __fmaf_rn(__fmul_rn(dw, dx[k]), __int2float_rn(d[i] - xs[k]), a[i]);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) acc[q * 4 + i] = a[i];
+    }
+}
+
+// T-token GEMM over this workgroup's segments of W, one segment at a time: its
+// chunks spread over the eight waves (chunk sums -> P[chunk][token][row]), then wave
+// t adds token t's chunk sums left to right and hands out(g, s, t, value) the row
+// g*64 + lane.
+template <class F>
+__device__ __forceinline__ void tgemm(const PMat W, int wg, int nwg, const uint8_t* XT, int nblk, int T, float* P, int wave,
+                                      int lane, F out) {
+    const int nseg = (W.rows >> 6) * W.ks;
+    const int col = lane & 15, kg = lane >> 4;
+    for (int t = wg; t < nseg; t += nwg) {
+        const int g = t / W.ks, s = t % W.ks, c0 = seg_c0(W, s), c1 = seg_c0(W, s + 1);
+        for (int c = c0 + wave; c < c1; c += kPWaves) {
+            float acc[16];
+            if (W.cb == 8) chunk_mfma<8>(tile_ptr(W, g, c), XT, nblk, c * 8, T, acc, lane);
+            else chunk_mfma<4>(tile_ptr(W, g, c), XT, nblk, c * 4, T, acc, lane);
+            if (col < T) {
+                float* pc = P + ((size_t)(c - c0) * kMaxT + col) * 64;
+#pragma unroll
+                for (int q = 0; q < 4; q++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++) pc[q * 16 + 4 * kg + i] = acc[q * 4 + i];
+            }
+        }
+        __syncthreads();
+        if (wave < T) {
+            float v = P[(size_t)wave * 64 + lane];
+            for (int c = 1; c < c1 - c0; c++) v = __fadd_rn(v, P[((size_t)c * kMaxT + wave) * 64 + lane]);
+            out(g, s, wave, v);
+        }
+        __syncthreads();
+    }
+}
+
+// prologue of a norm phase, wave t = token t: x = h + split-K partials (layer 0 of
+// qkv: the token's embedding row) -> hT (workgroup 0) -> RMSNorm -> int8 records
+__device__ __forceinline__ void tnorm_prologue(MPtr M, int l, int kind, int pos, int T, int wg, float* xs, uint8_t* XT,
+                                               int wave, int lane) {
+    if (wave >= T) return;
+    const int t = wave, n = M->E, nblk = n / 32;
+    const bool qkv = kind == PH_QKV, lm = kind == PH_LM;
+    float* x = xs + (size_t)t * kMaxE;
+    if (qkv && l == 0) {
+        const float* er = M->emb + (size_t)M->tokbuf[pos + t] * n;
+#pragma unroll 2
+        for (int e0 = 4 * lane; e0 < n; e0 += 256) st4(x, e0, ldg4(er + e0));
+    } else {
+        const int pl = qkv ? l - 1 : lm ? M->NL - 1 : l;
+        const bool dsrc = kind != PH_GU;
+        const int ks = dsrc ? LY(M, pl)->d.ks : LY(M, pl)->o.ks;
+        const float* part = dsrc ? M->dT + (size_t)pl * LY(M, 0)->d.ks * kMaxT * n : M->oT + (size_t)pl * LY(M, 0)->o.ks * kMaxT * n;
+        const float* h = M->hT + hT_at(M, dsrc ? 2 * pl + 1 : 2 * l, t);
+#pragma unroll 2
+        for (int e0 = 4 * lane; e0 < n; e0 += 256) {
+            float4 p[kMaxKsRes];
+#pragma unroll
+            for (int s = 0; s < kMaxKsRes; s++)
+                if (s < ks) p[s] = ldg4(part + ((size_t)s * kMaxT + t) * n + e0);
+            float4 v = p[0];
+#pragma unroll
+            for (int s = 1; s < kMaxKsRes; s++)
+                if (s < ks) v = f4add(v, p[s]);
+            st4(x, e0, f4add(ldg4(h + e0), v));
+        }
+    }
+    wave_lds_sync();
+    if (wg == 0 && !lm) {
+        float* dst = M->hT + hT_at(M, qkv ? 2 * l : 2 * l + 1, t);
+        for (int e0 = 4 * lane; e0 < n; e0 += 256) {
+            const float4 v = ld4(x + e0);
+            stc(dst + e0, v.x); stc(dst + e0 + 1, v.y); stc(dst + e0 + 2, v.z); stc(dst + e0 + 3, v.w);
+        }
+    }
+    const float* w = lm ? M->out_norm : qkv ? LY(M, l)->an : LY(M, l)->fn;
+    const float sc = rms_scale(x, n, M->eps, lane);
+    uint8_t* xr = XT + (size_t)t * nblk * kTRec;
+    for (int j = 0; 256 * j < n; j++) {
+        const int e0 = 256 * j + 4 * lane;
+        const bool own = e0 < n;
+        float4 y = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (own) {
+            const float4 xv = ld4(x + e0), wv = ldg4(w + e0);
+            y = make_float4(__fmul_rn(__fmul_rn(xv.x, sc), wv.x), __fmul_rn(__fmul_rn(xv.y, sc), wv.y),
+                            __fmul_rn(__fmul_rn(xv.z, sc), wv.z), __fmul_rn(__fmul_rn(xv.w, sc), wv.w));
+        }
+        quant_slice(y, own, e0, xr, lane, kTRec);
+    }
+}
+
+__device__ __forceinline__ float* qkvT_at(MPtr M, int l) { return M->qkvT + (size_t)l * LY(M, 0)->qkv.ks * kMaxT * M->QKV; }
+__device__ __forceinline__ float* oT_at(MPtr M, int l) { return M->oT + (size_t)l * LY(M, 0)->o.ks * kMaxT * M->E; }
+__device__ __forceinline__ float* dT_at(MPtr M, int l) { return M->dT + (size_t)l * LY(M, 0)->d.ks * kMaxT * M->E; }
+__device__ __forceinline__ float* attT_at(MPtr M, int l, int t) {
+    return M->attT + ((size_t)l * kMaxT + t) * M->NH * M->maxch * M->arec;
+}
+__device__ __forceinline__ uint8_t* actT_at(MPtr M, int l, int t) {
+    return M->actT + ((size_t)l * kMaxT + t) * (M->FF / 32) * kActRec;
+}
+
+#define TPRELUDE(BYTES)                                                                          \
+    const MPtr M = (MPtr)Mp;                                                                     \
+    __shared__ __align__(16) uint8_t smem[BYTES];                                                \
+    const int wg = blockIdx.x, nwg = gridDim.x, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+
+__global__ __launch_bounds__(kPThreads) void kT_qkv(const DModel* Mp, int l, int pos, int T) {
+    TPRELUDE(kTNormLds)
+    float* xs = reinterpret_cast<float*>(smem);
+    uint8_t* XT = smem + kTxsBytes;
+    float* P = reinterpret_cast<float*>(smem + kTxsBytes + kTXeBytes);
+    tnorm_prologue(M, l, PH_QKV, pos, T, wg, xs, XT, wave, lane);
+    __syncthreads();
+    const PMat W = ldmat(&LY(M, l)->qkv);
+    float* part = qkvT_at(M, l);
+    tgemm(W, wg, nwg, XT, M->E / 32, T, P, wave, lane, [&](int g, int s, int t, float v) {
+        part[((size_t)s * kMaxT + t) * W.rows + g * 64 + lane] = v;
+    });
+}
+
+// attention items (token t, query head h, 64-position chunk c of positions
+// 0..pos+t). The chunk's K/V rows come from the cache; rows of this step's
+// positions pos..pos+t are finished here from the QKV rows (bias, RoPE, fp16) as
+// the single-token step does for its own position, written into the LDS tiles, and
+// appended to the cache by the items of the last token and of one query head per
+// kv head.
+template <int HD>
+__device__ __forceinline__ void tattn_item(MPtr M, int l, int pos, int T, int t, int h, int c, uint8_t* lds, int lane) {
+    constexpr int half = HD / 2, DPL = HD / 64;
+    uint4* kls = reinterpret_cast<uint4*>(lds);
+    __half* vls = reinterpret_cast<__half*>(lds + 64 * HD * 2);
+    float* qs = reinterpret_cast<float*>(lds + 2 * 64 * HD * 2);
+    const LPtr Ly = LY(M, l);
+    const int ks = Ly->qkv.ks, kvh = h / M->G, QKV = M->QKV;
+    const int L = pos + t + 1, t0 = c * kAttnChunk, n = min(kAttnChunk, L - t0);
+    const size_t rowbase = ((size_t)l * M->NKV + kvh) * M->maxseq;
+    attn_issue_kv<HD>(M->kc + rowbase * HD, M->vc + rowbase * HD, t0, n, kls, vls, lane);
+    drain_vm();
+    wave_lds_sync();
+    const float* part = qkvT_at(M, l);
+    const float* bq = Ly->bqkv;
+    const int ip = lane % half;
+    const int rq = h * HD, rk = M->NH * HD + kvh * HD, rv = M->NH * HD + M->KVD + kvh * HD;
+    auto fin = [&](int tok, int row) {
+        float v = part[(size_t)tok * QKV + row];
+        for (int s = 1; s < ks; s++) v = __fadd_rn(v, part[((size_t)s * kMaxT + tok) * QKV + row]);
+        return __fadd_rn(v, bq[row]);
+    };
+    if (lane < half) {
+        const float2 cz = M->rope[(size_t)(pos + t) * half + ip];
+        const float x0 = fin(t, rq + ip), x1 = fin(t, rq + ip + half);
+        qs[ip] = __fsub_rn(__fmul_rn(x0, cz.x), __fmul_rn(x1, cz.y));
+        qs[ip + half] = __fadd_rn(__fmul_rn(x0, cz.y), __fmul_rn(x1, cz.x));
+        // this step's positions inside the chunk: pos + u for u = 0..t
+        const bool append = t == T - 1 && h % M->G == 0;
+        for (int u = max(0, t0 - pos); u <= t && pos + u < t0 + n; u++) {
+            const int p = pos + u, r = p - t0;
+            const float2 cu = M->rope[(size_t)p * half + ip];
+            const float k0 = fin(u, rk + ip), k1 = fin(u, rk + ip + half);
+            const __half y0 = __float2half(__fsub_rn(__fmul_rn(k0, cu.x), __fmul_rn(k1, cu.y)));
+            const __half y1 = __float2half(__fadd_rn(__fmul_rn(k0, cu.y), __fmul_rn(k1, cu.x)));
+            const __half v0 = __float2half(fin(u, rv + ip));
+            const __half v1 = __float2half(fin(u, rv + ip + half));
+            __half* kh = reinterpret_cast<__half*>(kls);
+            kh[((ip >> 3) * 64 + r) * 8 + (ip & 7)] = y0;
+            kh[(((ip + half) >> 3) * 64 + r) * 8 + ((ip + half) & 7)] = y1;
+            vls[r * HD + ip] = v0;
+            vls[r * HD + ip + half] = v1;
+            if (append) {
+                __half* kd = M->kc + (rowbase + p) * HD;
+                __half* vd = M->vc + (rowbase + p) * HD;
+                kd[ip] = y0; kd[ip + half] = y1;
+                vd[ip] = v0; vd[ip + half] = v1;
+            }
+        }
+    }
+    wave_lds_sync();
+    float m, lsum, acc[DPL];
+    attn_core<HD>(kls, qs, vls, n, M->scale, lane, m, lsum, acc);
+    float* rec = attT_at(M, l, t) + ((size_t)h * M->maxch + c) * M->arec;
+#pragma unroll
+    for (int e = 0; e < DPL; e++) rec[DPL * lane + e] = acc[e];
+    if (lane == 0) { rec[HD] = m; rec[HD + 1] = lsum; }
+    wave_lds_sync();
+}
+
+template <int HD>
+__global__ __launch_bounds__(kPThreads) void kT_attn(const DModel* Mp, int l, int pos, int T) {
+    TPRELUDE(kTAttnWaves * attn_wave_lds<HD>())
+    (void)wg;
+    if (wave >= kTAttnWaves) return;
+    // items of token t: NH heads x chunks of positions 0..pos+t; enumerated token-major
+    const int NH = M->NH;
+    int total = 0;
+    for (int t = 0; t < T; t++) total += NH * ((pos + t + kAttnChunk) / kAttnChunk);
+    for (int i = blockIdx.x + nwg * wave; i < total; i += nwg * kTAttnWaves) {
+        int t = 0, r = i;
+        for (;; t++) {
+            const int cnt = NH * ((pos + t + kAttnChunk) / kAttnChunk);
+            if (r < cnt) break;
+            r -= cnt;
+        }
+        const int nch = (pos + t + kAttnChunk) / kAttnChunk;
+        tattn_item<HD>(M, l, pos, T, t, r / nch, r % nch, smem + wave * attn_wave_lds<HD>(), lane);
+    }
+}
+
+// chunk merge per (token, head, dim) into att_outT (used when the last token's
+// context has more than kInlineComb chunks; same arithmetic as the inline merge)
+__global__ __launch_bounds__(kPThreads) void kT_comb(const DModel* Mp, int l, int pos, int T) {
+    const MPtr M = (MPtr)Mp;
+    const int n = M->E;
+    for (int it = blockIdx.x * blockDim.x + threadIdx.x; it < T * n; it += gridDim.x * blockDim.x) {
+        const int t = it / n, e = it - t * n, nch = (pos + t + kAttnChunk) / kAttnChunk;
+        M->att_outT[((size_t)l * kMaxT + t) * n + e] =
+            combine_one(attT_at(M, l, t) + (size_t)(e / M->HD) * M->maxch * M->arec, M->arec, M->HD, e % M->HD, nch);
+    }
+}
+
+__global__ __launch_bounds__(kPThreads) void kT_o(const DModel* Mp, int l, int pos, int T, int merged) {
+    TPRELUDE(kTNormLds)
+    uint8_t* XT = smem + kTxsBytes;
+    float* P = reinterpret_cast<float*>(smem + kTxsBytes + kTXeBytes);
+    const int n = M->E, nblk = n / 32;
+    if (wave < T) {
+        const int t = wave, nch = (pos + t + kAttnChunk) / kAttnChunk, HD = M->HD, arec = M->arec;
+        const float* att = attT_at(M, l, t);
+        for (int j = 0; 256 * j < n; j++) {
+            const int e0 = 256 * j + 4 * lane;
+            const bool own = e0 < n;
+            float4 y = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (own && merged) {
+                y = ldg4(M->att_outT + ((size_t)l * kMaxT + t) * n + e0);
+            } else if (own) {
+                const int hh = e0 / HD, d = e0 - hh * HD;
+                const float* r = att + (size_t)hh * M->maxch * arec;
+                float mx = -__builtin_inff();
+                for (int c = 0; c < nch; c++) mx = fmaxf(mx, r[c * arec + HD]);
+                float den = 0.f;
+                float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+                for (int c = 0; c < nch; c++) {
+                    const float wc = mi_expf(__fsub_rn(r[c * arec + HD], mx));
+                    den = __fmaf_rn(r[c * arec + HD + 1], wc, den);
+                    const float4 o = ldg4(r + c * arec + d);
+                    acc = make_float4(__fmaf_rn(o.x, wc, acc.x), __fmaf_rn(o.y, wc, acc.y), __fmaf_rn(o.z, wc, acc.z),
+                                      __fmaf_rn(o.w, wc, acc.w));
+                }
+                y = make_float4(__fdiv_rn(acc.x, den), __fdiv_rn(acc.y, den), __fdiv_rn(acc.z, den), __fdiv_rn(acc.w, den));
+            }
+            quant_slice(y, own, e0, XT + (size_t)t * nblk * kTRec, lane, kTRec);
+        }
+    }
+    __syncthreads();
+    const PMat W = ldmat(&LY(M, l)->o);
+    float* part = oT_at(M, l);
+    tgemm(W, wg, nwg, XT, nblk, T, P, wave, lane, [&](int g, int s, int t, float v) {
+        part[((size_t)s * kMaxT + t) * W.rows + g * 64 + lane] = v;
+    });
+}
+
+__global__ __launch_bounds__(kPThreads) void kT_gu(const DModel* Mp, int l, int T) {
+    TPRELUDE(kTNormLds)
+    float* xs = reinterpret_cast<float*>(smem);
+    uint8_t* XT = smem + kTxsBytes;
+    float* P = reinterpret_cast<float*>(smem + kTxsBytes + kTXeBytes);
+    tnorm_prologue(M, l, PH_GU, 0, T, wg, xs, XT, wave, lane);
+    __syncthreads();
+    const PMat W = ldmat(&LY(M, l)->gu);
+    tgemm(W, wg, nwg, XT, M->E / 32, T, P, wave, lane, [&](int g, int s, int t, float v) {
+        (void)s;
+        const float u = __shfl(v, (lane & 31) + 32);
+        const float e = mi_expf(-v);
+        const float a = __fmul_rn(__fdiv_rn(v, __fadd_rn(1.0f, e)), u);
+        int q, s8;
+        float d;
+        quant32_vals(a, q, d, s8);
+        const uint32_t b = (uint32_t)(q & 0xFF);
+        const uint32_t wd = b | (__shfl_down(b, 1) << 8) | (__shfl_down(b, 2) << 16) | (__shfl_down(b, 3) << 24);
+        if (lane < 32) {
+            uint32_t* r = reinterpret_cast<uint32_t*>(actT_at(M, l, t) + (size_t)g * kActRec);
+            if ((lane & 3) == 0) r[lane / 4] = wd;
+            if (lane == 0) { r[8] = __float_as_uint(d); r[9] = (uint32_t)s8; }
+        }
+    });
+}
+
+__global__ __launch_bounds__(kPThreads) void kT_down(const DModel* Mp, int l, int T) {
+    TPRELUDE(kTDownLds)
+    uint8_t* XT = smem;
+    float* P = reinterpret_cast<float*>(smem + kTXfBytes);
+    const int nblk = M->FF / 32;
+    // act records of the T tokens, compacted to kTRec bytes per block
+    for (int i = threadIdx.x; i < T * nblk; i += blockDim.x) {
+        const int t = i / nblk, b = i - t * nblk;
+        const uint2* src = reinterpret_cast<const uint2*>(actT_at(M, l, t) + (size_t)b * kActRec);
+        uint2* dst = reinterpret_cast<uint2*>(XT + ((size_t)t * nblk + b) * kTRec);   // 8-byte aligned records
+#pragma unroll
+        for (int k = 0; k < kTRec / 8; k++) dst[k] = src[k];
+    }
+    __syncthreads();
+    const PMat W = ldmat(&LY(M, l)->d);
+    float* part = dT_at(M, l);
+    tgemm(W, wg, nwg, XT, nblk, T, P, wave, lane, [&](int g, int s, int t, float v) {
+        part[((size_t)s * kMaxT + t) * W.rows + g * 64 + lane] = v;
+    });
+}
+
+__global__ __launch_bounds__(kPThreads) void kT_lm(const DModel* Mp, int T) {
+    TPRELUDE(kTNormLds)
+    float* xs = reinterpret_cast<float*>(smem);
+    uint8_t* XT = smem + kTxsBytes;
+    float* P = reinterpret_cast<float*>(smem + kTxsBytes + kTXeBytes);
+    tnorm_prologue(M, M->NL - 1, PH_LM, 0, T, wg, xs, XT, wave, lane);
+    __syncthreads();
+    const PMat W = ldmat(&M->lm);
+    Top2 tp{-__builtin_inff(), INT_MAX, -__builtin_inff()};
+    tgemm(W, wg, nwg, XT, M->E / 32, T, P, wave, lane, [&](int g, int s, int t, float v) {
+        (void)s;
+        const int row = g * 64 + lane;
+        if (M->logitsT) M->logitsT[(size_t)t * M->V + row] = v;
+        top2_push(tp, v, row);
+    });
+    if (wave < T) {
+        top2_wave(tp);
+        if (lane == 0) {
+            float* cd = M->candT + ((size_t)wg * kMaxT + wave) * 4;
+            cd[0] = tp.best;
+            cd[1] = __int_as_float(tp.idx);
+            cd[2] = tp.second;
+        }
+    }
+}
+
+__global__ __launch_bounds__(kPThreads) void kT_argmax(const DModel* Mp, int ncand, int pos, int T) {
+    const MPtr M = (MPtr)Mp;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    if (wave >= T) return;
+    Top2 tp{-__builtin_inff(), INT_MAX, -__builtin_inff()};
+    for (int i = lane; i < ncand; i += 64) {
+        const float* cd = M->candT + ((size_t)i * kMaxT + wave) * 4;
+        top2_merge(tp, cd[0], __float_as_int(cd[1]), cd[2]);
+    }
+    top2_wave(tp);
+    if (lane == 0) {
+        M->out_tok[pos + wave] = tp.idx;
+        M->out_margin[pos + wave] = __fsub_rn(tp.best, tp.second);
+    }
+}
+
 // ------------------------------------------------------------------ standalone kernels
 __global__ __launch_bounds__(kThreads) void k_quant(const float* x, int n, int8_t* xq, float* xd, int32_t* xs8) {
     const int lane = threadIdx.x & 63;
@@ -1162,7 +1588,6 @@ __global__ __launch_bounds__(kThreads) void k_attn_standalone(const float* q, co
     uint4* kls = reinterpret_cast<uint4*>(lds);
     __half* vls = reinterpret_cast<__half*>(lds + 64 * HD * 2);
     float* qs = reinterpret_cast<float*>(lds + 2 * 64 * HD * 2) + 3 * kMaxKsQkv * HD;
-    float* ps = qs + 2 * HD;
     for (int it = blockIdx.x * kAttnWaves + wave; it < items; it += gridDim.x * kAttnWaves) {
         const int h = it / nch, c = it % nch, kvh = h / G, t0 = c * kAttnChunk, n = min(kAttnChunk, L - t0);
         attn_issue_kv<HD>(kc + (size_t)kvh * ctx * HD, vc + (size_t)kvh * ctx * HD, t0, n, kls, vls, lane);
@@ -1170,7 +1595,7 @@ __global__ __launch_bounds__(kThreads) void k_attn_standalone(const float* q, co
         drain_vm();
         wave_lds_sync();
         float m, lsum, acc[DPL];
-        attn_core<HD>(kls, qs, qs, -1, vls, ps, n, scale, lane, m, lsum, acc);
+        attn_core<HD>(kls, qs, vls, n, scale, lane, m, lsum, acc);
         float* rec = recs + ((size_t)h * nch + c) * REC;
 #pragma unroll
         for (int e = 0; e < DPL; e++) rec[DPL * lane + e] = acc[e];
@@ -1267,6 +1692,22 @@ hipError_t launch_step_persistent(const DModel& M, const DModel* dM, int nwg, in
     });
     return err;
 }
+
+void launch_step_multi(const DModel& M, const DModel* dM, int nwg, int pos, int T, hipStream_t s) {
+    const int nch_last = (pos + T - 1 + kAttnChunk) / kAttnChunk, merged = nch_last > kInlineComb;
+    for (int l = 0; l < M.NL; l++) {
+        LAUNCH(kT_qkv, nwg, kPThreads, s, dM, l, pos, T);
+        with_hd(M.HD, [&](auto hd) { LAUNCH((kT_attn<decltype(hd)::value>), nwg, kPThreads, s, dM, l, pos, T); });
+        if (merged) LAUNCH(kT_comb, nwg, kPThreads, s, dM, l, pos, T);
+        LAUNCH(kT_o, nwg, kPThreads, s, dM, l, pos, T, merged);
+        LAUNCH(kT_gu, nwg, kPThreads, s, dM, l, T);
+        LAUNCH(kT_down, nwg, kPThreads, s, dM, l, T);
+    }
+    LAUNCH(kT_lm, nwg, kPThreads, s, dM, T);
+    LAUNCH(kT_argmax, 1, kPThreads, s, dM, nwg, pos, T);
+}
+int kernels_max_tokens() { return kMaxT; }
+int kernels_max_chunks_multi() { return kTChunks; }
 
 hipError_t launch_barriers(uint32_t* bar, int32_t* err, int nwg, int n, hipStream_t s) {
     hipError_t e = hipMemsetAsync(bar, 0, sizeof(uint32_t) * kBarWords, s);

@@ -173,13 +173,20 @@ class Engine:
         return first.value, mg.value
 
     def step(self, tok, pos, want_logits=False):
-        am, mg = (C.c_int32 * 1)(), (C.c_float * 1)()
-        lg = (C.c_float * self.info.n_vocab)() if want_logits else None
-        _check(lib().mi_step(self._h, _i32([tok]), 1, pos, am, mg, lg), self._h)
+        """One step at position pos. tok: one token id (returns argmax, margin[,
+        logits [V]]) or a list of T <= 8 ids (returns lists, logits [T][V])."""
+        many = isinstance(tok, (list, tuple))
+        toks = list(tok) if many else [tok]
+        T = len(toks)
+        am, mg = (C.c_int32 * T)(), (C.c_float * T)()
+        lg = (C.c_float * (self.info.n_vocab * T))() if want_logits else None
+        _check(lib().mi_step(self._h, _i32(toks), T, pos, am, mg, lg), self._h)
+        a, m = (list(am), list(mg)) if many else (am[0], mg[0])
         if want_logits:
             import numpy as np
-            return am[0], mg[0], np.frombuffer(lg, dtype=np.float32).copy()
-        return am[0], mg[0]
+            l = np.frombuffer(lg, dtype=np.float32).copy()
+            return a, m, (l.reshape(T, -1) if many else l)
+        return a, m
 
     def generate(self, n_gen, callback=None):
         out = (C.c_int32 * max(n_gen, 1))()

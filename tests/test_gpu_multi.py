@@ -1,0 +1,118 @@
+"""GPU parity of the multi-token (verify) step: T tokens at positions pos..pos+T-1
+in one pass over the weights through int8 MFMA tiles (mi_step with T > 1).
+
+Bar (the reference's own exactness check, mega.cu:1198-1204, is a hash of the
+logits across T): every token's logits are bit-identical to running the same
+tokens one at a time with T = 1, which is itself bit-identical to the q8act
+oracle (test_gpu_engine.py); one case is also checked against the oracle directly.
+Cases cover both chunk sizes of the q4 tiles (cb 8 and cb 4), a step that crosses
+a 64-position attention chunk, and a context past the inline chunk merge.
+"""
+import sys
+
+import numpy as np
+import pytest
+
+import minfer
+import oracle_lib as O
+from conftest import synth_cached
+
+pytestmark = pytest.mark.gpu
+TINY = dict(n_layer=2, n_embd=256, n_ff=512, n_head=4, n_head_kv=2, n_vocab=4096)
+SMALL = dict(n_layer=3, n_embd=512, n_ff=1536, n_head=8, n_head_kv=2, n_vocab=8192)
+
+
+def say(*a):
+    print("[gpu-multi]", *a, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module", autouse=True)
+def gpu():
+    import torch
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+
+
+def bits(x):
+    return np.asarray(x, np.float32).view(np.uint32)
+
+
+def multi_vs_single(eng, prompt, pos, T, seed, V):
+    """prefill prompt[:pos], then one T-token step vs T single steps, same tokens"""
+    eng.prefill(prompt[:pos])
+    toks = minfer.prompt_ids(seed, T, V)
+    am, mg, lg = eng.step(toks, pos, want_logits=True)
+    for t in range(T):
+        a, m, l1 = eng.step(toks[t], pos + t, want_logits=True)
+        assert np.array_equal(bits(lg[t]), bits(l1)), "token %d of %d at pos %d: logits differ" % (t, T, pos)
+        assert am[t] == a and bits(mg[t]) == bits(m)
+    return toks, lg
+
+
+@pytest.mark.parametrize("pos,T", [(12, 2), (12, 5), (61, 8), (3, 8)])
+def test_tiny_multi_bit_identical(pos, T):
+    path = synth_cached("eng-256", TINY, 7)
+    say("tiny pos %d T %d" % (pos, T))
+    eng = minfer.Engine(path, max_ctx=256)
+    prompt = minfer.prompt_ids(11, pos, TINY["n_vocab"])
+    multi_vs_single(eng, prompt, pos, T, 100 + pos + T, TINY["n_vocab"])
+    eng.close()
+
+
+def test_small_multi_bit_identical_and_oracle():
+    path = synth_cached("eng-512", SMALL, 21)
+    pos, T = 70, 8
+    say("small pos %d T %d (+ oracle)" % (pos, T))
+    eng = minfer.Engine(path, max_ctx=256)
+    prompt = minfer.prompt_ids(12, pos, SMALL["n_vocab"])
+    toks, lg = multi_vs_single(eng, prompt, pos, T, 5, SMALL["n_vocab"])
+    p = eng.plan
+    eng.close()
+    orc = O.Model(path, O.MODE_Q8ACT, plan=O.Plan.make(p["cb"], p["ks"], p["attn_chunk"], p["kv_f16"]), max_seq=256)
+    for i, tok in enumerate(list(prompt) + list(toks)):
+        _, _, lo = orc.forward(tok, i, True)
+        if i >= pos:
+            assert np.array_equal(bits(lo), bits(lg[i - pos])), "oracle differs at pos %d" % i
+
+
+def test_config0_multi_cb4_bit_identical():
+    """S05 (hidden 896): q4 chunks of 4 blocks in the E-row matrices, head_dim 64"""
+    shape = minfer.SHAPES["S05"]
+    path = synth_cached("config0", shape, minfer.CONFIGS["config0"][1])
+    say("config0 pos 16 T 8")
+    eng = minfer.Engine(path, max_ctx=64)
+    assert eng.plan["cb"][0] == 4
+    prompt = minfer.prompt_ids(minfer.CONFIGS["config0"][2], 16, shape["n_vocab"])
+    multi_vs_single(eng, prompt, 16, 8, 17, shape["n_vocab"])
+    eng.close()
+
+
+def test_config2_multi_bit_identical():
+    """S15: head_dim 128, the down matrix split into 7 K segments"""
+    shape = minfer.SHAPES["S15"]
+    path = synth_cached("config2", shape, minfer.CONFIGS["config2"][1])
+    say("config2 pos 64 T 8")
+    eng = minfer.Engine(path, max_ctx=128)
+    prompt = minfer.prompt_ids(minfer.CONFIGS["config2"][2], 64, shape["n_vocab"])
+    multi_vs_single(eng, prompt, 64, 8, 19, shape["n_vocab"])
+    eng.close()
+
+
+def test_long_context_multi_merge_phase():
+    """past kInlineComb chunks the chunk records are merged by their own kernel"""
+    path = synth_cached("eng-256", TINY, 7)
+    say("tiny long context pos 1000 T 6")
+    eng = minfer.Engine(path, max_ctx=1100)
+    prompt = minfer.prompt_ids(13, 1000, TINY["n_vocab"])
+    multi_vs_single(eng, prompt, 1000, 6, 23, TINY["n_vocab"])
+    eng.close()
+
+
+def test_multi_step_rejects_bad_T():
+    path = synth_cached("eng-256", TINY, 7)
+    eng = minfer.Engine(path, max_ctx=64)
+    eng.prefill([1, 2, 3])
+    with pytest.raises(minfer.MinferError):
+        eng.step(list(range(9)), 3)
+    eng.close()
