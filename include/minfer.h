@@ -90,13 +90,24 @@ int mi_prefill(mi_engine* e, const int32_t* ids, int32_t n, int32_t* first, floa
 int mi_step(mi_engine* e, const int32_t* toks, int32_t T, int32_t pos,
             int32_t* argmax, float* margin, float* logits);
 
+/* Host side of speculative decoding (mega.cu:557-589), exported so callers and tests
+ * can use them directly. mi_ngram_draft: for n = ngmax..1, the latest earlier
+ * occurrence of the last n tokens of h[0..len) proposes the up to kmax tokens that
+ * followed it; returns the draft length. mi_best_draft_len: the K in 0..tmax-1 that
+ * maximises (1-alpha^(K+1))/(1-alpha) / (1+slope*K). */
+int32_t mi_ngram_draft(const int32_t* h, int32_t len, int32_t ngmax, int32_t kmax, int32_t* out);
+int32_t mi_best_draft_len(float alpha, float slope, int32_t tmax);
+
 /* Token callback for mi_generate; returning nonzero stops generation. */
 typedef int (*mi_token_cb)(int32_t id, void* user);
 
 /* Greedy generation after mi_prefill (cuda_infer.cu:1170-1200, mega.cu:819-895):
  * emits n_gen tokens, the first being mi_prefill's prediction. out[n_gen] and
  * margins[n_gen] (nullable) receive them; *n_out the count actually emitted
- * (fewer when stop_eos hits eos or the callback stops). */
+ * (fewer when stop_eos hits eos or the callback stops). With opts.spec = 1 each step
+ * verifies [current token, n-gram draft] in one multi-token step and commits the
+ * predictions up to the first one that disagrees with its draft (mega.cu:863-895):
+ * the output is token for token the plain greedy decode. */
 int mi_generate(mi_engine* e, int32_t n_gen, int32_t* out, float* margins, int32_t* n_out,
                 mi_token_cb cb, void* user);
 
@@ -104,10 +115,12 @@ int mi_generate(mi_engine* e, int32_t n_gen, int32_t* out, float* margins, int32
  * HIP events on the engine stream (the reference prints the same figure,
  * mega.cu:1186-1190, cuda_infer.cu:1196-1199). */
 typedef struct mi_stats {
-    int32_t steps;          /* decode steps run */
+    int32_t steps;          /* decode steps run (with speculation: verify steps) */
     int32_t tokens;         /* tokens emitted by those steps */
-    double decode_ms;       /* device time of those steps */
+    double decode_ms;       /* device time of those steps (with speculation: wall time) */
     double prefill_ms;      /* device time of the last mi_prefill */
+    int32_t drafted;        /* draft tokens proposed (speculation; mega.cu stats[1]) */
+    int32_t accepted;       /* draft tokens accepted (speculation; mega.cu stats[2]) */
 } mi_stats;
 int mi_get_stats(const mi_engine* e, mi_stats* out);
 

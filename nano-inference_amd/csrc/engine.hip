@@ -13,6 +13,7 @@
 #include "minfer.h"
 
 #include <algorithm>
+#include <chrono>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -555,10 +556,95 @@ int mi_prefill(mi_engine* e, const int32_t* ids, int32_t n, int32_t* first, floa
     return MI_OK;
 }
 
+}  // extern "C"
+
+// T tokens already in tokbuf[pos..pos+T-1]: one step, predictions back to the host
+static int run_tokens(mi_engine* e, int pos, int T, int32_t* tok, float* mg) {
+    if (T == 1) {
+        if (int rc = run_step(e, pos, 1, false)) return rc;
+    } else {
+        launch_step_multi(e->M, e->dM, e->n_cu, pos, T, e->stream);
+        HIPCHK(e, hipGetLastError());
+    }
+    HIPCHK(e, hipMemcpyAsync(tok, e->M.out_tok + pos, 4 * T, hipMemcpyDeviceToHost, e->stream));
+    HIPCHK(e, hipMemcpyAsync(mg, e->M.out_margin + pos, 4 * T, hipMemcpyDeviceToHost, e->stream));
+    HIPCHK(e, hipStreamSynchronize(e->stream));
+    return T == 1 ? check_barrier(e) : MI_OK;
+}
+
+// Lossless speculative generation (mega.cu:863-895): each step runs [cur, draft]
+// at positions pos..pos+K and commits the predictions up to and including the first
+// one that disagrees with its draft. A token's logits do not depend on how many
+// tokens share the step, so the output is the plain greedy decode token for token.
+static int generate_spec(mi_engine* e, int n_gen, int32_t* out, float* margins, int32_t* n_out, mi_token_cb cb,
+                         void* user) {
+    const int p0 = e->cur_len;                   // position of the current (first) token
+    const int TM = kernels_max_tokens();
+    std::vector<int32_t> hist((size_t)p0 + n_gen + TM + 1);
+    HIPCHK(e, hipMemcpy(hist.data(), e->M.tokbuf, sizeof(int32_t) * (p0 + 1), hipMemcpyDeviceToHost));
+    float mg0 = 0.f;
+    HIPCHK(e, hipMemcpy(&mg0, e->M.out_margin + p0 - 1, 4, hipMemcpyDeviceToHost));
+    int pos = p0, emitted = 0, last_pos = p0, steps = 0, drafted = 0, accepted = 0;
+    bool done = n_gen == 0;
+    auto emit = [&](int32_t t, float m, int at) {
+        if (out) out[emitted] = t;
+        if (margins) margins[emitted] = m;
+        emitted++;
+        last_pos = at;
+        done = emitted >= n_gen || (cb && cb(t, user)) || (e->opts.stop_eos && t == e->eos);
+    };
+    int32_t cur = hist[p0];
+    if (!done) emit(cur, mg0, p0);
+    float acc_num = 0.6f, acc_den = 1.f;         // EWMA of accepted drafts / (accepted + rejections), mega.cu:613
+    const auto t_start = std::chrono::steady_clock::now();
+    while (!done) {
+        const float alpha = std::min(std::max(acc_num / acc_den, 0.01f), 0.99f);
+        const int kmax = std::min(mi_best_draft_len(alpha, e->opts.spec_slope, TM),
+                                  std::min(n_gen - emitted - 1, e->maxseq - 1 - pos));
+        int32_t toks[16], y[16];
+        float ym[16];
+        toks[0] = cur;
+        const int K = kmax > 0 ? mi_ngram_draft(hist.data(), pos + 1, e->opts.ngmax, kmax, toks + 1) : 0;
+        HIPCHK(e, hipMemcpyAsync(e->M.tokbuf + pos, toks, sizeof(int32_t) * (K + 1), hipMemcpyHostToDevice, e->stream));
+        if (int rc = run_tokens(e, pos, K + 1, y, ym)) return rc;
+        int a = 0;
+        while (a < K && toks[1 + a] == y[a]) a++;
+        for (int i = 0; i <= a && !done; i++) {
+            hist[pos + 1 + i] = y[i];
+            emit(y[i], ym[i], pos + 1 + i);
+        }
+        cur = y[a];
+        pos += a + 1;
+        if (K > 0) {
+            acc_num = 0.85f * acc_num + 0.15f * a;
+            acc_den = 0.85f * acc_den + 0.15f * (a + (a < K ? 1 : 0));
+        }
+        steps++;
+        drafted += K;
+        accepted += a;
+    }
+    const double ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t_start).count();
+    // the last emitted token sits at last_pos with its K/V not yet computed (as after a plain generate)
+    HIPCHK(e, hipMemcpy(e->M.tokbuf + last_pos, &hist[last_pos], 4, hipMemcpyHostToDevice));
+    e->stats.decode_ms = ms;
+    e->stats.steps = steps;
+    e->stats.tokens = emitted;
+    e->stats.drafted = drafted;
+    e->stats.accepted = accepted;
+    e->cur_len = last_pos;
+    e->next_ready = true;
+    if (n_out) *n_out = emitted;
+    return MI_OK;
+}
+
+extern "C" {
+
 int mi_generate(mi_engine* e, int32_t n_gen, int32_t* out, float* margins, int32_t* n_out, mi_token_cb cb, void* user) {
     if (!e || n_gen < 0) return MI_ERR_ARG;
     if (!e->next_ready || e->cur_len < 1) return set_err(e, MI_ERR_STATE, "mi_generate needs mi_prefill first");
     if (e->cur_len + n_gen > e->maxseq) return set_err(e, MI_ERR_ARG, "n_gen %d exceeds the context capacity", n_gen);
+    if (e->opts.spec) return generate_spec(e, n_gen, out, margins, n_out, cb, user);
+    e->stats.drafted = e->stats.accepted = 0;
     const int p0 = e->cur_len;                   // position of the first generated token
     const bool sync_each = cb != nullptr || e->opts.stop_eos;
     int emitted = 0;

@@ -39,7 +39,8 @@ class ModelInfo(C.Structure):
 
 
 class Stats(C.Structure):
-    _fields_ = [("steps", C.c_int32), ("tokens", C.c_int32), ("decode_ms", C.c_double), ("prefill_ms", C.c_double)]
+    _fields_ = [("steps", C.c_int32), ("tokens", C.c_int32), ("decode_ms", C.c_double), ("prefill_ms", C.c_double),
+                ("drafted", C.c_int32), ("accepted", C.c_int32)]
 
 
 class SynthShape(C.Structure):
@@ -78,6 +79,8 @@ SIGNATURES = {
     "mi_stream_read": (C.c_int, [_P, C.c_size_t, _P, _P]),
     "mi_stream_sync": (C.c_int, [_P]),
     "mi_device_count": (C.c_int, [C.POINTER(C.c_int32)]),
+    "mi_ngram_draft": (C.c_int32, [C.POINTER(C.c_int32), C.c_int32, C.c_int32, C.c_int32, C.POINTER(C.c_int32)]),
+    "mi_best_draft_len": (C.c_int32, [C.c_float, C.c_float, C.c_int32]),
 }
 
 _lib = None
@@ -246,7 +249,8 @@ class Engine:
     def stats(self):
         s = Stats()
         _check(lib().mi_get_stats(self._h, C.byref(s)), self._h)
-        return dict(steps=s.steps, tokens=s.tokens, decode_ms=s.decode_ms, prefill_ms=s.prefill_ms)
+        return dict(steps=s.steps, tokens=s.tokens, decode_ms=s.decode_ms, prefill_ms=s.prefill_ms,
+                    drafted=s.drafted, accepted=s.accepted)
 
 
 # ---------------------------------------------------------------- kernel-level helpers

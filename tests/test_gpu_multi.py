@@ -7,6 +7,10 @@ tokens one at a time with T = 1, which is itself bit-identical to the q8act
 oracle (test_gpu_engine.py); one case is also checked against the oracle directly.
 Cases cover both chunk sizes of the q4 tiles (cb 8 and cb 4), a step that crosses
 a 64-position attention chunk, and a context past the inline chunk merge.
+
+Speculative generation (n-gram drafts verified by these steps) must be lossless:
+its tokens and margins equal the plain greedy decode (tools/specbench.sh:36 checks
+the same invariant on the reference).
 """
 import sys
 
@@ -116,3 +120,40 @@ def test_multi_step_rejects_bad_T():
     with pytest.raises(minfer.MinferError):
         eng.step(list(range(9)), 3)
     eng.close()
+
+
+def spec_vs_plain(path, prompt, n_gen, max_ctx):
+    res = {}
+    for spec in (0, 1):
+        eng = minfer.Engine(path, max_ctx=max_ctx, spec=spec)
+        eng.prefill(prompt)
+        toks, margins = eng.generate(n_gen)
+        res[spec] = (toks, margins, eng.stats())
+        eng.close()
+    (pt, pm, _), (st, sm, ss) = res[0], res[1]
+    assert st == pt, "speculative output differs from plain greedy at %d" % next(
+        i for i, (a, b) in enumerate(zip(st, pt)) if a != b)
+    assert np.array_equal(bits(sm), bits(pm))
+    return ss
+
+
+@pytest.mark.parametrize("name", ["config0", "config2"])
+def test_spec_generate_equals_plain(name):
+    cfg = minfer.CONFIGS[name]
+    shape = minfer.SHAPES[cfg[0]]
+    path = synth_cached(name, shape, cfg[1])
+    prompt = minfer.prompt_ids(cfg[2], cfg[3], shape["n_vocab"])
+    st = spec_vs_plain(path, prompt, 128, cfg[3] + 160)
+    say("%s speculative: %d verify steps for %d tokens, %d drafted, %d accepted" %
+        (name, st["steps"], st["tokens"], st["drafted"], st["accepted"]))
+    assert st["tokens"] == 128 and st["steps"] <= 128
+
+
+def test_spec_generate_repetitive_prompt():
+    """a prompt that repeats a 12-token pattern: the drafter proposes from the start"""
+    path = synth_cached("eng-512", SMALL, 21)
+    pattern = minfer.prompt_ids(31, 12, SMALL["n_vocab"])
+    st = spec_vs_plain(path, pattern * 6, 96, 200)
+    say("repetitive prompt: %d verify steps for %d tokens, %d drafted, %d accepted" %
+        (st["steps"], st["tokens"], st["drafted"], st["accepted"]))
+    assert st["drafted"] > 0
