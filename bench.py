@@ -118,6 +118,61 @@ def stream_bw(torch, gib=4, reps=5):
     return gbps
 
 
+def ensure_gguf(name):
+    shape, mseed, _, _, _ = minfer.CONFIGS[name]
+    tmp = os.path.join(os.environ.get("TMPDIR", "/tmp"), "mi-bench")
+    os.makedirs(tmp, exist_ok=True)
+    path = os.path.join(tmp, "%s-%d.gguf" % (name, mseed))
+    if not os.path.exists(path + ".ok"):
+        t = time.time()
+        minfer.synth_gguf(path, shape, mseed)
+        open(path + ".ok", "w").close()
+        log("wrote %s in %.1f s" % (path, time.time() - t))
+    return path
+
+
+def spec_decode(path, prompt, n_gen=128):
+    """config2 with speculative decoding (n-gram drafts, verify steps): lossless, so
+    the tokens equal the plain run's; wall-clock tok/s of the generation"""
+    eng = minfer.Engine(path, max_ctx=len(prompt) + n_gen + 16, spec=1)
+    eng.prefill(prompt)
+    eng.generate(8)
+    eng.prefill(prompt)
+    t0 = time.perf_counter()
+    toks, _ = eng.generate(n_gen)
+    dt = time.perf_counter() - t0
+    st = eng.stats()
+    eng.close()
+    return toks, dict(tok_s=round(n_gen / dt, 2), verify_steps=st["steps"], drafted=st["drafted"],
+                      accepted=st["accepted"], tokens_per_step=round(n_gen / max(st["steps"], 1), 3))
+
+
+def verify_cost(reps=10):
+    """config4: S3 (hidden 2048, 36 layers), context 1024; a T=8 verify step (the
+    current token + 7 drafts, TMAX = 8) against a T=1 step at the same position.
+    Wall time per mi_step call (upload, step, copy-back), mean of reps."""
+    shape, _, pseed, ctx, _ = minfer.CONFIGS["config4"]
+    path = ensure_gguf("config4")
+    V = minfer.SHAPES[shape]["n_vocab"]
+    eng = minfer.Engine(path, max_ctx=ctx + 16)
+    prompt = minfer.prompt_ids(pseed, ctx, V)
+    eng.prefill(prompt)
+    toks = minfer.prompt_ids(pseed + 1, 8, V)
+    out = {}
+    for T in (1, 8):
+        arg = toks[:T] if T > 1 else toks[0]
+        for _ in range(3):
+            eng.step(arg, ctx)
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            eng.step(arg, ctx)
+        out[T] = (time.perf_counter() - t0) / reps * 1e3
+    eng.close()
+    return dict(workload="config4: S3 q4_0, context 1024, verify T=8 vs T=1", t1_ms=round(out[1], 3),
+                t8_ms=round(out[8], 3), ratio=round(out[8] / out[1], 3),
+                note="T=8 = current token + 7 drafts (TMAX 8, mega.cu:50); the config's 8 drafts + 1 would be T=9")
+
+
 def cpu_baseline(path, prompt, n_prompt=64, n_gen=129):
     """oracle fp32 (cpu_infer semantics) on the host cores: the whole config2
     workload (64-token prompt, 128 decode steps), about 15 s on 16 threads"""
@@ -141,6 +196,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-micro", action="store_true")
     ap.add_argument("--persistent", type=int, default=1)
+    ap.add_argument("--no-extra", action="store_true", help="skip the speculative and verify-step measurements")
     ap.add_argument("--copy-calib", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB three times (calibrates the "
                          "rocprofv3 FETCH_SIZE/WRITE_SIZE counters) and exit")
@@ -161,14 +217,7 @@ def main():
     import torch
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     shape, mseed, pseed, n_prompt, _ = minfer.CONFIGS["config2"]
-    tmp = os.path.join(os.environ.get("TMPDIR", "/tmp"), "mi-bench")
-    os.makedirs(tmp, exist_ok=True)
-    path = os.path.join(tmp, "config2-%d.gguf" % mseed)
-    if not os.path.exists(path + ".ok"):
-        t = time.time()
-        minfer.synth_gguf(path, shape, mseed)
-        open(path + ".ok", "w").close()
-        log("wrote %s in %.1f s" % (path, time.time() - t))
+    path = ensure_gguf("config2")
     V = minfer.SHAPES[shape]["n_vocab"]
     prompt = minfer.prompt_ids(pseed, n_prompt, V)
     t = time.time()
@@ -213,6 +262,13 @@ def main():
     micro = [] if args.no_micro else gemv_microbench(torch)
     for m in micro:
         log("gemv %-8s %6d x %5d: %8.2f us  %7.1f GB/s" % (m["shape"], m["rows"], m["k"], m["us"], m["gbps"]))
+    spec = verify = None
+    if not args.no_extra:
+        stoks, spec = spec_decode(path, prompt, args.steps + 1)
+        spec["identical_to_plain"] = stoks == toks
+        log("speculative decode: %s" % spec)
+        verify = verify_cost()
+        log("verify step: %s" % verify)
     cpu = None if args.no_cpu else cpu_baseline(path, prompt)
     if cpu:
         log("cpu baseline: %s" % cpu)
@@ -239,6 +295,8 @@ def main():
         "gemv": micro,
         "device_decode_ms": round(st["decode_ms"], 3),
         "cpu_baseline": cpu,
+        "speculative": spec,
+        "verify_step": verify,
         "tokens_head": toks[:8],
     }
     print(json.dumps(rec), flush=True)
