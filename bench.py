@@ -22,6 +22,8 @@ Prints ONE JSON line on stdout. Besides the contract keys it carries:
   stream_gbps   one-launch stream read of a 4 GiB buffer (> the 256 MB MALL)
   gemv          config 1 microbench: each S15 GEMV shape, rotated over copies
                 totalling > 512 MB so every launch reads from HBM
+  attention_depth  config 3: S15 decode attention at L = 512..32768, 28 rotated
+                layer caches, GB/s of K/V read per layer
   cpu_baseline  the oracle's fp32 mode (a restatement of cpu_infer.cpp whose
                 token streams equal the reference binary's) on this host's cores
 """
@@ -173,6 +175,36 @@ def verify_cost(reps=10):
                 note="T=8 = current token + 7 drafts (TMAX 8, mega.cu:50); the config's 8 drafts + 1 would be T=9")
 
 
+def attention_depth(torch, lengths=(512, 4096, 16384, 32768), layers=28, reps=3):
+    """config3: S15 split-KV decode attention (12/2 heads, hd 128), one query, fp16 K/V
+    N(0,1) at context L, rotated over 28 layers' caches (28 x 32 MB at L = 32768 > the
+    256 MB MALL). Algorithmic bytes per layer: 1024*L (K and V) + q/out."""
+    nh, nkv, hd = 12, 2, 128
+    res = []
+    for L in lengths:
+        kc = torch.randn(layers, nkv, L, hd, device="cuda").half()
+        vc = torch.randn(layers, nkv, L, hd, device="cuda").half()
+        q = torch.randn(nh, hd, device="cuda")
+        scratch = torch.zeros(minfer.attn_scratch_floats(nh, hd, L), device="cuda")
+        out = torch.empty(nh * hd, device="cuda")
+        scale = 1.0 / hd ** 0.5
+        for l in range(2):
+            minfer.attn_decode(q, kc[l], vc[l], nh, nkv, hd, L, L, scale, scratch, out)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            for l in range(layers):
+                minfer.attn_decode(q, kc[l], vc[l], nh, nkv, hd, L, L, scale, scratch, out)
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / (reps * layers)
+        byt = 1024 * L + 2 * nh * hd * 4
+        res.append(dict(L=L, us_per_layer=round(us, 2), gbps=round(byt / us / 1e3, 1)))
+        del kc, vc
+    torch.cuda.empty_cache()
+    return res
+
+
 def cpu_baseline(path, prompt, n_prompt=64, n_gen=129):
     """oracle fp32 (cpu_infer semantics) on the host cores: the whole config2
     workload (64-token prompt, 128 decode steps), about 15 s on 16 threads"""
@@ -262,6 +294,9 @@ def main():
     micro = [] if args.no_micro else gemv_microbench(torch)
     for m in micro:
         log("gemv %-8s %6d x %5d: %8.2f us  %7.1f GB/s" % (m["shape"], m["rows"], m["k"], m["us"], m["gbps"]))
+    attn = [] if args.no_micro else attention_depth(torch)
+    for a in attn:
+        log("attention L=%-6d %8.2f us/layer  %7.1f GB/s" % (a["L"], a["us_per_layer"], a["gbps"]))
     spec = verify = None
     if not args.no_extra:
         stoks, spec = spec_decode(path, prompt, args.steps + 1)
@@ -293,6 +328,7 @@ def main():
                           "roofline_tok_s": round(stream * 1e9 / bpt, 1)},
         "stream_gbps": round(stream, 1),
         "gemv": micro,
+        "attention_depth": attn,
         "device_decode_ms": round(st["decode_ms"], 3),
         "cpu_baseline": cpu,
         "speculative": spec,

@@ -31,6 +31,7 @@ constexpr int kMaxWaves = 8;
 constexpr int kAttnWaves = 2;      // waves per workgroup that take attention items (LDS bound)
 constexpr int kAttnChunk = 64;     // positions per attention partial
 constexpr int kInlineComb = 4;     // up to this many chunks the O phase merges them itself
+constexpr int kAttnSplit = 16;     // past this many chunks the records merge as a two-level tree
 constexpr int kActRec = 128;       // bytes per act block record (32 int8, scale, 8*sum, padding)
 constexpr int kMaxE = 2048;        // largest hidden size the LDS staging holds
 constexpr int kMaxFF = 11264;      // largest FFN width the LDS staging holds

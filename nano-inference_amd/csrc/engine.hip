@@ -824,6 +824,10 @@ int mi_attn_decode(const float* q, const uint16_t* kc, const uint16_t* vc, int32
     return hipGetLastError() == hipSuccess ? MI_OK : MI_ERR_DEVICE;
 }
 
+size_t mi_attn_scratch_floats(int32_t n_head, int32_t hd, int32_t L) {
+    return n_head < 1 || hd < 1 || L < 1 ? 0 : attn_scratch_floats(n_head, hd, L);
+}
+
 int mi_stream_read(const void* buf, size_t bytes, uint32_t* sink, void* stream) {
     if (!buf || !sink || bytes % 16) return MI_ERR_ARG;
     launch_stream(buf, bytes, sink, ncu(), (hipStream_t)stream);

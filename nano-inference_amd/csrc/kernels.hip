@@ -826,15 +826,65 @@ __device__ __forceinline__ void attn_run(MPtr M, int l, int pos, int wg, int nwg
     }
 }
 
-// merge of one (head, dim) from the chunk records in chunk order (cuda_infer.cu:688-702)
+// max-first merge of the chunk records [c0, c1) for dim d (cuda_infer.cu:688-702
+// attn_combine): M = max m_c, w_c = exp(m_c - M), den and acc as fma chains over the
+// chunks in order. Returns acc (not yet divided by den). UNROLL: c1 - c0 <=
+// kAttnSplit, all loads issued before the arithmetic.
+template <bool UNROLL>
+__device__ __forceinline__ float merge_recs(const float* r, int rec, int hd, int d, int c0, int c1, float& Mo,
+                                            float& deno) {
+    float M = -__builtin_inff(), den = 0.f, acc = 0.f;
+    if constexpr (UNROLL) {
+        float mv[kAttnSplit], lv[kAttnSplit], ov[kAttnSplit];
+#pragma unroll
+        for (int i = 0; i < kAttnSplit; i++) {
+            const int c = min(c0 + i, c1 - 1);
+            mv[i] = r[c * rec + hd];
+            lv[i] = r[c * rec + hd + 1];
+            ov[i] = r[c * rec + d];
+        }
+#pragma unroll
+        for (int i = 0; i < kAttnSplit; i++)
+            if (c0 + i < c1) M = fmaxf(M, mv[i]);
+#pragma unroll
+        for (int i = 0; i < kAttnSplit; i++)
+            if (c0 + i < c1) {
+                const float w = mi_expf(__fsub_rn(mv[i], M));
+                den = __fmaf_rn(lv[i], w, den);
+                acc = __fmaf_rn(ov[i], w, acc);
+            }
+    } else {
+        for (int c = c0; c < c1; c++) M = fmaxf(M, r[c * rec + hd]);
+        for (int c = c0; c < c1; c++) {
+            const float w = mi_expf(__fsub_rn(r[c * rec + hd], M));
+            den = __fmaf_rn(r[c * rec + hd + 1], w, den);
+            acc = __fmaf_rn(r[c * rec + d], w, acc);
+        }
+    }
+    Mo = M;
+    deno = den;
+    return acc;
+}
+// all nch records of one (head, dim) merged in one level
 __device__ __forceinline__ float combine_one(const float* recs, int rec, int hd, int d, int nch) {
+    float M, den;
+    const float acc = merge_recs<false>(recs, rec, hd, d, 0, nch, M, den);
+    return __fdiv_rn(acc, den);
+}
+// the canonical merge: one level up to kAttnSplit chunks, else each split of kAttnSplit
+// chunks merged (M_s, den_s, acc_s), then the splits in order the same way; the
+// global max equals the max over the split maxima
+__device__ __forceinline__ float combine_tree(const float* recs, int rec, int hd, int d, int nch) {
+    if (nch <= kAttnSplit) return combine_one(recs, rec, hd, d, nch);
     float Mx = -__builtin_inff();
     for (int c = 0; c < nch; c++) Mx = fmaxf(Mx, recs[c * rec + hd]);
     float den = 0.f, acc = 0.f;
-    for (int c = 0; c < nch; c++) {
-        const float w = mi_expf(__fsub_rn(recs[c * rec + hd], Mx));
-        den = __fmaf_rn(recs[c * rec + hd + 1], w, den);
-        acc = __fmaf_rn(recs[c * rec + d], w, acc);
+    for (int c0 = 0; c0 < nch; c0 += kAttnSplit) {
+        float Ms, ds;
+        const float as = merge_recs<false>(recs, rec, hd, d, c0, min(nch, c0 + kAttnSplit), Ms, ds);
+        const float w = mi_expf(__fsub_rn(Ms, Mx));
+        den = __fmaf_rn(ds, w, den);
+        acc = __fmaf_rn(as, w, acc);
     }
     return __fdiv_rn(acc, den);
 }
@@ -845,7 +895,7 @@ __device__ __forceinline__ void phase_comb(MPtr M, int l, int pos, int wg, int n
     const float* att = att_rec(M, l);
     float* out = M->att_out + (size_t)l * M->E;
     for (int it = wg * blockDim.x + threadIdx.x; it < M->E; it += nwg * blockDim.x)
-        stc(out + it, combine_one(att + (size_t)(it / M->HD) * M->maxch * M->arec, M->arec, M->HD, it % M->HD, nch));
+        stc(out + it, combine_tree(att + (size_t)(it / M->HD) * M->maxch * M->arec, M->arec, M->HD, it % M->HD, nch));
 }
 
 // ------------------------------------------------------------------ the persistent step
@@ -1381,7 +1431,7 @@ __global__ __launch_bounds__(kPThreads) void kT_comb(const DModel* Mp, int l, in
     for (int it = blockIdx.x * blockDim.x + threadIdx.x; it < T * n; it += gridDim.x * blockDim.x) {
         const int t = it / n, e = it - t * n, nch = (pos + t + kAttnChunk) / kAttnChunk;
         M->att_outT[((size_t)l * kMaxT + t) * n + e] =
-            combine_one(attT_at(M, l, t) + (size_t)(e / M->HD) * M->maxch * M->arec, M->arec, M->HD, e % M->HD, nch);
+            combine_tree(attT_at(M, l, t) + (size_t)(e / M->HD) * M->maxch * M->arec, M->arec, M->HD, e % M->HD, nch);
     }
 }
 
@@ -1575,37 +1625,222 @@ __global__ __launch_bounds__(64) void k_isums(PMat W, const int8_t* xq, int32_t*
     isum[(size_t)(g * 64 + lane) * W.nb + b] = dot_q4(w, xp[0], xp[1]);
 }
 
-// standalone attention: q[nh][hd] and an fp16 cache [nkv][ctx][hd]; records [nh][nch][hd+32]
+// ------------------------------------------------------------------ standalone attention
+// q[nh][hd] fp32 and an fp16 cache [nkv][ctx][hd]; one launch does the whole
+// attention. One item = (kv head, 64-position chunk, group of g query heads of that
+// kv head). The wave loads the chunk's K rows lane = position (16-byte pieces) and V
+// rows lane = dims (4 or 2 bytes per position) straight into registers, so K/V are
+// read once per item and never staged in LDS; the g heads then reuse them. Per head
+// the arithmetic is attn_core's: scores as four fma chains over d mod 4, the chunk
+// softmax with the 64-lane butterfly sum, p.v as an fma chain over positions.
+// The merge is combine_tree's, done by the last arrivals: after its chunk records
+// (o[hd], m, l) are stored and drained, an item bumps its split's counter; the wave
+// that completes a split merges its chunks (and writes the output if there is one
+// split), then bumps the head group's counter, whose last arrival merges the splits.
+// Records are written with agent-coherent stores (through the per-XCD L2) and
+// drained before the arrival atomic; every record line has one writer and one
+// reader in a launch, and the merging wave reads it (by DMA) only after all its
+// writers arrived, so no L2 can hold an older copy. No wave ever waits on another.
+// Each last arrival puts its counter back to zero.
+// scratch: counters [kAttnCounters] (zero before the first call, left zero by each
+// call) | chunk records [nh][nch][hd + 32] | split records [nh][nsp][hd + 32].
+constexpr int kItemWaves = 4;       // waves per workgroup
+constexpr int kItemMaxG = 8;        // query heads one item can take
+constexpr int kItemWgsPerXcd = 64;  // two workgroups per CU
+constexpr int kItemTarget = 2048;   // items to aim for: two per SIMD
+constexpr int kAttnCounters = 1 << 16;
+
+template <int HD, bool FULL>
+__device__ __forceinline__ void attn_item_heads(const __half* kr, const __half* vr, int n, const float* qsrc, float* qg,
+                                                float* pg, int g, float scale, int lane, float* rec, size_t hstride) {
+    constexpr int NV = HD / 8, DPL = HD / 64;
+    using VT = typename std::conditional<DPL == 2, uint32_t, uint16_t>::type;
+    uint4 kw[NV];
+    VT vw[64];
+    const uint4* kp = reinterpret_cast<const uint4*>(kr + (size_t)(FULL ? lane : min(lane, n - 1)) * HD);
+#pragma unroll
+    for (int j = 0; j < NV; j++) kw[j] = kp[j];
+#pragma unroll
+    for (int t = 0; t < 64; t++)
+        vw[t] = *reinterpret_cast<const VT*>(vr + (size_t)(FULL ? t : min(t, n - 1)) * HD + DPL * lane);
+    for (int i = lane; i < g * HD; i += 64) qg[i] = qsrc[i];   // the g query rows, behind the K/V loads
+    wave_lds_sync();
+    float kf[HD];
+#pragma unroll
+    for (int j = 0; j < NV; j++) {
+        kf[8 * j + 0] = h2f_lo(kw[j].x); kf[8 * j + 1] = h2f_hi(kw[j].x);
+        kf[8 * j + 2] = h2f_lo(kw[j].y); kf[8 * j + 3] = h2f_hi(kw[j].y);
+        kf[8 * j + 4] = h2f_lo(kw[j].z); kf[8 * j + 5] = h2f_hi(kw[j].z);
+        kf[8 * j + 6] = h2f_lo(kw[j].w); kf[8 * j + 7] = h2f_hi(kw[j].w);
+    }
+    const bool valid = FULL || lane < n;
+    for (int hh = 0; hh < g; hh++) {
+        const float* qh = qg + hh * HD;
+        float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+#pragma unroll
+        for (int j = 0; j < NV; j++) {
+            const float4 q0 = ld4(qh + 8 * j), q1 = ld4(qh + 8 * j + 4);
+            a0 = __fmaf_rn(q0.x, kf[8 * j + 0], a0); a1 = __fmaf_rn(q0.y, kf[8 * j + 1], a1);
+            a2 = __fmaf_rn(q0.z, kf[8 * j + 2], a2); a3 = __fmaf_rn(q0.w, kf[8 * j + 3], a3);
+            a0 = __fmaf_rn(q1.x, kf[8 * j + 4], a0); a1 = __fmaf_rn(q1.y, kf[8 * j + 5], a1);
+            a2 = __fmaf_rn(q1.z, kf[8 * j + 6], a2); a3 = __fmaf_rn(q1.w, kf[8 * j + 7], a3);
+        }
+        const float sc = __fmul_rn(__fadd_rn(__fadd_rn(a0, a1), __fadd_rn(a2, a3)), scale);
+        const float sv = valid ? sc : -__builtin_inff();
+        const float m = wave_max(sv);
+        const float p = valid ? mi_expf(__fsub_rn(sv, m)) : 0.f;
+        const float lsum = bfly_sum64(p);
+        pg[hh * 64 + lane] = p;
+        if (lane == 0) {
+            stc(rec + hh * hstride + HD, m);
+            stc(rec + hh * hstride + HD + 1, lsum);
+        }
+    }
+    wave_lds_sync();
+    float vf[64 * DPL];
+#pragma unroll
+    for (int t = 0; t < 64; t++) {
+        if constexpr (DPL == 2) {
+            vf[2 * t] = h2f_lo(vw[t]);
+            vf[2 * t + 1] = h2f_hi(vw[t]);
+        } else {
+            vf[t] = __half2float(__ushort_as_half(vw[t]));
+        }
+    }
+    for (int hh = 0; hh < g; hh++) {
+        const float* ph = pg + hh * 64;
+        float acc[DPL];
+#pragma unroll
+        for (int e = 0; e < DPL; e++) acc[e] = 0.f;
+#pragma unroll
+        for (int t4 = 0; t4 < 16; t4++) {
+            const float4 p4 = ld4(ph + 4 * t4);
+            const float pv[4] = {p4.x, p4.y, p4.z, p4.w};
+#pragma unroll
+            for (int u = 0; u < 4; u++)
+                if (FULL || 4 * t4 + u < n) {
+#pragma unroll
+                    for (int e = 0; e < DPL; e++) acc[e] = __fmaf_rn(pv[u], vf[(4 * t4 + u) * DPL + e], acc[e]);
+                }
+        }
+#pragma unroll
+        for (int e = 0; e < DPL; e++) stc(rec + hh * hstride + DPL * lane + e, acc[e]);
+    }
+    wave_lds_sync();   // the wave's q/p staging is reused by its next item
+}
+
+// One wave merges the records [c0, c1) of one head (contiguous, REC floats each)
+// as merge_recs does, lane = dims DPL*lane + e: M = max over all records, w_i =
+// exp(m_i - M), then den and acc as fma chains in record order. The records come
+// into LDS 16 at a time by DMA (lds: 16 * REC floats); w_i and l_i reach every lane
+// by readlane. The loops stay rolled: this code runs once per split on a CU that
+// has not run it before, so its size is paid in instruction fetches.
 template <int HD>
-__global__ __launch_bounds__(kThreads) void k_attn_standalone(const float* q, const __half* kc, const __half* vc, int nh,
-                                                               int nkv, int L, int ctx, float scale, float* recs) {
-    constexpr int DPL = HD / 64, REC = HD + 32;
-    __shared__ __align__(16) uint8_t smem[kAttnWaves * attn_wave_lds<HD>()];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    if (wave >= kAttnWaves) return;
-    const int nch = (L + kAttnChunk - 1) / kAttnChunk, items = nh * nch, G = nh / nkv;
-    uint8_t* lds = smem + wave * attn_wave_lds<HD>();
-    uint4* kls = reinterpret_cast<uint4*>(lds);
-    __half* vls = reinterpret_cast<__half*>(lds + 64 * HD * 2);
-    float* qs = reinterpret_cast<float*>(lds + 2 * 64 * HD * 2) + 3 * kMaxKsQkv * HD;
-    for (int it = blockIdx.x * kAttnWaves + wave; it < items; it += gridDim.x * kAttnWaves) {
-        const int h = it / nch, c = it % nch, kvh = h / G, t0 = c * kAttnChunk, n = min(kAttnChunk, L - t0);
-        attn_issue_kv<HD>(kc + (size_t)kvh * ctx * HD, vc + (size_t)kvh * ctx * HD, t0, n, kls, vls, lane);
-        for (int i = lane; i < HD; i += 64) qs[i] = q[(size_t)h * HD + i];
+__device__ __forceinline__ void lds_merge(const float* r, int c0, int c1, float* lds, int lane, float& Mo, float& deno,
+                                          float (&acc)[HD / 64]) {
+    constexpr int REC = HD + 32, DPL = HD / 64;
+    float M = -__builtin_inff();
+    if (c1 - c0 > kAttnSplit) {                       // the max first when it spans batches
+        for (int b = c0; b < c1; b += 64) M = fmaxf(M, b + lane < c1 ? r[(size_t)(b + lane) * REC + HD] : -__builtin_inff());
+        M = wave_max(M);
+    }
+    float den = 0.f;
+#pragma unroll
+    for (int e = 0; e < DPL; e++) acc[e] = 0.f;
+    for (int b = c0; b < c1; b += kAttnSplit) {
+        const int n = min(kAttnSplit, c1 - b);
+        dma_wave(r + (size_t)b * REC, lds, n * REC * 4, lane);
         drain_vm();
         wave_lds_sync();
-        float m, lsum, acc[DPL];
-        attn_core<HD>(kls, qs, vls, n, scale, lane, m, lsum, acc);
-        float* rec = recs + ((size_t)h * nch + c) * REC;
+        const float m = lane < n ? lds[lane * REC + HD] : -__builtin_inff();
+        if (c1 - c0 <= kAttnSplit) M = wave_max(m);
+        const float w = lane < n ? mi_expf(__fsub_rn(m, M)) : 0.f;
+        const int wb = __float_as_int(w), lb = __float_as_int(lane < n ? lds[lane * REC + HD + 1] : 0.f);
+        for (int i = 0; i < n; i++) {
+            const float wi = __int_as_float(__builtin_amdgcn_readlane(wb, i));
+            den = __fmaf_rn(__int_as_float(__builtin_amdgcn_readlane(lb, i)), wi, den);
 #pragma unroll
-        for (int e = 0; e < DPL; e++) rec[DPL * lane + e] = acc[e];
-        if (lane == 0) { rec[HD] = m; rec[HD + 1] = lsum; }
+            for (int e = 0; e < DPL; e++) acc[e] = __fmaf_rn(lds[i * REC + DPL * lane + e], wi, acc[e]);
+        }
         wave_lds_sync();
     }
+    Mo = M;
+    deno = den;
 }
-__global__ __launch_bounds__(kThreads) void k_comb_standalone(const float* recs, int nh, int hd, int nch, float* out) {
-    for (int it = blockIdx.x * blockDim.x + threadIdx.x; it < nh * hd; it += gridDim.x * blockDim.x)
-        out[it] = combine_one(recs + (size_t)(it / hd) * nch * (hd + 32), hd + 32, hd, it % hd, nch);
+
+// the wave's arrival on a counter of `need` arrivals: true for the last one, which
+// puts the counter back to zero (every arrival of this launch is in by then)
+__device__ __forceinline__ bool last_arrival(uint32_t* cnt, uint32_t need, int lane) {
+    drain_vm();                                    // this wave's record stores are done
+    uint32_t old = 0;
+    if (lane == 0) old = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    old = __builtin_amdgcn_readfirstlane(old);
+    if (old + 1 != need) return false;
+    if (lane == 0) stc(cnt, 0u);
+    return true;
+}
+
+// Items of unit u = kvh * nch + c and head group hg go to XCD u % 8 (workgroups
+// x, x + 8, ... share XCD x), so the groups of one unit read its K/V through one L2.
+// Within XCD x the items k = (u / 8) * ngrp + hg are dealt to (workgroup, wave) in
+// turn; the grid is a multiple of 8.
+template <int HD>
+__global__ __launch_bounds__(64 * kItemWaves) __attribute__((amdgpu_waves_per_eu(2))) void k_attn_fused(const float* q, const __half* kc, const __half* vc,
+                                                                int nh, int nkv, int L, int ctx, float scale, int g,
+                                                                float* scratch, float* out) {
+    constexpr int REC = HD + 32, DPL = HD / 64;
+    constexpr int WLDS = kItemMaxG * (HD + 64) > kAttnSplit * REC ? kItemMaxG * (HD + 64) : kAttnSplit * REC;
+    __shared__ __align__(16) float smem[kItemWaves * WLDS];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    float* qg = smem + wave * WLDS;
+    float* pg = qg + kItemMaxG * HD;
+    const int nch = (L + kAttnChunk - 1) / kAttnChunk, G = nh / nkv, ngrp = G / g, units = nkv * nch;
+    const int nsp = (nch + kAttnSplit - 1) / kAttnSplit;
+    uint32_t* scnt = reinterpret_cast<uint32_t*>(scratch);          // [nkv][nsp][ngrp]
+    uint32_t* hcnt = scnt + (size_t)nkv * nsp * ngrp;                // [nkv][ngrp]
+    float* recs = scratch + kAttnCounters;
+    float* srecs = recs + (size_t)nh * nch * REC;
+    const int per = gridDim.x / 8, x = blockIdx.x % 8;
+    for (int k = kItemWaves * (blockIdx.x / 8) + wave;; k += kItemWaves * per) {
+        const int u = 8 * (k / ngrp) + x, hg = k % ngrp;
+        if (u >= units) break;
+        const int kvh = u / nch, c = u % nch, h0 = kvh * G + hg * g, t0 = c * kAttnChunk, n = min(kAttnChunk, L - t0);
+        const size_t row = (size_t)kvh * ctx + t0;
+        float* rec = recs + ((size_t)h0 * nch + c) * REC;
+        if (n == kAttnChunk)
+            attn_item_heads<HD, true>(kc + row * HD, vc + row * HD, n, q + (size_t)h0 * HD, qg, pg, g, scale, lane, rec,
+                                      (size_t)nch * REC);
+        else
+            attn_item_heads<HD, false>(kc + row * HD, vc + row * HD, n, q + (size_t)h0 * HD, qg, pg, g, scale, lane,
+                                       rec, (size_t)nch * REC);
+        const int sp = c / kAttnSplit, c0 = sp * kAttnSplit, c1 = min(nch, c0 + kAttnSplit);
+        if (!last_arrival(scnt + ((size_t)kvh * nsp + sp) * ngrp + hg, c1 - c0, lane)) continue;
+        for (int hh = 0; hh < g; hh++) {      // level 1: the split's chunks -> the output or a split record
+            const int h = h0 + hh;
+            float M, den, acc[DPL];
+            lds_merge<HD>(recs + (size_t)h * nch * REC, c0, c1, qg, lane, M, den, acc);
+            if (nsp == 1) {
+#pragma unroll
+                for (int e = 0; e < DPL; e++) out[(size_t)h * HD + DPL * lane + e] = __fdiv_rn(acc[e], den);
+            } else {
+                float* sr = srecs + ((size_t)h * nsp + sp) * REC;
+#pragma unroll
+                for (int e = 0; e < DPL; e++) stc(sr + DPL * lane + e, acc[e]);
+                if (lane == 0) {
+                    stc(sr + HD, M);
+                    stc(sr + HD + 1, den);
+                }
+            }
+        }
+        if (nsp == 1 || !last_arrival(hcnt + (size_t)kvh * ngrp + hg, nsp, lane)) continue;
+        for (int hh = 0; hh < g; hh++) {      // level 2: the splits -> the output
+            const int h = h0 + hh;
+            float M, den, acc[DPL];
+            lds_merge<HD>(srecs + (size_t)h * nsp * REC, 0, nsp, qg, lane, M, den, acc);
+#pragma unroll
+            for (int e = 0; e < DPL; e++) out[(size_t)h * HD + DPL * lane + e] = __fdiv_rn(acc[e], den);
+        }
+    }
 }
 
 __global__ __launch_bounds__(kThreads) void k_stream(const u32x4* __restrict__ p, size_t n4, uint32_t* sink) {
@@ -1741,15 +1976,28 @@ void launch_gemv(const PMat& W, const int8_t* xq, const float* xd, const int32_t
 void launch_isums(const PMat& W, const int8_t* xq, int32_t* isum, hipStream_t s) {
     hipLaunchKernelGGL(k_isums, dim3(W.rows / 64, W.nb), dim3(64), 0, s, W, xq, isum);
 }
+size_t attn_scratch_floats(int nh, int hd, int L) {
+    const int nch = (L + kAttnChunk - 1) / kAttnChunk, nsp = (nch + kAttnSplit - 1) / kAttnSplit;
+    return kAttnCounters + (size_t)nh * (nch + (nsp > 1 ? nsp : 0)) * (hd + 32);
+}
 bool launch_attn_decode(const float* q, const __half* kc, const __half* vc, int nh, int nkv, int hd, int L, int ctx,
                         float scale, float* scratch, float* out, hipStream_t s) {
-    if (nh % nkv || !kernels_support(nh / nkv, hd)) return false;
-    const int nch = (L + kAttnChunk - 1) / kAttnChunk;
-    const int grid = std::max(1, std::min(1 << 16, (nh * nch + kAttnWaves - 1) / kAttnWaves));
+    if (nh % nkv || !kernels_support(nh / nkv, hd) || nh / nkv > kItemMaxG) return false;
+    const int G = nh / nkv, nch = (L + kAttnChunk - 1) / kAttnChunk, units = nkv * nch;
+    const int nsp = (nch + kAttnSplit - 1) / kAttnSplit;
+    // counters: nkv * nsp * ngrp + nkv * ngrp <= nh * (nsp + 1)
+    if ((size_t)nh * (nsp + 1) > (size_t)kAttnCounters) return false;
+    // head groups per unit: the fewest (largest g, K/V read by fewer items) that still
+    // give kItemTarget items
+    int ngrp = 1;
+    while (ngrp < G && units * ngrp < kItemTarget) {
+        do ngrp++; while (G % ngrp);
+    }
+    const int per = std::max(1, std::min(kItemWgsPerXcd, ((units + 7) / 8 * ngrp + kItemWaves - 1) / kItemWaves));
     with_hd(hd, [&](auto h) {
-        LAUNCH((k_attn_standalone<decltype(h)::value>), grid, kThreads, s, q, kc, vc, nh, nkv, L, ctx, scale, scratch);
+        LAUNCH((k_attn_fused<decltype(h)::value>), 8 * per, 64 * kItemWaves, s, q, kc, vc, nh, nkv, L, ctx, scale,
+               G / ngrp, scratch, out);
     });
-    LAUNCH(k_comb_standalone, (nh * hd + kThreads - 1) / kThreads, kThreads, s, scratch, nh, hd, nch, out);
     return true;
 }
 void launch_stream(const void* buf, size_t bytes, uint32_t* sink, int n_cu, hipStream_t s) {

@@ -42,6 +42,7 @@ void launch_quant(const float* x, int n, int8_t* xq, float* xd, int32_t* xs8, hi
 void launch_gemv(const PMat& W, const int8_t* xq, const float* xd, const int32_t* xs8, float* part, float* y,
                  int n_cu, hipStream_t s);
 void launch_isums(const PMat& W, const int8_t* xq, int32_t* isum, hipStream_t s);
+size_t attn_scratch_floats(int nh, int hd, int L);
 bool launch_attn_decode(const float* q, const __half* kc, const __half* vc, int nh, int nkv, int hd, int L, int ctx,
                         float scale, float* scratch, float* out, hipStream_t s);
 void launch_stream(const void* buf, size_t bytes, uint32_t* sink, int n_cu, hipStream_t s);

@@ -76,6 +76,7 @@ SIGNATURES = {
     "mi_q4_block_isums": (C.c_int, [_P, C.c_int32, C.c_int32, C.c_int32, _P, _P, _P]),
     "mi_attn_decode": (C.c_int, [_P, _P, _P, C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_float,
                                  _P, _P, _P]),
+    "mi_attn_scratch_floats": (C.c_size_t, [C.c_int32, C.c_int32, C.c_int32]),
     "mi_stream_read": (C.c_int, [_P, C.c_size_t, _P, _P]),
     "mi_stream_sync": (C.c_int, [_P]),
     "mi_device_count": (C.c_int, [C.POINTER(C.c_int32)]),
@@ -292,6 +293,11 @@ def gemv_q4(packed, rows, nb, cb, ks, xq, xd, xs8, part, y=None, stream=None):
 
 def q4_block_isums(packed, rows, nb, cb, xq, isum, stream=None):
     _check(lib().mi_q4_block_isums(_ptr(packed), rows, nb, cb, _ptr(xq), _ptr(isum), _stream(stream)))
+
+
+def attn_scratch_floats(n_head, hd, L):
+    """floats of scratch attn_decode needs for n_head heads of size hd over L positions"""
+    return int(lib().mi_attn_scratch_floats(n_head, hd, L))
 
 
 def attn_decode(q, kc, vc, n_head, n_head_kv, hd, L, ctx, scale, scratch, out, stream=None):

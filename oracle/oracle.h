@@ -112,6 +112,10 @@ int orc_generate(orc_model* m, const int32_t* prompt, int32_t n_prompt, int32_t 
                  int32_t* out, float* margins, double* t_prefill, double* t_decode);
 
 /* ---------------- kernel-level references ---------------- */
+/* attention contexts of more than this many 64-position chunks merge their chunk
+ * records as a two-level tree (splits of this many chunks, then the splits) */
+#define ORC_ATTN_SPLIT 16
+
 /* attention of one query head over cached fp32 K/V rows (already fp16-rounded values
  * when the plan says so): q[hd], k/v rows at stride `stride` floats, positions 0..L-1 */
 void orc_attention_canon(const float* q, const float* k, const float* v, int L, int hd,

@@ -139,21 +139,43 @@ void orc_rmsnorm_canon(const float* x, const float* w, int n, float eps, float* 
     for (int i = 0; i < n; i++) out[i] = (x[i] * scale) * w[i];
 }
 
+/* max-first merge of chunk records [c0, c1) (cuda_infer.cu:688-702 attn_combine):
+ * M = max m_c, w_c = exp(m_c - M), den and acc[d] as fma-chains over the chunks in
+ * order; writes M, den and the weighted sums acc[hd] (not yet divided by den) */
+static void merge_records(const float* mc, const float* lc, const float* oc, int c0, int c1, int hd,
+                          float* Mo, float* deno, float* acc) {
+    float M = -INFINITY;
+    for (int c = c0; c < c1; c++) M = fmaxf(M, mc[c]);
+    float den = 0.f;
+    for (int d = 0; d < hd; d++) acc[d] = 0.f;
+    for (int c = c0; c < c1; c++) {
+        const float w = orc_expf(mc[c] - M);
+        den = fmaf(lc[c], w, den);
+        for (int d = 0; d < hd; d++) acc[d] = fmaf(oc[(size_t)c * hd + d], w, acc[d]);
+    }
+    *Mo = M;
+    *deno = den;
+}
+
 /* cpu_infer.cpp:121-140 as split-KV partials (cuda_infer.cu:650-702):
  *   chunk c = positions [64c, 64c+64) of 0..L-1
  *   score  = (a0 + a1) + (a2 + a3) with a_j = fma-chain over dims d = 4i + j; times scale
  *   m_c    = max score; p_t = exp(score - m_c); l_c = butterfly64 over the chunk's lanes
  *   o_c[d] = fma-chain over positions in order of p_t * v_t[d]
- *   merge  : M = max m_c, w_c = exp(m_c - M), den and o as fma-chains over chunks in
- *            order, out = o / den
+ *   merge  : up to ORC_ATTN_SPLIT chunks: M = max m_c, w_c = exp(m_c - M), den and o as
+ *            fma-chains over chunks in order, out = o / den. More chunks merge as a
+ *            two-level tree: each split of ORC_ATTN_SPLIT consecutive chunks that way
+ *            (giving M_s, den_s, o_s), then the splits in order the same way with
+ *            (M_s, den_s, o_s) in place of (m_c, l_c, o_c), out = o / den.
  * Parity: tolerance vs fp64 brute-force softmax and vs orc_attention_fp32. */
 void orc_attention_canon(const float* q, const float* k, const float* v, int L, int hd,
                          int stride, float scale, int chunk, float* out) {
     (void)chunk;  /* the canonical order is defined for 64-position chunks */
     const int nch = (L + 63) / 64;
-    float* mc = (float*)malloc(sizeof(float) * nch);
-    float* lc = (float*)malloc(sizeof(float) * nch);
-    float* oc = (float*)malloc(sizeof(float) * (size_t)nch * hd);
+    const int nsp = nch > ORC_ATTN_SPLIT ? (nch + ORC_ATTN_SPLIT - 1) / ORC_ATTN_SPLIT : 0;
+    float* mc = (float*)malloc(sizeof(float) * (nch + nsp));
+    float* lc = (float*)malloc(sizeof(float) * (nch + nsp));
+    float* oc = (float*)malloc(sizeof(float) * (size_t)(nch + nsp) * hd);
     for (int c = 0; c < nch; c++) {
         const int t0 = 64 * c, n = L - t0 < 64 ? L - t0 : 64;
         float sc[64], p[64];
@@ -175,14 +197,15 @@ void orc_attention_canon(const float* q, const float* k, const float* v, int L, 
             oc[(size_t)c * hd + d] = a;
         }
     }
-    float M = -INFINITY;
-    for (int c = 0; c < nch; c++) M = fmaxf(M, mc[c]);
-    float den = 0.f;
-    for (int d = 0; d < hd; d++) out[d] = 0.f;
-    for (int c = 0; c < nch; c++) {
-        const float w = orc_expf(mc[c] - M);
-        den = fmaf(lc[c], w, den);
-        for (int d = 0; d < hd; d++) out[d] = fmaf(oc[(size_t)c * hd + d], w, out[d]);
+    float M, den;
+    if (nsp == 0) {
+        merge_records(mc, lc, oc, 0, nch, hd, &M, &den, out);
+    } else {
+        for (int s = 0; s < nsp; s++) {
+            const int c0 = s * ORC_ATTN_SPLIT, c1 = c0 + ORC_ATTN_SPLIT < nch ? c0 + ORC_ATTN_SPLIT : nch;
+            merge_records(mc, lc, oc, c0, c1, hd, mc + nch + s, lc + nch + s, oc + (size_t)(nch + s) * hd);
+        }
+        merge_records(mc, lc, oc, nch, nch + nsp, hd, &M, &den, out);
     }
     for (int d = 0; d < hd; d++) out[d] = out[d] / den;
     free(mc); free(lc); free(oc);

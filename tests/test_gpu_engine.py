@@ -116,7 +116,8 @@ def test_config_stream_128(name, persistent):
 
 
 def test_long_context_chunk_merge_phase():
-    """past 16 chunks the merge runs as its own phase: positions 0..1100 (18 chunks)"""
+    """past 4 chunks the merge runs as its own phase, past 16 as a two-level tree of
+    16-chunk splits: positions 0..1101 (18 chunks), tokens and margins vs the oracle"""
     path = synth_cached("eng-256", TINY, 7)
     say("long context 1100 positions")
     ids = minfer.prompt_ids(9, 1090, TINY["n_vocab"])
@@ -124,12 +125,15 @@ def test_long_context_chunk_merge_phase():
     for persistent in (1, 0):
         eng = minfer.Engine(path, max_ctx=1200, persistent=persistent)
         eng.prefill(ids)
-        toks, _ = eng.generate(12)
-        res[persistent] = toks
+        toks, margins = eng.generate(12)
+        res[persistent] = (toks, np.float32(margins).view(np.uint32))
         eng.close()
     orc = O.Model(path, O.MODE_Q8ACT, plan=plan_of(minfer.Engine(path, max_ctx=1200)), max_seq=1200)
-    rt, _, _, _ = orc.generate(ids, 12)
-    assert res[1] == rt and res[0] == rt
+    rt, rm, _, _ = orc.generate(ids, 12)
+    rm = np.float32(rm).view(np.uint32)
+    for persistent in (1, 0):
+        assert res[persistent][0] == rt, persistent
+        assert np.array_equal(res[persistent][1], rm), persistent
 
 
 def test_rewind_and_restep():

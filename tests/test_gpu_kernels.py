@@ -98,16 +98,19 @@ def test_gemv_bit_exact(torch, rows, n_in, cb, ks):
 
 
 @pytest.mark.parametrize("nh,nkv,hd,L", [(12, 2, 128, 1), (12, 2, 128, 64), (12, 2, 128, 65), (12, 2, 128, 300),
-                                         (14, 2, 64, 200), (16, 2, 128, 1024), (4, 2, 64, 130)])
+                                         (14, 2, 64, 200), (16, 2, 128, 1024), (4, 2, 64, 130),
+                                         (14, 2, 64, 1100), (16, 2, 128, 2049), (8, 1, 128, 5000),
+                                         (32, 4, 64, 32768), (24, 4, 128, 32700)])
 def test_attention_bit_exact(torch, nh, nkv, hd, L):
+    """chunked attention vs the oracle's canonical order; the last two cases give
+    items of all 8 and all 6 query heads of a kv head"""
     say("attention nh=%d nkv=%d hd=%d L=%d" % (nh, nkv, hd, L))
     ctx = L + 5
     q = RNG.standard_normal((nh, hd)).astype(np.float32)
     k16 = RNG.standard_normal((nkv, ctx, hd)).astype(np.float16)
     v16 = RNG.standard_normal((nkv, ctx, hd)).astype(np.float16)
     scale = np.float32(1.0) / np.float32(math.sqrt(hd))
-    nch = (L + 63) // 64
-    scratch = torch.zeros(nh * nch * (hd + 32), device="cuda")
+    scratch = torch.zeros(minfer.attn_scratch_floats(nh, hd, L), device="cuda")
     out = torch.zeros(nh * hd, device="cuda")
     minfer.attn_decode(dev(torch, q), dev(torch, k16.view(np.int16)), dev(torch, v16.view(np.int16)), nh, nkv, hd,
                        L, ctx, float(scale), scratch, out)
@@ -128,3 +131,77 @@ def test_stream_read_runs(torch):
     minfer.stream_read(buf, buf.numel(), sink)
     torch.cuda.synchronize()
     assert int(sink.abs().sum()) == 0
+
+
+def attention_case(torch, nh, nkv, hd, L, scratch, rng):
+    ctx = L + 3
+    q = rng.standard_normal((nh, hd)).astype(np.float32)
+    k16 = rng.standard_normal((nkv, ctx, hd)).astype(np.float16)
+    v16 = rng.standard_normal((nkv, ctx, hd)).astype(np.float16)
+    scale = np.float32(1.0) / np.float32(math.sqrt(hd))
+    out = torch.zeros(nh * hd, device="cuda")
+    minfer.attn_decode(dev(torch, q), dev(torch, k16.view(np.int16)), dev(torch, v16.view(np.int16)), nh, nkv, hd,
+                       L, ctx, float(scale), scratch, out)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy().reshape(nh, hd)
+    G = nh // nkv
+    for h in range(nh):
+        kf = np.ascontiguousarray(k16[h // G].astype(np.float32))
+        vf = np.ascontiguousarray(v16[h // G].astype(np.float32))
+        ref = O.attention_canon(np.ascontiguousarray(q[h]), kf.ravel(), vf.ravel(), L, hd, hd, float(scale))
+        assert np.array_equal(got[h].view(np.uint32), ref.view(np.uint32)), (nh, L, h)
+
+
+def test_attention_scratch_reuse(torch):
+    """one scratch buffer, zero-filled once, through calls of different shapes: each
+    call leaves its arrival counters at zero, so the next one merges correctly"""
+    rng = np.random.default_rng(5)
+    scratch = torch.zeros(minfer.attn_scratch_floats(16, 128, 5000), device="cuda")
+    for nh, nkv, hd, L in [(12, 2, 128, 3000), (4, 2, 64, 100), (12, 2, 128, 3000), (16, 2, 128, 5000),
+                           (14, 2, 64, 1100), (12, 2, 128, 64)]:
+        say("scratch reuse nh=%d hd=%d L=%d" % (nh, hd, L))
+        attention_case(torch, nh, nkv, hd, L, scratch, rng)
+        assert int(torch.count_nonzero(scratch[:65536])) == 0
+
+
+def rope_rows(x, pos0, base=1e6):
+    """NEOX RoPE of rows x[t] at absolute positions pos0 + t (float64)"""
+    hd = x.shape[-1]
+    half = hd // 2
+    inv = base ** (-np.arange(half, dtype=np.float64) * 2 / hd)
+    ang = (pos0 + np.arange(x.shape[-2], dtype=np.float64))[:, None] * inv[None, :]
+    c, s = np.cos(ang), np.sin(ang)
+    a, b = x[..., :half], x[..., half:]
+    return np.concatenate([a * c - b * s, a * s + b * c], axis=-1)
+
+
+@pytest.mark.parametrize("L", [512, 4096, 16384, 24001, 32768])
+def test_attention_depth_config3(torch, L):
+    """config 3: S15 attention (12 query / 2 kv heads, head_dim 128), one query, an
+    fp16 K/V cache N(0,1) with RoPE at absolute positions 0..L-1. Bit-exact against
+    the oracle's canonical order (past 16 chunks a two-level merge), within 1e-3
+    relative of an fp64 softmax. 24001 takes items of 2 query heads and ends in a
+    one-position chunk; 32768 takes items of 3 heads."""
+    nh, nkv, hd = 12, 2, 128
+    say("attention at depth L=%d" % L)
+    rng = np.random.default_rng(L)
+    q = rope_rows(rng.standard_normal((nh, 1, hd)), L - 1)[:, 0].astype(np.float32)
+    k16 = rope_rows(rng.standard_normal((nkv, L, hd)), 0).astype(np.float16)
+    v16 = rng.standard_normal((nkv, L, hd)).astype(np.float16)
+    scale = np.float32(1.0) / np.float32(math.sqrt(hd))
+    scratch = torch.zeros(minfer.attn_scratch_floats(nh, hd, L), device="cuda")
+    out = torch.zeros(nh * hd, device="cuda")
+    minfer.attn_decode(dev(torch, q), dev(torch, k16.view(np.int16)), dev(torch, v16.view(np.int16)), nh, nkv, hd,
+                       L, L, float(scale), scratch, out)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy().reshape(nh, hd)
+    G = nh // nkv
+    for h in range(nh):
+        kf = np.ascontiguousarray(k16[h // G].astype(np.float32))
+        vf = np.ascontiguousarray(v16[h // G].astype(np.float32))
+        ref = O.attention_canon(np.ascontiguousarray(q[h]), kf.ravel(), vf.ravel(), L, hd, hd, float(scale))
+        assert np.array_equal(got[h].view(np.uint32), ref.view(np.uint32)), h
+        sc = (kf.astype(np.float64) @ q[h].astype(np.float64)) * float(scale)
+        p = np.exp(sc - sc.max())
+        r64 = (p / p.sum()) @ vf.astype(np.float64)
+        assert np.abs(got[h] - r64).max() <= 1e-3 * np.abs(r64).max(), h

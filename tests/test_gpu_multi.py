@@ -103,13 +103,15 @@ def test_config2_multi_bit_identical():
     eng.close()
 
 
-def test_long_context_multi_merge_phase():
-    """past kInlineComb chunks the chunk records are merged by their own kernel"""
+@pytest.mark.parametrize("pos,T", [(1000, 6), (1020, 8)])
+def test_long_context_multi_merge_phase(pos, T):
+    """past 4 chunks the chunk records are merged by their own kernel, past 16 as a
+    two-level tree (1020 + 8: the step's tokens see 16 and 17 chunks)"""
     path = synth_cached("eng-256", TINY, 7)
-    say("tiny long context pos 1000 T 6")
+    say("tiny long context pos %d T %d" % (pos, T))
     eng = minfer.Engine(path, max_ctx=1100)
-    prompt = minfer.prompt_ids(13, 1000, TINY["n_vocab"])
-    multi_vs_single(eng, prompt, 1000, 6, 23, TINY["n_vocab"])
+    prompt = minfer.prompt_ids(13, pos, TINY["n_vocab"])
+    multi_vs_single(eng, prompt, pos, T, 23, TINY["n_vocab"])
     eng.close()
 
 

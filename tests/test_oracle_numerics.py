@@ -159,7 +159,7 @@ def test_butterfly64_sum():
     assert O.lib().orc_butterfly64(O.ptr(ones)) == 64.0
 
 
-@pytest.mark.parametrize("L", [1, 5, 63, 64, 65, 200, 700])
+@pytest.mark.parametrize("L", [1, 5, 63, 64, 65, 200, 700, 1024, 1025, 1088, 3000])
 def test_attention_canon_matches_float64(L):
     hd = 128
     q = RNG.standard_normal(hd).astype(np.float32)
@@ -173,6 +173,25 @@ def test_attention_canon_matches_float64(L):
     assert np.abs(got - ref).max() <= 1e-5 * max(1.0, np.abs(ref).max())
     got32 = O.attention_fp32(q, k.ravel(), v.ravel(), L, hd, hd, float(scale))
     assert np.abs(got32 - ref).max() <= 1e-5 * max(1.0, np.abs(ref).max())
+
+
+@pytest.mark.parametrize("L,peak", [(1025, 1024), (2100, 40), (2100, 1500), (4096, 4095)])
+def test_attention_canon_split_tree_peaked(L, peak):
+    """past 16 chunks the records merge as a two-level tree: a sharp score peak in one
+    split (first, middle or last, including a split of one position) must carry its
+    weight through both levels; a dropped or misweighted split fails the fp64 check"""
+    hd = 64
+    q = RNG.standard_normal(hd).astype(np.float32)
+    k = RNG.standard_normal((L, hd)).astype(np.float32) * 0.3
+    k[peak] = q * (6.0 * math.sqrt(hd) / float(q @ q))      # score 6 against scores ~N(0, 0.3)
+    v = RNG.standard_normal((L, hd)).astype(np.float32)
+    scale = np.float32(1 / math.sqrt(hd))
+    s = k.astype(np.float64) @ q.astype(np.float64) * float(scale)
+    p = np.exp(s - s.max())
+    ref = (p / p.sum()) @ v.astype(np.float64)
+    assert p[peak] == 1.0 and 0.05 < 1 / p.sum() < 0.5   # the peak weighs, so do the others
+    got = O.attention_canon(q, k.ravel(), v.ravel(), L, hd, hd, float(scale))
+    assert np.abs(got - ref).max() <= 1e-5 * max(1.0, np.abs(ref).max())
 
 
 def test_rope_cs_float_theta():
