@@ -232,7 +232,18 @@ def main():
     ap.add_argument("--copy-calib", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB three times (calibrates the "
                          "rocprofv3 FETCH_SIZE/WRITE_SIZE counters) and exit")
+    ap.add_argument("--attention-only", type=str, default="", metavar="L[,L...]",
+                    help="only run the config3 attention-at-depth measurement at these context "
+                         "lengths, print its JSON and exit")
     args = ap.parse_args()
+    if args.attention_only:
+        import torch
+        lens = tuple(int(x) for x in args.attention_only.split(","))
+        res = attention_depth(torch, lengths=lens)
+        for a in res:
+            log("attention L=%-6d %8.2f us/layer  %7.1f GB/s" % (a["L"], a["us_per_layer"], a["gbps"]))
+        print(json.dumps({"attention_depth": res}), flush=True)
+        return
     if args.copy_calib:
         import torch
         src = torch.ones(args.copy_calib << 20, dtype=torch.uint8, device="cuda")
