@@ -74,9 +74,10 @@ typedef struct mi_model_info {
 } mi_model_info;
 int mi_info(const mi_engine* e, mi_model_info* out);
 
-/* Prefill: cuda_infer.cu:1151-1159 / mega.cu prompt steps. Runs ids[0..n) at
- * positions 0..n-1 (from an empty cache) and returns the greedy prediction after
- * the last one (= the first generated token) and its logit margin. */
+/* Prefill: cuda_infer.cu:1133-1159 / mega.cu:622, 819-820 prompt steps. Runs ids[0..n)
+ * at positions 0..n-1 (from an empty cache) in chunks of opts.tchunk tokens (each chunk
+ * one multi-token step; results bit-identical to one step per token) and returns the
+ * greedy prediction after the last one (= the first generated token) and its margin. */
 int mi_prefill(mi_engine* e, const int32_t* ids, int32_t n, int32_t* first, float* margin);
 
 /* One step: forward_batch(toks, T, pos0) (cuda_infer.cu:990-1026). Runs toks[0..T)
@@ -123,6 +124,15 @@ typedef struct mi_stats {
     int32_t accepted;       /* draft tokens accepted (speculation; mega.cu stats[2]) */
 } mi_stats;
 int mi_get_stats(const mi_engine* e, mi_stats* out);
+
+/* Text of one token (src/detok.h:28-41 detok_piece over the GGUF's
+ * tokenizer.ggml.tokens): the vocab piece decoded from byte-level BPE code points to
+ * raw bytes into out[0..cap). Returns the byte count (only the first cap are written;
+ * it may exceed cap) or a negative status (MI_ERR_ARG for an id outside the vocab). */
+int32_t mi_token_text(const mi_engine* e, int32_t id, char* out, int32_t cap);
+/* The same decoding for any piece of `len` bytes (src/detok.h:13-41); -1 on bad
+ * arguments. Needs no engine and no device. */
+int32_t mi_detok_piece(const char* piece, int32_t len, char* out, int32_t cap);
 
 /* Measurement hook, no counterpart in the reference (which profiles with nsys/ncu and
  * in-kernel clock64 marks, mega.cu:111-119): re-launches one phase kernel of the

@@ -472,8 +472,21 @@ int mi_info(const mi_engine* e, mi_model_info* o) {
 static int run_step(mi_engine* e, int pos, int gen, bool want_logits) {
     const DModel& M = want_logits ? e->M_logits : e->M;
     const DModel* dM = e->dM + (want_logits ? 1 : 0);
-    if (e->nwg_persistent) HIPCHK(e, launch_step_persistent(M, dM, e->nwg_persistent, pos, gen, e->stream));
-    else launch_step_phases(M, dM, e->n_cu, pos, gen, e->stream);
+    if (e->nwg_persistent) {
+        const hipError_t err = launch_step_persistent(M, dM, e->nwg_persistent, pos, gen, e->stream);
+        if (err == hipErrorIllegalState || err == hipErrorCooperativeLaunchTooLarge) {
+            // The runtime refused the cooperative launch itself (seen while another process
+            // holds the device's cooperative dispatch); nothing ran. The per-phase launches
+            // compute the same values, so the engine continues in that mode (mi_info reports it).
+            (void)hipGetLastError();
+            e->nwg_persistent = 0;
+            launch_step_phases(M, dM, e->n_cu, pos, gen, e->stream);
+        } else {
+            HIPCHK(e, err);
+        }
+    } else {
+        launch_step_phases(M, dM, e->n_cu, pos, gen, e->stream);
+    }
     HIPCHK(e, hipGetLastError());
     return MI_OK;
 }
@@ -535,9 +548,21 @@ int mi_prefill(mi_engine* e, const int32_t* ids, int32_t n, int32_t* first, floa
         if (ids[i] < 0 || ids[i] >= e->V) return set_err(e, MI_ERR_ARG, "prompt token %d out of range", ids[i]);
     HIPCHK(e, hipMemcpyAsync(e->M.tokbuf, ids, sizeof(int32_t) * n, hipMemcpyHostToDevice, e->stream));
     HIPCHK(e, hipEventRecord(e->ev0, e->stream));
-    for (int p = 0; p < n; p++) {
-        const int rc = run_step(e, p, p == n - 1, false);
-        if (rc) return rc;
+    // chunks of tchunk tokens through the multi-token step (cuda_infer.cu:1133-1144,
+    // mega.cu:622, 819-820); its results equal one step per token bit for bit
+    bool ran_single = false;
+    for (int p = 0; p < n;) {
+        const int T = std::min(e->opts.tchunk, n - p);
+        if (T == 1) {
+            if (int rc = run_step(e, p, p == n - 1, false)) return rc;
+            ran_single = true;
+        } else {
+            launch_step_multi(e->M, e->dM, e->n_cu, p, T, e->stream);
+            HIPCHK(e, hipGetLastError());
+            if (p + T == n)   // the next position's token is the last prediction
+                HIPCHK(e, hipMemcpyAsync(e->M.tokbuf + n, e->M.out_tok + n - 1, 4, hipMemcpyDeviceToDevice, e->stream));
+        }
+        p += T;
     }
     HIPCHK(e, hipEventRecord(e->ev1, e->stream));
     int32_t tok = 0;
@@ -545,7 +570,8 @@ int mi_prefill(mi_engine* e, const int32_t* ids, int32_t n, int32_t* first, floa
     HIPCHK(e, hipMemcpyAsync(&tok, e->M.out_tok + n - 1, 4, hipMemcpyDeviceToHost, e->stream));
     HIPCHK(e, hipMemcpyAsync(&mg, e->M.out_margin + n - 1, 4, hipMemcpyDeviceToHost, e->stream));
     HIPCHK(e, hipStreamSynchronize(e->stream));
-    if (int rc = check_barrier(e)) return rc;
+    if (ran_single)
+        if (int rc = check_barrier(e)) return rc;
     float ms = 0.f;
     HIPCHK(e, hipEventElapsedTime(&ms, e->ev0, e->ev1));
     e->stats.prefill_ms = ms;
@@ -591,7 +617,8 @@ static int generate_spec(mi_engine* e, int n_gen, int32_t* out, float* margins, 
         if (margins) margins[emitted] = m;
         emitted++;
         last_pos = at;
-        done = emitted >= n_gen || (cb && cb(t, user)) || (e->opts.stop_eos && t == e->eos);
+        const bool stop = cb && cb(t, user);     // every emitted token reaches the callback
+        done = stop || emitted >= n_gen || (e->opts.stop_eos && t == e->eos);
     };
     int32_t cur = hist[p0];
     if (!done) emit(cur, mg0, p0);
@@ -778,6 +805,13 @@ int mi_get_stats(const mi_engine* e, mi_stats* out) {
     if (!e || !out) return MI_ERR_ARG;
     *out = e->stats;
     return MI_OK;
+}
+
+int32_t mi_token_text(const mi_engine* e, int32_t id, char* out, int32_t cap) {
+    if (!e || cap < 0 || (cap > 0 && !out)) return MI_ERR_ARG;
+    const auto& v = e->gguf.tokens();
+    if (id < 0 || id >= (int32_t)v.size()) return MI_ERR_ARG;
+    return mi_detok_piece(v[id].data(), (int32_t)v[id].size(), out, cap);
 }
 
 // ---------------------------------------------------------------- kernel-level entry points

@@ -82,6 +82,8 @@ SIGNATURES = {
     "mi_device_count": (C.c_int, [C.POINTER(C.c_int32)]),
     "mi_ngram_draft": (C.c_int32, [C.POINTER(C.c_int32), C.c_int32, C.c_int32, C.c_int32, C.POINTER(C.c_int32)]),
     "mi_best_draft_len": (C.c_int32, [C.c_float, C.c_float, C.c_int32]),
+    "mi_token_text": (C.c_int32, [_P, C.c_int32, C.c_char_p, C.c_int32]),
+    "mi_detok_piece": (C.c_int32, [C.c_char_p, C.c_int32, C.c_char_p, C.c_int32]),
 }
 
 _lib = None
@@ -247,6 +249,17 @@ class Engine:
         out["total"] = round(float(t[:, -1].max()), 1)
         return out
 
+    def token_text(self, tok):
+        """bytes of one token's text (the GGUF vocab piece, byte-level BPE decoded)"""
+        buf = C.create_string_buffer(256)
+        n = lib().mi_token_text(self._h, tok, buf, 256)
+        if n < 0:
+            raise MinferError(n, "token %d outside the vocabulary" % tok)
+        if n > 256:
+            buf = C.create_string_buffer(n)
+            lib().mi_token_text(self._h, tok, buf, n)
+        return buf.raw[:n]
+
     def stats(self):
         s = Stats()
         _check(lib().mi_get_stats(self._h, C.byref(s)), self._h)
@@ -255,6 +268,17 @@ class Engine:
 
 
 # ---------------------------------------------------------------- kernel-level helpers
+def detok_piece(piece):
+    """raw bytes of a byte-level BPE vocab piece (str or UTF-8 bytes)"""
+    p = piece.encode("utf-8") if isinstance(piece, str) else bytes(piece)
+    cap = len(p) + 1
+    buf = C.create_string_buffer(cap)
+    n = lib().mi_detok_piece(p, len(p), buf, cap)
+    if n < 0:
+        raise MinferError(n, "bad piece")
+    return buf.raw[:n]
+
+
 def packed_bytes(rows, nb, cb):
     return lib().mi_q4_packed_bytes(rows, nb, cb)
 

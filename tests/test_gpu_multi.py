@@ -129,7 +129,9 @@ def spec_vs_plain(path, prompt, n_gen, max_ctx):
     for spec in (0, 1):
         eng = minfer.Engine(path, max_ctx=max_ctx, spec=spec)
         eng.prefill(prompt)
-        toks, margins = eng.generate(n_gen)
+        seen = []
+        toks, margins = eng.generate(n_gen, callback=lambda t: seen.append(t) and False)
+        assert seen == toks, "spec=%d: the callback saw %d of %d tokens" % (spec, len(seen), len(toks))
         res[spec] = (toks, margins, eng.stats())
         eng.close()
     (pt, pm, _), (st, sm, ss) = res[0], res[1]
