@@ -77,16 +77,6 @@ __device__ __forceinline__ float mi_expf(float x) {
     return __builtin_ldexpf(p, (int)n);
 }
 
-__device__ __forceinline__ float bfly_sum64(float v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v = __fadd_rn(v, __shfl_xor(v, off));
-    return v;
-}
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
-    return v;
-}
 // LDS hand-off between lanes of one wave (waves run independently, so a workgroup
 // barrier cannot be used): DS operations of one wave complete in order
 // (the s_waitcnt builtin, unlike inline asm, is seen by the compiler's own wait
@@ -97,19 +87,98 @@ __device__ __forceinline__ float h2f_lo(uint32_t u) { return __half2float(__usho
 __device__ __forceinline__ float h2f_hi(uint32_t u) { return __half2float(__ushort_as_half((unsigned short)(u >> 16))); }
 __device__ __forceinline__ float fp16_round(float v) { return __half2float(__float2half(v)); }
 
+// Cross-lane partners without the LDS pipe. The xor butterfly pairs lane l with
+// l ^ off for off = 32, 16, ..., 1; every step leaves a pair holding the same value
+// (IEEE add and max are commutative), which the cheaper permutations rely on:
+//   off 32, 16: v_permlane32_swap / v_permlane16_swap of v with itself leave the two
+//               values of each pair (l, l ^ off) in the two results on lane l;
+//   off 8:      DPP row_ror:8 is l ^ 8 inside each 16-lane row;
+//   off 4:      DPP row_ror:4 reads lane (l + 4) mod 16, which holds the value of
+//               l ^ 4 once the values are symmetric under xor 8;
+//   off 2, 1:   DPP quad_perm [2,3,0,1] and [1,0,3,2] are l ^ 2 and l ^ 1.
+// So each step adds exactly the same two values as the xor butterfly.
+template <int CTRL>
+__device__ __forceinline__ float dppf(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+template <int CTRL>
+__device__ __forceinline__ int dppi(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+constexpr int kDppXor1 = 0xB1, kDppXor2 = 0x4E, kDppRor4 = 0x124, kDppRor8 = 0x128, kDppHalfMirror = 0x141;
+__device__ __forceinline__ void pair32(float v, float& a, float& b) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    a = __uint_as_float(r[0]);
+    b = __uint_as_float(r[1]);
+}
+__device__ __forceinline__ void pair16(float v, float& a, float& b) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    a = __uint_as_float(r[0]);
+    b = __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float bfly_sum64(float v) {
+    float a, b;
+    pair32(v, a, b);
+    v = __fadd_rn(a, b);
+    pair16(v, a, b);
+    v = __fadd_rn(a, b);
+    v = __fadd_rn(v, dppf<kDppRor8>(v));
+    v = __fadd_rn(v, dppf<kDppRor4>(v));
+    v = __fadd_rn(v, dppf<kDppXor2>(v));
+    return __fadd_rn(v, dppf<kDppXor1>(v));
+}
+__device__ __forceinline__ float wave_max(float v) {
+    float a, b;
+    pair32(v, a, b);
+    v = fmaxf(a, b);
+    pair16(v, a, b);
+    v = fmaxf(a, b);
+    v = fmaxf(v, dppf<kDppRor8>(v));
+    v = fmaxf(v, dppf<kDppRor4>(v));
+    v = fmaxf(v, dppf<kDppXor2>(v));
+    return fmaxf(v, dppf<kDppXor1>(v));
+}
+// max / integer sum over aligned groups of 8 lanes (exact in any order): quad steps,
+// then the half-row mirror pairs lane i of a quad with the other quad of its 8
+__device__ __forceinline__ float max8(float v) {
+    v = fmaxf(v, dppf<kDppXor1>(v));
+    v = fmaxf(v, dppf<kDppXor2>(v));
+    return fmaxf(v, dppf<kDppHalfMirror>(v));
+}
+__device__ __forceinline__ int sum8(int v) {
+    v += dppi<kDppXor1>(v);
+    v += dppi<kDppXor2>(v);
+    return v + dppi<kDppHalfMirror>(v);
+}
+
+// max / integer sum over each 32-lane half (exact in any order; pairings as in
+// bfly_sum64: permlane16 swap, then DPP inside 16-lane rows)
+__device__ __forceinline__ float max32(float v) {
+    float a, b;
+    pair16(v, a, b);
+    v = fmaxf(a, b);
+    v = fmaxf(v, dppf<kDppRor8>(v));
+    v = fmaxf(v, dppf<kDppRor4>(v));
+    v = fmaxf(v, dppf<kDppXor2>(v));
+    return fmaxf(v, dppf<kDppXor1>(v));
+}
+__device__ __forceinline__ int sum32(int v) {
+    const auto r = __builtin_amdgcn_permlane16_swap((unsigned)v, (unsigned)v, false, false);
+    v = (int)(r[0] + r[1]);
+    v += dppi<kDppRor8>(v);
+    v += dppi<kDppRor4>(v);
+    v += dppi<kDppXor2>(v);
+    return v + dppi<kDppXor1>(v);
+}
+
 // quantize one 32-element block per half-wave: the lane's code, the block scale and
 // 8*sum(q) on every lane (cuda_infer.cu:80-89, mega.cu:303-325)
 __device__ __forceinline__ void quant32_vals(float v, int& q, float& d, int& s8) {
-    float a = fabsf(v);
-#pragma unroll
-    for (int off = 16; off >= 1; off >>= 1) a = fmaxf(a, __shfl_xor(a, off));
+    const float a = max32(fabsf(v));
     const float inv = a > 0.f ? __fdiv_rn(127.f, a) : 0.f;
     q = __float2int_rn(__fmul_rn(v, inv));
-    int s = q;
-#pragma unroll
-    for (int off = 16; off >= 1; off >>= 1) s += __shfl_xor(s, off);
     d = fp16_round(__fdiv_rn(a, 127.f));
-    s8 = 8 * s;
+    s8 = 8 * sum32(q);
 }
 
 // ------------------------------------------------------------------ memory helpers
@@ -333,10 +402,24 @@ __device__ __forceinline__ void top2_merge(Top2& a, float ob, int oi, float os) 
     a.second = fmaxf(fmaxf(a.second, os), take ? a.best : ob);
     if (take) { a.best = ob; a.idx = oi; }
 }
+// the xor butterfly over 64 lanes with the pairings of bfly_sum64; the pair merge is
+// symmetric (max, lowest index on ties), so each step gives the xor result
 __device__ __forceinline__ void top2_wave(Top2& t) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1)
-        top2_merge(t, __shfl_xor(t.best, off), __shfl_xor(t.idx, off), __shfl_xor(t.second, off));
+    auto swap_merge = [&](bool p32) {
+        const unsigned b = __float_as_uint(t.best), i = (unsigned)t.idx, s2 = __float_as_uint(t.second);
+        const auto rb = p32 ? __builtin_amdgcn_permlane32_swap(b, b, false, false) : __builtin_amdgcn_permlane16_swap(b, b, false, false);
+        const auto ri = p32 ? __builtin_amdgcn_permlane32_swap(i, i, false, false) : __builtin_amdgcn_permlane16_swap(i, i, false, false);
+        const auto rs = p32 ? __builtin_amdgcn_permlane32_swap(s2, s2, false, false) : __builtin_amdgcn_permlane16_swap(s2, s2, false, false);
+        Top2 x{__uint_as_float(rb[0]), (int)ri[0], __uint_as_float(rs[0])};
+        top2_merge(x, __uint_as_float(rb[1]), (int)ri[1], __uint_as_float(rs[1]));
+        t = x;
+    };
+    swap_merge(true);
+    swap_merge(false);
+    top2_merge(t, dppf<kDppRor8>(t.best), dppi<kDppRor8>(t.idx), dppf<kDppRor8>(t.second));
+    top2_merge(t, dppf<kDppRor4>(t.best), dppi<kDppRor4>(t.idx), dppf<kDppRor4>(t.second));
+    top2_merge(t, dppf<kDppXor2>(t.best), dppi<kDppXor2>(t.idx), dppf<kDppXor2>(t.second));
+    top2_merge(t, dppf<kDppXor1>(t.best), dppi<kDppXor1>(t.idx), dppf<kDppXor1>(t.second));
 }
 
 // ------------------------------------------------------------------ grid barrier
@@ -410,17 +493,11 @@ __device__ __forceinline__ void st4(float* p, int i, float4 v) { *reinterpret_ca
 // 8 lanes x 4 elements
 __device__ __forceinline__ void quant_slice(float4 y, bool own, int e0, uint8_t* X, int lane, int rs = kXRec) {
     if (!own) y = make_float4(0.f, 0.f, 0.f, 0.f);
-    float a = fmaxf(fmaxf(fabsf(y.x), fabsf(y.y)), fmaxf(fabsf(y.z), fabsf(y.w)));
-    a = fmaxf(a, __shfl_xor(a, 1));
-    a = fmaxf(a, __shfl_xor(a, 2));
-    a = fmaxf(a, __shfl_xor(a, 4));
+    const float a = max8(fmaxf(fmaxf(fabsf(y.x), fabsf(y.y)), fmaxf(fabsf(y.z), fabsf(y.w))));
     const float inv = a > 0.f ? __fdiv_rn(127.f, a) : 0.f;
     const int q0 = __float2int_rn(__fmul_rn(y.x, inv)), q1 = __float2int_rn(__fmul_rn(y.y, inv));
     const int q2 = __float2int_rn(__fmul_rn(y.z, inv)), q3 = __float2int_rn(__fmul_rn(y.w, inv));
-    int s = q0 + q1 + q2 + q3;
-    s += __shfl_xor(s, 1);
-    s += __shfl_xor(s, 2);
-    s += __shfl_xor(s, 4);
+    const int s = sum8(q0 + q1 + q2 + q3);
     if (own) {
         uint8_t* rec = X + (e0 >> 5) * rs;
         *reinterpret_cast<uint32_t*>(rec + (e0 & 31)) =
@@ -454,35 +531,58 @@ __device__ __forceinline__ int norm_src_layer(MPtr M, int l, int kind) {
     return kind == PH_QKV ? l - 1 : kind == PH_LM ? M->NL - 1 : l;
 }
 
-// control wave: DMA the inputs of phase (l, kind) into LDS and wait for them
-__device__ __forceinline__ void ctl_stage(MPtr M, int l, int kind, int pos, const Lds& S, int lane, bool resident) {
+// One wave's share of a workgroup's DMA: the transfers of a staging step are cut into
+// 1-KB units numbered across calls, and wave `wave` of `nw` issues units wave, wave +
+// nw, ... (a single wave issuing ~50 units back to back was most of the staging time).
+struct DmaShare { int wave, nw, unit; };
+__device__ __forceinline__ void dma_share(const void* g, void* lds, int bytes, DmaShare& d, int lane) {
+    const int n = (bytes + 1023) >> 10;
+    for (int k = ((d.wave - d.unit) % d.nw + d.nw) % d.nw; k < n; k += d.nw) {
+        const int off = k << 10;
+        if (off + lane * 16 < bytes)
+            __builtin_amdgcn_global_load_lds(static_cast<const uint8_t*>(g) + off + lane * 16,
+                                             (lds_ptr)(static_cast<uint8_t*>(lds) + off), 16, 0, 0);
+    }
+    d.unit += n;
+}
+
+// DMA the inputs of phase (l, kind) into LDS, shared by waves wave = 0..nw-1 (all of
+// them call it), each of which waits for its own transfers; a workgroup barrier then
+// publishes them
+__device__ __forceinline__ void stage(MPtr M, int l, int kind, int pos, const Lds& S, int wave, int nw, int lane,
+                                      bool resident) {
     const int n = M->E;
+    DmaShare d{wave, nw, 0};
     if (kind == PH_DOWN) {
-        dma_wave(act_rec(M, l), S.U, (M->FF / 32) * kActRec, lane);
+        dma_share(act_rec(M, l), S.U, (M->FF / 32) * kActRec, d, lane);
     } else if (kind == PH_O) {
         const int nch = (pos + 1 + kAttnChunk - 1) / kAttnChunk, arec = M->arec;
         if (nch <= kInlineComb) {
             const float* att = att_rec(M, l);
             const int hb = nch * arec;
             for (int h = 0; h < M->NH; h++)
-                dma_wave(att + (size_t)h * M->maxch * arec, reinterpret_cast<float*>(S.U) + h * hb, hb * 4, lane);
+                dma_share(att + (size_t)h * M->maxch * arec, reinterpret_cast<float*>(S.U) + h * hb, hb * 4, d, lane);
         } else {
-            dma_wave(M->att_out + (size_t)l * n, S.T, n * 4, lane);
+            dma_share(M->att_out + (size_t)l * n, S.T, n * 4, d, lane);
         }
     } else if (kind != PH_ATTN) {
         float* w = reinterpret_cast<float*>(S.U);
-        dma_wave(kind == PH_LM ? M->out_norm : kind == PH_QKV ? LY(M, l)->an : LY(M, l)->fn, w, n * 4, lane);
+        dma_share(kind == PH_LM ? M->out_norm : kind == PH_QKV ? LY(M, l)->an : LY(M, l)->fn, w, n * 4, d, lane);
         if (kind == PH_QKV && l == 0) {
-            dma_wave(M->emb + (size_t)M->tokbuf[pos] * n, resident ? S.R : S.T, n * 4, lane);
+            dma_share(M->emb + (size_t)M->tokbuf[pos] * n, resident ? S.R : S.T, n * 4, d, lane);
         } else {
             const int pl = norm_src_layer(M, l, kind);
             const bool dsrc = kind != PH_GU;
-            if (!resident) dma_wave(M->hbuf + (dsrc ? hmid(pl, n) : hin(l, n)), w + n, n * 4, lane);
-            dma_wave(dsrc ? d_part(M, pl) : o_part(M, pl), w + (resident ? n : 2 * n),
-                     (dsrc ? LY(M, pl)->d.ks : LY(M, pl)->o.ks) * n * 4, lane);
+            if (!resident) dma_share(M->hbuf + (dsrc ? hmid(pl, n) : hin(l, n)), w + n, n * 4, d, lane);
+            dma_share(dsrc ? d_part(M, pl) : o_part(M, pl), w + (resident ? n : 2 * n),
+                      (dsrc ? LY(M, pl)->d.ks : LY(M, pl)->o.ks) * n * 4, d, lane);
         }
     }
     drain_vm();
+}
+// the control wave alone (the per-phase kernels, whose workers prefetch meanwhile)
+__device__ __forceinline__ void ctl_stage(MPtr M, int l, int kind, int pos, const Lds& S, int lane, bool resident) {
+    stage(M, l, kind, pos, S, 0, 1, lane, resident);
 }
 
 // all waves: the phase input records X from the staged data (see ctl_stage)
@@ -967,8 +1067,8 @@ __global__ __launch_bounds__(kPThreads) void k_step(const DModel* Mp, int pos, i
     unsigned epoch = 0;
     Tile tl[2];
     stamp(M, 0);
-    if (ctl) ctl_stage(M, 0, PH_QKV, pos, S, lane, true);
-    else phase_prefetch(M, 0, PH_QKV, wg, nwg, kw, tl, lane);
+    stage(M, 0, PH_QKV, pos, S, wave, kPWaves, lane, true);
+    if (!ctl) phase_prefetch(M, 0, PH_QKV, wg, nwg, kw, tl, lane);
     int l = 0, kind = PH_QKV;
     for (int sb = 1;; sb += 5) {
         __syncthreads();
@@ -1026,8 +1126,9 @@ __global__ __launch_bounds__(kPThreads) void k_step(const DModel* Mp, int pos, i
         if (ctl) {
             ctl_barrier(M->bar, M->err, epoch);
             stamp(M, sb + 4);
-            ctl_stage(M, nl, nk, pos, S, lane, true);
         }
+        __syncthreads();
+        stage(M, nl, nk, pos, S, wave, kPWaves, lane, true);
         l = nl;
         kind = nk;
     }
