@@ -163,11 +163,15 @@ int mi_barrier_cost(int32_t nwg, int32_t n, double* us_per_barrier);
 typedef struct mi_synth_shape {
     int32_t n_layer, n_embd, n_ff, n_head, n_head_kv, n_vocab;
     float rope_base, rms_eps;
-    int32_t emb_type;      /* 0: F32 token embedding (the configs), 2: q4_0 */
+    int32_t emb_type;      /* token embedding: 0 F32 (the configs), 2 q4_0, 8 q8_0 */
+    int32_t head_type;     /* output.weight: 0 or 2 q4_0, 8 q8_0, 14 q6_K (real Qwen files carry q6_K) */
+    int32_t down_type;     /* ffn_down.weight: 0 or 2 q4_0, 3 q4_1 (llama.cpp's q4_0 recipe) */
+    int32_t tied;          /* 1: no output.weight, the embedding serves as lm_head */
 } mi_synth_shape;
 /* Writes a seeded random-init qwen2 GGUF: q4_0 matrices (uniform nibbles, fp16
  * |N(0,0.002)| scales), fp32 N(0,0.02) norms/biases/embedding, a token list of
- * n_vocab entries. Same seed -> same bytes. No reference counterpart (the
+ * n_vocab entries. Same seed -> same bytes. Other matrix types, when asked for, have
+ * random codes with scales of a similar weight range. No reference counterpart (the
  * reference runs downloaded Qwen files, README.md:58). */
 int mi_synth_gguf(const char* path, const mi_synth_shape* shape, uint64_t seed);
 

@@ -124,12 +124,49 @@ void dequant_row(const GTensor& t, int64_t r, float* out) {
             }
             break;
         }
+        case GT_Q4_1: {     // 20-byte blocks: fp16 d, fp16 m, 16 B of nibbles (element j low, j+16 high)
+            const uint8_t* p = t.data + (size_t)r * (c / 32) * 20;
+            for (int64_t b = 0; b < c / 32; b++, p += 20) {
+                uint16_t hd, hm; memcpy(&hd, p, 2); memcpy(&hm, p + 2, 2);
+                const float d = f16_to_f32(hd), m = f16_to_f32(hm);
+                for (int j = 0; j < 16; j++) {
+                    out[b * 32 + j] = (p[4 + j] & 0x0F) * d + m;
+                    out[b * 32 + j + 16] = (p[4 + j] >> 4) * d + m;
+                }
+            }
+            break;
+        }
         case GT_Q8_0: {
             const uint8_t* p = t.data + (size_t)r * (c / 32) * 34;
             for (int64_t b = 0; b < c / 32; b++, p += 34) {
                 uint16_t hd; memcpy(&hd, p, 2);
                 const float d = f16_to_f32(hd);
                 for (int j = 0; j < 32; j++) out[b * 32 + j] = (int8_t)p[2 + j] * d;
+            }
+            break;
+        }
+        case GT_Q6_K: {
+            // 210-byte superblocks of 256: ql[128] low nibbles, qh[64] 2-bit highs, int8
+            // scales[16] (one per 16 values), fp16 d. Each 128-value half: value l (l < 32)
+            // of quarter k takes its low nibble from ql[l + 32 (k & 1)] (low nibble for
+            // k < 2, high for k >= 2) and its two high bits from qh[l] bits 2k..2k+1;
+            // q - 32 times d times the scale of its 16-value group.
+            const uint8_t* p = t.data + (size_t)r * (c / 256) * 210;
+            for (int64_t b = 0; b < c / 256; b++, p += 210) {
+                uint16_t hd; memcpy(&hd, p + 208, 2);
+                const float d = f16_to_f32(hd);
+                for (int half = 0; half < 2; half++) {
+                    const uint8_t* ql = p + 64 * half;
+                    const uint8_t* qh = p + 128 + 32 * half;
+                    const int8_t* sc = reinterpret_cast<const int8_t*>(p + 192 + 8 * half);
+                    float* y = out + b * 256 + 128 * half;
+                    for (int l = 0; l < 32; l++)
+                        for (int k = 0; k < 4; k++) {
+                            const int lo = k < 2 ? (ql[l + 32 * (k & 1)] & 0x0F) : (ql[l + 32 * (k & 1)] >> 4);
+                            const int q = (lo | (((qh[l] >> (2 * k)) & 3) << 4)) - 32;
+                            y[32 * k + l] = d * sc[l / 16 + 2 * k] * q;
+                        }
+                }
             }
             break;
         }

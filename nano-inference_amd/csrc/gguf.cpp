@@ -15,7 +15,9 @@ size_t GTensor::nbytes() const {
         case GT_F32: return (size_t)(c * r) * 4;
         case GT_F16: return (size_t)(c * r) * 2;
         case GT_Q4_0: return (size_t)(c / 32 * r) * 18;
+        case GT_Q4_1: return (size_t)(c / 32 * r) * 20;
         case GT_Q8_0: return (size_t)(c / 32 * r) * 34;
+        case GT_Q6_K: return (size_t)(c / 256 * r) * 210;
         default: return 0;
     }
 }
@@ -112,7 +114,7 @@ bool GGUFFile::parse() {
         GTensor& t = kv.second;
         t.data = base_ + start + t.offset;
         const size_t nb = t.nbytes();
-        if (t.type != GT_F32 && t.type != GT_F16 && t.type != GT_Q4_0 && t.type != GT_Q8_0) {
+        if (!gtype_known(t.type)) {
             // kept (a model may carry tensors the engine never reads); size unknown
         } else if (start + t.offset + nb > size_) {
             err_ = "tensor " + kv.first + " runs past the end of the file"; return false;

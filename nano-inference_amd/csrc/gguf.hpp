@@ -15,7 +15,11 @@
 
 namespace mi {
 
-enum GType : uint32_t { GT_F32 = 0, GT_F16 = 1, GT_Q4_0 = 2, GT_Q8_0 = 8 };
+enum GType : uint32_t { GT_F32 = 0, GT_F16 = 1, GT_Q4_0 = 2, GT_Q4_1 = 3, GT_Q8_0 = 8, GT_Q6_K = 14 };
+// the tensor types the loader reads (gguf.h:22-35 lists the same set)
+inline bool gtype_known(uint32_t t) {
+    return t == GT_F32 || t == GT_F16 || t == GT_Q4_0 || t == GT_Q4_1 || t == GT_Q8_0 || t == GT_Q6_K;
+}
 
 struct GTensor {
     uint32_t type = 0;

@@ -113,6 +113,42 @@ void fill_q4(Out& t, uint64_t seed, uint64_t tid, int64_t nblocks, float sigma) 
     });
 }
 
+// q8_0 (int8 codes uniform in [-127, 127], fp16 d = |N(0, sigma)| / 16), q4_1 (nibbles
+// uniform, d = |N(0, sigma)|, m = -8 d rounded to fp16) and q6_K (random 6-bit codes,
+// int8 group scales uniform in [1, 63], fp16 d = |N(0, sigma)| / 256) blocks
+void fill_blocks(Out& t, uint64_t seed, uint64_t tid, int64_t nblocks, float sigma) {
+    const size_t bs = t.type == mi::GT_Q8_0 ? 34 : t.type == mi::GT_Q4_1 ? 20 : 210;
+    t.bytes.resize((size_t)nblocks * bs);
+    uint8_t* p = t.bytes.data();
+    const int64_t nseg = (nblocks + kSegQ4 - 1) / kSegQ4;
+    const uint32_t type = t.type;
+    parallel_segments(nseg, [=](int64_t sgi) {
+        Rng r(mix64(seed ^ mix64(tid * 0x100000001B3ull + (uint64_t)sgi)));
+        const int64_t a = sgi * kSegQ4, b = std::min<int64_t>(nblocks, a + kSegQ4);
+        for (int64_t i = a; i < b; i++) {
+            uint8_t* blk = p + i * bs;
+            const double g = std::fabs(sigma * normal(r));
+            if (type == mi::GT_Q8_0) {
+                const uint16_t d = mi::f32_to_f16((float)(g / 16.0));
+                memcpy(blk, &d, 2);
+                for (int j = 0; j < 32; j++) blk[2 + j] = (uint8_t)(int8_t)((int)(r.next() % 255) - 127);
+            } else if (type == mi::GT_Q4_1) {
+                const uint16_t d = mi::f32_to_f16((float)g), m = mi::f32_to_f16((float)(-8.0 * g));
+                memcpy(blk, &d, 2);
+                memcpy(blk + 2, &m, 2);
+                const uint64_t w0 = r.next(), w1 = r.next();
+                memcpy(blk + 4, &w0, 8);
+                memcpy(blk + 12, &w1, 8);
+            } else {
+                for (int j = 0; j < 192; j += 8) { const uint64_t w = r.next(); memcpy(blk + j, &w, 8); }
+                for (int j = 0; j < 16; j++) blk[192 + j] = (uint8_t)(int8_t)(1 + (int)(r.next() % 63));
+                const uint16_t d = mi::f32_to_f16((float)(g / 256.0));
+                memcpy(blk + 208, &d, 2);
+            }
+        }
+    });
+}
+
 // GPT-2 byte-level alphabet (the inverse of detok.h's byte decoder): printable
 // bytes map to themselves, the rest to U+0100 + k
 std::string byte_token(int b) {
@@ -155,7 +191,13 @@ extern "C" int mi_synth_gguf(const char* path, const mi_synth_shape* sh, uint64_
         return ts.size() - 1;
     };
     // tensor list and shapes: ne[0] is the input (row) length
-    add("token_embd.weight", sh->emb_type == 2 ? mi::GT_Q4_0 : mi::GT_F32, {E, V});
+    auto mtype = [](int32_t t, uint32_t def) -> uint32_t { return t == 0 ? def : (uint32_t)t; };
+    const uint32_t emb_t = sh->emb_type == 2 ? mi::GT_Q4_0 : sh->emb_type == 8 ? mi::GT_Q8_0 : mi::GT_F32;
+    const uint32_t head_t = mtype(sh->head_type, mi::GT_Q4_0), down_t = mtype(sh->down_type, mi::GT_Q4_0);
+    if ((head_t != mi::GT_Q4_0 && head_t != mi::GT_Q8_0 && head_t != mi::GT_Q6_K) ||
+        (down_t != mi::GT_Q4_0 && down_t != mi::GT_Q4_1) || (head_t == mi::GT_Q6_K && E % 256))
+        return MI_ERR_ARG;
+    add("token_embd.weight", emb_t, {E, V});
     for (int l = 0; l < L; l++) {
         const std::string p = "blk." + std::to_string(l) + ".";
         add(p + "attn_norm.weight", mi::GT_F32, {E});
@@ -169,10 +211,10 @@ extern "C" int mi_synth_gguf(const char* path, const mi_synth_shape* sh, uint64_
         add(p + "ffn_norm.weight", mi::GT_F32, {E});
         add(p + "ffn_gate.weight", mi::GT_Q4_0, {E, FF});
         add(p + "ffn_up.weight", mi::GT_Q4_0, {E, FF});
-        add(p + "ffn_down.weight", mi::GT_Q4_0, {FF, E});
+        add(p + "ffn_down.weight", down_t, {FF, E});
     }
     add("output_norm.weight", mi::GT_F32, {E});
-    add("output.weight", mi::GT_Q4_0, {E, V});
+    if (!sh->tied) add("output.weight", head_t, {E, V});
 
     FILE* f = fopen(path, "wb");
     if (!f) return MI_ERR_IO;
@@ -205,7 +247,13 @@ extern "C" int mi_synth_gguf(const char* path, const mi_synth_shape* sh, uint64_
     // tensor infos with 32-byte aligned offsets
     auto nbytes = [](const Out& t) {
         int64_t n = 1; for (auto e : t.ne) n *= e;
-        return t.type == mi::GT_F32 ? (uint64_t)n * 4 : (uint64_t)(n / 32) * 18;
+        switch (t.type) {
+            case mi::GT_F32: return (uint64_t)n * 4;
+            case mi::GT_Q4_1: return (uint64_t)(n / 32) * 20;
+            case mi::GT_Q8_0: return (uint64_t)(n / 32) * 34;
+            case mi::GT_Q6_K: return (uint64_t)(n / 256) * 210;
+            default: return (uint64_t)(n / 32) * 18;
+        }
     };
     uint64_t off = 0;
     std::vector<uint64_t> offs;
@@ -224,7 +272,8 @@ extern "C" int mi_synth_gguf(const char* path, const mi_synth_shape* sh, uint64_
         Out& t = ts[i];
         int64_t n = 1; for (auto e : t.ne) n *= e;
         if (t.type == mi::GT_F32) fill_f32(t, seed, i, n, 0.02f);
-        else fill_q4(t, seed, i, n / 32, 0.002f);
+        else if (t.type == mi::GT_Q4_0) fill_q4(t, seed, i, n / 32, 0.002f);
+        else fill_blocks(t, seed, i, t.type == mi::GT_Q6_K ? n / 256 : n / 32, 0.002f);
         pos = ftell(f);
         const long want = start + (long)offs[i];
         if (want > pos) w.raw(zeros, (size_t)(want - pos));

@@ -18,7 +18,7 @@ static void matvec(const orc_tensor* W, const float* x, float* y, int nthr) {
     #pragma omp parallel for schedule(static) num_threads(nthr)
     for (int64_t j = 0; j < out; j++) {
         float row[16384];
-        orc_dequant_row(W, j, row);
+        orc_dequant_row_fma(W, j, row);
         float acc = 0.f;
         for (int64_t k = 0; k < in; k++) acc += row[k] * x[k];
         y[j] = acc;
@@ -86,7 +86,7 @@ void orc_attention_fp32(const float* qh, const float* k, const float* v, int L, 
 int32_t orc_forward_fp32(struct orc_model* m, int32_t token, int32_t pos) {
     const orc_config* c = &m->c;
     const int kv_dim = c->n_head_kv * c->head_dim, gqa = c->n_head / c->n_head_kv;
-    orc_dequant_row(m->tok_emb, token, m->h);
+    orc_dequant_row_fma(m->tok_emb, token, m->h);
     for (int l = 0; l < c->n_layer; l++) {
         const orc_layer* ly = &m->L[l];
         rmsnorm(m->h, ly->an, c->n_embd, c->rms_eps, m->xb);

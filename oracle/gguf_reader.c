@@ -12,6 +12,7 @@
 #include <fcntl.h>
 #include <stdio.h>
 #include <stdlib.h>
+#include <math.h>
 #include <string.h>
 #include <sys/mman.h>
 #include <sys/stat.h>
@@ -197,8 +198,8 @@ uint16_t orc_f32_to_f16(float f) {
     return (uint16_t)(sign | q);
 }
 
-/* gguf.h:85-102, 110-115 (F32, F16, Q4_0, Q8_0) */
-void orc_dequant_row(const orc_tensor* t, int64_t r, float* out) {
+/* gguf.h:85-142 (F32, F16, Q4_0, Q4_1, Q8_0, Q6_K) */
+static void dequant(const orc_tensor* t, int64_t r, float* out, int fma_q41) {
     const int64_t cols = t->ne[0];
     switch (t->type) {
         case ORC_F32: memcpy(out, t->data + (size_t)r * cols * 4, (size_t)cols * 4); return;
@@ -221,6 +222,21 @@ void orc_dequant_row(const orc_tensor* t, int64_t r, float* out) {
             }
             return;
         }
+        case ORC_Q4_1: {   /* gguf.h:103-113: fp16 d, fp16 m, 16 B of nibbles */
+            const int64_t bpr = cols / 32;
+            const uint8_t* p = t->data + (size_t)(r * bpr) * 20;
+            for (int64_t b = 0; b < bpr; b++, p += 20) {
+                uint16_t hd, hm; memcpy(&hd, p, 2); memcpy(&hm, p + 2, 2);
+                const float d = orc_f16_to_f32(hd), m = orc_f16_to_f32(hm);
+                const uint8_t* qs = p + 4; float* y = out + b * 32;
+                for (int j = 0; j < 16; j++) {
+                    const float q0 = (float)(qs[j] & 0x0F), q1 = (float)(qs[j] >> 4);
+                    y[j] = fma_q41 ? fmaf(q0, d, m) : q0 * d + m;
+                    y[j + 16] = fma_q41 ? fmaf(q1, d, m) : q1 * d + m;
+                }
+            }
+            return;
+        }
         case ORC_Q8_0: {
             const int64_t bpr = cols / 32;
             const uint8_t* p = t->data + (size_t)(r * bpr) * 34;
@@ -232,6 +248,49 @@ void orc_dequant_row(const orc_tensor* t, int64_t r, float* out) {
             }
             return;
         }
+        case ORC_Q6_K: {   /* gguf.h:120-139: ql[128], qh[64], int8 scales[16], fp16 d per 256 */
+            const int64_t bpr = cols / 256;
+            const uint8_t* p = t->data + (size_t)(r * bpr) * 210;
+            for (int64_t b = 0; b < bpr; b++, p += 210) {
+                uint16_t hd; memcpy(&hd, p + 208, 2);
+                const float d = orc_f16_to_f32(hd);
+                const uint8_t* ql = p; const uint8_t* qh = p + 128; const int8_t* sc = (const int8_t*)(p + 192);
+                float* y = out + b * 256;
+                for (int n = 0; n < 256; n += 128) {
+                    for (int l = 0; l < 32; l++) {
+                        const int is = l / 16;
+                        const int q1 = ((ql[l] & 0xF) | (((qh[l] >> 0) & 3) << 4)) - 32;
+                        const int q2 = ((ql[l + 32] & 0xF) | (((qh[l] >> 2) & 3) << 4)) - 32;
+                        const int q3 = ((ql[l] >> 4) | (((qh[l] >> 4) & 3) << 4)) - 32;
+                        const int q4 = ((ql[l + 32] >> 4) | (((qh[l] >> 6) & 3) << 4)) - 32;
+                        y[l] = d * sc[is + 0] * q1;
+                        y[l + 32] = d * sc[is + 2] * q2;
+                        y[l + 64] = d * sc[is + 4] * q3;
+                        y[l + 96] = d * sc[is + 6] * q4;
+                    }
+                    ql += 64; qh += 32; sc += 8; y += 128;
+                }
+            }
+            return;
+        }
         default: for (int64_t i = 0; i < cols; i++) out[i] = 0.f; return;
+    }
+}
+void orc_dequant_row(const orc_tensor* t, int64_t r, float* out) { dequant(t, r, out, 0); }
+void orc_dequant_row_fma(const orc_tensor* t, int64_t r, float* out) { dequant(t, r, out, 1); }
+
+void orc_requant_q4_0_row(const float* y, int n, uint8_t* out) {
+    for (int b = 0; b < n / 32; b++, y += 32, out += 18) {
+        float amax = 0.f;
+        for (int j = 0; j < 32; j++) amax = fmaxf(amax, fabsf(y[j]));
+        const float d = amax / 7.f, inv = d > 0.f ? 1.f / d : 0.f;
+        const uint16_t hd = orc_f32_to_f16(d);
+        memcpy(out, &hd, 2);
+        for (int j = 0; j < 16; j++) {
+            int q0 = (int)lrintf(y[j] * inv) + 8, q1 = (int)lrintf(y[j + 16] * inv) + 8;
+            q0 = q0 < 0 ? 0 : (q0 > 15 ? 15 : q0);
+            q1 = q1 < 0 ? 0 : (q1 > 15 ? 15 : q1);
+            out[2 + j] = (uint8_t)(q0 | (q1 << 4));
+        }
     }
 }

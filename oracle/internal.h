@@ -22,6 +22,9 @@ struct orc_model {
     int8_t* xq; float* xd; int32_t* xs8;
     float* rope_c; float* rope_s;   /* [max_seq][head_dim/2], cpu_infer.cpp:54-55 values */
     float* scores;                   /* [max_seq] */
+    /* q8act: q4_0 copies of the matrices stored in other types (the engine requantizes
+     * them at load, mega.cu:1091-1111) */
+    orc_tensor* own_t; uint8_t** own_buf; int n_own;
 };
 
 int32_t orc_forward_fp32(struct orc_model* m, int32_t token, int32_t pos);

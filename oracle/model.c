@@ -55,7 +55,8 @@ orc_model* orc_model_new(const orc_gguf* g, int mode, const orc_plan* plan, int 
 #endif
     int ok = 1;
     m->tok_emb = need_t(g, "token_embd.weight", &ok);
-    m->out_w = need_t(g, "output.weight", &ok);
+    m->out_w = orc_gguf_tensor(g, "output.weight");
+    if (!m->out_w) m->out_w = m->tok_emb;          /* tied embeddings (mega.cu:1071) */
     m->out_norm = need_t(g, "output_norm.weight", &ok);
     m->L = (orc_layer*)calloc((size_t)c->n_layer, sizeof(orc_layer));
     char name[128];
@@ -68,6 +69,40 @@ orc_model* orc_model_new(const orc_gguf* g, int mode, const orc_plan* plan, int 
     }
 #undef T
     if (!ok || c->n_vocab <= 0) { orc_model_free(m); return NULL; }
+    if (mode == ORC_MODE_Q8ACT) {
+        const int nmat = 7 * c->n_layer + 1;
+        m->own_t = (orc_tensor*)calloc((size_t)nmat, sizeof(orc_tensor));
+        m->own_buf = (uint8_t**)calloc((size_t)nmat, sizeof(uint8_t*));
+        for (int i = 0; i <= c->n_layer; i++) {
+            const orc_tensor** mats[7];
+            int k = 0;
+            if (i < c->n_layer) {
+                orc_layer* Ly = &m->L[i];
+                mats[k++] = &Ly->wq; mats[k++] = &Ly->wk; mats[k++] = &Ly->wv; mats[k++] = &Ly->wo;
+                mats[k++] = &Ly->wg; mats[k++] = &Ly->wu; mats[k++] = &Ly->wd;
+            } else {
+                mats[k++] = &m->out_w;
+            }
+            for (int j = 0; j < k; j++) {
+                const orc_tensor* t = *mats[j];
+                if (t->type == ORC_Q4_0) continue;
+                const int64_t n = t->ne[0], rows = t->ne[1] * t->ne[2] * t->ne[3];
+                uint8_t* buf = (uint8_t*)malloc((size_t)rows * (n / 32) * 18);
+                float* row = (float*)malloc(sizeof(float) * (size_t)n);
+                for (int64_t r = 0; r < rows; r++) {
+                    orc_dequant_row(t, r, row);
+                    orc_requant_q4_0_row(row, (int)n, buf + (size_t)r * (n / 32) * 18);
+                }
+                free(row);
+                orc_tensor* o = &m->own_t[m->n_own];
+                *o = *t;
+                o->type = ORC_Q4_0;
+                o->data = buf;
+                m->own_buf[m->n_own++] = buf;
+                *mats[j] = o;
+            }
+        }
+    }
     const int kvd = c->n_head_kv * c->head_dim, E = c->n_embd;
     m->kc = (float*)calloc((size_t)c->n_layer * max_seq * kvd, 4);
     m->vc = (float*)calloc((size_t)c->n_layer * max_seq * kvd, 4);
@@ -93,6 +128,8 @@ void orc_model_free(orc_model* m) {
     free(m->L); free(m->kc); free(m->vc); free(m->h); free(m->xb); free(m->q); free(m->k); free(m->v);
     free(m->att); free(m->proj); free(m->gbuf); free(m->ubuf); free(m->logits);
     free(m->xq); free(m->xd); free(m->xs8); free(m->rope_c); free(m->rope_s); free(m->scores);
+    for (int i = 0; i < m->n_own; i++) free(m->own_buf[i]);
+    free(m->own_buf); free(m->own_t);
     free(m);
 }
 

@@ -40,7 +40,7 @@ extern "C" {
 #endif
 
 /* ---------------- GGUF v3 reader (restates src/gguf.h:19-222) ---------------- */
-enum { ORC_F32 = 0, ORC_F16 = 1, ORC_Q4_0 = 2, ORC_Q8_0 = 8 };
+enum { ORC_F32 = 0, ORC_F16 = 1, ORC_Q4_0 = 2, ORC_Q4_1 = 3, ORC_Q8_0 = 8, ORC_Q6_K = 14 };
 
 typedef struct {
     uint32_t type;
@@ -61,7 +61,12 @@ const char* orc_gguf_error(void);
 /* ---------------- scalar building blocks ---------------- */
 float orc_f16_to_f32(uint16_t h);                       /* gguf.h:37-52 */
 uint16_t orc_f32_to_f16(float f);                       /* IEEE round-to-nearest-even */
-void orc_dequant_row(const orc_tensor* t, int64_t r, float* out);   /* gguf.h:85-102 (F32/F16/Q4_0/Q8_0) */
+void orc_dequant_row(const orc_tensor* t, int64_t r, float* out);   /* gguf.h:85-142, no fma contraction */
+/* the same with Q4_1's q*d + m as one fma, as cpu_infer's -march=native build contracts it */
+void orc_dequant_row_fma(const orc_tensor* t, int64_t r, float* out);
+/* mega.cu:924-936 quant_row_q4_0 / cuda_infer.cu:809-843: n floats -> n/32 q4_0 blocks
+ * (d = amax/7 rounded to fp16, q = clamp(lrintf(y / d) + 8, 0, 15) with 1/d unrounded) */
+void orc_requant_q4_0_row(const float* y, int n, uint8_t* out);
 float orc_expf(float x);                                /* the engine's exp: Cody-Waite + Taylor-7 */
 
 /* per-32 int8 quantization of n floats (n % 32 == 0): xq[n], xd[n/32], xs8[n/32] = 8*sum(q) */

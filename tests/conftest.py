@@ -21,13 +21,15 @@ def tmpdir_mi():
     return TMP
 
 
-def synth_cached(name, shape, seed, expect_hash=None):
-    """Regenerate a synthetic GGUF (or reuse an identical one) under TMP."""
+def synth_cached(name, shape, seed, expect_hash=None, **types):
+    """Regenerate a synthetic GGUF (or reuse an identical one) under TMP. types:
+    emb_type / head_type / down_type / tied, as minfer.synth_gguf takes them."""
     import minfer
     os.makedirs(TMP, exist_ok=True)
-    path = os.path.join(TMP, "%s-%d.gguf" % (name, seed))
+    tag = "".join("-%s%s" % (k, int(v)) for k, v in sorted(types.items()))
+    path = os.path.join(TMP, "%s-%d%s.gguf" % (name, seed, tag))
     marker = path + ".ok"
     if not (os.path.exists(path) and os.path.exists(marker)):
-        minfer.synth_gguf(path, shape, seed)
+        minfer.synth_gguf(path, shape, seed, **types)
         open(marker, "w").close()
     return path

@@ -6,7 +6,10 @@ small JSON fixtures here. The GGUF inputs are regenerated bit-identically from
 their seeds by mi_synth_gguf; the fixture records the file's xxh64 so a test can
 prove the regeneration.
 
-    python tests/golden/make_golden.py [config0] [config2] [tiny]
+    python tests/golden/make_golden.py [config0] [config2] [tiny] [mixed]
+
+`mixed` is the tiny shape with the tensor types of a real Qwen2.5 q4_0 file
+(q6_K output.weight, q4_1 ffn_down) and a q8_0 token embedding.
 """
 import json
 import os
@@ -23,6 +26,7 @@ import minfer  # noqa: E402
 REF = os.path.join(ROOT, "oracle", "_ref", "cpu_infer")
 TMP = os.environ.get("MI_TMP", "/tmp/mi")
 TINY = dict(n_layer=2, n_embd=256, n_ff=512, n_head=4, n_head_kv=2, n_vocab=4096)
+MIXED = dict(head_type=minfer.GT_Q6_K, down_type=minfer.GT_Q4_1, emb_type=minfer.GT_Q8_0)
 
 
 def file_hash(path):
@@ -36,16 +40,16 @@ def file_hash(path):
     return h.hexdigest()
 
 
-def run(name, shape, mseed, pseed, n_prompt, n_gen):
+def run(name, shape, mseed, pseed, n_prompt, n_gen, types=None):
     os.makedirs(TMP, exist_ok=True)
     path = os.path.join(TMP, "%s.gguf" % name)
-    minfer.synth_gguf(path, shape, mseed)
+    minfer.synth_gguf(path, shape, mseed, **(types or {}))
     V = (minfer.SHAPES[shape] if isinstance(shape, str) else shape)["n_vocab"]
     ids = minfer.prompt_ids(pseed, n_prompt, V)
     t = time.time()
     r = subprocess.run([REF, path, str(n_gen)] + [str(i) for i in ids], capture_output=True, text=True, check=True)
     toks = [int(x) for x in r.stdout.split()]
-    fx = dict(config=name, shape=shape, model_seed=mseed, prompt_seed=pseed, prompt=ids, n_gen=n_gen,
+    fx = dict(config=name, shape=shape, types=types or {}, model_seed=mseed, prompt_seed=pseed, prompt=ids, n_gen=n_gen,
               tokens=toks, gguf_xxh64=file_hash(path), gguf_bytes=os.path.getsize(path),
               source="reference src/cpu_infer.cpp built by oracle/Makefile (g++ -std=gnu++17 -O3 -march=native -fopenmp)",
               ref_seconds=round(time.time() - t, 1))
@@ -60,6 +64,8 @@ if __name__ == "__main__":
     for w in which:
         if w == "tiny":
             run("tiny", TINY, 7, 8, 8, 64)
+        elif w == "mixed":
+            run("mixed", TINY, 17, 18, 12, 64, types=MIXED)
         else:
             shape, ms, ps, npr, ng = minfer.CONFIGS[w]
             run(w, shape, ms, ps, npr, ng)

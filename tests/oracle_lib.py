@@ -68,6 +68,9 @@ def lib():
             "orc_attention_canon": (None, [_P, _P, _P, C.c_int, C.c_int, C.c_int, C.c_float, C.c_int, _P]),
             "orc_attention_fp32": (None, [_P, _P, _P, C.c_int, C.c_int, C.c_int, C.c_float, _P]),
             "orc_rope_cs": (None, [C.c_int, C.c_int, C.c_int, C.c_float, _F, _F]),
+            "orc_dequant_row": (None, [_P, C.c_int64, _P]),
+            "orc_dequant_row_fma": (None, [_P, C.c_int64, _P]),
+            "orc_requant_q4_0_row": (None, [_P, C.c_int, _P]),
         }
         for k, (r, a) in sig.items():
             f = getattr(L, k)

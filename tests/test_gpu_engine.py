@@ -115,6 +115,36 @@ def test_config_stream_128(name, persistent):
         % (name, d, margins[d] if d < len(margins) else float("nan")))
 
 
+REAL_TYPES = [
+    pytest.param(dict(head_type=minfer.GT_Q6_K, down_type=minfer.GT_Q4_1, emb_type=minfer.GT_Q8_0), id="q6k-head-q41-down-q8-emb"),
+    pytest.param(dict(tied=True), id="tied-f32-emb"),
+    pytest.param(dict(tied=True, emb_type=minfer.GT_Q8_0), id="tied-q8-emb"),
+    pytest.param(dict(head_type=minfer.GT_Q8_0), id="q8-head"),
+]
+
+
+@pytest.mark.parametrize("types", REAL_TYPES)
+def test_real_model_tensor_types(types):
+    """The tensor types of real Qwen2.5 q4_0 files (mega.cu:924-936, 1071, 1091-1111):
+    non-q4_0 matrices requantized to q4_0 at load, tied embeddings, a q8_0 embedding
+    gathered as fp32. Logits bit-identical to the q8act oracle, which requantizes from
+    its own dequantization (pinned to the reference by the mixed-types golden stream)."""
+    path = synth_cached("eng-256", TINY, 7, **types)
+    say("real-model tensor types", types)
+    eng = minfer.Engine(path, max_ctx=128)
+    orc = O.Model(path, O.MODE_Q8ACT, plan=plan_of(eng), max_seq=128)
+    toks = minfer.prompt_ids(5, 10, TINY["n_vocab"])
+    nxt = None
+    for pos in range(40):
+        tok = toks[pos] if pos < len(toks) else nxt
+        a, ma, la = eng.step(tok, pos, want_logits=True)
+        b, mb, lb = orc.forward(tok, pos, True)
+        assert np.array_equal(la.view(np.uint32), lb.view(np.uint32)), "logits differ at pos %d" % pos
+        assert a == b and ma == mb
+        nxt = a
+    eng.close()
+
+
 def test_long_context_chunk_merge_phase():
     """past 4 chunks the merge runs as its own phase, past 16 as a two-level tree of
     16-chunk splits: positions 0..1101 (18 chunks), tokens and margins vs the oracle"""

@@ -36,7 +36,7 @@ def file_hash(path):
 
 
 def model_path(fx):
-    return synth_cached(fx["config"], fx["shape"], fx["model_seed"])
+    return synth_cached(fx["config"], fx["shape"], fx["model_seed"], **fx.get("types", {}))
 
 
 def check_stream(fx, n=None):
@@ -53,6 +53,14 @@ def check_stream(fx, n=None):
 
 def test_tiny_stream_matches_reference_cpu_infer():
     check_stream(load("tiny"))
+
+
+def test_mixed_types_stream_matches_reference_cpu_infer():
+    """q6_K output.weight, q4_1 ffn_down and a q8_0 embedding (gguf.h:85-142): the
+    fp32 oracle's dequantization of each type must give the reference's stream"""
+    fx = load("mixed")
+    assert fx["types"] == {"head_type": 14, "down_type": 3, "emb_type": 8}
+    check_stream(fx)
 
 
 @pytest.mark.slow

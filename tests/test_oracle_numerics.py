@@ -204,3 +204,90 @@ def test_rope_cs_float_theta():
             assert abs(c.value - math.cos(float(theta))) <= 2e-7 and abs(s.value - math.sin(float(theta))) <= 2e-7
     O.lib().orc_rope_cs(0, 5, 128, C.c_float(1e6), C.byref(c), C.byref(s))
     assert c.value == 1.0 and s.value == 0.0
+
+
+class _Tensor(__import__("ctypes").Structure):
+    import ctypes as C
+    _fields_ = [("type", C.c_uint32), ("nd", C.c_int32), ("ne", C.c_int64 * 4), ("data", C.c_void_p)]
+
+
+def _dequant(buf, type_, cols, rows=1, fma=False):
+    import ctypes as C
+    t = _Tensor(type_, 2, (C.c_int64 * 4)(cols, rows, 1, 1), buf.ctypes.data)
+    out = np.zeros(cols * rows, np.float32)
+    f = O.lib().orc_dequant_row_fma if fma else O.lib().orc_dequant_row
+    for r in range(rows):
+        f(C.addressof(t), r, out[r * cols:].ctypes.data)
+    return out.reshape(rows, cols)
+
+
+def _f16(x):
+    return np.float16(x).view(np.uint16).tobytes()
+
+
+def test_dequant_q8_0_codes_times_scale():
+    rng = np.random.default_rng(41)
+    codes = rng.integers(-128, 128, (3, 32), dtype=np.int8)
+    ds = np.float16([0.5, -0.0078125, 3.25])
+    buf = np.frombuffer(b"".join(_f16(d) + c.tobytes() for d, c in zip(ds, codes)), np.uint8).copy()
+    got = _dequant(buf, 8, 96)[0]
+    assert np.array_equal(got, (codes.astype(np.float32) * ds.astype(np.float32)[:, None]).ravel())
+
+
+def test_dequant_q4_1_nibbles_scale_and_min():
+    """GGUF q4_1: element j of a block in the low nibble of byte j, j + 16 in the high"""
+    rng = np.random.default_rng(42)
+    n = rng.integers(0, 16, (2, 32))
+    d, m = np.float16([0.25, 1.5]), np.float16([-2.0, 0.125])
+    packed = [(n[b, :16] | (n[b, 16:] << 4)).astype(np.uint8) for b in range(2)]
+    buf = np.frombuffer(b"".join(_f16(d[b]) + _f16(m[b]) + packed[b].tobytes() for b in range(2)), np.uint8).copy()
+    want = (n * d.astype(np.float32)[:, None] + m.astype(np.float32)[:, None]).astype(np.float32).ravel()
+    # scales and mins chosen so that q*d + m is exact in fp32: fused or not, the same value
+    assert np.array_equal(_dequant(buf, 3, 64)[0], want)
+    assert np.array_equal(_dequant(buf, 3, 64, fma=True)[0], want)
+
+
+def _q6k_encode(q, sc, d):
+    """ggml's q6_K layout from its definition: 256 values as two halves of 128; in a
+    half, value 32k + l (k = 0..3, l = 0..31) keeps its low 4 bits in ql[l + 32 (k & 1)]
+    (low nibble for k < 2, high for k >= 2) and its high 2 bits in qh[l] bits 2k..2k+1;
+    16 int8 scales (one per 16 values), fp16 d at the end"""
+    ql = np.zeros(128, np.uint8)
+    qh = np.zeros(64, np.uint8)
+    for half in range(2):
+        for k in range(4):
+            for l in range(32):
+                v = int(q[128 * half + 32 * k + l])
+                i = 64 * half + l + 32 * (k & 1)
+                ql[i] |= (v & 15) << (4 * (k >= 2))
+                qh[32 * half + l] |= (v >> 4) << (2 * k)
+    return ql.tobytes() + qh.tobytes() + sc.astype(np.int8).tobytes() + _f16(d)
+
+
+def test_dequant_q6_k_round_trip():
+    rng = np.random.default_rng(43)
+    q = rng.integers(0, 64, 512)
+    sc = rng.integers(-64, 64, 32)
+    d = np.float16([0.03125, 0.5])
+    buf = np.frombuffer(_q6k_encode(q[:256], sc[:16], d[0]) + _q6k_encode(q[256:], sc[16:], d[1]), np.uint8).copy()
+    assert buf.size == 420
+    got = _dequant(buf, 14, 512)[0]
+    grp = np.repeat(np.arange(32), 16)           # value i of superblock b uses scale 16 b + i // 16
+    dd = np.repeat(d.astype(np.float32), 256)
+    want = (dd * sc[grp].astype(np.float32)) * (q - 32).astype(np.float32)
+    assert np.array_equal(got, want.astype(np.float32))
+
+
+def test_requant_q4_0_recipe():
+    """mega.cu:924-936: d = amax/7 stored as fp16, q = clamp(rint(y / d) + 8, 0, 15)
+    with the unrounded 1/d; an all-zero block keeps d = 0 and codes 8"""
+    y = np.zeros(64, np.float32)
+    y[:32] = np.linspace(-3.5, 3.5, 32, dtype=np.float32)
+    out = np.zeros(36, np.uint8)
+    O.lib().orc_requant_q4_0_row(y.ctypes.data, 64, out.ctypes.data)
+    d = np.frombuffer(out[:2].tobytes(), np.float16)[0]
+    assert d == np.float16(np.float32(3.5) / np.float32(7))
+    inv = np.float32(1) / (np.float32(3.5) / np.float32(7))
+    q = np.clip(np.rint(y[:32] * inv).astype(int) + 8, 0, 15)
+    assert np.array_equal(out[2:18], (q[:16] | (q[16:] << 4)).astype(np.uint8))
+    assert np.frombuffer(out[18:20].tobytes(), np.float16)[0] == 0 and np.all(out[20:36] == 0x88)
