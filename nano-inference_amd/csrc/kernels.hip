@@ -776,16 +776,35 @@ __device__ __forceinline__ void attn_core(const uint4* kls, const float* qs, con
 #pragma unroll
     for (int e = 0; e < DPL; e++) acc[e] = 0.f;
     const int pb = __float_as_int(p);
-#pragma unroll 8
-    for (int t = 0; t < n; t++) {
+    // V rows in batches of 8: the LDS reads of a batch are issued together, then the
+    // fma chain (positions in order) consumes them; n is wave-uniform (scalar loop)
+    constexpr int B = 8;
+    using VT = typename std::conditional<DPL == 2, uint32_t, uint16_t>::type;
+    const int ns = __builtin_amdgcn_readfirstlane(n);
+    auto step = [&](VT w, int t) {
         const float pt = __int_as_float(__builtin_amdgcn_readlane(pb, t));
         if constexpr (DPL == 2) {
-            const uint32_t w2 = *reinterpret_cast<const uint32_t*>(vls + t * HD + 2 * lane);
-            acc[0] = __fmaf_rn(pt, h2f_lo(w2), acc[0]);
-            acc[1] = __fmaf_rn(pt, h2f_hi(w2), acc[1]);
+            acc[0] = __fmaf_rn(pt, h2f_lo(w), acc[0]);
+            acc[1] = __fmaf_rn(pt, h2f_hi(w), acc[1]);
         } else {
-            acc[0] = __fmaf_rn(pt, __half2float(vls[t * HD + lane]), acc[0]);
+            acc[0] = __fmaf_rn(pt, __half2float(__ushort_as_half(w)), acc[0]);
         }
+    };
+    int t0 = 0;
+    for (; t0 + B <= ns; t0 += B) {
+        VT w[B];
+#pragma unroll
+        for (int u = 0; u < B; u++) w[u] = *reinterpret_cast<const VT*>(vls + (t0 + u) * HD + DPL * lane);
+#pragma unroll
+        for (int u = 0; u < B; u++) step(w[u], t0 + u);
+    }
+    for (; t0 < ns; t0 += 4) {       // the tail, four rows per batch
+        VT w[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) w[u] = *reinterpret_cast<const VT*>(vls + min(t0 + u, ns - 1) * HD + DPL * lane);
+#pragma unroll
+        for (int u = 0; u < 4; u++)
+            if (t0 + u < ns) step(w[u], t0 + u);
     }
 }
 
