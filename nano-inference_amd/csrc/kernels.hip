@@ -1025,12 +1025,13 @@ __device__ __forceinline__ void phase_comb(MPtr M, int l, int pos, int wg, int n
 // The phases run as one loop over the flattened sequence (layer, kind), so each
 // piece of code exists once: the whole kernel stays within the instruction cache
 // (an unrolled body of ~115 KB missed it on every layer).
-// Per phase: [control: barrier, prologue] sync [workers: tiles] sync [workers:
-// segment sums, stores, store drain, next phase's prefetch] sync.
+// Per phase: [all waves: staging DMA shares] sync [prologue] sync [workers: tiles]
+// sync [workers: segment sums, stores, store drain] sync [control: grid barrier |
+// workers: next phase's prefetch] sync.
 // Profile slots (every workgroup): 0 = start; then five per phase in the sequence
 // (qkv, attention, o, gate/up, down per layer, then lm_head): prologue end, first
-// worker's tiles done, its stores drained (its next-phase prefetch follows; lm:
-// the control wave's candidate written), phase end, barrier exit.
+// worker's tiles done, its stores drained (lm: the control wave's candidate
+// written), phase end, barrier exit.
 __device__ __forceinline__ PMat phase_mat(MPtr M, int l, int kind) {
     if (kind == PH_LM) return ldmat(&M->lm);
     const LPtr L = LY(M, l);
@@ -1134,7 +1135,6 @@ __global__ __launch_bounds__(kPThreads) void k_step(const DModel* Mp, int pos, i
             phase_store(M, l, kind, wg, nwg, S, kw, lane);
             drain_vm();
             stamp(M, sb + 2, 64);
-            phase_prefetch(M, nl, nk, wg, nwg, kw, tl, lane);
         } else {
             drain_vm();
             tl[0] = Tile{};
@@ -1145,6 +1145,10 @@ __global__ __launch_bounds__(kPThreads) void k_step(const DModel* Mp, int pos, i
         if (ctl) {
             ctl_barrier(M->bar, M->err, epoch);
             stamp(M, sb + 4);
+        } else {
+            // the next phase's first tiles, issued while the control wave waits at the
+            // grid barrier (issuing ~60-120 KB per CU takes the texture unit ~1 us)
+            phase_prefetch(M, nl, nk, wg, nwg, kw, tl, lane);
         }
         __syncthreads();
         stage(M, nl, nk, pos, S, wave, kPWaves, lane, true);
