@@ -578,7 +578,7 @@ __device__ __forceinline__ void stage(MPtr M, int l, int kind, int pos, const Ld
                       (dsrc ? LY(M, pl)->d.ks : LY(M, pl)->o.ks) * n * 4, d, lane);
         }
     }
-    drain_vm();
+    if (kind != PH_ATTN) drain_vm();     // (attention stages nothing; its waves' K/V prefetch stays in flight)
 }
 // the control wave alone (the per-phase kernels, whose workers prefetch meanwhile)
 __device__ __forceinline__ void ctl_stage(MPtr M, int l, int kind, int pos, const Lds& S, int lane, bool resident) {
@@ -1099,11 +1099,6 @@ __global__ __launch_bounds__(kPThreads) void k_step(const DModel* Mp, int pos, i
             phase_work<HD>(M, l, kind, pos, wg, nwg, S, kw, tl, lane);
             tl[0] = Tile{};        // consumed: dead (and not in registers) until the next prefetch
             tl[1] = Tile{};
-        } else if (kind == PH_QKV) {
-            // U is free while the QKV tiles run: the K/V rows of the attention waves'
-            // first items, drained before the control wave leaves this branch
-            for (int a = 0; a < kAttnWaves; a++) attn_prefetch<HD>(M, l, pos, wg, nwg, S.U, a, lane);
-            drain_vm();
         }
         if (kind == PH_ATTN && nch > kInlineComb) {           // the chunk merge as a phase of its own
             drain_vm();
@@ -1145,6 +1140,12 @@ __global__ __launch_bounds__(kPThreads) void k_step(const DModel* Mp, int pos, i
         if (ctl) {
             ctl_barrier(M->bar, M->err, epoch);
             stamp(M, sb + 4);
+        } else if (nk == PH_ATTN) {
+            // the attention waves' first items: their K/V rows into LDS (U is free once
+            // the QKV prologue is done); attn_finish waits for them
+            tl[0] = Tile{};
+            tl[1] = Tile{};
+            attn_prefetch<HD>(M, nl, pos, wg, nwg, S.U, kw, lane);
         } else {
             // the next phase's first tiles, issued while the control wave waits at the
             // grid barrier (issuing ~60-120 KB per CU takes the texture unit ~1 us)
