@@ -273,7 +273,16 @@ __device__ __forceinline__ float chunk_dot(const Tile& t, int cb, const uint8_t*
 __device__ __forceinline__ const uint8_t* tile_ptr(const PMat W, int g, int c) {
     return W.base + ((size_t)g * W.nc + c) * tile_bytes(W.cb);
 }
-__device__ __forceinline__ int seg_c0(const PMat W, int s) { return s * W.nc / W.ks; }
+// floor(k / d) for 0 <= k < 2^22, d >= 1, without the ~30-instruction integer divide:
+// the float estimate is at most one off, then corrected
+__device__ __forceinline__ int div_small(int k, int d) {
+    int q = (int)((float)k * __builtin_amdgcn_rcpf((float)d));
+    if (q * d > k) q--;
+    else if ((q + 1) * d <= k) q++;
+    return q;
+}
+// first chunk of K segment s: s * nc / ks (integer division, the oracle's boundaries)
+__device__ __forceinline__ int seg_c0(const PMat W, int s) { return W.ks == 1 ? s * W.nc : div_small(s * W.nc, W.ks); }
 
 // ------------------------------------------------------------------ workgroup work split
 constexpr int kWorkers = kPWaves - 1;      // waves 1..7
@@ -291,21 +300,21 @@ __device__ __forceinline__ bool wg_tile(const PMat W, int wg, int nwg, int k, Ti
     const int nseg = (W.rows >> 6) * W.ks;
     int t, c;
     if (W.ks == 1) {
-        const int round = k / W.nc;
+        const int round = div_small(k, W.nc);
         t = wg + round * nwg;
         c = k - round * W.nc;
         if (t >= nseg) return false;
+        r.p = tile_ptr(W, t, c);
     } else {
         t = wg;
         for (;;) {
             if (t >= nseg) return false;
-            const int s = t % W.ks, c0 = seg_c0(W, s), len = seg_c0(W, s + 1) - c0;
-            if (k < len) { c = c0 + k; break; }
+            const int g = div_small(t, W.ks), s = t - g * W.ks, c0 = seg_c0(W, s), len = seg_c0(W, s + 1) - c0;
+            if (k < len) { c = c0 + k; r.p = tile_ptr(W, g, c); break; }
             k -= len;
             t += nwg;
         }
     }
-    r.p = tile_ptr(W, t / W.ks, c);
     r.b0 = c * W.cb;
     return true;
 }
@@ -315,10 +324,14 @@ __device__ __forceinline__ bool wg_tile(const PMat W, int wg, int nwg, int k, Ti
 template <class F>
 __device__ __forceinline__ void wg_segments(const PMat W, int wg, int nwg, int kw, F f) {
     const int nseg = (W.rows >> 6) * W.ks;
+    if (W.ks == 1) {          // every segment is a whole row group of nc chunks
+        for (int t = wg + kw * nwg, r = kw; t < nseg; t += kWorkers * nwg, r += kWorkers) f(t, 0, r * W.nc, (r + 1) * W.nc);
+        return;
+    }
     int k0 = 0, r = 0;
     for (int t = wg; t < nseg; t += nwg, r++) {
-        const int s = t % W.ks, len = seg_c0(W, s + 1) - seg_c0(W, s);
-        if (r % kWorkers == kw) f(t / W.ks, s, k0, k0 + len);
+        const int g = div_small(t, W.ks), s = t - g * W.ks, len = seg_c0(W, s + 1) - seg_c0(W, s);
+        if (r % kWorkers == kw) f(g, s, k0, k0 + len);
         k0 += len;
     }
 }
@@ -1354,7 +1367,7 @@ __device__ __forceinline__ void tgemm(const PMat W, int wg, int nwg, const uint8
     const int nseg = (W.rows >> 6) * W.ks;
     const int col = lane & 15, kg = lane >> 4;
     for (int t = wg; t < nseg; t += nwg) {
-        const int g = t / W.ks, s = t % W.ks, c0 = seg_c0(W, s), c1 = seg_c0(W, s + 1);
+        const int g = div_small(t, W.ks), s = t - g * W.ks, c0 = seg_c0(W, s), c1 = seg_c0(W, s + 1);
         for (int c = c0 + wave; c < c1; c += kPWaves) {
             float acc[16];
             if (W.cb == 8) chunk_mfma<8>(tile_ptr(W, g, c), XT, nblk, c * 8, T, acc, lane);
@@ -1720,7 +1733,7 @@ __global__ __launch_bounds__(kThreads) void k_gemv(PMat W, const int8_t* xq, con
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int ntask = (W.rows / 64) * W.ks;
     for (int task = blockIdx.x * kWaves + wave; task < ntask; task += gridDim.x * kWaves) {
-        const int g = task / W.ks, s = task % W.ks, c0 = seg_c0(W, s), c1 = seg_c0(W, s + 1);
+        const int g = div_small(task, W.ks), s = task - g * W.ks, c0 = seg_c0(W, s), c1 = seg_c0(W, s + 1);
         float seg = 0.f;
         for (int c = c0; c < c1; c++) {
             Tile t;
@@ -1743,7 +1756,7 @@ __global__ void k_seg_sum(const float* part, int rows, int ks, float* y) {
 // isum[row][block] of the packed matrix, lane = row of a 64-row group
 __global__ __launch_bounds__(64) void k_isums(PMat W, const int8_t* xq, int32_t* isum) {
     const int g = blockIdx.x, b = blockIdx.y, lane = threadIdx.x;
-    const int c = b / W.cb, k = b % W.cb;
+    const int c = W.cb == 8 ? b >> 3 : b >> 2, k = b & (W.cb - 1);      // cb is 8 or 4
     const uint8_t* t = tile_ptr(W, g, c);
     const uint4 w = *reinterpret_cast<const uint4*>(t + k * 1024 + lane * 16);
     const int4* xp = reinterpret_cast<const int4*>(xq + 32 * b);
