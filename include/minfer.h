@@ -46,6 +46,10 @@ typedef struct mi_opts {
     int32_t persistent;    /* 1: one persistent cooperative kernel per step; 0: one launch per phase */
     int32_t stop_eos;      /* mi_generate stops after tokenizer.ggml.eos_token_id */
     int32_t device;        /* HIP device ordinal */
+    int32_t graphs;        /* 1: each multi-token step replays a HIP graph captured once per (T, logits)
+                              instead of ~300 kernel launches (same results; saves host launch work).
+                              Default 0: rocprofv3 --kernel-trace crashed in the HIP runtime while
+                              capturing on this ROCm image, and the GPU time differs by <1%. */
 } mi_opts;
 
 /* reference defaults: TCHUNK 8, SPEC 1 (mega) / 0 (cuda_infer), NGMAX 3, SPEC_SLOPE 0.074 */

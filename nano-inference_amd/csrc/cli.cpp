@@ -9,7 +9,8 @@
 // stderr: the stat lines the reference's tools parse ("... = X tok/s", and with SPEC=1
 // "N generation steps, X tokens/step | drafted D, accepted A (P%)").
 // Environment: RAWIDS, SPEC (n-gram speculative decode, output identical to greedy),
-// NG (longest n-gram drafted, default 3), PERSISTENT (0: one launch per phase), DEVICE.
+// NG (longest n-gram drafted, default 3), PERSISTENT (0: one launch per phase), GRAPHS (1:
+// multi-token steps replay a HIP graph instead of launching kernel by kernel), DEVICE.
 #include "minfer.h"
 
 #include <cstdio>
@@ -74,6 +75,7 @@ int main(int argc, char** argv) {
     o.ngmax = env_int("NG", o.ngmax);
     o.persistent = env_int("PERSISTENT", o.persistent);
     o.device = env_int("DEVICE", o.device);
+    o.graphs = env_int("GRAPHS", o.graphs);
     o.stop_eos = raw ? 0 : 1;
 
     mi_engine* e = nullptr;

@@ -33,6 +33,7 @@ constexpr int kAttnChunk = 64;     // positions per attention partial
 constexpr int kInlineComb = 4;     // up to this many chunks the O phase merges them itself
 constexpr int kAttnSplit = 16;     // past this many chunks the records merge as a two-level tree
 constexpr int kActRec = 128;       // bytes per act block record (32 int8, scale, 8*sum, padding)
+constexpr int kTRec = 40;          // block record stride of the multi-token steps: 32 codes, scale, 8*sum
 constexpr int kMaxE = 2048;        // largest hidden size the LDS staging holds
 constexpr int kMaxFF = 11264;      // largest FFN width the LDS staging holds
 constexpr int kMaxT = 8;           // tokens of one multi-token step (mega.cu:50 TMAX)
@@ -81,12 +82,13 @@ struct DModel {
     float* out_margin;             // [maxseq]
     // multi-token steps (T <= kMaxT tokens at positions pos..pos+T-1, one launch per
     // phase): per-token copies of the exchange buffers, token index after the segment
+    int32_t* posT;                 // [1] position of the step's first token (set before each launch sequence)
     float* hT;                     // [2*NL+1][kMaxT][E]
     float* qkvT;                   // [NL][ks_qkv][kMaxT][QKV]
     float* attT;                   // [NL][kMaxT][NH][maxch][arec]
-    float* att_outT;               // [NL][kMaxT][E]
     float* oT;                     // [NL][ks_o][kMaxT][E]
     uint8_t* actT;                 // [NL][kMaxT][FF/32][kActRec]
+    uint8_t* xT;                   // [kMaxT][E/32][kTRec] int8 records of the current GEMM input
     float* dT;                     // [NL][ks_d][kMaxT][E]
     float* candT;                  // [workgroups][kMaxT][4]
     float* logitsT;                // [kMaxT][V] (written when non-null)

@@ -47,11 +47,17 @@ struct mi_engine {
     hipStream_t stream = nullptr;
     hipEvent_t ev0 = nullptr, ev1 = nullptr;
     int nwg_persistent = 0;       // workgroups of the persistent step kernel (0: per-phase launches)
+    int32_t* h_iota = nullptr;    // pinned host memory, h_iota[p] = p: the source of posT
+    hipGraphExec_t gexec[2][kMaxT + 1] = {};   // multi-token step per (logits, T), captured on first use
     int cur_len = 0;              // positions holding valid K/V
     bool next_ready = false;      // tokbuf[cur_len] holds the prediction of the last step
     mi_stats stats{};
     ~mi_engine() {
         if (stream) (void)hipStreamSynchronize(stream);
+        for (auto& row : gexec)
+            for (hipGraphExec_t g : row)
+                if (g) (void)hipGraphExecDestroy(g);
+        if (h_iota) (void)hipHostFree(h_iota);
         for (void* p : allocs) (void)hipFree(p);
         if (ev0) (void)hipEventDestroy(ev0);
         if (ev1) (void)hipEventDestroy(ev1);
@@ -198,6 +204,7 @@ void mi_default_opts(mi_opts* o) {
     o->persistent = 1;
     o->stop_eos = 0;
     o->device = 0;
+    o->graphs = 0;
 }
 
 size_t mi_q4_packed_bytes(int32_t rows, int32_t nb, int32_t cb) {
@@ -447,10 +454,10 @@ static int load_impl(mi_engine* e, const char* path) {
         return rc;
     // multi-token step buffers (mi_step with T > 1)
     const size_t TM = kMaxT;
-    if ((rc = alloc_buf(e, &M.hT, (size_t)(2 * e->NL + 1) * TM * e->E)) ||
+    if ((rc = alloc_buf(e, &M.posT, 1)) || (rc = alloc_buf(e, &M.hT, (size_t)(2 * e->NL + 1) * TM * e->E)) ||
         (rc = alloc_buf(e, &M.qkvT, NL * e->ks[0] * TM * e->QKV)) ||
         (rc = alloc_buf(e, &M.attT, NL * TM * e->NH * e->maxch * M.arec)) ||
-        (rc = alloc_buf(e, &M.att_outT, NL * TM * e->E)) ||
+        (rc = alloc_buf(e, &M.xT, TM * (e->E / 32) * kTRec)) ||
         (rc = alloc_buf(e, &M.oT, NL * e->ks[1] * TM * e->E)) ||
         (rc = alloc_buf(e, &M.actT, NL * TM * (e->FF / 32) * kActRec)) ||
         (rc = alloc_buf(e, &M.dT, NL * e->ks[3] * TM * e->E)) ||
@@ -466,6 +473,8 @@ static int load_impl(mi_engine* e, const char* path) {
     HIPCHK(e, hipMemcpy(e->dM, &e->M, sizeof(DModel), hipMemcpyHostToDevice));
     HIPCHK(e, hipMemcpy(e->dM + 1, &e->M_logits, sizeof(DModel), hipMemcpyHostToDevice));
     HIPCHK(e, hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking));
+    HIPCHK(e, hipHostMalloc((void**)&e->h_iota, sizeof(int32_t) * ((size_t)e->maxseq + 1), hipHostMallocDefault));
+    for (int p = 0; p <= e->maxseq; p++) e->h_iota[p] = p;
     HIPCHK(e, hipEventCreate(&e->ev0));
     HIPCHK(e, hipEventCreate(&e->ev1));
     HIPCHK(e, hipDeviceSynchronize());
@@ -505,6 +514,36 @@ int mi_info(const mi_engine* e, mi_model_info* o) {
 }
 
 }  // extern "C"
+
+// One multi-token step (T > 1) at positions pos..pos+T-1. The kernels read the
+// position from posT, so the launch sequence of each (logits, T) is captured once into
+// a HIP graph and replayed at any position: ~300 launches cost one graph launch.
+static int run_multi(mi_engine* e, int pos, int T, bool want_logits) {
+    const DModel& M = want_logits ? e->M_logits : e->M;
+    const DModel* dM = e->dM + (want_logits ? 1 : 0);
+    HIPCHK(e, hipMemcpyAsync(e->M.posT, e->h_iota + pos, sizeof(int32_t), hipMemcpyHostToDevice, e->stream));
+    if (!e->opts.graphs) {
+        launch_step_multi(M, dM, e->n_cu, T, e->stream);
+        HIPCHK(e, hipGetLastError());
+        return MI_OK;
+    }
+    hipGraphExec_t& g = e->gexec[want_logits ? 1 : 0][T];
+    if (!g) {
+        hipGraph_t graph = nullptr;
+        HIPCHK(e, hipStreamBeginCapture(e->stream, hipStreamCaptureModeThreadLocal));
+        launch_step_multi(M, dM, e->n_cu, T, e->stream);
+        const hipError_t launched = hipGetLastError();
+        const hipError_t ended = hipStreamEndCapture(e->stream, &graph);
+        HIPCHK(e, launched);
+        HIPCHK(e, ended);
+        const hipError_t inst = hipGraphInstantiate(&g, graph, nullptr, nullptr, 0);
+        (void)hipGraphDestroy(graph);
+        if (inst != hipSuccess) g = nullptr;
+        HIPCHK(e, inst);
+    }
+    HIPCHK(e, hipGraphLaunch(g, e->stream));
+    return MI_OK;
+}
 
 static int run_step(mi_engine* e, int pos, int gen, bool want_logits) {
     const DModel& M = want_logits ? e->M_logits : e->M;
@@ -551,10 +590,7 @@ int mi_step(mi_engine* e, const int32_t* toks, int32_t T, int32_t pos, int32_t* 
     if (T == 1) {
         rc = run_step(e, pos, 1, logits != nullptr);
     } else {
-        const DModel& M = logits ? e->M_logits : e->M;
-        launch_step_multi(M, e->dM + (logits ? 1 : 0), e->n_cu, pos, T, e->stream);
-        rc = MI_OK;
-        HIPCHK(e, hipGetLastError());
+        rc = run_multi(e, pos, T, logits != nullptr);
     }
     if (rc) return rc;
     std::vector<int32_t> tok(T);
@@ -594,8 +630,7 @@ int mi_prefill(mi_engine* e, const int32_t* ids, int32_t n, int32_t* first, floa
             if (int rc = run_step(e, p, p == n - 1, false)) return rc;
             ran_single = true;
         } else {
-            launch_step_multi(e->M, e->dM, e->n_cu, p, T, e->stream);
-            HIPCHK(e, hipGetLastError());
+            if (int rc = run_multi(e, p, T, false)) return rc;
             if (p + T == n)   // the next position's token is the last prediction
                 HIPCHK(e, hipMemcpyAsync(e->M.tokbuf + n, e->M.out_tok + n - 1, 4, hipMemcpyDeviceToDevice, e->stream));
         }
@@ -626,8 +661,7 @@ static int run_tokens(mi_engine* e, int pos, int T, int32_t* tok, float* mg) {
     if (T == 1) {
         if (int rc = run_step(e, pos, 1, false)) return rc;
     } else {
-        launch_step_multi(e->M, e->dM, e->n_cu, pos, T, e->stream);
-        HIPCHK(e, hipGetLastError());
+        if (int rc = run_multi(e, pos, T, false)) return rc;
     }
     HIPCHK(e, hipMemcpyAsync(tok, e->M.out_tok + pos, 4 * T, hipMemcpyDeviceToHost, e->stream));
     HIPCHK(e, hipMemcpyAsync(mg, e->M.out_margin + pos, 4 * T, hipMemcpyDeviceToHost, e->stream));

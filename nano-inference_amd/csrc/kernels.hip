@@ -1279,108 +1279,191 @@ __global__ __launch_bounds__(64) void k_argmax(const DModel* Mp, int ncand, int 
 // ================================================================== multi-token steps
 // T <= kMaxT tokens at positions pos..pos+T-1 in one pass over the weights: the
 // verify step of speculative decoding (forward_batch, cuda_infer.cu:990-1026; mega.cu
-// gemv_part T>1 :259-265, tile_dot :197-244). One launch per phase, one 512-thread
-// workgroup per CU, all eight waves work. Every value equals the single-token
-// step's bit for bit: the per-block integer dot of q4 nibbles and int8 activations
-// comes from int8 MFMA (exact), and the float work keeps the same plan (block fma
-// chain per chunk, chunk sums left to right, segment sums left to right), the same
-// prologue arithmetic and the same attention items.
-constexpr int kTRec = 40;          // block record stride in the multi-token kernels: 32 codes, scale, 8*sum
-constexpr int kTChunks = 16;       // chunks of one segment staged in LDS
+// gemv_part T>1 :259-265, tile_dot :197-244). One launch per phase. Every value
+// equals the single-token step's bit for bit: the per-block integer dot of q4 nibbles
+// and int8 activations comes from int8 MFMA (exact), and the float work keeps the same
+// plan (block fma chain per chunk, chunk sums left to right, segment sums left to
+// right), the same norm/quant arithmetic and the same attention items.
+// The GEMM phases read their input as int8 block records from xT, written once per
+// token by kT_in (residual + RMSNorm + quant, one workgroup per token) or kT_comb
+// (chunk merge + quant), so no workgroup repeats the per-token prologue.
+constexpr int kTChunks = 16;       // chunk sums of one segment held in LDS
 constexpr int kTAttnWaves = 4;     // attention waves per workgroup (LDS bound)
-constexpr int kTxsBytes = kMaxT * kMaxE * 4;
 constexpr int kTXeBytes = kMaxT * (kMaxE / 32) * kTRec;
 constexpr int kTXfBytes = kMaxT * (kMaxFF / 32) * kTRec;
 constexpr int kTPBytes = kTChunks * kMaxT * 64 * 4;
-constexpr int kTNormLds = kTxsBytes + kTXeBytes + kTPBytes;   // qkv, o, gate/up, lm_head
-constexpr int kTDownLds = kTXfBytes + kTPBytes;               // down
+constexpr int kTGemvLds = kTXeBytes + kTPBytes;    // qkv, o, gate/up, lm_head
+constexpr int kTDownLds = kTXfBytes + kTPBytes;    // down
 
 typedef int v4i __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ size_t hT_at(MPtr M, int slot, int t) { return ((size_t)slot * kMaxT + t) * M->E; }
 __device__ __forceinline__ float4 ldg4(const float* p) { return *reinterpret_cast<const float4*>(p); }
+__device__ __forceinline__ uint2 ntload8(const uint8_t* p) {
+    const u32x2 v = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(p));
+    return make_uint2(v.x, v.y);
+}
 
-// chunk sums of one tile (64 rows x CB blocks) for T tokens. MFMA 16x16x32 i8 per
-// block and 16-row subgroup q: lane l feeds A[row q*16 + l%16][k = 8*(l/16) ..+7]
-// (the q4 nibbles of block elements 8*(l/16)..: low nibbles of bytes 0-7 / 8-15,
-// then high nibbles) and B[k][token l%16]; D[4*(l/16) + i][l%16] lands in d[i]. The
-// float epilogue per (row, token) is the single-token chain in block order.
-// acc[q*4 + i]: row q*16 + 4*(l/16) + i, token l%16.
+// One chunk (64 rows x CB blocks) as one lane holds it for v_mfma_i32_16x16x64_i8.
+// One MFMA covers row group q (rows 16q..16q+15) and block pair p (blocks 2p, 2p+1):
+// the 16 x 64 "A" side is 8 token slots per block (slot m < 8: token m, block 2p, its
+// codes in the K lanes of groups kg = 0, 1 and zeros in kg = 2, 3; slot m >= 8: token
+// m-8, block 2p+1, codes in kg = 2, 3), the "B" side is the rows' nibbles (block 2p in
+// kg = 0, 1, block 2p+1 in kg = 2, 3). So D[m][row] is the integer dot of one token
+// and one block, and all 16 x 16 outputs are used at T = 8. Within a block, lane group
+// h = kg%2 carries elements 8h..8h+7 (low nibbles of bytes 8h..8h+7) and 16+8h..+7
+// (their high nibbles); any pairing of K indices gives the same exact dot as long as
+// both sides use it.
+// w[q][p]: 8 nibble bytes of row 16q + l%16, block 2p + kg/2, bytes 8h..8h+7.
+// s[j][.]: the fp16 scale line (CB halves) of row 16(2*(kg/2) + j) + l%16.
 template <int CB>
-__device__ __forceinline__ void chunk_mfma(const uint8_t* tile, const uint8_t* XT, int nblk, int b0, int T, float (&acc)[16],
-                                           int lane) {
+struct TTile {
+    uint2 w[4][CB / 2];
+    uint32_t s[2][CB / 2];
+};
+
+template <int CB>
+__device__ __forceinline__ void ttile_load(TTile<CB>& t, const uint8_t* tile, int lane) {
     const int col = lane & 15, kg = lane >> 4;
-    const bool tok = col < T;
-    const uint8_t* xt = XT + (size_t)(tok ? col : 0) * nblk * kTRec;
-    long bv[CB];
-    float dx[CB];
-    int xs[CB];
 #pragma unroll
-    for (int k = 0; k < CB; k++) {
-        const uint8_t* xb = xt + (b0 + k) * kTRec;
-        bv[k] = tok ? *reinterpret_cast<const long*>(xb + 8 * kg) : 0;
-        dx[k] = tok ? *reinterpret_cast<const float*>(xb + 32) : 0.f;
-        xs[k] = tok ? *reinterpret_cast<const int*>(xb + 36) : 0;
-    }
-    const uint32_t sh = (kg >> 1) * 4;
+    for (int q = 0; q < 4; q++)
 #pragma unroll
-    for (int q = 0; q < 4; q++) {
-        uint2 wa[CB];
+        for (int p = 0; p < CB / 2; p++)
+            t.w[q][p] = ntload8(tile + (2 * p + (kg >> 1)) * 1024 + (q * 16 + col) * 16 + 8 * (kg & 1));
 #pragma unroll
-        for (int k = 0; k < CB; k++)
-            wa[k] = *reinterpret_cast<const uint2*>(tile + k * 1024 + (q * 16 + col) * 16 + 8 * (kg & 1));
-        uint32_t sc[4][CB / 2];
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const uint8_t* sp = tile + CB * 1024 + (q * 16 + 4 * kg + i) * CB * 2;
-            if constexpr (CB == 8) {
-                const uint4 v = *reinterpret_cast<const uint4*>(sp);
-                sc[i][0] = v.x; sc[i][1] = v.y; sc[i][2] = v.z; sc[i][3] = v.w;
-            } else {
-                const uint2 v = *reinterpret_cast<const uint2*>(sp);
-                sc[i][0] = v.x; sc[i][1] = v.y;
-            }
+    for (int j = 0; j < 2; j++) {
+        const uint8_t* sp = tile + CB * 1024 + ((2 * (kg >> 1) + j) * 16 + col) * CB * 2;
+        if constexpr (CB == 8) {
+            const uint4 v = ntload16(sp);
+            t.s[j][0] = v.x; t.s[j][1] = v.y; t.s[j][2] = v.z; t.s[j][3] = v.w;
+        } else {
+            const uint2 v = ntload8(sp);
+            t.s[j][0] = v.x; t.s[j][1] = v.y;
         }
-        float a[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int k = 0; k < CB; k++) {
-            const uint32_t lo = (wa[k].x >> sh) & 0x0F0F0F0Fu, hi = (wa[k].y >> sh) & 0x0F0F0F0Fu;
-            const long av = (long)((unsigned long)lo | ((unsigned long)hi << 32));
-            const v4i d = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, bv[k], v4i{0, 0, 0, 0}, 0, 0, 0);
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const uint32_t sw = sc[i][k >> 1];
-                const float dw = (k & 1) ? h2f_hi(sw) : h2f_lo(sw);
-                a[i] = __fmaf_rn(__fmul_rn(dw, dx[k]), __int2float_rn(d[i] - xs[k]), a[i]);
-            }
-        }
-#pragma unroll
-        for (int i = 0; i < 4; i++) acc[q * 4 + i] = a[i];
     }
 }
 
-// T-token GEMM over this workgroup's segments of W, one segment at a time: its
-// chunks spread over the eight waves (chunk sums -> P[chunk][token][row]), then wave
-// t adds token t's chunk sums left to right and hands out(g, s, t, value) the row
-// g*64 + lane.
-template <class F>
-__device__ __forceinline__ void tgemm(const PMat W, int wg, int nwg, const uint8_t* XT, int nblk, int T, float* P, int wave,
-                                      int lane, F out) {
-    const int nseg = (W.rows >> 6) * W.ks;
-    const int col = lane & 15, kg = lane >> 4;
-    for (int t = wg; t < nseg; t += nwg) {
-        const int g = div_small(t, W.ks), s = t - g * W.ks, c0 = seg_c0(W, s), c1 = seg_c0(W, s + 1);
-        for (int c = c0 + wave; c < c1; c += kPWaves) {
-            float acc[16];
-            if (W.cb == 8) chunk_mfma<8>(tile_ptr(W, g, c), XT, nblk, c * 8, T, acc, lane);
-            else chunk_mfma<4>(tile_ptr(W, g, c), XT, nblk, c * 4, T, acc, lane);
-            if (col < T) {
-                float* pc = P + ((size_t)(c - c0) * kMaxT + col) * 64;
+// chunk sums of one tile for the T tokens whose block records (kTRec bytes: 32 codes,
+// fp32 scale, 8*sum) are in LDS at XT[token][block]. acc[j][i]: row 16(2*(kg/2) + j) +
+// l%16, token 4*(kg%2) + i. Per (row, token) the float work is the single-token
+// chain: acc = fma(dw*dx, float(dot - 8*sum), acc) over the CB blocks in order, from 0.
+// The MFMA leaves block 2p's dot in lanes kg < 2 and block 2p+1's in kg >= 2 for each
+// row group; v_permlane32_swap of groups (q, q+2) hands each lane both blocks of
+// one row group (q = 2*(kg/2) + j), so every lane runs two chains per token.
+template <int CB>
+__device__ __forceinline__ void ttile_sums(const TTile<CB>& W, const uint8_t* XT, int nblk, int b0, int T,
+                                           float (&acc)[2][4], int lane) {
+    const int col = lane & 15, kg = lane >> 4, h = kg & 1, atok = col & 7;
+    const bool aon = ((col < 8) == (kg < 2)) && atok < T;
+    const uint8_t* xa = XT + ((size_t)atok * nblk + b0 + (col >> 3)) * kTRec + 8 * h;
 #pragma unroll
-                for (int q = 0; q < 4; q++)
+    for (int j = 0; j < 2; j++)
 #pragma unroll
-                    for (int i = 0; i < 4; i++) pc[q * 16 + 4 * kg + i] = acc[q * 4 + i];
+        for (int i = 0; i < 4; i++) acc[j][i] = 0.f;
+#pragma unroll
+    for (int p = 0; p < CB / 2; p++) {
+        v4i a = v4i{0, 0, 0, 0};
+        if (aon) {
+            const uint2 lo = *reinterpret_cast<const uint2*>(xa + 2 * p * kTRec);
+            const uint2 hi = *reinterpret_cast<const uint2*>(xa + 2 * p * kTRec + 16);
+            a = v4i{(int)lo.x, (int)lo.y, (int)hi.x, (int)hi.y};
+        }
+        int d[4][4];
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const uint2 w = W.w[q][p];
+            const v4i b = v4i{(int)(w.x & 0x0F0F0F0Fu), (int)(w.y & 0x0F0F0F0Fu), (int)((w.x >> 4) & 0x0F0F0F0Fu),
+                              (int)((w.y >> 4) & 0x0F0F0F0Fu)};
+            const v4i r = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, v4i{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 4; i++) d[q][i] = r[i];
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int tok = 4 * h + i;
+            float dx0 = 0.f, dx1 = 0.f;
+            int xs0 = 0, xs1 = 0;
+            if (tok < T) {
+                const uint8_t* xr = XT + ((size_t)tok * nblk + b0 + 2 * p) * kTRec;
+                const float2 e0 = *reinterpret_cast<const float2*>(xr + 32);
+                const float2 e1 = *reinterpret_cast<const float2*>(xr + kTRec + 32);
+                dx0 = e0.x; xs0 = __float_as_int(e0.y);
+                dx1 = e1.x; xs1 = __float_as_int(e1.y);
             }
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                const auto r = __builtin_amdgcn_permlane32_swap((unsigned)d[j][i], (unsigned)d[j + 2][i], false, false);
+                const uint32_t sw = W.s[j][p];
+                acc[j][i] = __fmaf_rn(__fmul_rn(h2f_lo(sw), dx0), __int2float_rn((int)r[0] - xs0), acc[j][i]);
+                acc[j][i] = __fmaf_rn(__fmul_rn(h2f_hi(sw), dx1), __int2float_rn((int)r[1] - xs1), acc[j][i]);
+            }
+        }
+    }
+}
+
+// segment (row group g, K segment s) of work item t
+__device__ __forceinline__ void tseg(const PMat W, int t, int& g, int& s, int& c0, int& c1) {
+    g = W.ks == 1 ? t : div_small(t, W.ks);
+    s = t - g * W.ks;
+    c0 = seg_c0(W, s);
+    c1 = seg_c0(W, s + 1);
+}
+// this wave's next chunk: k (index inside segment t) + kPWaves, else chunk `wave` of the
+// workgroup's next segment (t + nwg, ...) that has one. Start with t = wg, k = wave - kPWaves.
+__device__ __forceinline__ bool tnext(const PMat W, int nseg, int nwg, int wave, int& t, int& k) {
+    k += kPWaves;
+    for (; t < nseg; t += nwg, k = wave) {
+        int g, s, c0, c1;
+        tseg(W, t, g, s, c0, c1);
+        if (k < c1 - c0) return true;
+    }
+    return false;
+}
+
+// T-token GEMM over this workgroup's segments (t = wg, wg + nwg, ...). Each wave takes
+// chunks wave, wave + 8, ... of every segment and holds the next chunk's loads in
+// flight while it computes one (the first is issued before `stage` fills XT). Chunk
+// sums go to P[chunk][token][row]; after a segment, wave t adds token t's chunk sums
+// left to right and hands out(g, s, t, value) the row g*64 + lane.
+template <int CB, class S, class F>
+__device__ __forceinline__ void tgemm_cb(const PMat W, int wg, int nwg, const uint8_t* XT, int nblk, int T, float* P,
+                                         int wave, int lane, S stage, F out) {
+    const int nseg = (W.rows >> 6) * W.ks;
+    int t = wg, k = wave - kPWaves;
+    bool have = tnext(W, nseg, nwg, wave, t, k);
+    TTile<CB> cur, nx;
+    if (have) {
+        int g, s, c0, c1;
+        tseg(W, t, g, s, c0, c1);
+        ttile_load<CB>(cur, tile_ptr(W, g, c0 + k), lane);
+    }
+    stage();
+    __syncthreads();
+    int nt = t, nk = k;
+    bool hn = have && tnext(W, nseg, nwg, wave, nt, nk);
+    for (int ts = wg; ts < nseg; ts += nwg) {
+        int g, s, c0, c1;
+        tseg(W, ts, g, s, c0, c1);
+        while (have && t == ts) {
+            if (hn) {
+                int g2, s2, a0, a1;
+                tseg(W, nt, g2, s2, a0, a1);
+                ttile_load<CB>(nx, tile_ptr(W, g2, a0 + nk), lane);
+            }
+            float acc[2][4];
+            ttile_sums<CB>(cur, XT, nblk, (c0 + k) * CB, T, acc, lane);
+            const int col = lane & 15, kg = lane >> 4;
+            float* pc = P + (size_t)k * kMaxT * 64;
+#pragma unroll
+            for (int j = 0; j < 2; j++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) pc[(4 * (kg & 1) + i) * 64 + (2 * (kg >> 1) + j) * 16 + col] = acc[j][i];
+            cur = nx;
+            t = nt;
+            k = nk;
+            have = hn;
+            if (hn) hn = tnext(W, nseg, nwg, wave, nt, nk);
         }
         __syncthreads();
         if (wave < T) {
@@ -1391,50 +1474,59 @@ __device__ __forceinline__ void tgemm(const PMat W, int wg, int nwg, const uint8
         __syncthreads();
     }
 }
+template <class S, class F>
+__device__ __forceinline__ void tgemm(const PMat W, int wg, int nwg, const uint8_t* XT, int nblk, int T, float* P, int wave,
+                                      int lane, S stage, F out) {
+    if (W.cb == 8) tgemm_cb<8>(W, wg, nwg, XT, nblk, T, P, wave, lane, stage, out);
+    else tgemm_cb<4>(W, wg, nwg, XT, nblk, T, P, wave, lane, stage, out);
+}
 
-// prologue of a norm phase, wave t = token t: x = h + split-K partials (layer 0 of
-// qkv: the token's embedding row) -> hT (workgroup 0) -> RMSNorm -> int8 records
-__device__ __forceinline__ void tnorm_prologue(MPtr M, int l, int kind, int pos, int T, int wg, float* xs, uint8_t* XT,
-                                               int wave, int lane) {
-    if (wave >= T) return;
-    const int t = wave, n = M->E, nblk = n / 32;
-    const bool qkv = kind == PH_QKV, lm = kind == PH_LM;
-    float* x = xs + (size_t)t * kMaxE;
-    if (qkv && l == 0) {
-        const float* er = M->emb + (size_t)M->tokbuf[pos + t] * n;
-#pragma unroll 2
-        for (int e0 = 4 * lane; e0 < n; e0 += 256) st4(x, e0, ldg4(er + e0));
-    } else {
-        const int pl = qkv ? l - 1 : lm ? M->NL - 1 : l;
-        const bool dsrc = kind != PH_GU;
-        const int ks = dsrc ? LY(M, pl)->d.ks : LY(M, pl)->o.ks;
-        const float* part = dsrc ? M->dT + (size_t)pl * LY(M, 0)->d.ks * kMaxT * n : M->oT + (size_t)pl * LY(M, 0)->o.ks * kMaxT * n;
-        const float* h = M->hT + hT_at(M, dsrc ? 2 * pl + 1 : 2 * l, t);
-#pragma unroll 2
-        for (int e0 = 4 * lane; e0 < n; e0 += 256) {
+// T tokens' records of the E-wide phase input: xT -> LDS (all threads)
+__device__ __forceinline__ void tstage_x(MPtr M, int T, uint8_t* XT) {
+    const int n8 = T * (M->E / 32) * (kTRec / 8);
+    const uint2* src = reinterpret_cast<const uint2*>(M->xT);
+    uint2* dst = reinterpret_cast<uint2*>(XT);
+    for (int i = threadIdx.x; i < n8; i += blockDim.x) dst[i] = src[i];
+}
+
+// phase input of token blockIdx.x for the qkv (kind PH_QKV), gate/up (PH_GU) and
+// lm_head (PH_LM) GEMMs: x = h + split-K partials in order (layer 0 of qkv: the
+// token's embedding row) -> hT -> RMSNorm -> int8 records in xT. The same arithmetic
+// as the single-token step's norm prologue (cuda_infer.cu:43-60 rmsnorm, 80-89 quant).
+__global__ __launch_bounds__(kPThreads) void kT_in(const DModel* Mp, int l, int kind) {
+    const MPtr M = (MPtr)Mp;
+    const int pos = *M->posT;
+    __shared__ __align__(16) float x[kMaxE];
+    const int t = blockIdx.x, wave = threadIdx.x >> 6, lane = threadIdx.x & 63, n = M->E, nblk = n / 32;
+    const bool qkv = kind == PH_QKV, lm = kind == PH_LM, dsrc = kind != PH_GU;
+    const int pl = qkv ? l - 1 : lm ? M->NL - 1 : l;
+    float* hdst = M->hT + hT_at(M, qkv ? 2 * l : 2 * l + 1, t);
+    for (int e0 = 256 * wave + 4 * lane; e0 < n; e0 += 256 * kPWaves) {
+        float4 v;
+        if (qkv && l == 0) {
+            v = ldg4(M->emb + (size_t)M->tokbuf[pos + t] * n + e0);
+        } else {
+            const int ks = dsrc ? LY(M, pl)->d.ks : LY(M, pl)->o.ks;
+            const float* part = dsrc ? M->dT + (size_t)pl * LY(M, 0)->d.ks * kMaxT * n : M->oT + (size_t)pl * LY(M, 0)->o.ks * kMaxT * n;
+            const float* h = M->hT + hT_at(M, dsrc ? 2 * pl + 1 : 2 * l, t);
             float4 p[kMaxKsRes];
 #pragma unroll
             for (int s = 0; s < kMaxKsRes; s++)
                 if (s < ks) p[s] = ldg4(part + ((size_t)s * kMaxT + t) * n + e0);
-            float4 v = p[0];
+            float4 sum = p[0];
 #pragma unroll
             for (int s = 1; s < kMaxKsRes; s++)
-                if (s < ks) v = f4add(v, p[s]);
-            st4(x, e0, f4add(ldg4(h + e0), v));
+                if (s < ks) sum = f4add(sum, p[s]);
+            v = f4add(ldg4(h + e0), sum);
         }
+        st4(x, e0, v);
+        if (!lm) *reinterpret_cast<float4*>(hdst + e0) = v;
     }
-    wave_lds_sync();
-    if (wg == 0 && !lm) {
-        float* dst = M->hT + hT_at(M, qkv ? 2 * l : 2 * l + 1, t);
-        for (int e0 = 4 * lane; e0 < n; e0 += 256) {
-            const float4 v = ld4(x + e0);
-            stc(dst + e0, v.x); stc(dst + e0 + 1, v.y); stc(dst + e0 + 2, v.z); stc(dst + e0 + 3, v.w);
-        }
-    }
+    __syncthreads();
     const float* w = lm ? M->out_norm : qkv ? LY(M, l)->an : LY(M, l)->fn;
     const float sc = rms_scale(x, n, M->eps, lane);
-    uint8_t* xr = XT + (size_t)t * nblk * kTRec;
-    for (int j = 0; 256 * j < n; j++) {
+    uint8_t* xr = M->xT + (size_t)t * nblk * kTRec;
+    for (int j = wave; 256 * j < n; j += kPWaves) {
         const int e0 = 256 * j + 4 * lane;
         const bool own = e0 < n;
         float4 y = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -1462,16 +1554,13 @@ __device__ __forceinline__ uint8_t* actT_at(MPtr M, int l, int t) {
     __shared__ __align__(16) uint8_t smem[BYTES];                                                \
     const int wg = blockIdx.x, nwg = gridDim.x, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
 
-__global__ __launch_bounds__(kPThreads) void kT_qkv(const DModel* Mp, int l, int pos, int T) {
-    TPRELUDE(kTNormLds)
-    float* xs = reinterpret_cast<float*>(smem);
-    uint8_t* XT = smem + kTxsBytes;
-    float* P = reinterpret_cast<float*>(smem + kTxsBytes + kTXeBytes);
-    tnorm_prologue(M, l, PH_QKV, pos, T, wg, xs, XT, wave, lane);
-    __syncthreads();
+__global__ __launch_bounds__(kPThreads) void kT_qkv(const DModel* Mp, int l, int T) {
+    TPRELUDE(kTGemvLds)
+    uint8_t* XT = smem;
+    float* P = reinterpret_cast<float*>(smem + kTXeBytes);
     const PMat W = ldmat(&LY(M, l)->qkv);
     float* part = qkvT_at(M, l);
-    tgemm(W, wg, nwg, XT, M->E / 32, T, P, wave, lane, [&](int g, int s, int t, float v) {
+    tgemm(W, wg, nwg, XT, M->E / 32, T, P, wave, lane, [&] { tstage_x(M, T, XT); }, [&](int g, int s, int t, float v) {
         part[((size_t)s * kMaxT + t) * W.rows + g * 64 + lane] = v;
     });
 }
@@ -1543,8 +1632,9 @@ __device__ __forceinline__ void tattn_item(MPtr M, int l, int pos, int T, int t,
 }
 
 template <int HD>
-__global__ __launch_bounds__(kPThreads) void kT_attn(const DModel* Mp, int l, int pos, int T) {
+__global__ __launch_bounds__(kPThreads) void kT_attn(const DModel* Mp, int l, int T) {
     TPRELUDE(kTAttnWaves * attn_wave_lds<HD>())
+    const int pos = *M->posT;
     (void)wg;
     if (wave >= kTAttnWaves) return;
     // items of token t: NH heads x chunks of positions 0..pos+t; enumerated token-major
@@ -1563,68 +1653,96 @@ __global__ __launch_bounds__(kPThreads) void kT_attn(const DModel* Mp, int l, in
     }
 }
 
-// chunk merge per (token, head, dim) into att_outT (used when the last token's
-// context has more than kInlineComb chunks; same arithmetic as the inline merge)
-__global__ __launch_bounds__(kPThreads) void kT_comb(const DModel* Mp, int l, int pos, int T) {
+
+// chunk merge of token t's records for query head h (one wave per (t, h); lane = dims
+// lane + 64j) into the O phase's int8 records in xT. The merge is combine_tree's
+// arithmetic (cuda_infer.cu:688-702 attn_combine), with each split's 16 chunk maxima,
+// weights and sums taken lane-parallel and the fma chains run in chunk order.
+template <int HD>
+__global__ __launch_bounds__(256) void kT_comb(const DModel* Mp, int l, int T) {
     const MPtr M = (MPtr)Mp;
-    const int n = M->E;
-    for (int it = blockIdx.x * blockDim.x + threadIdx.x; it < T * n; it += gridDim.x * blockDim.x) {
-        const int t = it / n, e = it - t * n, nch = (pos + t + kAttnChunk) / kAttnChunk;
-        M->att_outT[((size_t)l * kMaxT + t) * n + e] =
-            combine_tree(attT_at(M, l, t) + (size_t)(e / M->HD) * M->maxch * M->arec, M->arec, M->HD, e % M->HD, nch);
+    const int pos = *M->posT;
+    constexpr int DPL = HD / 64;
+    const int lane = threadIdx.x & 63, item = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (item >= T * M->NH) return;
+    const int t = item / M->NH, hh = item - t * M->NH, nch = (pos + t + kAttnChunk) / kAttnChunk, arec = M->arec;
+    const float* r = attT_at(M, l, t) + (size_t)hh * M->maxch * arec;
+    float Mx = -__builtin_inff();
+    if (nch > kAttnSplit) {
+        for (int c = lane; c < nch; c += 64) Mx = fmaxf(Mx, r[c * arec + HD]);
+        Mx = wave_max(Mx);
+    }
+    float den = 0.f, acc[DPL];
+#pragma unroll
+    for (int e = 0; e < DPL; e++) acc[e] = 0.f;
+    for (int c0 = 0; c0 < nch; c0 += kAttnSplit) {
+        const int len = min(kAttnSplit, nch - c0);
+        const float* rs = r + (size_t)c0 * arec;
+        const float mv = lane < len ? rs[lane * arec + HD] : -__builtin_inff();
+        const float lv = lane < len ? rs[lane * arec + HD + 1] : 0.f;
+        float ov[kAttnSplit][DPL];
+#pragma unroll
+        for (int i = 0; i < kAttnSplit; i++)
+#pragma unroll
+            for (int e = 0; e < DPL; e++) ov[i][e] = i < len ? rs[i * arec + 64 * e + lane] : 0.f;
+        const float Ms = wave_max(mv);
+        const float wv = lane < len ? mi_expf(__fsub_rn(mv, Ms)) : 0.f;
+        float ds = 0.f, as[DPL];
+#pragma unroll
+        for (int e = 0; e < DPL; e++) as[e] = 0.f;
+#pragma unroll
+        for (int i = 0; i < kAttnSplit; i++)
+            if (i < len) {
+                const float wi = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wv), i));
+                const float li = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(lv), i));
+                ds = __fmaf_rn(li, wi, ds);
+#pragma unroll
+                for (int e = 0; e < DPL; e++) as[e] = __fmaf_rn(ov[i][e], wi, as[e]);
+            }
+        if (nch <= kAttnSplit) {
+            den = ds;
+#pragma unroll
+            for (int e = 0; e < DPL; e++) acc[e] = as[e];
+        } else {
+            const float ws = mi_expf(__fsub_rn(Ms, Mx));
+            den = __fmaf_rn(ds, ws, den);
+#pragma unroll
+            for (int e = 0; e < DPL; e++) acc[e] = __fmaf_rn(as[e], ws, acc[e]);
+        }
+    }
+    const int nblk = M->E / 32;
+#pragma unroll
+    for (int e = 0; e < DPL; e++) {
+        int q, s8;
+        float d;
+        quant32_vals(__fdiv_rn(acc[e], den), q, d, s8);
+        const int el = hh * HD + 64 * e + lane;
+        uint8_t* rec = M->xT + ((size_t)t * nblk + (el >> 5)) * kTRec;
+        rec[el & 31] = (uint8_t)(q & 0xFF);
+        if ((lane & 31) == 0) {
+            *reinterpret_cast<float*>(rec + 32) = d;
+            *reinterpret_cast<int*>(rec + 36) = s8;
+        }
     }
 }
 
-__global__ __launch_bounds__(kPThreads) void kT_o(const DModel* Mp, int l, int pos, int T, int merged) {
-    TPRELUDE(kTNormLds)
-    uint8_t* XT = smem + kTxsBytes;
-    float* P = reinterpret_cast<float*>(smem + kTxsBytes + kTXeBytes);
-    const int n = M->E, nblk = n / 32;
-    if (wave < T) {
-        const int t = wave, nch = (pos + t + kAttnChunk) / kAttnChunk, HD = M->HD, arec = M->arec;
-        const float* att = attT_at(M, l, t);
-        for (int j = 0; 256 * j < n; j++) {
-            const int e0 = 256 * j + 4 * lane;
-            const bool own = e0 < n;
-            float4 y = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (own && merged) {
-                y = ldg4(M->att_outT + ((size_t)l * kMaxT + t) * n + e0);
-            } else if (own) {
-                const int hh = e0 / HD, d = e0 - hh * HD;
-                const float* r = att + (size_t)hh * M->maxch * arec;
-                float mx = -__builtin_inff();
-                for (int c = 0; c < nch; c++) mx = fmaxf(mx, r[c * arec + HD]);
-                float den = 0.f;
-                float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-                for (int c = 0; c < nch; c++) {
-                    const float wc = mi_expf(__fsub_rn(r[c * arec + HD], mx));
-                    den = __fmaf_rn(r[c * arec + HD + 1], wc, den);
-                    const float4 o = ldg4(r + c * arec + d);
-                    acc = make_float4(__fmaf_rn(o.x, wc, acc.x), __fmaf_rn(o.y, wc, acc.y), __fmaf_rn(o.z, wc, acc.z),
-                                      __fmaf_rn(o.w, wc, acc.w));
-                }
-                y = make_float4(__fdiv_rn(acc.x, den), __fdiv_rn(acc.y, den), __fdiv_rn(acc.z, den), __fdiv_rn(acc.w, den));
-            }
-            quant_slice(y, own, e0, XT + (size_t)t * nblk * kTRec, lane, kTRec);
-        }
-    }
-    __syncthreads();
+__global__ __launch_bounds__(kPThreads) void kT_o(const DModel* Mp, int l, int T) {
+    TPRELUDE(kTGemvLds)
+    uint8_t* XT = smem;
+    float* P = reinterpret_cast<float*>(smem + kTXeBytes);
     const PMat W = ldmat(&LY(M, l)->o);
     float* part = oT_at(M, l);
-    tgemm(W, wg, nwg, XT, nblk, T, P, wave, lane, [&](int g, int s, int t, float v) {
+    tgemm(W, wg, nwg, XT, M->E / 32, T, P, wave, lane, [&] { tstage_x(M, T, XT); }, [&](int g, int s, int t, float v) {
         part[((size_t)s * kMaxT + t) * W.rows + g * 64 + lane] = v;
     });
 }
 
 __global__ __launch_bounds__(kPThreads) void kT_gu(const DModel* Mp, int l, int T) {
-    TPRELUDE(kTNormLds)
-    float* xs = reinterpret_cast<float*>(smem);
-    uint8_t* XT = smem + kTxsBytes;
-    float* P = reinterpret_cast<float*>(smem + kTxsBytes + kTXeBytes);
-    tnorm_prologue(M, l, PH_GU, 0, T, wg, xs, XT, wave, lane);
-    __syncthreads();
+    TPRELUDE(kTGemvLds)
+    uint8_t* XT = smem;
+    float* P = reinterpret_cast<float*>(smem + kTXeBytes);
     const PMat W = ldmat(&LY(M, l)->gu);
-    tgemm(W, wg, nwg, XT, M->E / 32, T, P, wave, lane, [&](int g, int s, int t, float v) {
+    tgemm(W, wg, nwg, XT, M->E / 32, T, P, wave, lane, [&] { tstage_x(M, T, XT); }, [&](int g, int s, int t, float v) {
         (void)s;
         const float u = __shfl(v, (lane & 31) + 32);
         const float e = mi_expf(-v);
@@ -1647,32 +1765,38 @@ __global__ __launch_bounds__(kPThreads) void kT_down(const DModel* Mp, int l, in
     uint8_t* XT = smem;
     float* P = reinterpret_cast<float*>(smem + kTXfBytes);
     const int nblk = M->FF / 32;
-    // act records of the T tokens, compacted to kTRec bytes per block
-    for (int i = threadIdx.x; i < T * nblk; i += blockDim.x) {
-        const int t = i / nblk, b = i - t * nblk;
-        const uint2* src = reinterpret_cast<const uint2*>(actT_at(M, l, t) + (size_t)b * kActRec);
-        uint2* dst = reinterpret_cast<uint2*>(XT + ((size_t)t * nblk + b) * kTRec);   // 8-byte aligned records
-#pragma unroll
-        for (int k = 0; k < kTRec / 8; k++) dst[k] = src[k];
-    }
-    __syncthreads();
     const PMat W = ldmat(&LY(M, l)->d);
     float* part = dT_at(M, l);
-    tgemm(W, wg, nwg, XT, nblk, T, P, wave, lane, [&](int g, int s, int t, float v) {
+    // act records of the T tokens over the blocks this workgroup's segments cover,
+    // compacted to kTRec bytes per block
+    auto stage = [&] {
+        const int nseg = (W.rows >> 6) * W.ks;
+        int blo = nblk, bhi = 0;
+        for (int t = wg; t < nseg; t += nwg) {
+            int g, s, c0, c1;
+            tseg(W, t, g, s, c0, c1);
+            blo = min(blo, c0 * W.cb);
+            bhi = max(bhi, c1 * W.cb);
+        }
+        const int nb = max(0, bhi - blo);
+        for (int i = threadIdx.x; i < T * nb * (kTRec / 8); i += blockDim.x) {
+            const int rcd = i / (kTRec / 8), k = i - rcd * (kTRec / 8), t = rcd / max(nb, 1), b = blo + rcd - t * nb;
+            reinterpret_cast<uint2*>(XT + ((size_t)t * nblk + b) * kTRec)[k] =
+                reinterpret_cast<const uint2*>(actT_at(M, l, t) + (size_t)b * kActRec)[k];
+        }
+    };
+    tgemm(W, wg, nwg, XT, nblk, T, P, wave, lane, stage, [&](int g, int s, int t, float v) {
         part[((size_t)s * kMaxT + t) * W.rows + g * 64 + lane] = v;
     });
 }
 
 __global__ __launch_bounds__(kPThreads) void kT_lm(const DModel* Mp, int T) {
-    TPRELUDE(kTNormLds)
-    float* xs = reinterpret_cast<float*>(smem);
-    uint8_t* XT = smem + kTxsBytes;
-    float* P = reinterpret_cast<float*>(smem + kTxsBytes + kTXeBytes);
-    tnorm_prologue(M, M->NL - 1, PH_LM, 0, T, wg, xs, XT, wave, lane);
-    __syncthreads();
+    TPRELUDE(kTGemvLds)
+    uint8_t* XT = smem;
+    float* P = reinterpret_cast<float*>(smem + kTXeBytes);
     const PMat W = ldmat(&M->lm);
     Top2 tp{-__builtin_inff(), INT_MAX, -__builtin_inff()};
-    tgemm(W, wg, nwg, XT, M->E / 32, T, P, wave, lane, [&](int g, int s, int t, float v) {
+    tgemm(W, wg, nwg, XT, M->E / 32, T, P, wave, lane, [&] { tstage_x(M, T, XT); }, [&](int g, int s, int t, float v) {
         (void)s;
         const int row = g * 64 + lane;
         if (M->logitsT) M->logitsT[(size_t)t * M->V + row] = v;
@@ -1689,8 +1813,9 @@ __global__ __launch_bounds__(kPThreads) void kT_lm(const DModel* Mp, int T) {
     }
 }
 
-__global__ __launch_bounds__(kPThreads) void kT_argmax(const DModel* Mp, int ncand, int pos, int T) {
+__global__ __launch_bounds__(kPThreads) void kT_argmax(const DModel* Mp, int ncand, int T) {
     const MPtr M = (MPtr)Mp;
+    const int pos = *M->posT;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     if (wave >= T) return;
     Top2 tp{-__builtin_inff(), INT_MAX, -__builtin_inff()};
@@ -2068,18 +2193,23 @@ hipError_t launch_step_persistent(const DModel& M, const DModel* dM, int nwg, in
     return err;
 }
 
-void launch_step_multi(const DModel& M, const DModel* dM, int nwg, int pos, int T, hipStream_t s) {
-    const int nch_last = (pos + T - 1 + kAttnChunk) / kAttnChunk, merged = nch_last > kInlineComb;
+void launch_step_multi(const DModel& M, const DModel* dM, int nwg, int T, hipStream_t s) {
+    const int ncomb = (T * M.NH + 3) / 4;
     for (int l = 0; l < M.NL; l++) {
-        LAUNCH(kT_qkv, nwg, kPThreads, s, dM, l, pos, T);
-        with_hd(M.HD, [&](auto hd) { LAUNCH((kT_attn<decltype(hd)::value>), nwg, kPThreads, s, dM, l, pos, T); });
-        if (merged) LAUNCH(kT_comb, nwg, kPThreads, s, dM, l, pos, T);
-        LAUNCH(kT_o, nwg, kPThreads, s, dM, l, pos, T, merged);
+        LAUNCH(kT_in, T, kPThreads, s, dM, l, (int)PH_QKV);
+        LAUNCH(kT_qkv, nwg, kPThreads, s, dM, l, T);
+        with_hd(M.HD, [&](auto hd) {
+            LAUNCH((kT_attn<decltype(hd)::value>), nwg, kPThreads, s, dM, l, T);
+            LAUNCH((kT_comb<decltype(hd)::value>), ncomb, 256, s, dM, l, T);
+        });
+        LAUNCH(kT_o, nwg, kPThreads, s, dM, l, T);
+        LAUNCH(kT_in, T, kPThreads, s, dM, l, (int)PH_GU);
         LAUNCH(kT_gu, nwg, kPThreads, s, dM, l, T);
         LAUNCH(kT_down, nwg, kPThreads, s, dM, l, T);
     }
+    LAUNCH(kT_in, T, kPThreads, s, dM, M.NL - 1, (int)PH_LM);
     LAUNCH(kT_lm, nwg, kPThreads, s, dM, T);
-    LAUNCH(kT_argmax, 1, kPThreads, s, dM, nwg, pos, T);
+    LAUNCH(kT_argmax, 1, kPThreads, s, dM, nwg, T);
 }
 int kernels_max_tokens() { return kMaxT; }
 int kernels_max_chunks_multi() { return kTChunks; }

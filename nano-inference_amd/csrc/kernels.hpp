@@ -19,10 +19,11 @@ int kernels_max_tiles_per_wg();
 void launch_step_phases(const DModel& M, const DModel* dM, int nwg, int pos, int gen, hipStream_t s);
 // the same step as one cooperative launch of nwg workgroups (zeroes the barrier counter first)
 hipError_t launch_step_persistent(const DModel& M, const DModel* dM, int nwg, int pos, int gen, hipStream_t s);
-// T tokens (2 <= T <= kernels_max_tokens()) at positions pos..pos+T-1 in one pass
-// over the weights (int8 MFMA tiles), one launch per phase on nwg workgroups; the
-// predictions land in out_tok/out_margin[pos..pos+T-1], logits in logitsT if set
-void launch_step_multi(const DModel& M, const DModel* dM, int nwg, int pos, int T, hipStream_t s);
+// T tokens (2 <= T <= kernels_max_tokens()) at positions p..p+T-1, p = *M.posT (device
+// memory: the launch sequence depends on T only, so it can be captured once and
+// replayed), in one pass over the weights (int8 MFMA tiles), one launch per phase;
+// the predictions land in out_tok/out_margin[p..p+T-1], logits in logitsT if set
+void launch_step_multi(const DModel& M, const DModel* dM, int nwg, int T, hipStream_t s);
 int kernels_max_tokens();
 int kernels_max_chunks_multi();   // chunks per K segment the multi-token kernels stage
 // co-resident workgroups per CU of the persistent kernel (0: cannot launch)

@@ -27,7 +27,8 @@ class MinferError(RuntimeError):
 
 class Opts(C.Structure):
     _fields_ = [("max_ctx", C.c_int32), ("tchunk", C.c_int32), ("spec", C.c_int32), ("ngmax", C.c_int32),
-                ("spec_slope", C.c_float), ("persistent", C.c_int32), ("stop_eos", C.c_int32), ("device", C.c_int32)]
+                ("spec_slope", C.c_float), ("persistent", C.c_int32), ("stop_eos", C.c_int32), ("device", C.c_int32),
+                ("graphs", C.c_int32)]
 
 
 class ModelInfo(C.Structure):

@@ -115,6 +115,35 @@ def test_long_context_multi_merge_phase(pos, T):
     eng.close()
 
 
+def test_graph_replays_equal_direct_launches():
+    """The multi-token step replays one captured HIP graph per (T, logits) with the
+    position read from device memory. Replays at several positions, with eager
+    single-token steps and host synchronizations in between, equal the same steps
+    launched kernel by kernel, bit for bit, on every replay."""
+    path = synth_cached("eng-512", SMALL, 21)
+    V = SMALL["n_vocab"]
+    prompt = minfer.prompt_ids(5, 100, V)
+    g = minfer.Engine(path, max_ctx=256, graphs=1)
+    d = minfer.Engine(path, max_ctx=256, graphs=0)
+    for e in (g, d):
+        e.prefill(prompt)            # 12 replays of the T=8 graph and one of T=4 in g
+    cases = [(100, 8, True), (100, 8, False), (64, 5, True), (69, 8, True), (60, 8, False), (68, 2, True),
+             (70, 8, True), (70, 8, True)]
+    for i, (pos, T, want) in enumerate(cases):
+        say("graph replay %d: pos %d T %d logits %d" % (i, pos, T, want))
+        toks = minfer.prompt_ids(300 + i, T, V)
+        rg = g.step(toks, pos, want_logits=want)
+        rd = d.step(toks, pos, want_logits=want)
+        assert rg[0] == rd[0] and np.array_equal(bits(rg[1]), bits(rd[1])), "replay %d: predictions differ" % i
+        if want:
+            assert np.array_equal(bits(rg[2]), bits(rd[2])), "replay %d: logits differ" % i
+        a1 = g.step(toks[-1], pos + T)    # eager work between replays
+        a2 = d.step(toks[-1], pos + T)
+        assert a1[0] == a2[0] and bits(a1[1]) == bits(a2[1])
+    g.close()
+    d.close()
+
+
 def test_multi_step_rejects_bad_T():
     path = synth_cached("eng-256", TINY, 7)
     eng = minfer.Engine(path, max_ctx=64)
