@@ -43,7 +43,10 @@ typedef struct mi_opts {
     int32_t spec;          /* n-gram speculative decoding inside mi_generate (0/1) */
     int32_t ngmax;         /* longest n-gram the drafter matches (mega.cu:561-578) */
     float spec_slope;      /* cost of each extra token in a step, relative to a 1-token step */
-    int32_t persistent;    /* 1: one persistent cooperative kernel per step; 0: one launch per phase */
+    int32_t persistent;    /* 1: one persistent kernel per step (a plain launch of one workgroup per CU;
+                              if a grid barrier ever gives up because the workgroups were not all
+                              resident, the engine recomputes with cooperative launches from then
+                              on); 0: one launch per phase */
     int32_t stop_eos;      /* mi_generate stops after tokenizer.ggml.eos_token_id */
     int32_t device;        /* HIP device ordinal */
     int32_t graphs;        /* 1: each multi-token step replays a HIP graph captured once per (T, logits)
@@ -75,6 +78,7 @@ typedef struct mi_model_info {
     int32_t n_cu;          /* compute units of the device */
     int32_t persistent;    /* step mode in use */
     uint64_t weight_bytes; /* q4_0 bytes streamed per token (all layers + lm_head) */
+    int32_t coop;          /* 1: the persistent kernel goes out as a cooperative launch */
 } mi_model_info;
 int mi_info(const mi_engine* e, mi_model_info* out);
 
@@ -162,6 +166,12 @@ int mi_profile_step(mi_engine* e, double* us, int32_t n);
 /* Cost of a grid barrier of the persistent kernel: one cooperative launch of nwg
  * workgroups doing n barriers and nothing else; returns microseconds per barrier. */
 int mi_barrier_cost(int32_t nwg, int32_t n, double* us_per_barrier);
+
+/* Test hook of the launch-mode fallback: raise the persistent kernel's barrier error
+ * flag from the host, as a grid barrier that gave up would. The next completed
+ * single-token step then takes the recovery path (clear, switch to cooperative
+ * launches, recompute); the kernels themselves run normally. */
+int mi_debug_flag_barrier(mi_engine* e);
 
 /* ---------------- synthetic model files ---------------- */
 typedef struct mi_synth_shape {

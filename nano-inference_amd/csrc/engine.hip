@@ -47,6 +47,7 @@ struct mi_engine {
     hipStream_t stream = nullptr;
     hipEvent_t ev0 = nullptr, ev1 = nullptr;
     int nwg_persistent = 0;       // workgroups of the persistent step kernel (0: per-phase launches)
+    bool coop = false;            // launch it cooperatively (after a plain launch's barrier failed)
     int32_t* h_iota = nullptr;    // pinned host memory, h_iota[p] = p: the source of posT
     hipGraphExec_t gexec[2][kMaxT + 1] = {};   // multi-token step per (logits, T), captured on first use
     int cur_len = 0;              // positions holding valid K/V
@@ -510,6 +511,15 @@ int mi_info(const mi_engine* e, mi_model_info* o) {
     o->n_cu = e->n_cu;
     o->persistent = e->nwg_persistent > 0;
     o->weight_bytes = e->weight_bytes;
+    o->coop = e->coop ? 1 : 0;
+    return MI_OK;
+}
+
+int mi_debug_flag_barrier(mi_engine* e) {
+    if (!e) return MI_ERR_ARG;
+    if (!e->nwg_persistent) return set_err(e, MI_ERR_STATE, "no persistent step kernel");
+    const int32_t one = 1;
+    HIPCHK(e, hipMemcpy(e->M.err, &one, 4, hipMemcpyHostToDevice));
     return MI_OK;
 }
 
@@ -549,7 +559,7 @@ static int run_step(mi_engine* e, int pos, int gen, bool want_logits) {
     const DModel& M = want_logits ? e->M_logits : e->M;
     const DModel* dM = e->dM + (want_logits ? 1 : 0);
     if (e->nwg_persistent) {
-        const hipError_t err = launch_step_persistent(M, dM, e->nwg_persistent, pos, gen, e->stream);
+        const hipError_t err = launch_step_persistent(M, dM, e->nwg_persistent, pos, gen, e->coop, e->stream);
         if (err == hipErrorIllegalState || err == hipErrorCooperativeLaunchTooLarge) {
             // The runtime refused the cooperative launch itself (seen while another process
             // holds the device's cooperative dispatch); nothing ran. The per-phase launches
@@ -567,12 +577,26 @@ static int run_step(mi_engine* e, int pos, int gen, bool want_logits) {
     return MI_OK;
 }
 
-// after a synchronization: a grid barrier that timed out leaves a flag
+// after a synchronization: a grid barrier that timed out leaves a flag. The persistent
+// kernel goes out as a plain launch, which needs every workgroup resident at once (true
+// on an otherwise idle device). If a barrier gave up (another process held CUs), the
+// barrier state is cleared, the engine switches to cooperative launches (the runtime
+// then waits until all workgroups fit) and the caller recomputes: kRetry.
+constexpr int kRetry = 1 << 20;
 static int check_barrier(mi_engine* e) {
     if (!e->nwg_persistent) return MI_OK;
     int32_t flag = 0;
     HIPCHK(e, hipMemcpy(&flag, e->M.err, 4, hipMemcpyDeviceToHost));
-    if (flag) return set_err(e, MI_ERR_DEVICE, "grid barrier timed out (workgroups not co-resident?)");
+    if (flag) {
+        // a failed launch may leave its counters set: clear them for the next launch
+        HIPCHK(e, hipMemset(e->M.bar, 0, sizeof(uint32_t) * barrier_words()));
+        HIPCHK(e, hipMemset(e->M.err, 0, 4));
+        if (!e->coop) {
+            e->coop = true;
+            return kRetry;
+        }
+        return set_err(e, MI_ERR_DEVICE, "grid barrier timed out under a cooperative launch");
+    }
     return MI_OK;
 }
 
@@ -601,7 +625,8 @@ int mi_step(mi_engine* e, const int32_t* toks, int32_t T, int32_t pos, int32_t* 
         HIPCHK(e, hipMemcpyAsync(logits, T == 1 ? e->M_logits.logits : e->M_logits.logitsT, sizeof(float) * e->V * T,
                                  hipMemcpyDeviceToHost, e->stream));
     HIPCHK(e, hipStreamSynchronize(e->stream));
-    if (T == 1 && (rc = check_barrier(e))) return rc;
+    if (T == 1 && (rc = check_barrier(e)))
+        return rc == kRetry ? mi_step(e, toks, T, pos, argmax, margin, logits) : rc;
     for (int t = 0; t < T; t++) {
         if (argmax) argmax[t] = tok[t];
         if (margin) margin[t] = mg[t];
@@ -643,7 +668,7 @@ int mi_prefill(mi_engine* e, const int32_t* ids, int32_t n, int32_t* first, floa
     HIPCHK(e, hipMemcpyAsync(&mg, e->M.out_margin + n - 1, 4, hipMemcpyDeviceToHost, e->stream));
     HIPCHK(e, hipStreamSynchronize(e->stream));
     if (ran_single)
-        if (int rc = check_barrier(e)) return rc;
+        if (int rc = check_barrier(e)) return rc == kRetry ? mi_prefill(e, ids, n, first, margin) : rc;
     float ms = 0.f;
     HIPCHK(e, hipEventElapsedTime(&ms, e->ev0, e->ev1));
     e->stats.prefill_ms = ms;
@@ -666,7 +691,8 @@ static int run_tokens(mi_engine* e, int pos, int T, int32_t* tok, float* mg) {
     HIPCHK(e, hipMemcpyAsync(tok, e->M.out_tok + pos, 4 * T, hipMemcpyDeviceToHost, e->stream));
     HIPCHK(e, hipMemcpyAsync(mg, e->M.out_margin + pos, 4 * T, hipMemcpyDeviceToHost, e->stream));
     HIPCHK(e, hipStreamSynchronize(e->stream));
-    return T == 1 ? check_barrier(e) : MI_OK;
+    const int rc = T == 1 ? check_barrier(e) : MI_OK;
+    return rc == kRetry ? run_tokens(e, pos, T, tok, mg) : rc;
 }
 
 // Lossless speculative generation (mega.cu:863-895): each step runs [cur, draft]
@@ -767,7 +793,8 @@ int mi_generate(mi_engine* e, int32_t n_gen, int32_t* out, float* margins, int32
             HIPCHK(e, hipMemcpyAsync(mg.data(), e->M.out_margin + p0 - 1, sizeof(float) * n_gen, hipMemcpyDeviceToHost, e->stream));
         }
         HIPCHK(e, hipStreamSynchronize(e->stream));
-        if (int rc = check_barrier(e)) return rc;
+        if (int rc = check_barrier(e))   // the launches only wrote positions p0.. and tokbuf[p0+1..]
+            return rc == kRetry ? mi_generate(e, n_gen, out, margins, n_out, cb, user) : rc;
         for (int t = 0; t < n_gen; t++) {
             if (out) out[t] = tk[t];
             if (margins) margins[t] = mg[t];
@@ -781,8 +808,13 @@ int mi_generate(mi_engine* e, int32_t n_gen, int32_t* out, float* margins, int32
                 steps++;
             }
             int32_t tok; float m;
-            const int rc = fetch(p0 + t - 1, &tok, &m);
+            int rc = fetch(p0 + t - 1, &tok, &m);
             if (rc) return rc;
+            if (t > 0 && (rc = check_barrier(e))) {
+                if (rc != kRetry) return rc;
+                if ((rc = run_step(e, p0 + t - 1, 1, false)) || (rc = fetch(p0 + t - 1, &tok, &m))) return rc;
+                if ((rc = check_barrier(e))) return rc == kRetry ? MI_ERR_DEVICE : rc;
+            }
             if (out) out[t] = tok;
             if (margins) margins[t] = m;
             emitted++;
@@ -808,13 +840,16 @@ int mi_time_phase(mi_engine* e, int32_t phase, int32_t layer, int32_t reps, doub
     const int pos = e->cur_len - 1;
     HIPCHK(e, hipEventRecord(e->ev0, e->stream));
     for (int r = 0; r < reps; r++) {
-        if (phase == 8) HIPCHK(e, launch_step_persistent(e->M, e->dM, e->nwg_persistent, pos, 1, e->stream));
+        if (phase == 8) HIPCHK(e, launch_step_persistent(e->M, e->dM, e->nwg_persistent, pos, 1, e->coop, e->stream));
         else launch_phase(e->M, e->dM, e->n_cu, phase, layer, pos, 1, e->stream);
     }
     HIPCHK(e, hipGetLastError());
     HIPCHK(e, hipEventRecord(e->ev1, e->stream));
     HIPCHK(e, hipEventSynchronize(e->ev1));
-    if (phase == 8) { int rc = check_barrier(e); if (rc) return rc; }
+    if (phase == 8) {
+        const int rc = check_barrier(e);
+        if (rc) return rc == kRetry ? mi_time_phase(e, phase, layer, reps, avg_ms) : rc;
+    }
     float ms = 0.f;
     HIPCHK(e, hipEventElapsedTime(&ms, e->ev0, e->ev1));
     *avg_ms = ms / reps;
@@ -833,7 +868,7 @@ int mi_profile_step(mi_engine* e, double* us, int32_t n) {
     DModel M = e->M;
     M.prof = prof;
     hipError_t st = hipMemcpy(e->dM + 2, &M, sizeof(DModel), hipMemcpyHostToDevice);
-    if (st == hipSuccess) st = launch_step_persistent(M, e->dM + 2, nwg, e->cur_len - 1, 1, e->stream);
+    if (st == hipSuccess) st = launch_step_persistent(M, e->dM + 2, nwg, e->cur_len - 1, 1, e->coop, e->stream);
     std::vector<uint64_t> t(total);
     if (st == hipSuccess) st = hipStreamSynchronize(e->stream);
     if (st == hipSuccess) st = hipMemcpy(t.data(), prof, sizeof(uint64_t) * total, hipMemcpyDeviceToHost);
@@ -842,7 +877,8 @@ int mi_profile_step(mi_engine* e, double* us, int32_t n) {
     uint64_t t0 = t[0];
     for (int w = 1; w < nwg; w++) t0 = std::min(t0, t[(size_t)w * nslot]);
     for (size_t i = 0; i < total; i++) us[i] = (double)(int64_t)(t[i] - t0) * 0.01;   // 100 MHz ticks
-    return check_barrier(e);
+    const int rc = check_barrier(e);
+    return rc == kRetry ? mi_profile_step(e, us, n) : rc;
 }
 
 int mi_barrier_cost(int32_t nwg, int32_t n, double* us_per_barrier) {

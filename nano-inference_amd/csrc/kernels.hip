@@ -444,25 +444,61 @@ __device__ __forceinline__ void top2_wave(Top2& t) {
 // (256 atomics on one address). Run by the whole control wave after the workgroup
 // barrier that follows every worker's own store drain; it drains its own stores
 // first. A poll that outlives kSpinLimit sets *err and returns, so no wave can wait
-// forever. bar[]: counter k at 64*k (zeroed before each launch).
-constexpr unsigned kSpinLimit = 1u << 26;
+// forever. bar[]: counter k at 64*k, the exit counter at 64*kBarGroups; all zero when a
+// launch starts (zeroed at allocation, and each launch leaves them zero: see ctl_exit).
+constexpr unsigned kSpinLimit = 1u << 16;   // polls (~1 us each) before a barrier gives up
 constexpr int kBarGroups = 16;
 constexpr int kBarWords = 64 * (kBarGroups + 2);
-__device__ __forceinline__ void ctl_barrier(uint32_t* bar, int32_t* err, unsigned& epoch) {
+// per-launch barrier state of one control wave (computed once: no integer divides on
+// the barrier path)
+struct GridBar {
+    uint32_t* arrive;          // this workgroup's group counter
+    const uint32_t* poll;      // the counter this lane polls (lanes >= groups: counter 0)
+    unsigned per;              // arrivals per epoch on the polled counter (0: always met)
+    unsigned need;             // this lane's target of the current epoch
+    unsigned dead;             // a barrier of this launch failed: the rest do not wait
+};
+__device__ __forceinline__ GridBar bar_init(uint32_t* bar) {
+    const int lane = threadIdx.x & 63, ng = min(kBarGroups, (int)gridDim.x);
+    const bool mine = lane < ng;
+    GridBar b;
+    b.arrive = bar + 64 * ((int)blockIdx.x % ng);
+    b.poll = bar + 64 * (mine ? lane : 0);
+    b.per = mine ? gridDim.x / ng + ((int)(gridDim.x % ng) > lane ? 1u : 0u) : 0u;
+    b.need = 0;
+    b.dead = 0;
+    return b;
+}
+__device__ __forceinline__ void ctl_barrier(GridBar& b, int32_t* err) {
     drain_vm();
+    if (b.dead) return;
     const int lane = threadIdx.x & 63;
-    epoch++;
-    const int ng = min(kBarGroups, (int)gridDim.x), g = blockIdx.x % ng;
-    if (lane == 0) __hip_atomic_fetch_add(bar + 64 * g, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const unsigned need = lane < ng ? (gridDim.x / ng + ((int)(gridDim.x % ng) > lane ? 1u : 0u)) * epoch : 0u;
-    unsigned spins = 0;
-    for (;;) {
-        const unsigned v = lane < ng ? ldc(bar + 64 * lane) : 0u;
-        if (__all(lane >= ng || (int)(v - need) >= 0)) break;
-        if (++spins > kSpinLimit) {
+    b.need += b.per;
+    if (lane == 0) __hip_atomic_fetch_add(b.arrive, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // every lane loads and the exit test is one ballot: the loop is scalar control flow.
+    // Every 1024 polls the wave also reads *err: once any barrier of this launch (or of
+    // an earlier launch in the stream) has failed, nobody waits any more.
+    for (unsigned spins = 1;; spins++) {
+        const unsigned v = ldc(b.poll);
+        if (__builtin_amdgcn_ballot_w64((int)(v - b.need) < 0) == 0) break;
+        if ((spins & 1023u) == 0 && (spins >= kSpinLimit || ldc(reinterpret_cast<const uint32_t*>(err)) != 0)) {
             if (lane == 0) stc(reinterpret_cast<uint32_t*>(err), 1u);
+            b.dead = 1;
             break;
         }
+    }
+}
+// after the launch's last barrier: each control wave counts itself out; the last one
+// (every workgroup has then finished polling) zeroes the counters for the next launch
+// in the stream, which saves a memset dispatch per token
+__device__ __forceinline__ void ctl_exit(uint32_t* bar) {
+    const int lane = threadIdx.x & 63, ng = min(kBarGroups, (int)gridDim.x);
+    unsigned last = 0;
+    if (lane == 0)
+        last = __hip_atomic_fetch_add(bar + 64 * kBarGroups, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gridDim.x - 1;
+    if (__shfl(last, 0)) {
+        if (lane < ng) stc(bar + 64 * lane, 0u);
+        if (lane == 0) stc(bar + 64 * kBarGroups, 0u);
     }
 }
 
@@ -1099,7 +1135,7 @@ __global__ __launch_bounds__(kPThreads) void k_step(const DModel* Mp, int pos, i
     const bool ctl = wave == 0;
     const int kw = wave - 1;
     const int nch = (pos + 1 + kAttnChunk - 1) / kAttnChunk;
-    unsigned epoch = 0;
+    GridBar gb = bar_init(M->bar);
     Tile tl[2];
     stamp(M, 0);
     stage(M, 0, PH_QKV, pos, S, wave, kPWaves, lane, true);
@@ -1118,7 +1154,7 @@ __global__ __launch_bounds__(kPThreads) void k_step(const DModel* Mp, int pos, i
         if (kind == PH_ATTN && nch > kInlineComb) {           // the chunk merge as a phase of its own
             drain_vm();
             __syncthreads();
-            if (ctl) ctl_barrier(M->bar, M->err, epoch);
+            if (ctl) ctl_barrier(gb, M->err);
             __syncthreads();
             phase_comb(M, l, pos, wg, nwg);
         }
@@ -1130,7 +1166,8 @@ __global__ __launch_bounds__(kPThreads) void k_step(const DModel* Mp, int pos, i
             __syncthreads();
             stamp(M, sb + 3);
             if (ctl) {
-                ctl_barrier(M->bar, M->err, epoch);
+                ctl_barrier(gb, M->err);
+                ctl_exit(M->bar);
                 stamp(M, sb + 4);
                 if (wg == 0) {
                     const Top2 a = wave_merge_cands(M->cand, nwg, lane);
@@ -1153,7 +1190,7 @@ __global__ __launch_bounds__(kPThreads) void k_step(const DModel* Mp, int pos, i
         __syncthreads();
         stamp(M, sb + 3);
         if (ctl) {
-            ctl_barrier(M->bar, M->err, epoch);
+            ctl_barrier(gb, M->err);
             stamp(M, sb + 4);
         } else if (nk == PH_ATTN) {
             // the attention waves' first items: their K/V rows into LDS (U is free once
@@ -1175,10 +1212,10 @@ __global__ __launch_bounds__(kPThreads) void k_step(const DModel* Mp, int pos, i
 
 // barrier cost: n grid barriers and nothing else
 __global__ __launch_bounds__(kPThreads) void k_barriers(uint32_t* bar, int32_t* err, int n) {
-    unsigned epoch = 0;
+    GridBar gb = bar_init(bar);
     for (int i = 0; i < n; i++) {
         __syncthreads();
-        if (threadIdx.x < 64) ctl_barrier(bar, err, epoch);
+        if (threadIdx.x < 64) ctl_barrier(gb, err);
     }
 }
 
@@ -2181,14 +2218,15 @@ void launch_step_phases(const DModel& M, const DModel* dM, int nwg, int pos, int
     launch_phase(M, dM, nwg, 7, 0, pos, gen, s);
 }
 
-hipError_t launch_step_persistent(const DModel& M, const DModel* dM, int nwg, int pos, int gen, hipStream_t s) {
-    hipError_t err = hipMemsetAsync(M.bar, 0, sizeof(uint32_t) * kBarWords, s);
-    if (err != hipSuccess) return err;
+hipError_t launch_step_persistent(const DModel& M, const DModel* dM, int nwg, int pos, int gen, bool coop,
+                                  hipStream_t s) {
+    hipError_t err = hipSuccess;
     with_hd(M.HD, [&](auto hd) {
         const DModel* m = dM;
         void* args[] = {&m, &pos, &gen};
-        err = hipLaunchCooperativeKernel(reinterpret_cast<const void*>(&k_step<decltype(hd)::value>), dim3(nwg),
-                                         dim3(kPThreads), args, 0, s);
+        const void* f = reinterpret_cast<const void*>(&k_step<decltype(hd)::value>);
+        err = coop ? hipLaunchCooperativeKernel(f, dim3(nwg), dim3(kPThreads), args, 0, s)
+                   : hipLaunchKernel(f, dim3(nwg), dim3(kPThreads), args, 0, s);
     });
     return err;
 }

@@ -17,8 +17,13 @@ int kernels_max_tiles_per_wg();
 // one decode step at position pos as one launch per phase (nwg workgroups each);
 // gen != 0 stores the prediction as the token of position pos + 1
 void launch_step_phases(const DModel& M, const DModel* dM, int nwg, int pos, int gen, hipStream_t s);
-// the same step as one cooperative launch of nwg workgroups (zeroes the barrier counter first)
-hipError_t launch_step_persistent(const DModel& M, const DModel* dM, int nwg, int pos, int gen, hipStream_t s);
+// the same step as one launch of nwg workgroups that must all be resident at once
+// (grid barriers). coop: a cooperative launch, which the runtime only starts when
+// they are; otherwise a plain launch (~18 us less per token on MI355X: no cooperative
+// queue hand-off), which relies on an idle device and reports a failed barrier through
+// M.err. M.bar must be zero (it is after allocation, and every launch leaves it zero).
+hipError_t launch_step_persistent(const DModel& M, const DModel* dM, int nwg, int pos, int gen, bool coop,
+                                  hipStream_t s);
 // T tokens (2 <= T <= kernels_max_tokens()) at positions p..p+T-1, p = *M.posT (device
 // memory: the launch sequence depends on T only, so it can be captured once and
 // replayed), in one pass over the weights (int8 MFMA tiles), one launch per phase;

@@ -36,7 +36,8 @@ class ModelInfo(C.Structure):
                 ("n_head_kv", C.c_int32), ("head_dim", C.c_int32), ("n_vocab", C.c_int32), ("eos", C.c_int32),
                 ("rope_base", C.c_float), ("rms_eps", C.c_float), ("max_ctx", C.c_int32),
                 ("plan_cb", C.c_int32 * 5), ("plan_ks", C.c_int32 * 5), ("attn_chunk", C.c_int32),
-                ("kv_f16", C.c_int32), ("n_cu", C.c_int32), ("persistent", C.c_int32), ("weight_bytes", C.c_uint64)]
+                ("kv_f16", C.c_int32), ("n_cu", C.c_int32), ("persistent", C.c_int32), ("weight_bytes", C.c_uint64),
+                ("coop", C.c_int32)]
 
 
 class Stats(C.Structure):
@@ -69,6 +70,7 @@ SIGNATURES = {
     "mi_time_phase": (C.c_int, [_P, C.c_int32, C.c_int32, C.c_int32, C.POINTER(C.c_double)]),
     "mi_profile_step": (C.c_int, [_P, C.POINTER(C.c_double), C.c_int32]),
     "mi_barrier_cost": (C.c_int, [C.c_int32, C.c_int32, C.POINTER(C.c_double)]),
+    "mi_debug_flag_barrier": (C.c_int, [_P]),
     "mi_synth_gguf": (C.c_int, [C.c_char_p, C.POINTER(SynthShape), C.c_uint64]),
     "mi_q4_packed_bytes": (C.c_size_t, [C.c_int32, C.c_int32, C.c_int32]),
     "mi_q4_pack": (C.c_int, [_P, C.c_int32, C.c_int32, C.c_int32, _P]),
@@ -201,6 +203,14 @@ class Engine:
             l = np.frombuffer(lg, dtype=np.float32).copy()
             return a, m, (l.reshape(T, -1) if many else l)
         return a, m
+
+    def debug_flag_barrier(self):
+        """raise the barrier error flag from the host (test hook of the launch-mode fallback)"""
+        _check(lib().mi_debug_flag_barrier(self._h), self._h)
+
+    def refresh_info(self):
+        _check(lib().mi_info(self._h, C.byref(self.info)), self._h)
+        return self.info
 
     def generate(self, n_gen, callback=None):
         out = (C.c_int32 * max(n_gen, 1))()

@@ -181,3 +181,39 @@ def test_rewind_and_restep():
     with pytest.raises(minfer.MinferError):
         eng.step(TINY["n_vocab"], 3)                # token out of range
     eng.close()
+
+
+@pytest.mark.parametrize("mode", ["generate", "generate_cb", "step"])
+def test_barrier_failure_recomputes_cooperatively(mode):
+    """The persistent kernel goes out as a plain launch; if a grid barrier gives up
+    (flagged here from the host: every kernel still runs normally), the engine clears
+    the barrier state, switches to cooperative launches and recomputes, so the output
+    equals an undisturbed run's."""
+    path = synth_cached("eng-512", SMALL, 21)
+    V = SMALL["n_vocab"]
+    ids = minfer.prompt_ids(17, 20, V)
+    ref = minfer.Engine(path, max_ctx=128)
+    ref.prefill(ids)
+    want, wm = ref.generate(12)
+    assert ref.refresh_info().coop == 0
+    ref.close()
+    say("barrier fallback via %s" % mode)
+    eng = minfer.Engine(path, max_ctx=128)
+    first, _ = eng.prefill(ids)
+    eng.debug_flag_barrier()
+    if mode == "generate":
+        got, gm = eng.generate(12)
+    elif mode == "generate_cb":
+        seen = []
+        got, gm = eng.generate(12, callback=lambda t: seen.append(t) and False)
+        assert seen == want
+    else:
+        got, gm = [first], [wm[0]]
+        for p in range(len(ids), len(ids) + 11):
+            a, m = eng.step(got[-1], p)
+            got.append(a)
+            gm.append(m)
+    assert got == want
+    assert np.array_equal(np.float32(gm).view(np.uint32), np.float32(wm).view(np.uint32))
+    assert eng.refresh_info().coop == 1
+    eng.close()
