@@ -57,7 +57,9 @@ def bytes_per_token(info, pos):
 
 
 def gemv_microbench(torch, reps=40):
-    """config 1: the five S15 GEMV shapes, weights rotated over > 512 MB of copies."""
+    """config 1: the five S15 GEMV shapes, weights rotated over > 512 MB of copies
+    (each rep reads a copy the previous reps did not touch, so the 256 MB MALL holds
+    none of it); time per GEMV = graph replay of `reps` launches / reps."""
     import numpy as np
     out = []
     rng = np.random.default_rng(0)
@@ -74,15 +76,28 @@ def gemv_microbench(torch, reps=40):
         xs8 = torch.empty(nb, dtype=torch.int32, device="cuda")
         minfer.quant_q8(x, xq, xd, xs8)
         part = torch.empty(ks * rows, device="cuda")
+        ref = torch.empty(ks * rows, device="cuda")
         for i in range(4):
             minfer.gemv_q4(w[i % copies], rows, nb, cb, ks, xq, xd, xs8, part)
+        # the reps launched back to back from a captured graph (ctypes launches from
+        # Python would leave the GPU idle between the short kernels); each rep reads
+        # another copy of the weights
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for i in range(reps):
+                minfer.gemv_q4(w[i % copies], rows, nb, cb, ks, xq, xd, xs8, part)
+        minfer.gemv_q4(w[(reps - 1) % copies], rows, nb, cb, ks, xq, xd, xs8, ref)
+        g.replay()
+        torch.cuda.synchronize()
+        # bit patterns: the random weight bytes include NaN fp16 scales
+        assert torch.equal(part.view(torch.int32), ref.view(torch.int32)), "graph replay differs from the eager launch"
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record()
-        for i in range(reps):
-            minfer.gemv_q4(w[i % copies], rows, nb, cb, ks, xq, xd, xs8, part)
+        g.replay()
         e1.record()
         torch.cuda.synchronize()
         us = e0.elapsed_time(e1) * 1000 / reps
+        del g
         alg = rows * nb * 18 + n_in + nb * 4 + rows * 4
         out.append(dict(shape=name, rows=rows, k=n_in, us=round(us, 2), gbps=round(alg / us / 1e3, 1)))
         del w

@@ -1883,27 +1883,62 @@ __global__ __launch_bounds__(kThreads) void k_quant(const float* x, int n, int8_
 
 // split-K partials part[s][row] of a packed matrix: one wave per (group, segment),
 // its chunks in order (chunk sums added left to right)
+// Standalone GEMV (q4 tiles x int8 records -> split-K partials): one wave per segment
+// (64-row group g, K segment s); chunk sums add left to right. Two launch shapes:
+// SPREAD (at most kGemvWgsPerCu segments per CU: small matrices, long segments): one
+// segment per workgroup, so the matrix spreads over as many CUs as it has segments,
+// and the wave keeps its next chunk's loads in flight while it computes one (the first
+// is issued before the activation records are staged). Otherwise four segments per
+// workgroup, one chunk in flight per wave: the lower register use keeps ~20 waves per
+// CU resident, which is what feeds HBM for large matrices.
+constexpr int kGemvWgsPerCu = 2;
+template <bool SPREAD>
 __global__ __launch_bounds__(kThreads) void k_gemv(PMat W, const int8_t* xq, const float* xd, const int32_t* xs8, float* part) {
     __shared__ __align__(16) uint8_t X[(kMaxFF / 32) * kXRec];
-    for (int b = threadIdx.x; b < W.nb; b += kThreads) {
-        uint8_t* r = X + b * kXRec;
-        const uint4* src = reinterpret_cast<const uint4*>(xq + 32 * b);
-        reinterpret_cast<uint4*>(r)[0] = src[0];
-        reinterpret_cast<uint4*>(r)[1] = src[1];
-        *reinterpret_cast<float*>(r + 32) = xd[b];
-        *reinterpret_cast<int32_t*>(r + 36) = xs8[b];
-    }
-    __syncthreads();
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int ntask = (W.rows / 64) * W.ks;
-    for (int task = blockIdx.x * kWaves + wave; task < ntask; task += gridDim.x * kWaves) {
-        const int g = div_small(task, W.ks), s = task - g * W.ks, c0 = seg_c0(W, s), c1 = seg_c0(W, s + 1);
+    auto stage = [&] {
+        for (int b = threadIdx.x; b < W.nb; b += kThreads) {
+            uint8_t* r = X + b * kXRec;
+            const uint4* src = reinterpret_cast<const uint4*>(xq + 32 * b);
+            reinterpret_cast<uint4*>(r)[0] = src[0];
+            reinterpret_cast<uint4*>(r)[1] = src[1];
+            *reinterpret_cast<float*>(r + 32) = xd[b];
+            *reinterpret_cast<int32_t*>(r + 36) = xs8[b];
+        }
+        __syncthreads();
+    };
+    if constexpr (!SPREAD) {
+        stage();
+        for (int task = blockIdx.x * kWaves + wave; task < ntask; task += gridDim.x * kWaves) {
+            int g, s, c0, c1;
+            tseg(W, task, g, s, c0, c1);
+            float seg = 0.f;
+            for (int c = c0; c < c1; c++) {
+                Tile t;
+                tile_load(t, tile_ptr(W, g, c), W.cb, lane);
+                const float p = chunk_dot(t, W.cb, X, kXRec, c * W.cb);
+                seg = c == c0 ? p : __fadd_rn(seg, p);
+            }
+            part[(size_t)s * W.rows + g * 64 + lane] = seg;
+        }
+    } else {
+        const int task = blockIdx.x;
+        const bool have = wave == 0 && task < ntask;
+        int g = 0, s = 0, c0 = 0, c1 = 0;
+        Tile cur, nxt;
+        if (have) {
+            tseg(W, task, g, s, c0, c1);
+            tile_load(cur, tile_ptr(W, g, c0), W.cb, lane);
+        }
+        stage();
+        if (!have) return;
         float seg = 0.f;
         for (int c = c0; c < c1; c++) {
-            Tile t;
-            tile_load(t, tile_ptr(W, g, c), W.cb, lane);
-            const float p = chunk_dot(t, W.cb, X, kXRec, c * W.cb);
+            if (c + 1 < c1) tile_load(nxt, tile_ptr(W, g, c + 1), W.cb, lane);
+            const float p = chunk_dot(cur, W.cb, X, kXRec, c * W.cb);
             seg = c == c0 ? p : __fadd_rn(seg, p);
+            cur = nxt;
         }
         part[(size_t)s * W.rows + g * 64 + lane] = seg;
     }
@@ -2277,8 +2312,10 @@ void launch_quant(const float* x, int n, int8_t* xq, float* xd, int32_t* xs8, hi
 void launch_gemv(const PMat& W, const int8_t* xq, const float* xd, const int32_t* xs8, float* part, float* y,
                  int n_cu, hipStream_t s) {
     const int tasks = (W.rows / 64) * W.ks;
-    const int grid = std::max(1, std::min(4 * n_cu, (tasks + kWaves - 1) / kWaves));
-    LAUNCH(k_gemv, grid, kThreads, s, W, xq, xd, xs8, part);
+    if (tasks <= kGemvWgsPerCu * n_cu)
+        LAUNCH(k_gemv<true>, tasks, kThreads, s, W, xq, xd, xs8, part);
+    else
+        LAUNCH(k_gemv<false>, std::min(4 * n_cu, (tasks + kWaves - 1) / kWaves), kThreads, s, W, xq, xd, xs8, part);
     if (y) LAUNCH(k_seg_sum, (W.rows + 255) / 256, 256, s, part, W.rows, W.ks, y);
 }
 void launch_isums(const PMat& W, const int8_t* xq, int32_t* isum, hipStream_t s) {
