@@ -1325,7 +1325,6 @@ __global__ __launch_bounds__(64) void k_argmax(const DModel* Mp, int ncand, int 
 // token by kT_in (residual + RMSNorm + quant, one workgroup per token) or kT_comb
 // (chunk merge + quant), so no workgroup repeats the per-token prologue.
 constexpr int kTChunks = 16;       // chunk sums of one segment held in LDS
-constexpr int kTAttnWaves = 4;     // attention waves per workgroup (LDS bound)
 constexpr int kTXeBytes = kMaxT * (kMaxE / 32) * kTRec;
 constexpr int kTXfBytes = kMaxT * (kMaxFF / 32) * kTRec;
 constexpr int kTPBytes = kTChunks * kMaxT * 64 * 4;
@@ -1602,94 +1601,109 @@ __global__ __launch_bounds__(kPThreads) void kT_qkv(const DModel* Mp, int l, int
     });
 }
 
-// attention items (token t, query head h, 64-position chunk c of positions
-// 0..pos+t). The chunk's K/V rows come from the cache; rows of this step's
-// positions pos..pos+t are finished here from the QKV rows (bias, RoPE, fp16) as
-// the single-token step does for its own position, written into the LDS tiles, and
-// appended to the cache by the items of the last token and of one query head per
-// kv head.
+// Multi-token attention. Item = (kv head, 64-position chunk c, group of tg consecutive
+// tokens): the workgroup stages the chunk's K/V once (cached rows by DMA; the rows of
+// this step's positions pos..pos+T-1 finished from the QKV rows: bias, RoPE, fp16, as
+// the single-token step does for its own position) and its waves run the (token, query
+// head) pairs of the group against it, one attn_core each (the single-token chunk
+// arithmetic), writing record (t, h, c). Token t uses the chunk's rows up to pos + t.
+// The item holding token T-1 appends the step's rows of the chunk to the cache.
 template <int HD>
-__device__ __forceinline__ void tattn_item(MPtr M, int l, int pos, int T, int t, int h, int c, uint8_t* lds, int lane) {
+constexpr int kt_attn_lds() { return 2 * 64 * HD * 2 + kPWaves * HD * 4; }
+
+template <int HD>
+__global__ __launch_bounds__(kPThreads) void kT_attn(const DModel* Mp, int l, int T) {
+    TPRELUDE(kt_attn_lds<HD>())
     constexpr int half = HD / 2, DPL = HD / 64;
-    uint4* kls = reinterpret_cast<uint4*>(lds);
-    __half* vls = reinterpret_cast<__half*>(lds + 64 * HD * 2);
-    float* qs = reinterpret_cast<float*>(lds + 2 * 64 * HD * 2);
+    const int pos = *M->posT;
+    uint4* kls = reinterpret_cast<uint4*>(smem);
+    __half* vls = reinterpret_cast<__half*>(smem + 64 * HD * 2);
+    float* qs = reinterpret_cast<float*>(smem + 2 * 64 * HD * 2) + wave * HD;
     const LPtr Ly = LY(M, l);
-    const int ks = Ly->qkv.ks, kvh = h / M->G, QKV = M->QKV;
-    const int L = pos + t + 1, t0 = c * kAttnChunk, n = min(kAttnChunk, L - t0);
-    const size_t rowbase = ((size_t)l * M->NKV + kvh) * M->maxseq;
-    attn_issue_kv<HD>(M->kc + rowbase * HD, M->vc + rowbase * HD, t0, n, kls, vls, lane);
-    drain_vm();
-    wave_lds_sync();
+    const int G = M->G, NKV = M->NKV, ks = Ly->qkv.ks, QKV = M->QKV;
+    const int nchx = (pos + T - 1 + kAttnChunk) / kAttnChunk;
+    // tokens per item: the smallest power of two that keeps the items within one per
+    // workgroup (more tokens per item: fewer K/V stagings, more pairs per wave)
+    int tg = 1;
+    while (tg < T && NKV * nchx * ((T + tg - 1) / tg) > nwg) tg *= 2;
+    const int ngrp = (T + tg - 1) / tg;
+    const int total = NKV * nchx * ngrp, ip = lane % half;
     const float* part = qkvT_at(M, l);
     const float* bq = Ly->bqkv;
-    const int ip = lane % half;
-    const int rq = h * HD, rk = M->NH * HD + kvh * HD, rv = M->NH * HD + M->KVD + kvh * HD;
     auto fin = [&](int tok, int row) {
         float v = part[(size_t)tok * QKV + row];
         for (int s = 1; s < ks; s++) v = __fadd_rn(v, part[((size_t)s * kMaxT + tok) * QKV + row]);
         return __fadd_rn(v, bq[row]);
     };
-    if (lane < half) {
-        const float2 cz = M->rope[(size_t)(pos + t) * half + ip];
-        const float x0 = fin(t, rq + ip), x1 = fin(t, rq + ip + half);
-        qs[ip] = __fsub_rn(__fmul_rn(x0, cz.x), __fmul_rn(x1, cz.y));
-        qs[ip + half] = __fadd_rn(__fmul_rn(x0, cz.y), __fmul_rn(x1, cz.x));
-        // this step's positions inside the chunk: pos + u for u = 0..t
-        const bool append = t == T - 1 && h % M->G == 0;
-        for (int u = max(0, t0 - pos); u <= t && pos + u < t0 + n; u++) {
-            const int p = pos + u, r = p - t0;
+    // q of (token t, head h), rotated at position pos + t, into the wave's qs
+    auto load_q = [&](int t, int h) {
+        if (lane < half) {
+            const int rq = h * HD;
+            const float2 cz = M->rope[(size_t)(pos + t) * half + ip];
+            const float x0 = fin(t, rq + ip), x1 = fin(t, rq + ip + half);
+            qs[ip] = __fsub_rn(__fmul_rn(x0, cz.x), __fmul_rn(x1, cz.y));
+            qs[ip + half] = __fadd_rn(__fmul_rn(x0, cz.y), __fmul_rn(x1, cz.x));
+        }
+    };
+    for (int it = wg; it < total; it += nwg) {
+        const int grp = it % ngrp, rest = it / ngrp, c = rest % nchx, kvh = rest / nchx;
+        const int ta = grp * tg, tb = min(T, ta + tg) - 1, t0 = c * kAttnChunk;
+        if (t0 > pos + tb) continue;                               // uniform over the workgroup
+        const int ncached = min(kAttnChunk, max(0, pos - t0));
+        const size_t rowbase = ((size_t)l * NKV + kvh) * M->maxseq;
+        if (wave == 0 && ncached > 0)
+            attn_issue_kv<HD>(M->kc + rowbase * HD, M->vc + rowbase * HD, t0, ncached, kls, vls, lane);
+        // this step's row pos + wave, if the chunk holds it and a token of the group sees it
+        const int p = pos + wave;
+        const bool mine = wave <= tb && p >= t0 && p < t0 + kAttnChunk;
+        __half y0 = __float2half(0.f), y1 = y0, v0 = y0, v1 = y0;
+        if (mine && lane < half) {
+            const int rk = M->NH * HD + kvh * HD, rv = M->NH * HD + M->KVD + kvh * HD;
             const float2 cu = M->rope[(size_t)p * half + ip];
-            const float k0 = fin(u, rk + ip), k1 = fin(u, rk + ip + half);
-            const __half y0 = __float2half(__fsub_rn(__fmul_rn(k0, cu.x), __fmul_rn(k1, cu.y)));
-            const __half y1 = __float2half(__fadd_rn(__fmul_rn(k0, cu.y), __fmul_rn(k1, cu.x)));
-            const __half v0 = __float2half(fin(u, rv + ip));
-            const __half v1 = __float2half(fin(u, rv + ip + half));
+            const float k0 = fin(wave, rk + ip), k1 = fin(wave, rk + ip + half);
+            y0 = __float2half(__fsub_rn(__fmul_rn(k0, cu.x), __fmul_rn(k1, cu.y)));
+            y1 = __float2half(__fadd_rn(__fmul_rn(k0, cu.y), __fmul_rn(k1, cu.x)));
+            v0 = __float2half(fin(wave, rv + ip));
+            v1 = __float2half(fin(wave, rv + ip + half));
+        }
+        // the wave's first (token, head) pair of the group
+        const int npair = (tb - ta + 1) * G;
+        if (wave < npair) load_q(ta + wave / G, kvh * G + wave % G);
+        if (wave == 0) drain_vm();
+        __syncthreads();                                           // cached rows landed
+        if (mine && lane < half) {
+            const int r = p - t0;
             __half* kh = reinterpret_cast<__half*>(kls);
             kh[((ip >> 3) * 64 + r) * 8 + (ip & 7)] = y0;
             kh[(((ip + half) >> 3) * 64 + r) * 8 + ((ip + half) & 7)] = y1;
             vls[r * HD + ip] = v0;
             vls[r * HD + ip + half] = v1;
-            if (append) {
+            if (tb == T - 1) {                                     // one item per (kv head, chunk) appends
                 __half* kd = M->kc + (rowbase + p) * HD;
                 __half* vd = M->vc + (rowbase + p) * HD;
                 kd[ip] = y0; kd[ip + half] = y1;
                 vd[ip] = v0; vd[ip + half] = v1;
             }
         }
-    }
-    wave_lds_sync();
-    float m, lsum, acc[DPL];
-    attn_core<HD>(kls, qs, vls, n, M->scale, lane, m, lsum, acc);
-    float* rec = attT_at(M, l, t) + ((size_t)h * M->maxch + c) * M->arec;
+        __syncthreads();                                           // the chunk's rows complete
+        for (int i = wave; i < npair; i += kPWaves) {
+            const int t = ta + i / G, h = kvh * G + i % G;
+            if (i != wave) {
+                wave_lds_sync();
+                load_q(t, h);
+            }
+            wave_lds_sync();
+            if (t0 > pos + t) continue;                            // the chunk is past this token
+            float m, lsum, acc[DPL];
+            attn_core<HD>(kls, qs, vls, min(kAttnChunk, pos + t + 1 - t0), M->scale, lane, m, lsum, acc);
+            float* rec = attT_at(M, l, t) + ((size_t)h * M->maxch + c) * M->arec;
 #pragma unroll
-    for (int e = 0; e < DPL; e++) rec[DPL * lane + e] = acc[e];
-    if (lane == 0) { rec[HD] = m; rec[HD + 1] = lsum; }
-    wave_lds_sync();
-}
-
-template <int HD>
-__global__ __launch_bounds__(kPThreads) void kT_attn(const DModel* Mp, int l, int T) {
-    TPRELUDE(kTAttnWaves * attn_wave_lds<HD>())
-    const int pos = *M->posT;
-    (void)wg;
-    if (wave >= kTAttnWaves) return;
-    // items of token t: NH heads x chunks of positions 0..pos+t; enumerated token-major
-    const int NH = M->NH;
-    int total = 0;
-    for (int t = 0; t < T; t++) total += NH * ((pos + t + kAttnChunk) / kAttnChunk);
-    for (int i = blockIdx.x + nwg * wave; i < total; i += nwg * kTAttnWaves) {
-        int t = 0, r = i;
-        for (;; t++) {
-            const int cnt = NH * ((pos + t + kAttnChunk) / kAttnChunk);
-            if (r < cnt) break;
-            r -= cnt;
+            for (int e = 0; e < DPL; e++) rec[DPL * lane + e] = acc[e];
+            if (lane == 0) { rec[HD] = m; rec[HD + 1] = lsum; }
         }
-        const int nch = (pos + t + kAttnChunk) / kAttnChunk;
-        tattn_item<HD>(M, l, pos, T, t, r / nch, r % nch, smem + wave * attn_wave_lds<HD>(), lane);
+        __syncthreads();                                           // LDS is reused by the next item
     }
 }
-
 
 // chunk merge of token t's records for query head h (one wave per (t, h); lane = dims
 // lane + 64j) into the O phase's int8 records in xT. The merge is combine_tree's
