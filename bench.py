@@ -63,8 +63,10 @@ def gemv_microbench(torch, reps=40):
     import numpy as np
     out = []
     rng = np.random.default_rng(0)
-    shapes = [("qkv", 2048, 1536, 6), ("o", 1536, 1536, 6), ("gate_up", 17920, 1536, 4),
-              ("down", 1536, 8960, 8), ("lm_head", 151936, 1536, 1)]
+    # ks per shape: the fastest split of K up to 8 (the most partials the engine's residual
+    # add takes), from a sweep on the box
+    shapes = [("qkv", 2048, 1536, 6), ("o", 1536, 1536, 6), ("gate_up", 17920, 1536, 6),
+              ("down", 1536, 8960, 7), ("lm_head", 151936, 1536, 1)]
     for name, rows, n_in, ks in shapes:
         nb, cb = n_in // 32, 8
         nbytes = minfer.packed_bytes(rows, nb, cb)
@@ -99,7 +101,7 @@ def gemv_microbench(torch, reps=40):
         us = e0.elapsed_time(e1) * 1000 / reps
         del g
         alg = rows * nb * 18 + n_in + nb * 4 + rows * 4
-        out.append(dict(shape=name, rows=rows, k=n_in, us=round(us, 2), gbps=round(alg / us / 1e3, 1)))
+        out.append(dict(shape=name, rows=rows, k=n_in, ks=ks, us=round(us, 2), gbps=round(alg / us / 1e3, 1)))
         del w
     torch.cuda.empty_cache()
     _ = rng

@@ -1898,13 +1898,15 @@ __global__ __launch_bounds__(kThreads) void k_quant(const float* x, int n, int8_
 // split-K partials part[s][row] of a packed matrix: one wave per (group, segment),
 // its chunks in order (chunk sums added left to right)
 // Standalone GEMV (q4 tiles x int8 records -> split-K partials): one wave per segment
-// (64-row group g, K segment s); chunk sums add left to right. Two launch shapes:
-// SPREAD (at most kGemvWgsPerCu segments per CU: small matrices, long segments): one
-// segment per workgroup, so the matrix spreads over as many CUs as it has segments,
-// and the wave keeps its next chunk's loads in flight while it computes one (the first
-// is issued before the activation records are staged). Otherwise four segments per
-// workgroup, one chunk in flight per wave: the lower register use keeps ~20 waves per
-// CU resident, which is what feeds HBM for large matrices.
+// (64-row group g, K segment s); chunk sums add left to right. Three launch shapes (the
+// launcher picks): with at most kGemvWgsPerCu segments per CU, a segment of several
+// chunks gets a workgroup whose waves share its chunks (k_gemv_seg below), and a
+// one-chunk segment a workgroup of its own (SPREAD), so the matrix spreads over as many
+// CUs as it has segments; the wave keeps its next chunk's loads in flight while it
+// computes one (the first is issued before the activation records are staged).
+// Otherwise four segments per workgroup, one chunk in flight per wave: the lower
+// register use keeps ~20 waves per CU resident, which is what feeds HBM for large
+// matrices.
 constexpr int kGemvWgsPerCu = 2;
 template <bool SPREAD>
 __global__ __launch_bounds__(kThreads) void k_gemv(PMat W, const int8_t* xq, const float* xd, const int32_t* xs8, float* part) {
@@ -1954,6 +1956,46 @@ __global__ __launch_bounds__(kThreads) void k_gemv(PMat W, const int8_t* xq, con
             seg = c == c0 ? p : __fadd_rn(seg, p);
             cur = nxt;
         }
+        part[(size_t)s * W.rows + g * 64 + lane] = seg;
+    }
+}
+
+// Segment-per-workgroup GEMV (segments of at most kSegMaxChunks chunks): workgroup t owns
+// segment t; wave j takes its chunks j, j + NW, ... (the next one's loads in flight while
+// it computes one), so all of a short segment's loads are issued at once. Chunk sums go
+// to LDS; wave 0 adds them left to right, as the one-wave loop does. Only the segment's
+// activation blocks are staged.
+constexpr int kSegMaxChunks = 48;
+template <int NW>
+__global__ __launch_bounds__(64 * NW) void k_gemv_seg(PMat W, const int8_t* xq, const float* xd, const int32_t* xs8,
+                                                      float* part) {
+    __shared__ __align__(16) uint8_t X[kSegMaxChunks * 8 * kXRec];
+    __shared__ float sums[kSegMaxChunks][64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    int g, s, c0, c1;
+    tseg(W, blockIdx.x, g, s, c0, c1);
+    int c = c0 + wave;
+    Tile cur, nxt;
+    if (c < c1) tile_load(cur, tile_ptr(W, g, c), W.cb, lane);
+    const int b0 = c0 * W.cb, nblk = (c1 - c0) * W.cb;
+    for (int b = threadIdx.x; b < nblk; b += 64 * NW) {
+        uint8_t* r = X + b * kXRec;
+        const uint4* src = reinterpret_cast<const uint4*>(xq + 32 * (b0 + b));
+        reinterpret_cast<uint4*>(r)[0] = src[0];
+        reinterpret_cast<uint4*>(r)[1] = src[1];
+        *reinterpret_cast<float*>(r + 32) = xd[b0 + b];
+        *reinterpret_cast<int32_t*>(r + 36) = xs8[b0 + b];
+    }
+    __syncthreads();
+    for (; c < c1; c += NW) {
+        if (c + NW < c1) tile_load(nxt, tile_ptr(W, g, c + NW), W.cb, lane);
+        sums[c - c0][lane] = chunk_dot(cur, W.cb, X, kXRec, (c - c0) * W.cb);
+        cur = nxt;
+    }
+    __syncthreads();
+    if (wave == 0) {
+        float seg = sums[0][lane];
+        for (int k = 1; k < c1 - c0; k++) seg = __fadd_rn(seg, sums[k][lane]);
         part[(size_t)s * W.rows + g * 64 + lane] = seg;
     }
 }
@@ -2326,7 +2368,18 @@ void launch_quant(const float* x, int n, int8_t* xq, float* xd, int32_t* xs8, hi
 void launch_gemv(const PMat& W, const int8_t* xq, const float* xd, const int32_t* xs8, float* part, float* y,
                  int n_cu, hipStream_t s) {
     const int tasks = (W.rows / 64) * W.ks;
-    if (tasks <= kGemvWgsPerCu * n_cu)
+    const int maxc = (W.nc + W.ks - 1) / W.ks;          // chunks of the longest segment
+    if (tasks <= kGemvWgsPerCu * n_cu && maxc >= 2 && maxc <= kSegMaxChunks) {
+        switch (std::min(maxc, 8)) {
+        case 2: LAUNCH(k_gemv_seg<2>, tasks, 128, s, W, xq, xd, xs8, part); break;
+        case 3: LAUNCH(k_gemv_seg<3>, tasks, 192, s, W, xq, xd, xs8, part); break;
+        case 4: LAUNCH(k_gemv_seg<4>, tasks, 256, s, W, xq, xd, xs8, part); break;
+        case 5: LAUNCH(k_gemv_seg<5>, tasks, 320, s, W, xq, xd, xs8, part); break;
+        case 6: LAUNCH(k_gemv_seg<6>, tasks, 384, s, W, xq, xd, xs8, part); break;
+        case 7: LAUNCH(k_gemv_seg<7>, tasks, 448, s, W, xq, xd, xs8, part); break;
+        default: LAUNCH(k_gemv_seg<8>, tasks, 512, s, W, xq, xd, xs8, part); break;
+        }
+    } else if (tasks <= kGemvWgsPerCu * n_cu)
         LAUNCH(k_gemv<true>, tasks, kThreads, s, W, xq, xd, xs8, part);
     else
         LAUNCH(k_gemv<false>, std::min(4 * n_cu, (tasks + kWaves - 1) / kWaves), kThreads, s, W, xq, xd, xs8, part);
