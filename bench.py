@@ -195,7 +195,8 @@ def verify_cost(reps=10):
 def attention_depth(torch, lengths=(512, 4096, 16384, 32768), layers=28, reps=3):
     """config3: S15 split-KV decode attention (12/2 heads, hd 128), one query, fp16 K/V
     N(0,1) at context L, rotated over 28 layers' caches (28 x 32 MB at L = 32768 > the
-    256 MB MALL). Algorithmic bytes per layer: 1024*L (K and V) + q/out."""
+    256 MB MALL), the 28 launches replayed from a graph. Algorithmic bytes per layer:
+    1024*L (K and V) + q/out."""
     nh, nkv, hd = 12, 2, 128
     res = []
     for L in lengths:
@@ -207,13 +208,25 @@ def attention_depth(torch, lengths=(512, 4096, 16384, 32768), layers=28, reps=3)
         scale = 1.0 / hd ** 0.5
         for l in range(2):
             minfer.attn_decode(q, kc[l], vc[l], nh, nkv, hd, L, L, scale, scratch, out)
+        # the layers' launches replayed from a captured graph (ctypes launches from
+        # Python would leave the GPU idle between the short kernels); the kernel's
+        # counters return to zero by themselves, so replays need no reset
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for l in range(layers):
+                minfer.attn_decode(q, kc[l], vc[l], nh, nkv, hd, L, L, scale, scratch, out)
+        ref = torch.empty_like(out)
+        minfer.attn_decode(q, kc[layers - 1], vc[layers - 1], nh, nkv, hd, L, L, scale, scratch, ref)
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int32), ref.view(torch.int32)), "graph replay differs from the eager launch"
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record()
         for _ in range(reps):
-            for l in range(layers):
-                minfer.attn_decode(q, kc[l], vc[l], nh, nkv, hd, L, L, scale, scratch, out)
+            g.replay()
         e1.record()
         torch.cuda.synchronize()
+        del g
         us = e0.elapsed_time(e1) * 1e3 / (reps * layers)
         byt = 1024 * L + 2 * nh * hd * 4
         res.append(dict(L=L, us_per_layer=round(us, 2), gbps=round(byt / us / 1e3, 1)))

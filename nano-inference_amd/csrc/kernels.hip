@@ -2161,6 +2161,75 @@ __device__ __forceinline__ void lds_merge(const float* r, int c0, int c1, float*
     deno = den;
 }
 
+// Up to 32 records of one head held in registers: lane i < n holds m and l of record i,
+// every lane its DPL dims of each record. rr_issue starts the loads (all of them at
+// once: the merge costs one memory round trip, and the next head's loads can be in
+// flight while rr_merge works on this one); rr_merge computes what lds_merge does
+// (M = max over the records, w_i = exp(m_i - M), den and acc as fma chains in record
+// order), so the two give the same bits.
+constexpr int kRegRecs = 32;
+template <int HD, int N>
+struct RegRecs { float m, l; float o[N][HD / 64]; };
+template <int HD, int N>
+__device__ __forceinline__ void rr_issue(RegRecs<HD, N>& b, const float* r, int n, int lane) {
+    constexpr int REC = HD + 32, DPL = HD / 64;
+    // opaque copy of the lane index: keeps the lane-derived addresses from being hoisted
+    // out of the item loop, where they would stay live across the items' register peak
+    asm volatile("" : "+v"(lane));
+    b.m = lane < n ? r[lane * REC + HD] : -__builtin_inff();
+    b.l = lane < n ? r[lane * REC + HD + 1] : 0.f;
+#pragma unroll
+    for (int i = 0; i < N; i++) {
+        if (i < n) {
+            if constexpr (DPL == 2) {
+                const float2 v = *reinterpret_cast<const float2*>(r + i * REC + 2 * lane);
+                b.o[i][0] = v.x;
+                b.o[i][1] = v.y;
+            } else {
+                b.o[i][0] = r[i * REC + lane];
+            }
+        }
+    }
+}
+template <int HD, int N>
+__device__ __forceinline__ void rr_merge(const RegRecs<HD, N>& b, int n, int lane, float& M, float& den,
+                                         float (&acc)[HD / 64]) {
+    constexpr int DPL = HD / 64;
+    M = wave_max(b.m);
+    const float w = lane < n ? mi_expf(__fsub_rn(b.m, M)) : 0.f;
+    const int wb = __float_as_int(w), lb = __float_as_int(b.l);
+    den = 0.f;
+#pragma unroll
+    for (int e = 0; e < DPL; e++) acc[e] = 0.f;
+#pragma unroll
+    for (int i = 0; i < N; i++) {
+        if (i < n) {
+            const float wi = __int_as_float(__builtin_amdgcn_readlane(wb, i));
+            den = __fmaf_rn(__int_as_float(__builtin_amdgcn_readlane(lb, i)), wi, den);
+#pragma unroll
+            for (int e = 0; e < DPL; e++) acc[e] = __fmaf_rn(b.o[i][e], wi, acc[e]);
+        }
+    }
+}
+// The merges of g heads (records of head hh at r0 + hh * hstride, n <= N of them),
+// two heads' records in flight at a time; done(hh, M, den, acc) takes each result.
+template <int HD, int N, class F>
+__device__ __forceinline__ void rr_heads(const float* r0, size_t hstride, int n, int g, int lane, F done) {
+    RegRecs<HD, N> a, b;
+    float M, den, acc[HD / 64];
+    rr_issue<HD, N>(a, r0, n, lane);
+    for (int hh = 0; hh < g; hh += 2) {
+        if (hh + 1 < g) rr_issue<HD, N>(b, r0 + (hh + 1) * hstride, n, lane);
+        rr_merge<HD, N>(a, n, lane, M, den, acc);
+        done(hh, M, den, acc);
+        if (hh + 1 < g) {
+            if (hh + 2 < g) rr_issue<HD, N>(a, r0 + (hh + 2) * hstride, n, lane);
+            rr_merge<HD, N>(b, n, lane, M, den, acc);
+            done(hh + 1, M, den, acc);
+        }
+    }
+}
+
 // the wave's arrival on a counter of `need` arrivals: true for the last one, which
 // puts the counter back to zero (every arrival of this launch is in by then)
 __device__ __forceinline__ bool last_arrival(uint32_t* cnt, uint32_t need, int lane) {
@@ -2177,7 +2246,7 @@ __device__ __forceinline__ bool last_arrival(uint32_t* cnt, uint32_t need, int l
 // x, x + 8, ... share XCD x), so the groups of one unit read its K/V through one L2.
 // Within XCD x the items k = (u / 8) * ngrp + hg are dealt to (workgroup, wave) in
 // turn; the grid is a multiple of 8.
-template <int HD>
+template <int HD, bool RR>
 __global__ __launch_bounds__(64 * kItemWaves) __attribute__((amdgpu_waves_per_eu(2))) void k_attn_fused(const float* q, const __half* kc, const __half* vc,
                                                                 int nh, int nkv, int L, int ctx, float scale, int g,
                                                                 float* scratch, float* out) {
@@ -2208,10 +2277,9 @@ __global__ __launch_bounds__(64 * kItemWaves) __attribute__((amdgpu_waves_per_eu
                                        rec, (size_t)nch * REC);
         const int sp = c / kAttnSplit, c0 = sp * kAttnSplit, c1 = min(nch, c0 + kAttnSplit);
         if (!last_arrival(scnt + ((size_t)kvh * nsp + sp) * ngrp + hg, c1 - c0, lane)) continue;
-        for (int hh = 0; hh < g; hh++) {      // level 1: the split's chunks -> the output or a split record
+        // level 1: the split's chunks -> the output or a split record
+        auto put1 = [&](int hh, float M, float den, const float (&acc)[DPL]) {
             const int h = h0 + hh;
-            float M, den, acc[DPL];
-            lds_merge<HD>(recs + (size_t)h * nch * REC, c0, c1, qg, lane, M, den, acc);
             if (nsp == 1) {
 #pragma unroll
                 for (int e = 0; e < DPL; e++) out[(size_t)h * HD + DPL * lane + e] = __fdiv_rn(acc[e], den);
@@ -2224,14 +2292,30 @@ __global__ __launch_bounds__(64 * kItemWaves) __attribute__((amdgpu_waves_per_eu
                     stc(sr + HD + 1, den);
                 }
             }
+        };
+        if constexpr (RR) {
+            rr_heads<HD, kAttnSplit>(recs + ((size_t)h0 * nch + c0) * REC, (size_t)nch * REC, c1 - c0, g, lane, put1);
+        } else {
+            for (int hh = 0; hh < g; hh++) {
+                float M, den, acc[DPL];
+                lds_merge<HD>(recs + (size_t)(h0 + hh) * nch * REC, c0, c1, qg, lane, M, den, acc);
+                put1(hh, M, den, acc);
+            }
         }
         if (nsp == 1 || !last_arrival(hcnt + (size_t)kvh * ngrp + hg, nsp, lane)) continue;
-        for (int hh = 0; hh < g; hh++) {      // level 2: the splits -> the output
-            const int h = h0 + hh;
-            float M, den, acc[DPL];
-            lds_merge<HD>(srecs + (size_t)h * nsp * REC, 0, nsp, qg, lane, M, den, acc);
+        // level 2: the splits -> the output
+        auto put = [&](int hh, float M, float den, const float (&acc)[DPL]) {
 #pragma unroll
-            for (int e = 0; e < DPL; e++) out[(size_t)h * HD + DPL * lane + e] = __fdiv_rn(acc[e], den);
+            for (int e = 0; e < DPL; e++) out[(size_t)(h0 + hh) * HD + DPL * lane + e] = __fdiv_rn(acc[e], den);
+        };
+        if (RR && nsp <= kRegRecs) {
+            rr_heads<HD, kRegRecs>(srecs + (size_t)h0 * nsp * REC, (size_t)nsp * REC, nsp, g, lane, put);
+        } else {
+            for (int hh = 0; hh < g; hh++) {
+                float M, den, acc[DPL];
+                lds_merge<HD>(srecs + (size_t)(h0 + hh) * nsp * REC, 0, nsp, qg, lane, M, den, acc);
+                put(hh, M, den, acc);
+            }
         }
     }
 }
@@ -2407,8 +2491,14 @@ bool launch_attn_decode(const float* q, const __half* kc, const __half* vc, int 
     }
     const int per = std::max(1, std::min(kItemWgsPerXcd, ((units + 7) / 8 * ngrp + kItemWaves - 1) / kItemWaves));
     with_hd(hd, [&](auto h) {
-        LAUNCH((k_attn_fused<decltype(h)::value>), 8 * per, 64 * kItemWaves, s, q, kc, vc, nh, nkv, L, ctx, scale,
-               G / ngrp, scratch, out);
+        // the register merges pay off when a merge takes several heads (their loads
+        // overlap); with one head the kernel without them runs faster
+        if (G / ngrp >= 2)
+            LAUNCH((k_attn_fused<decltype(h)::value, true>), 8 * per, 64 * kItemWaves, s, q, kc, vc, nh, nkv, L, ctx,
+                   scale, G / ngrp, scratch, out);
+        else
+            LAUNCH((k_attn_fused<decltype(h)::value, false>), 8 * per, 64 * kItemWaves, s, q, kc, vc, nh, nkv, L, ctx,
+                   scale, G / ngrp, scratch, out);
     });
     return true;
 }

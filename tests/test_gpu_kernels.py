@@ -102,10 +102,11 @@ def test_gemv_bit_exact(torch, rows, n_in, cb, ks):
 @pytest.mark.parametrize("nh,nkv,hd,L", [(12, 2, 128, 1), (12, 2, 128, 64), (12, 2, 128, 65), (12, 2, 128, 300),
                                          (14, 2, 64, 200), (16, 2, 128, 1024), (4, 2, 64, 130),
                                          (14, 2, 64, 1100), (16, 2, 128, 2049), (8, 1, 128, 5000),
-                                         (32, 4, 64, 32768), (24, 4, 128, 32700)])
+                                         (32, 4, 64, 32768), (24, 4, 128, 32700), (12, 2, 128, 33000)])
 def test_attention_bit_exact(torch, nh, nkv, hd, L):
-    """chunked attention vs the oracle's canonical order; the last two cases give
-    items of all 8 and all 6 query heads of a kv head"""
+    """chunked attention vs the oracle's canonical order; the last three cases give
+    items of all 8, of 3 and of 3 query heads of a kv head (the register-held record
+    merges), the last with more splits (33) than those merges hold"""
     say("attention nh=%d nkv=%d hd=%d L=%d" % (nh, nkv, hd, L))
     ctx = L + 5
     q = RNG.standard_normal((nh, hd)).astype(np.float32)
