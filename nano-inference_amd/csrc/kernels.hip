@@ -287,9 +287,9 @@ __device__ __forceinline__ int seg_c0(const PMat W, int s) { return W.ks == 1 ? 
 // ------------------------------------------------------------------ workgroup work split
 constexpr int kWorkers = kPWaves - 1;      // waves 1..7
 constexpr int kPartTiles = 96;             // chunk sums a workgroup stages per phase
-constexpr int kCtlBytes = 64 * 1024;       // control-wave DMA staging
+constexpr int kCtlBytes = 72 * 1024;       // phase-input DMA staging (hd 128's attention union is larger)
 constexpr int kMaxKsQkv = 2;               // q/k/v partials an attention item stages
-constexpr int kMaxKsRes = 8;               // split-K partials a residual add takes
+constexpr int kMaxKsRes = 12;              // split-K partials a residual add takes
 
 // Segments (64-row group g, K segment s; t = g*ks + s) go round-robin to
 // workgroups, t -> workgroup t % nwg. A workgroup's tiles are its segments'
@@ -2350,9 +2350,12 @@ static void with_hd(int HD, F f) {
 
 // Reduction plan: chunk size by row length (8 blocks, 4 when the block count is not
 // a multiple of 8); one K segment per row except the down matrix, whose rows are
-// split so a workgroup's segment has at most 5 chunks, within what the control
-// wave stages (the norm weights, the h vector and ks partials in kCtlBytes). The
-// plan depends only on the shape, so the float order is device-independent.
+// split into as many segments as leave one per workgroup of a 256-CU device (more
+// segments = shorter ones, and the down phase is a one-round latency chain; past one
+// per workgroup some workgroups take two), within what the phase prologue stages (the
+// norm weights, the h vector and ks partials in kCtlBytes). The plan depends only on
+// the shape, so the float order is device-independent.
+constexpr int kPlanWgs = 256;
 bool kernels_plan(int E, int FF, int cb[5], int ks[5]) {
     const int nbE = E / 32, nbF = FF / 32;
     const int cbE = nbE % 8 == 0 ? 8 : 4, cbF = nbF % 8 == 0 ? 8 : 4;
@@ -2361,7 +2364,7 @@ bool kernels_plan(int E, int FF, int cb[5], int ks[5]) {
     ks[0] = ks[1] = ks[2] = ks[4] = 1;
     const int ncF = nbF / cbF, cap = std::min(kMaxKsRes, kCtlBytes / (4 * E) - 2);
     if (cap < 1) return false;
-    ks[3] = std::max(1, std::min(std::min(cap, ncF), (ncF + 4) / 5));
+    ks[3] = std::max(1, std::min(std::min(cap, ncF), kPlanWgs / (E / 64)));
     return (FF / 32) * kActRec <= kCtlBytes;
 }
 
