@@ -772,10 +772,16 @@ __device__ __forceinline__ Top2 wave_merge_cands(const float* cand, int n, int l
     top2_wave(t);
     return t;
 }
+// The token of a merged top-2. Only when no logit compares greater than -inf (all NaN
+// or -inf) is no row taken and idx left at INT_MAX; the first-max argmax of
+// cpu_infer.cpp:153-154 returns row 0 then, and so does this. (It also keeps the next
+// step's embedding gather, which reads row tokbuf[pos + 1], inside the table.)
+__device__ __forceinline__ int top2_token(const Top2& a, int V) { return (unsigned)a.idx < (unsigned)V ? a.idx : 0; }
 __device__ __forceinline__ void emit_token(MPtr M, const Top2& a, int pos, int gen) {
-    M->out_tok[pos] = a.idx;
+    const int tok = top2_token(a, M->V);
+    M->out_tok[pos] = tok;
     M->out_margin[pos] = __fsub_rn(a.best, a.second);
-    if (gen) M->tokbuf[pos + 1] = a.idx;
+    if (gen) M->tokbuf[pos + 1] = tok;
 }
 
 // ------------------------------------------------------------------ attention
@@ -1876,7 +1882,7 @@ __global__ __launch_bounds__(kPThreads) void kT_argmax(const DModel* Mp, int nca
     }
     top2_wave(tp);
     if (lane == 0) {
-        M->out_tok[pos + wave] = tp.idx;
+        M->out_tok[pos + wave] = top2_token(tp, M->V);
         M->out_margin[pos + wave] = __fsub_rn(tp.best, tp.second);
     }
 }

@@ -115,6 +115,82 @@ def test_config_stream_128(name, persistent):
         % (name, d, margins[d] if d < len(margins) else float("nan")))
 
 
+def gguf_tensor_data(path):
+    """name -> (file offset of the data, GGUF type, dims) for each tensor of a GGUF v3 file"""
+    import struct
+    with open(path, "rb") as f:
+        b = f.read()
+    o = [4]
+
+    def rd(fmt):
+        v = struct.unpack_from("<" + fmt, b, o[0])[0]
+        o[0] += struct.calcsize("<" + fmt)
+        return v
+
+    def rstr():
+        n = rd("Q")
+        o[0] += n
+        return b[o[0] - n:o[0]].decode()
+
+    sizes = {0: 1, 1: 1, 2: 2, 3: 2, 4: 4, 5: 4, 6: 4, 7: 1, 10: 8, 11: 8, 12: 8}
+
+    def skip(t):
+        if t == 8:
+            rstr()
+        elif t == 9:
+            et, n = rd("I"), rd("Q")
+            for _ in range(n):
+                skip(et)
+        else:
+            o[0] += sizes[t]
+
+    assert b[:4] == b"GGUF" and rd("I") == 3
+    nt, nkv, align = rd("Q"), rd("Q"), 32
+    for _ in range(nkv):
+        key, t = rstr(), rd("I")
+        if key == "general.alignment":
+            align = rd("I")
+        else:
+            skip(t)
+    infos = []
+    for _ in range(nt):
+        name, nd = rstr(), rd("I")
+        dims = [rd("Q") for _ in range(nd)]
+        infos.append((name, rd("I"), dims, rd("Q")))
+    base = (o[0] + align - 1) // align * align
+    return {n: (base + off, t, dims) for n, t, dims, off in infos}
+
+
+@pytest.mark.parametrize("mode", [dict(persistent=1), dict(persistent=0), dict(persistent=1, spec=1)],
+                         ids=["persistent", "per-phase", "speculative"])
+def test_nan_logits_give_token_zero(tmp_path, mode):
+    """All logits NaN (a NaN output norm): no logit compares greater than row 0's, so
+    the first-max argmax of cpu_infer.cpp:153-154 (and the oracle) returns row 0, and so
+    must every step kind here (single, per-phase, multi-token prefill and verify); the
+    token fed back to the next step's embedding gather must stay inside the table."""
+    import shutil
+    src = synth_cached("eng-%d" % TINY["n_embd"], TINY, 7)
+    path = str(tmp_path / "nan-norm.gguf")
+    shutil.copy(src, path)
+    off, typ, dims = gguf_tensor_data(path)["output_norm.weight"]
+    assert typ == 0 and dims == [TINY["n_embd"]]
+    with open(path, "r+b") as f:
+        f.seek(off)
+        f.write(np.full(TINY["n_embd"], np.nan, np.float32).tobytes())
+    say("NaN logits", mode)
+    prompt = minfer.prompt_ids(7, 12, TINY["n_vocab"])
+    eng = minfer.Engine(path, max_ctx=64, stop_eos=0, **mode)
+    orc = O.Model(path, O.MODE_Q8ACT, plan=plan_of(eng), max_seq=64)
+    rt, _, _, _ = orc.generate(prompt, 6)
+    assert rt == [0] * 6
+    first, _ = eng.prefill(prompt)
+    toks, _ = eng.generate(6)
+    assert first == 0 and toks == rt
+    a, _ = eng.step([0, 3, 5], len(prompt) + len(toks) - 1)     # generate's first token is the prefill's
+    assert a == [0, 0, 0]
+    eng.close()
+
+
 REAL_TYPES = [
     pytest.param(dict(head_type=minfer.GT_Q6_K, down_type=minfer.GT_Q4_1, emb_type=minfer.GT_Q8_0), id="q6k-head-q41-down-q8-emb"),
     pytest.param(dict(tied=True), id="tied-f32-emb"),
