@@ -192,7 +192,7 @@ def verify_cost(reps=10):
                 note="T=8 = current token + 7 drafts (TMAX 8, mega.cu:50); the config's 8 drafts + 1 would be T=9")
 
 
-def attention_depth(torch, lengths=(512, 4096, 16384, 32768), layers=28, reps=3):
+def attention_depth(torch, lengths=(512, 4096, 16384, 32768), layers=28, reps=3, graph=True):
     """config3: S15 split-KV decode attention (12/2 heads, hd 128), one query, fp16 K/V
     N(0,1) at context L, rotated over 28 layers' caches (28 x 32 MB at L = 32768 > the
     256 MB MALL), the 28 launches replayed from a graph. Algorithmic bytes per layer:
@@ -210,20 +210,28 @@ def attention_depth(torch, lengths=(512, 4096, 16384, 32768), layers=28, reps=3)
             minfer.attn_decode(q, kc[l], vc[l], nh, nkv, hd, L, L, scale, scratch, out)
         # the layers' launches replayed from a captured graph (ctypes launches from
         # Python would leave the GPU idle between the short kernels); the kernel's
-        # counters return to zero by themselves, so replays need no reset
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g):
+        # counters return to zero by themselves, so replays need no reset. graph=False
+        # (for kernel traces, which time each launch themselves): eager launches.
+        def layer_loop():
             for l in range(layers):
                 minfer.attn_decode(q, kc[l], vc[l], nh, nkv, hd, L, L, scale, scratch, out)
-        ref = torch.empty_like(out)
-        minfer.attn_decode(q, kc[layers - 1], vc[layers - 1], nh, nkv, hd, L, L, scale, scratch, ref)
-        g.replay()
-        torch.cuda.synchronize()
-        assert torch.equal(out.view(torch.int32), ref.view(torch.int32)), "graph replay differs from the eager launch"
+        g = None
+        if graph:
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                layer_loop()
+            ref = torch.empty_like(out)
+            minfer.attn_decode(q, kc[layers - 1], vc[layers - 1], nh, nkv, hd, L, L, scale, scratch, ref)
+            g.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(out.view(torch.int32), ref.view(torch.int32)), "graph replay differs from the eager launch"
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record()
         for _ in range(reps):
-            g.replay()
+            if g is not None:
+                g.replay()
+            else:
+                layer_loop()
         e1.record()
         torch.cuda.synchronize()
         del g
@@ -265,11 +273,13 @@ def main():
     ap.add_argument("--attention-only", type=str, default="", metavar="L[,L...]",
                     help="only run the config3 attention-at-depth measurement at these context "
                          "lengths, print its JSON and exit")
+    ap.add_argument("--eager", action="store_true",
+                    help="with --attention-only: launch eagerly instead of replaying a graph (for kernel traces)")
     args = ap.parse_args()
     if args.attention_only:
         import torch
         lens = tuple(int(x) for x in args.attention_only.split(","))
-        res = attention_depth(torch, lengths=lens)
+        res = attention_depth(torch, lengths=lens, graph=not args.eager)
         for a in res:
             log("attention L=%-6d %8.2f us/layer  %7.1f GB/s" % (a["L"], a["us_per_layer"], a["gbps"]))
         print(json.dumps({"attention_depth": res}), flush=True)
