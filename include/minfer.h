@@ -120,6 +120,26 @@ typedef int (*mi_token_cb)(int32_t id, void* user);
 int mi_generate(mi_engine* e, int32_t n_gen, int32_t* out, float* margins, int32_t* n_out,
                 mi_token_cb cb, void* user);
 
+/* Teacher forcing: the TEACHER=<k> mode of mega.cu:28-29, 596, 857-862, 1192-1205. Runs
+ * ids[0..n) as the context at positions 0..n-1 (from an empty cache) in chunks of
+ * opts.tchunk tokens, as mi_prefill does, and returns every position's greedy
+ * prediction: pred[i], margin[i] = the argmax (lowest index on ties) and best - second
+ * after position i, i.e. the prediction for position i+1. The caller compares
+ * pred[i] with ids[i+1] for the positions past its prompt (the reference's "top-1
+ * agreement"). Leaves the context at length n. */
+int mi_teacher(mi_engine* e, const int32_t* ids, int32_t n, int32_t* pred, float* margin);
+
+/* The reference's exactness hash of a teacher-forced run (mega.cu:1197-1201): FNV-1a 64
+ * over, for i = 0..n-1, the 4 little-endian bytes of pred[i] then the 4 of margin[i]'s
+ * bit pattern, from the reference's offset basis 1469598103934665603 (mega.cu:1197;
+ * the published FNV basis is 14695981039346656037). Runs with different chunk sizes
+ * give the same hash exactly when every prediction and margin is bit-identical. */
+uint64_t mi_pred_hash(const int32_t* pred, const float* margin, int32_t n);
+/* FNV-1a 64 of n bytes from offset basis `basis` (prime 1099511628211): the building
+ * block of mi_pred_hash, exported so the published FNV vectors can pin it. No reference
+ * counterpart. */
+uint64_t mi_fnv1a64(const void* data, size_t n, uint64_t basis);
+
 /* Timing of the last mi_generate: device time of its decode steps measured with
  * HIP events on the engine stream (the reference prints the same figure,
  * mega.cu:1186-1190, cuda_infer.cu:1196-1199). */

@@ -22,7 +22,7 @@ HIP_FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-ffp-contra
 CXX_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-I", os.path.join(ROOT, "include"), "-I", SRC]
 
 HIP_SOURCES = ["kernels.hip", "engine.hip"]
-CXX_SOURCES = ["gguf.cpp", "synth.cpp", "spec.cpp", "detok.cpp"]
+CXX_SOURCES = ["gguf.cpp", "synth.cpp", "spec.cpp", "detok.cpp", "teacher.cpp"]
 
 
 def run(cmd):

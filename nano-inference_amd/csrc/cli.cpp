@@ -10,9 +10,16 @@
 // "N generation steps, X tokens/step | drafted D, accepted A (P%)").
 // Environment: RAWIDS, SPEC (n-gram speculative decode, output identical to greedy),
 // NG (longest n-gram drafted, default 3), PERSISTENT (0: one launch per phase), GRAPHS (1:
-// multi-token steps replay a HIP graph instead of launching kernel by kernel), DEVICE.
+// multi-token steps replay a HIP graph instead of launching kernel by kernel), TCHUNK
+// (prompt tokens per step, 1..8), DEVICE, and TEACHER=<k> (mega.cu:28-29, 1192-1205): the
+// ids are a reference sequence whose first k are the prompt; every position is predicted
+// under teacher forcing, and stderr gets the mismatches past the prompt and the line
+// "teacher-forced top-1 agreement: A/T | P positions in X ms (Y ms per C-token step) |
+// logit hash H" (H: the FNV-1a hash of all predictions and margins, equal across TCHUNK
+// exactly when the runs are bit-identical); MARGINS=1 adds every "i:token:margin".
 #include "minfer.h"
 
+#include <chrono>
 #include <cstdio>
 #include <cstdlib>
 #include <vector>
@@ -76,12 +83,42 @@ int main(int argc, char** argv) {
     o.persistent = env_int("PERSISTENT", o.persistent);
     o.device = env_int("DEVICE", o.device);
     o.graphs = env_int("GRAPHS", o.graphs);
+    o.tchunk = env_int("TCHUNK", o.tchunk);
     o.stop_eos = raw ? 0 : 1;
+    const int teacher = env_int("TEACHER", 0);
 
     mi_engine* e = nullptr;
     if (int rc = mi_load(argv[1], &o, &e)) return fail(e, "load", rc);
     mi_model_info info;
     mi_info(e, &info);
+
+    if (teacher > 0) {
+        const int P = (int)ids.size();
+        std::vector<int32_t> pred(P);
+        std::vector<float> mg(P);
+        const auto t0 = std::chrono::steady_clock::now();
+        if (int rc = mi_teacher(e, ids.data(), P, pred.data(), mg.data())) return fail(e, "teacher", rc);
+        const double ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+        int agree = 0, total = 0;
+        for (int i = teacher - 1; i + 1 < P; i++, total++) {
+            if (pred[i] == ids[i + 1]) {
+                agree++;
+                continue;
+            }
+            std::fprintf(stderr, "  pos %d: ref %d, minfer-hip %d (margin %.4f)\n", i + 1, ids[i + 1], pred[i], mg[i]);
+        }
+        std::printf("\n");
+        std::fflush(stdout);
+        std::fprintf(stderr,
+                     "teacher-forced top-1 agreement: %d/%d | %d positions in %.1f ms (%.2f ms per %d-token step) | "
+                     "logit hash %016llx\n",
+                     agree, total, P, ms, ms * o.tchunk / P, o.tchunk,
+                     (unsigned long long)mi_pred_hash(pred.data(), mg.data(), P));
+        if (env_int("MARGINS", 0))
+            for (int i = 0; i < P; i++) std::fprintf(stderr, "%d:%d:%.4f%c", i, pred[i], mg[i], i + 1 < P ? ' ' : '\n');
+        mi_free(e);
+        return 0;
+    }
 
     int32_t first = 0;
     if (int rc = mi_prefill(e, ids.data(), (int32_t)ids.size(), &first, nullptr)) return fail(e, "prefill", rc);

@@ -679,6 +679,36 @@ int mi_prefill(mi_engine* e, const int32_t* ids, int32_t n, int32_t* first, floa
     return MI_OK;
 }
 
+// Teacher forcing (mega.cu:857-862): the prefill's chunks over the whole sequence; every
+// step writes its positions' argmax and margin to out_tok / out_margin, which are read
+// back at the end. No step feeds its prediction forward (ids are the context).
+int mi_teacher(mi_engine* e, const int32_t* ids, int32_t n, int32_t* pred, float* margin) {
+    if (!e || !ids || !pred || !margin || n < 1) return MI_ERR_ARG;
+    if (n > e->maxseq) return set_err(e, MI_ERR_ARG, "teacher sequence of %d tokens exceeds the context capacity %d", n, e->maxseq);
+    for (int i = 0; i < n; i++)
+        if (ids[i] < 0 || ids[i] >= e->V) return set_err(e, MI_ERR_ARG, "teacher token %d out of range", ids[i]);
+    HIPCHK(e, hipMemcpyAsync(e->M.tokbuf, ids, sizeof(int32_t) * n, hipMemcpyHostToDevice, e->stream));
+    bool ran_single = false;
+    for (int p = 0; p < n;) {
+        const int T = std::min(e->opts.tchunk, n - p);
+        if (T == 1) {
+            if (int rc = run_step(e, p, 0, false)) return rc;
+            ran_single = true;
+        } else {
+            if (int rc = run_multi(e, p, T, false)) return rc;
+        }
+        p += T;
+    }
+    HIPCHK(e, hipMemcpyAsync(pred, e->M.out_tok, sizeof(int32_t) * n, hipMemcpyDeviceToHost, e->stream));
+    HIPCHK(e, hipMemcpyAsync(margin, e->M.out_margin, sizeof(float) * n, hipMemcpyDeviceToHost, e->stream));
+    HIPCHK(e, hipStreamSynchronize(e->stream));
+    if (ran_single)
+        if (int rc = check_barrier(e)) return rc == kRetry ? mi_teacher(e, ids, n, pred, margin) : rc;
+    e->cur_len = n;
+    e->next_ready = false;
+    return MI_OK;
+}
+
 }  // extern "C"
 
 // T tokens already in tokbuf[pos..pos+T-1]: one step, predictions back to the host

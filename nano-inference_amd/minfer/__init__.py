@@ -87,6 +87,9 @@ SIGNATURES = {
     "mi_best_draft_len": (C.c_int32, [C.c_float, C.c_float, C.c_int32]),
     "mi_token_text": (C.c_int32, [_P, C.c_int32, C.c_char_p, C.c_int32]),
     "mi_detok_piece": (C.c_int32, [C.c_char_p, C.c_int32, C.c_char_p, C.c_int32]),
+    "mi_teacher": (C.c_int, [_P, C.POINTER(C.c_int32), C.c_int32, C.POINTER(C.c_int32), C.POINTER(C.c_float)]),
+    "mi_pred_hash": (C.c_uint64, [C.POINTER(C.c_int32), C.POINTER(C.c_float), C.c_int32]),
+    "mi_fnv1a64": (C.c_uint64, [C.c_char_p, C.c_size_t, C.c_uint64]),
 }
 
 _lib = None
@@ -135,6 +138,18 @@ def synth_gguf(path, shape, seed, rope_base=1e6, rms_eps=1e-6, emb_q4=False, emb
                    rope_base, rms_eps, et, head_type, down_type, 1 if tied else 0)
     _check(lib().mi_synth_gguf(path.encode(), C.byref(s), C.c_uint64(seed)))
     return path
+
+
+def pred_hash(pred, margin):
+    """the reference's exactness hash of a teacher-forced run (mi_pred_hash)"""
+    n = len(pred)
+    assert len(margin) == n
+    return lib().mi_pred_hash(_i32(pred), (C.c_float * max(n, 1))(*margin), n)
+
+
+def fnv1a64(data, basis=14695981039346656037):
+    """FNV-1a 64 of a bytes object from `basis` (mi_fnv1a64; default: the published basis)"""
+    return lib().mi_fnv1a64(data, len(data), basis)
 
 
 def default_opts(**kw):
@@ -203,6 +218,14 @@ class Engine:
             l = np.frombuffer(lg, dtype=np.float32).copy()
             return a, m, (l.reshape(T, -1) if many else l)
         return a, m
+
+    def teacher(self, ids):
+        """Teacher-forced predictions over ids (mi_teacher): pred[i], margin[i] = the
+        greedy prediction after position i (for position i+1) and its margin."""
+        n = len(ids)
+        pred, mg = (C.c_int32 * n)(), (C.c_float * n)()
+        _check(lib().mi_teacher(self._h, _i32(ids), n, pred, mg), self._h)
+        return list(pred), list(mg)
 
     def debug_flag_barrier(self):
         """raise the barrier error flag from the host (test hook of the launch-mode fallback)"""

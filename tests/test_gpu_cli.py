@@ -107,3 +107,29 @@ def test_chunked_prefill_equals_single_steps(persistent):
         res[tchunk] = (first, int(bits(mg)), a, int(bits(m)), bits(lg).tobytes(), toks, bits(mgs).tobytes())
         say("tchunk %d: prefill %.2f ms" % (tchunk, st["prefill_ms"]))
     assert res[3] == res[1] and res[8] == res[1]
+
+
+def test_cli_teacher_mode():
+    """TEACHER=<k> (mega.cu:28-29, 1192-1205): the summary line with the top-1 agreement
+    and the exactness hash, the same hash for every TCHUNK and equal to mi_pred_hash of
+    the engine's own teacher-forced predictions; fed the engine's greedy stream, the
+    agreement past the prompt is total."""
+    path = synth_cached("eng-256", TINY, 7)
+    prompt = minfer.prompt_ids(9, 10, TINY["n_vocab"])
+    toks, _, _ = engine_stream(path, prompt, 24)
+    seq = list(prompt) + toks
+    eng = minfer.Engine(path, max_ctx=len(seq) + 16)
+    pred, mg = eng.teacher(seq)
+    eng.close()
+    want = minfer.pred_hash(pred, mg)
+    pat = re.compile(r"teacher-forced top-1 agreement: (\d+)/(\d+) \| (\d+) positions in [\d.]+ ms "
+                     r"\([\d.]+ ms per (\d+)-token step\) \| logit hash ([0-9a-f]{16})")
+    for tchunk in (1, 4, 8):
+        say("cli teacher tchunk", tchunk)
+        out, err = run_cli(path, 0, seq, TEACHER=len(prompt), TCHUNK=tchunk)
+        m = pat.search(err)
+        assert m, err
+        agree, total, npos, chunk, hsh = int(m.group(1)), int(m.group(2)), int(m.group(3)), int(m.group(4)), m.group(5)
+        assert (agree, total, npos, chunk) == (len(seq) - len(prompt), len(seq) - len(prompt), len(seq), tchunk)
+        assert int(hsh, 16) == want
+        assert out.strip() == b""

@@ -191,6 +191,45 @@ def test_nan_logits_give_token_zero(tmp_path, mode):
     eng.close()
 
 
+@pytest.mark.parametrize("shape,seed", [(TINY, 7), (SMALL, 21)])
+def test_teacher_forcing_exact(shape, seed):
+    """Teacher forcing (mega.cu:857-862, 1192-1205): every position's prediction and
+    margin bit-identical to the q8act oracle fed the same ids; the exactness hash the same
+    for prompt chunks of 1, 3 and 8 tokens in both step modes; fed the engine's own
+    greedy continuation, the top-1 agreement past the prompt is total."""
+    path = synth_cached("eng-%d" % shape["n_embd"], shape, seed)
+    V = shape["n_vocab"]
+    seq = minfer.prompt_ids(seed + 1, 45, V)
+    say("teacher", path)
+    runs = {}
+    plan = None
+    for persistent in (1, 0):
+        for tchunk in (1, 3, 8):
+            eng = minfer.Engine(path, max_ctx=128, persistent=persistent, tchunk=tchunk)
+            plan = plan_of(eng)
+            runs[(persistent, tchunk)] = eng.teacher(seq)
+            eng.close()
+    pred, mg = runs[(1, 8)]
+    h = minfer.pred_hash(pred, mg)
+    for key, (p2, m2) in runs.items():
+        assert p2 == pred, key
+        assert np.array_equal(np.float32(m2).view(np.uint32), np.float32(mg).view(np.uint32)), key
+        assert minfer.pred_hash(p2, m2) == h, key
+    orc = O.Model(path, O.MODE_Q8ACT, plan=plan, max_seq=128)
+    for i, tok in enumerate(seq):
+        a, m = orc.forward(tok, i)
+        assert a == pred[i] and np.float32(m).view(np.uint32) == np.float32(mg[i]).view(np.uint32), i
+    # the engine's own greedy stream as the reference sequence: all predictions agree
+    eng = minfer.Engine(path, max_ctx=128)
+    k = 12
+    eng.prefill(seq[:k])
+    toks, _ = eng.generate(30)
+    ref = list(seq[:k]) + toks
+    p3, _ = eng.teacher(ref)
+    eng.close()
+    assert all(p3[i] == ref[i + 1] for i in range(k - 1, len(ref) - 1))
+
+
 REAL_TYPES = [
     pytest.param(dict(head_type=minfer.GT_Q6_K, down_type=minfer.GT_Q4_1, emb_type=minfer.GT_Q8_0), id="q6k-head-q41-down-q8-emb"),
     pytest.param(dict(tied=True), id="tied-f32-emb"),

@@ -139,3 +139,30 @@ def test_engine_load_reports_errors(tmp_path):
     else:
         assert ei.value.code == -3
     del n, C_int
+
+
+def test_fnv1a64_published_vectors():
+    """the FNV-1a 64 step (offset basis 14695981039346656037, prime 1099511628211):
+    published test vectors of the FNV authors"""
+    assert minfer.fnv1a64(b"") == 0xcbf29ce484222325
+    assert minfer.fnv1a64(b"a") == 0xaf63dc4c8601ec8c
+    assert minfer.fnv1a64(b"foobar") == 0x85944171f73967e8
+
+
+def test_pred_hash_byte_layout():
+    """mi_pred_hash = FNV-1a over (token, margin bits) little-endian per position from the
+    reference's basis 1469598103934665603 (mega.cu:1197-1201); one changed margin bit or
+    two swapped positions change it"""
+    rng = np.random.default_rng(5)
+    pred = rng.integers(0, 151936, 37).astype(np.int32)
+    margin = rng.standard_normal(37).astype(np.float32)
+    stream = np.stack([pred.astype("<i4").view("<u4"), margin.astype("<f4").view("<u4")], axis=1).tobytes()
+    h = minfer.pred_hash(list(pred), list(margin))
+    assert h == minfer.fnv1a64(stream, 1469598103934665603)
+    assert minfer.pred_hash([], []) == 1469598103934665603
+    m2 = margin.copy()
+    m2.view(np.uint32)[3] ^= 1
+    assert minfer.pred_hash(list(pred), list(m2)) != h
+    p2 = pred.copy()
+    p2[[4, 5]] = p2[[5, 4]]
+    assert minfer.pred_hash(list(p2), list(margin)) != h
