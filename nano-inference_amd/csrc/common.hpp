@@ -80,6 +80,11 @@ struct DModel {
     int32_t* err;                  // set when a grid barrier times out
     int32_t* out_tok;              // [maxseq] prediction made at each position
     float* out_margin;             // [maxseq]
+    // streaming generation (k_step launched with gen = kGenRing): each launch also writes
+    // its (token, margin bits) as one 64-bit word to ring[pos], pinned host memory the
+    // host polls while later launches run (mega.cu:847-856, 1165-1178)
+    uint64_t* ring;                // [maxseq] device address of the mapped host ring
+    int32_t eos;                   // the GGUF's eos token: a kGenRing launch whose input is eos does nothing
     // multi-token steps (T <= kMaxT tokens at positions pos..pos+T-1, one launch per
     // phase): per-token copies of the exchange buffers, token index after the segment
     int32_t* posT;                 // [1] position of the step's first token (set before each launch sequence)
@@ -95,5 +100,13 @@ struct DModel {
 };
 
 inline __host__ __device__ size_t tile_bytes(int cb) { return (size_t)cb * 1152; }
+
+// k_step's gen argument: 0 = the prediction is only recorded (prefill, teacher, mi_step);
+// 1 = it is also the next position's input token; kGenRing = as 1, plus the ring entry,
+// and the step does nothing when its input token is eos (generation stopped there)
+constexpr int kGenRing = 2;
+// ring words: low 32 bits the token, high 32 the margin's bit pattern
+constexpr uint64_t kRingEmpty = ~0ull;                    // not written yet (token -1)
+constexpr uint64_t kRingFail = 0x00000000FFFFFFFEull;     // token -2: a grid barrier of that launch failed
 
 }  // namespace mi

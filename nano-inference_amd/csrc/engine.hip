@@ -20,6 +20,7 @@
 #include <cstring>
 #include <memory>
 #include <string>
+#include <thread>
 #include <vector>
 
 using namespace mi;
@@ -49,6 +50,7 @@ struct mi_engine {
     int nwg_persistent = 0;       // workgroups of the persistent step kernel (0: per-phase launches)
     bool coop = false;            // launch it cooperatively (after a plain launch's barrier failed)
     int32_t* h_iota = nullptr;    // pinned host memory, h_iota[p] = p: the source of posT
+    uint64_t* h_ring = nullptr;   // pinned, device-mapped host memory [maxseq]: streamed tokens (DModel::ring)
     hipGraphExec_t gexec[2][kMaxT + 1] = {};   // multi-token step per (logits, T), captured on first use
     int cur_len = 0;              // positions holding valid K/V
     bool next_ready = false;      // tokbuf[cur_len] holds the prediction of the last step
@@ -59,6 +61,7 @@ struct mi_engine {
             for (hipGraphExec_t g : row)
                 if (g) (void)hipGraphExecDestroy(g);
         if (h_iota) (void)hipHostFree(h_iota);
+        if (h_ring) (void)hipHostFree(h_ring);
         for (void* p : allocs) (void)hipFree(p);
         if (ev0) (void)hipEventDestroy(ev0);
         if (ev1) (void)hipEventDestroy(ev1);
@@ -467,6 +470,12 @@ static int load_impl(mi_engine* e, const char* path) {
     M.logits = nullptr;
     M.logitsT = nullptr;
     M.prof = nullptr;
+    // the token ring of streaming generation: fine-grained (coherent) pinned host memory,
+    // so the host sees each launch's system-scope store as soon as it lands
+    HIPCHK(e, hipHostMalloc((void**)&e->h_ring, sizeof(uint64_t) * (size_t)e->maxseq,
+                            hipHostMallocMapped | hipHostMallocCoherent));
+    HIPCHK(e, hipHostGetDevicePointer((void**)&M.ring, e->h_ring, 0));
+    M.eos = e->eos;
     e->M_logits = M;
     if ((rc = alloc_buf(e, &e->M_logits.logits, (size_t)e->V))) return rc;
     if ((rc = alloc_buf(e, &e->M_logits.logitsT, TM * e->V))) return rc;
@@ -597,6 +606,133 @@ static int check_barrier(mi_engine* e) {
         }
         return set_err(e, MI_ERR_DEVICE, "grid barrier timed out under a cooperative launch");
     }
+    return MI_OK;
+}
+
+// Generation that hands each token over as it is made (a callback, or a stop at eos),
+// from token t0 on: one step, then its token fetched and delivered. Token t is the
+// prediction at position p0 + t - 1 (t = 0: the prefill's). `steps0` steps already ran.
+static int generate_sync(mi_engine* e, int p0, int t0, int steps0, int n_gen, int32_t* out, float* margins,
+                         int32_t* n_out, mi_token_cb cb, void* user) {
+    auto fetch = [&](int pos, int32_t* t, float* m) -> int {
+        HIPCHK(e, hipMemcpyAsync(t, e->M.out_tok + pos, 4, hipMemcpyDeviceToHost, e->stream));
+        HIPCHK(e, hipMemcpyAsync(m, e->M.out_margin + pos, 4, hipMemcpyDeviceToHost, e->stream));
+        HIPCHK(e, hipStreamSynchronize(e->stream));
+        return MI_OK;
+    };
+    if (t0 == 0) HIPCHK(e, hipEventRecord(e->ev0, e->stream));
+    int emitted = t0, steps = steps0;
+    for (int t = t0; t < n_gen; t++) {
+        if (t > 0) {
+            const int rc = run_step(e, p0 + t - 1, 1, false);
+            if (rc) return rc;
+            steps++;
+        }
+        int32_t tok; float m;
+        int rc = fetch(p0 + t - 1, &tok, &m);
+        if (rc) return rc;
+        if (t > 0 && (rc = check_barrier(e))) {
+            if (rc != kRetry) return rc;
+            if ((rc = run_step(e, p0 + t - 1, 1, false)) || (rc = fetch(p0 + t - 1, &tok, &m))) return rc;
+            if ((rc = check_barrier(e))) return rc == kRetry ? MI_ERR_DEVICE : rc;
+        }
+        if (out) out[t] = tok;
+        if (margins) margins[t] = m;
+        emitted++;
+        if ((cb && cb(tok, user)) || (e->opts.stop_eos && tok == e->eos)) break;
+    }
+    HIPCHK(e, hipEventRecord(e->ev1, e->stream));
+    HIPCHK(e, hipStreamSynchronize(e->stream));
+    float ms = 0.f;
+    HIPCHK(e, hipEventElapsedTime(&ms, e->ev0, e->ev1));
+    e->stats.decode_ms = ms;
+    e->stats.steps = e->stats.tokens = steps;
+    e->cur_len = p0 + steps;
+    if (n_out) *n_out = emitted;
+    return MI_OK;
+}
+
+// Streaming generation with the persistent step (mega.cu:847-856, 1165-1178): the steps
+// go out up to kRingAhead launches ahead of the tokens the host has delivered; each
+// writes its token and margin to the mapped host ring (one 64-bit word at ring[pos]),
+// which the host polls, so no step waits for the host. A stop (the callback, or eos)
+// leaves at most kRingAhead - 1 queued steps to run past it; after an eos they return
+// at once (k_step passes the eos on). Their K/V rows lie past the context length the
+// call leaves, so nothing reads them. A ring entry kRingFail (a grid barrier of that
+// launch gave up) is never delivered: the launches drain, the barrier state is reset,
+// and the rest runs through generate_sync with cooperative launches.
+constexpr int kRingAhead = 8;
+static int generate_ring(mi_engine* e, int n_gen, int32_t* out, float* margins, int32_t* n_out, mi_token_cb cb,
+                         void* user) {
+    const int p0 = e->cur_len;
+    if (n_gen == 0) {
+        if (n_out) *n_out = 0;
+        e->stats.steps = e->stats.tokens = 0;
+        e->stats.decode_ms = 0;
+        return MI_OK;
+    }
+    int32_t tok = 0;
+    float m = 0.f;
+    HIPCHK(e, hipMemcpyAsync(&tok, e->M.out_tok + p0 - 1, 4, hipMemcpyDeviceToHost, e->stream));
+    HIPCHK(e, hipMemcpyAsync(&m, e->M.out_margin + p0 - 1, 4, hipMemcpyDeviceToHost, e->stream));
+    HIPCHK(e, hipStreamSynchronize(e->stream));
+    for (int p = p0; p < p0 + n_gen - 1; p++) __atomic_store_n(e->h_ring + p, kRingEmpty, __ATOMIC_RELAXED);
+    HIPCHK(e, hipEventRecord(e->ev0, e->stream));
+    int emitted = 0, got = 0, enq = 0;
+    bool stop = false, failed = false;
+    auto deliver = [&](int32_t t, float mg) {
+        if (out) out[emitted] = t;
+        if (margins) margins[emitted] = mg;
+        emitted++;
+        if ((cb && cb(t, user)) || (e->opts.stop_eos && t == e->eos)) stop = true;
+    };
+    deliver(tok, m);
+    auto last = std::chrono::steady_clock::now();
+    while (!stop && got < n_gen - 1) {
+        for (; enq < n_gen - 1 && enq < got + kRingAhead; enq++)
+            if (int rc = run_step(e, p0 + enq, kGenRing, false)) return rc;
+        const uint64_t w = __atomic_load_n(e->h_ring + p0 + got, __ATOMIC_ACQUIRE);
+        if (w == kRingEmpty) {
+            const hipError_t q = hipStreamQuery(e->stream);
+            if (q == hipSuccess) {
+                // the stream is idle: the entry is there now, or no launch will write it
+                if (__atomic_load_n(e->h_ring + p0 + got, __ATOMIC_ACQUIRE) != kRingEmpty) continue;
+                return set_err(e, MI_ERR_DEVICE, "streaming generate: no token for position %d", p0 + got);
+            }
+            if (q != hipErrorNotReady) return set_err(e, MI_ERR_DEVICE, "hipStreamQuery: %s", hipGetErrorString(q));
+            if (std::chrono::steady_clock::now() - last > std::chrono::seconds(30))
+                return set_err(e, MI_ERR_DEVICE, "streaming generate: no token for 30 s");
+            std::this_thread::sleep_for(std::chrono::microseconds(20));
+            continue;
+        }
+        if (w == kRingFail) {
+            failed = true;
+            break;
+        }
+        last = std::chrono::steady_clock::now();
+        got++;
+        const uint32_t mb = (uint32_t)(w >> 32);
+        float mg;
+        std::memcpy(&mg, &mb, 4);
+        deliver((int32_t)(uint32_t)w, mg);
+    }
+    HIPCHK(e, hipEventRecord(e->ev1, e->stream));
+    HIPCHK(e, hipStreamSynchronize(e->stream));
+    if (failed) {
+        const int rc = check_barrier(e);
+        if (rc != kRetry) return rc ? rc : set_err(e, MI_ERR_DEVICE, "streaming generate: failed step at %d", p0 + got);
+        // positions before p0 + got are good and tokbuf[p0 + got] holds their last token
+        return generate_sync(e, p0, got + 1, got, n_gen, out, margins, n_out, cb, user);
+    }
+    // a barrier that gave up only at a launch's last barrier (after its results were
+    // complete) still leaves the flag: reset it (the delivered tokens are right)
+    if (int rc = check_barrier(e); rc && rc != kRetry) return rc;
+    float ms = 0.f;
+    HIPCHK(e, hipEventElapsedTime(&ms, e->ev0, e->ev1));
+    e->stats.decode_ms = ms;
+    e->stats.steps = e->stats.tokens = got;
+    e->cur_len = p0 + got;
+    if (n_out) *n_out = emitted;
     return MI_OK;
 }
 
@@ -801,65 +937,34 @@ int mi_generate(mi_engine* e, int32_t n_gen, int32_t* out, float* margins, int32
     e->stats.drafted = e->stats.accepted = 0;
     const int p0 = e->cur_len;                   // position of the first generated token
     const bool sync_each = cb != nullptr || e->opts.stop_eos;
-    int emitted = 0;
-    auto fetch = [&](int pos, int32_t* t, float* m) -> int {
-        HIPCHK(e, hipMemcpyAsync(t, e->M.out_tok + pos, 4, hipMemcpyDeviceToHost, e->stream));
-        HIPCHK(e, hipMemcpyAsync(m, e->M.out_margin + pos, 4, hipMemcpyDeviceToHost, e->stream));
-        HIPCHK(e, hipStreamSynchronize(e->stream));
-        return MI_OK;
-    };
+    if (sync_each && e->nwg_persistent) return generate_ring(e, n_gen, out, margins, n_out, cb, user);
+    if (sync_each) return generate_sync(e, p0, 0, 0, n_gen, out, margins, n_out, cb, user);
     HIPCHK(e, hipEventRecord(e->ev0, e->stream));
     int steps = 0;
-    if (!sync_each) {
-        for (int t = 1; t < n_gen; t++, steps++) {
-            const int rc = run_step(e, p0 + t - 1, 1, false);
-            if (rc) return rc;
-        }
-        HIPCHK(e, hipEventRecord(e->ev1, e->stream));
-        std::vector<int32_t> tk(n_gen > 0 ? n_gen : 1);
-        std::vector<float> mg(n_gen > 0 ? n_gen : 1);
-        if (n_gen > 0) {
-            HIPCHK(e, hipMemcpyAsync(tk.data(), e->M.out_tok + p0 - 1, sizeof(int32_t) * n_gen, hipMemcpyDeviceToHost, e->stream));
-            HIPCHK(e, hipMemcpyAsync(mg.data(), e->M.out_margin + p0 - 1, sizeof(float) * n_gen, hipMemcpyDeviceToHost, e->stream));
-        }
-        HIPCHK(e, hipStreamSynchronize(e->stream));
-        if (int rc = check_barrier(e))   // the launches only wrote positions p0.. and tokbuf[p0+1..]
-            return rc == kRetry ? mi_generate(e, n_gen, out, margins, n_out, cb, user) : rc;
-        for (int t = 0; t < n_gen; t++) {
-            if (out) out[t] = tk[t];
-            if (margins) margins[t] = mg[t];
-        }
-        emitted = n_gen;
-    } else {
-        for (int t = 0; t < n_gen; t++) {
-            if (t > 0) {
-                const int rc = run_step(e, p0 + t - 1, 1, false);
-                if (rc) return rc;
-                steps++;
-            }
-            int32_t tok; float m;
-            int rc = fetch(p0 + t - 1, &tok, &m);
-            if (rc) return rc;
-            if (t > 0 && (rc = check_barrier(e))) {
-                if (rc != kRetry) return rc;
-                if ((rc = run_step(e, p0 + t - 1, 1, false)) || (rc = fetch(p0 + t - 1, &tok, &m))) return rc;
-                if ((rc = check_barrier(e))) return rc == kRetry ? MI_ERR_DEVICE : rc;
-            }
-            if (out) out[t] = tok;
-            if (margins) margins[t] = m;
-            emitted++;
-            if ((cb && cb(tok, user)) || (e->opts.stop_eos && tok == e->eos)) break;
-        }
-        HIPCHK(e, hipEventRecord(e->ev1, e->stream));
-        HIPCHK(e, hipStreamSynchronize(e->stream));
+    for (int t = 1; t < n_gen; t++, steps++) {
+        const int rc = run_step(e, p0 + t - 1, 1, false);
+        if (rc) return rc;
+    }
+    HIPCHK(e, hipEventRecord(e->ev1, e->stream));
+    std::vector<int32_t> tk(n_gen > 0 ? n_gen : 1);
+    std::vector<float> mg(n_gen > 0 ? n_gen : 1);
+    if (n_gen > 0) {
+        HIPCHK(e, hipMemcpyAsync(tk.data(), e->M.out_tok + p0 - 1, sizeof(int32_t) * n_gen, hipMemcpyDeviceToHost, e->stream));
+        HIPCHK(e, hipMemcpyAsync(mg.data(), e->M.out_margin + p0 - 1, sizeof(float) * n_gen, hipMemcpyDeviceToHost, e->stream));
+    }
+    HIPCHK(e, hipStreamSynchronize(e->stream));
+    if (int rc = check_barrier(e))   // the launches only wrote positions p0.. and tokbuf[p0+1..]
+        return rc == kRetry ? mi_generate(e, n_gen, out, margins, n_out, cb, user) : rc;
+    for (int t = 0; t < n_gen; t++) {
+        if (out) out[t] = tk[t];
+        if (margins) margins[t] = mg[t];
     }
     float ms = 0.f;
     HIPCHK(e, hipEventElapsedTime(&ms, e->ev0, e->ev1));
     e->stats.decode_ms = ms;
-    e->stats.steps = steps;
-    e->stats.tokens = steps;
+    e->stats.steps = e->stats.tokens = steps;
     e->cur_len = p0 + steps;
-    if (n_out) *n_out = emitted;
+    if (n_out) *n_out = n_gen;
     return MI_OK;
 }
 

@@ -453,17 +453,18 @@ constexpr int kBarWords = 64 * (kBarGroups + 2);
 // the barrier path)
 struct GridBar {
     uint32_t* arrive;          // this workgroup's group counter
-    const uint32_t* poll;      // the counter this lane polls (lanes >= groups: counter 0)
+    const uint32_t* poll;      // the word this lane polls (lanes >= groups: counter 0; lane 63: the error flag)
     unsigned per;              // arrivals per epoch on the polled counter (0: always met)
     unsigned need;             // this lane's target of the current epoch
     unsigned dead;             // a barrier of this launch failed: the rest do not wait
 };
-__device__ __forceinline__ GridBar bar_init(uint32_t* bar) {
+constexpr int kErrLane = 63;   // > kBarGroups: the lane that polls the error flag
+__device__ __forceinline__ GridBar bar_init(uint32_t* bar, const int32_t* err) {
     const int lane = threadIdx.x & 63, ng = min(kBarGroups, (int)gridDim.x);
     const bool mine = lane < ng;
     GridBar b;
     b.arrive = bar + 64 * ((int)blockIdx.x % ng);
-    b.poll = bar + 64 * (mine ? lane : 0);
+    b.poll = lane == kErrLane ? reinterpret_cast<const uint32_t*>(err) : bar + 64 * (mine ? lane : 0);
     b.per = mine ? gridDim.x / ng + ((int)(gridDim.x % ng) > lane ? 1u : 0u) : 0u;
     b.need = 0;
     b.dead = 0;
@@ -475,17 +476,19 @@ __device__ __forceinline__ void ctl_barrier(GridBar& b, int32_t* err) {
     const int lane = threadIdx.x & 63;
     b.need += b.per;
     if (lane == 0) __hip_atomic_fetch_add(b.arrive, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    // every lane loads and the exit test is one ballot: the loop is scalar control flow.
-    // Every 1024 polls the wave also reads *err: once any barrier of this launch (or of
-    // an earlier launch in the stream) has failed, nobody waits any more.
+    // every lane loads and the exit tests are ballots: the loop is scalar control flow.
+    // Lane kErrLane reads *err in the same round trip: once any barrier of this launch
+    // (or of an earlier launch in the stream) has failed, or the host raised the flag,
+    // nobody waits any more. A poll that runs kSpinLimit rounds raises it.
     for (unsigned spins = 1;; spins++) {
         const unsigned v = ldc(b.poll);
-        if (__builtin_amdgcn_ballot_w64((int)(v - b.need) < 0) == 0) break;
-        if ((spins & 1023u) == 0 && (spins >= kSpinLimit || ldc(reinterpret_cast<const uint32_t*>(err)) != 0)) {
+        const bool is_err = lane == kErrLane;
+        if (__builtin_amdgcn_ballot_w64(is_err && v != 0) != 0 || spins >= kSpinLimit) {
             if (lane == 0) stc(reinterpret_cast<uint32_t*>(err), 1u);
             b.dead = 1;
             break;
         }
+        if (__builtin_amdgcn_ballot_w64(!is_err && (int)(v - b.need) < 0) == 0) break;
     }
 }
 // after the launch's last barrier: each control wave counts itself out; the last one
@@ -735,8 +738,11 @@ __device__ __forceinline__ void gu_store(const PMat W, int wg, int nwg, int kw, 
 
 // ------------------------------------------------------------------ lm_head epilogue
 // workers: row values of the workgroup's vocab groups (logits when requested),
-// per-lane top-2, wave top-2 -> misc; control wave: the workgroup's candidate
-__device__ __forceinline__ void lm_epilogue(MPtr M, int wg, int nwg, const Lds& S, int wave, int lane) {
+// per-lane top-2, wave top-2 -> misc; control wave: the workgroup's candidate, and in
+// word 3 whether one of this launch's grid barriers gave up on this workgroup (`dead`,
+// the control wave's; its inputs may then be stale)
+__device__ __forceinline__ void lm_epilogue(MPtr M, int wg, int nwg, const Lds& S, int wave, int lane,
+                                            unsigned dead = 0) {
     if (wave > 0) {
         Top2 t{-__builtin_inff(), INT_MAX, -__builtin_inff()};
         wg_segments(ldmat(&M->lm), wg, nwg, wave - 1, [&](int g, int s, int k0, int k1) {
@@ -758,18 +764,23 @@ __device__ __forceinline__ void lm_epilogue(MPtr M, int wg, int nwg, const Lds& 
         stc(cd, a.best);
         stc(reinterpret_cast<uint32_t*>(cd + 1), (uint32_t)a.idx);
         stc(cd + 2, a.second);
+        stc(reinterpret_cast<uint32_t*>(cd + 3), dead);
     }
 }
 
 // merge of the workgroups' candidates by one wave (top-2 merging is associative and
-// commutative, so any order gives the same token and margin); result on every lane
-__device__ __forceinline__ Top2 wave_merge_cands(const float* cand, int n, int lane) {
+// commutative, so any order gives the same token and margin); result on every lane;
+// *failed: whether any workgroup reported a failed barrier
+__device__ __forceinline__ Top2 wave_merge_cands(const float* cand, int n, int lane, unsigned* failed = nullptr) {
     Top2 t{-__builtin_inff(), INT_MAX, -__builtin_inff()};
+    unsigned f = 0;
     for (int i = lane; i < n; i += 64) {
         const float* cd = cand + (size_t)i * 32;
         top2_merge(t, cd[0], __float_as_int(cd[1]), cd[2]);
+        f |= __float_as_uint(cd[3]);
     }
     top2_wave(t);
+    if (failed) *failed = __builtin_amdgcn_ballot_w64(f != 0) != 0;
     return t;
 }
 // The token of a merged top-2. Only when no logit compares greater than -inf (all NaN
@@ -777,11 +788,18 @@ __device__ __forceinline__ Top2 wave_merge_cands(const float* cand, int n, int l
 // cpu_infer.cpp:153-154 returns row 0 then, and so does this. (It also keeps the next
 // step's embedding gather, which reads row tokbuf[pos + 1], inside the table.)
 __device__ __forceinline__ int top2_token(const Top2& a, int V) { return (unsigned)a.idx < (unsigned)V ? a.idx : 0; }
-__device__ __forceinline__ void emit_token(MPtr M, const Top2& a, int pos, int gen) {
+__device__ __forceinline__ void emit_token(MPtr M, const Top2& a, int pos, int gen, unsigned failed = 0) {
     const int tok = top2_token(a, M->V);
+    const float margin = __fsub_rn(a.best, a.second);
     M->out_tok[pos] = tok;
-    M->out_margin[pos] = __fsub_rn(a.best, a.second);
+    M->out_margin[pos] = margin;
     if (gen) M->tokbuf[pos + 1] = tok;
+    if (gen == kGenRing) {
+        // one 64-bit vector store at system scope, through to the host's memory; a launch
+        // whose barrier failed reports that instead of its token
+        const uint64_t w = failed ? kRingFail : ((uint64_t)__float_as_uint(margin) << 32) | (uint32_t)tok;
+        __hip_atomic_store(M->ring + pos, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    }
 }
 
 // ------------------------------------------------------------------ attention
@@ -1141,7 +1159,17 @@ __global__ __launch_bounds__(kPThreads) void k_step(const DModel* Mp, int pos, i
     const bool ctl = wave == 0;
     const int kw = wave - 1;
     const int nch = (pos + 1 + kAttnChunk - 1) / kAttnChunk;
-    GridBar gb = bar_init(M->bar);
+    if (gen == kGenRing) {
+        // a streaming generation that stopped at eos: every workgroup sees the same input
+        // token and returns before any barrier; the eos is passed on, so the launches
+        // queued behind this one return too
+        const int in = M->tokbuf[pos];
+        if (in == M->eos) {
+            if (wg == 0 && threadIdx.x == 0) M->tokbuf[pos + 1] = in;
+            return;
+        }
+    }
+    GridBar gb = bar_init(M->bar, M->err);
     Tile tl[2];
     stamp(M, 0);
     stage(M, 0, PH_QKV, pos, S, wave, kPWaves, lane, true);
@@ -1167,7 +1195,7 @@ __global__ __launch_bounds__(kPThreads) void k_step(const DModel* Mp, int pos, i
         __syncthreads();
         stamp(M, sb + 1, 64);
         if (kind == PH_LM) {
-            lm_epilogue(M, wg, nwg, S, wave, lane);
+            lm_epilogue(M, wg, nwg, S, wave, lane, gb.dead);
             stamp(M, sb + 2);
             __syncthreads();
             stamp(M, sb + 3);
@@ -1176,8 +1204,9 @@ __global__ __launch_bounds__(kPThreads) void k_step(const DModel* Mp, int pos, i
                 ctl_exit(M->bar);
                 stamp(M, sb + 4);
                 if (wg == 0) {
-                    const Top2 a = wave_merge_cands(M->cand, nwg, lane);
-                    if (lane == 0) emit_token(M, a, pos, gen);
+                    unsigned failed;
+                    const Top2 a = wave_merge_cands(M->cand, nwg, lane, &failed);
+                    if (lane == 0) emit_token(M, a, pos, gen, failed);
                 }
             }
             return;
@@ -1218,7 +1247,7 @@ __global__ __launch_bounds__(kPThreads) void k_step(const DModel* Mp, int pos, i
 
 // barrier cost: n grid barriers and nothing else
 __global__ __launch_bounds__(kPThreads) void k_barriers(uint32_t* bar, int32_t* err, int n) {
-    GridBar gb = bar_init(bar);
+    GridBar gb = bar_init(bar, err);
     for (int i = 0; i < n; i++) {
         __syncthreads();
         if (threadIdx.x < 64) ctl_barrier(gb, err);

@@ -161,6 +161,104 @@ def gguf_tensor_data(path):
     return {n: (base + off, t, dims) for n, t, dims, off in infos}
 
 
+def gguf_kv_u32_offset(path, key):
+    """file offset of a u32 metadata value of a GGUF v3 file"""
+    import struct
+    with open(path, "rb") as f:
+        b = f.read()
+    o = [4]
+
+    def rd(fmt):
+        v = struct.unpack_from("<" + fmt, b, o[0])[0]
+        o[0] += struct.calcsize("<" + fmt)
+        return v
+
+    def rstr():
+        n = rd("Q")
+        o[0] += n
+        return b[o[0] - n:o[0]].decode()
+
+    sizes = {0: 1, 1: 1, 2: 2, 3: 2, 4: 4, 5: 4, 6: 4, 7: 1, 10: 8, 11: 8, 12: 8}
+
+    def skip(t):
+        if t == 8:
+            rstr()
+        elif t == 9:
+            et, n = rd("I"), rd("Q")
+            for _ in range(n):
+                skip(et)
+        else:
+            o[0] += sizes[t]
+
+    assert b[:4] == b"GGUF" and rd("I") == 3
+    _, nkv = rd("Q"), rd("Q")
+    for _ in range(nkv):
+        k, t = rstr(), rd("I")
+        if k == key:
+            assert t == 4
+            return o[0]
+        skip(t)
+    raise KeyError(key)
+
+
+def test_streaming_generate():
+    """Streaming generation (a callback or an eos stop: each step's token comes back
+    through the mapped host ring while later steps are already queued, mega.cu:847-856,
+    1165-1178) gives the batch path's tokens and margins; a callback stop after 5 tokens
+    and a second generate continue the same stream; an eos stop ends the output at the
+    eos and leaves the cache of the positions before it intact."""
+    import shutil
+    path = synth_cached("eng-512", SMALL, 21)
+    V = SMALL["n_vocab"]
+    ids = minfer.prompt_ids(17, 20, V)
+    ref = minfer.Engine(path, max_ctx=256)
+    ref.prefill(ids)
+    want, wm = ref.generate(40)
+    ref.close()
+    say("streaming: callback")
+    eng = minfer.Engine(path, max_ctx=256)
+    eng.prefill(ids)
+    seen = []
+    got, gm = eng.generate(40, callback=lambda t: seen.append(t) and False)
+    assert got == want and seen == want
+    assert np.array_equal(np.float32(gm).view(np.uint32), np.float32(wm).view(np.uint32))
+    eng.close()
+    say("streaming: callback stop and resume")
+    eng = minfer.Engine(path, max_ctx=256)
+    eng.prefill(ids)
+    seen = []
+    got1, _ = eng.generate(40, callback=lambda t: (seen.append(t), len(seen) >= 5)[1])
+    assert got1 == want[:5]
+    got2, _ = eng.generate(20)                 # its first token is the pending prediction
+    assert got2[0] == got1[-1] and got1 + got2[1:] == want[:24]
+    eng.close()
+    say("streaming: eos stop")
+    k = 7
+    first = want.index(want[k])                # the stream's first occurrence of that token
+    stop_path = os.path.join(os.path.dirname(path), "eos-stop.gguf")
+    shutil.copy(path, stop_path)
+    off = gguf_kv_u32_offset(stop_path, "tokenizer.ggml.eos_token_id")
+    with open(stop_path, "r+b") as f:
+        f.seek(off)
+        f.write(np.uint32(want[k]).tobytes())
+    eng = minfer.Engine(stop_path, max_ctx=256, stop_eos=1)
+    assert eng.info.eos == want[k]
+    eng.prefill(ids)
+    got, _ = eng.generate(40)
+    assert got == want[:first + 1]
+    # the positions before the stop hold the stream's K/V: one more step there gives
+    # the logits of the undisturbed engine at that position
+    pos = len(ids) + first
+    _, _, la = eng.step(want[first], pos, want_logits=True)
+    eng.close()
+    ref = minfer.Engine(path, max_ctx=256)
+    ref.prefill(ids)
+    ref.generate(first + 1)
+    _, _, lb = ref.step(want[first], pos, want_logits=True)
+    ref.close()
+    assert np.array_equal(la.view(np.uint32), lb.view(np.uint32))
+
+
 @pytest.mark.parametrize("mode", [dict(persistent=1), dict(persistent=0), dict(persistent=1, spec=1)],
                          ids=["persistent", "per-phase", "speculative"])
 def test_nan_logits_give_token_zero(tmp_path, mode):
