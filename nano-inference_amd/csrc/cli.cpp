@@ -140,9 +140,11 @@ int main(int argc, char** argv) {
     if (o.persistent && !after.persistent)
         std::fprintf(stderr, "minfer-hip: the persistent step was refused by the device (cooperative dispatch "
                              "busy); ran one launch per phase\n");
+    // the tokens the timed decode steps made (the first printed token is the prefill's),
+    // over their device time, as the reference's "n - 1 tok in ... ms" (mega.cu:1186-1190)
     const double ms = st.decode_ms;
-    std::fprintf(stderr, "minfer-hip decode: %d tok in %.1f ms = %.2f tok/s\n", sink.printed, ms,
-                 ms > 0 ? sink.printed * 1000.0 / ms : 0.0);
+    std::fprintf(stderr, "minfer-hip decode: %d tok in %.1f ms = %.2f tok/s\n", st.tokens, ms,
+                 ms > 0 ? st.tokens * 1000.0 / ms : 0.0);
     if (o.spec)
         std::fprintf(stderr, "minfer-hip: %d generation steps, %.2f tokens/step | drafted %d, accepted %d (%.0f%%)\n",
                      st.steps, st.steps ? (double)st.tokens / st.steps : 0.0, st.drafted, st.accepted,

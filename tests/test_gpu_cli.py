@@ -64,7 +64,8 @@ def test_cli_raw_ids_match_the_engine():
     assert [int(x) for x in out.split()] == toks
     assert out.endswith(b"\n")
     assert re.search(r"prefill: 20 tok in [0-9.]+ ms", err)
-    assert re.search(r"decode: 40 tok in [0-9.]+ ms = [0-9.]+ tok/s", err)
+    # the rate counts the tokens of the 39 decode steps (the first is the prefill's)
+    assert re.search(r"decode: 39 tok in [0-9.]+ ms = [0-9.]+ tok/s", err)
 
 
 def test_cli_text_mode_streams_token_text():
@@ -75,7 +76,9 @@ def test_cli_text_mode_streams_token_text():
     toks, texts, eos = engine_stream(path, ids, 30)
     n = toks.index(eos) if eos in toks else len(toks)
     assert out == b"".join(texts[:n]) + b"\n"
-    assert re.search(r"decode: %d tok in" % n, err)
+    # decode steps: one per emitted token after the prefill's (an eos is emitted, not printed)
+    steps = n if eos in toks else n - 1
+    assert re.search(r"decode: %d tok in" % steps, err)
 
 
 def test_cli_spec_and_per_phase_give_the_same_ids():
