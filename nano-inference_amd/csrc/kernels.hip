@@ -803,19 +803,34 @@ __device__ __forceinline__ void emit_token(MPtr M, const Top2& a, int pos, int g
 }
 
 // ------------------------------------------------------------------ attention
-// per-wave LDS: K [HD/8][64] 16-byte vectors (vector j of position t at j*64 + t, so
-// a lane-per-position read is conflict-free) | V [64][HD] | q partials [2][HD] |
-// k, v partials [2][2][HD] | q [HD] (+ spare)
+// per-wave LDS: K [64][HD/8] 16-byte vectors, row-major with the vectors of row t
+// permuted (kslot) | V [64][HD] | q partials [2][HD] | k, v partials [2][2][HD] | q [HD]
+// (+ spare)
 
-// DMA the chunk's K rows (swizzled) and V rows; rows past n repeat row n-1
+// K tile slot of 16-byte vector v of position t: t * NV + (v ^ kswz(t)). The XOR makes the
+// lane-per-position read of one vector conflict-free (each 16-lane pass of a 16-byte LDS
+// read touches 16 different 4-bank groups) while each row stays in its own 256 B (128 B
+// at hd 64), so the DMA that fills it reads whole rows: coalesced.
+template <int HD>
+__device__ __forceinline__ int kswz(int t) { return HD == 128 ? (t & 15) : ((t >> 1) & 7); }
+template <int HD>
+__device__ __forceinline__ int kslot(int t, int v) { return t * (HD / 8) + (v ^ kswz<HD>(t)); }
+
+// DMA the chunk's K rows (swizzled tile) and V rows; rows past n repeat row n-1. K load i
+// fills tile slots 64i..64i+63, i.e. rows (64/NV)i.. whole: lane l takes slot 64i + l =
+// (row t, place u) and fetches vector u ^ kswz(t) of row t, 1 KB of consecutive rows per
+// instruction (one row per lane touched 64 lines per instruction and was the slow part).
 template <int HD>
 __device__ __forceinline__ void attn_issue_kv(const __half* krows, const __half* vrows, int t0, int n, uint4* kls,
                                               __half* vls, int lane) {
     constexpr int NV = HD / 8, RPI = 64 / NV;
-    const __half* kr = krows + (size_t)(t0 + min(lane, n - 1)) * HD;
+    const int u = lane % NV;
 #pragma unroll
-    for (int j = 0; j < NV; j++)
-        __builtin_amdgcn_global_load_lds(kr + 8 * j, (lds_ptr)(kls + j * 64), 16, 0, 0);
+    for (int i = 0; i < NV; i++) {
+        const int t = i * RPI + lane / NV;
+        const __half* src = krows + (size_t)(t0 + min(t, n - 1)) * HD + 8 * (u ^ kswz<HD>(t));
+        __builtin_amdgcn_global_load_lds(src, (lds_ptr)(kls + i * 64), 16, 0, 0);
+    }
     const int r = lane / NV, col = (lane % NV) * 8;
 #pragma unroll
     for (int i = 0; i < 64 / RPI; i++) {
@@ -834,7 +849,7 @@ __device__ __forceinline__ void attn_core(const uint4* kls, const float* qs, con
     float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
 #pragma unroll 4
     for (int j = 0; j < NV; j++) {
-        const uint4 w = kls[j * 64 + lane];
+        const uint4 w = kls[kslot<HD>(lane, j)];
         const float4 q0 = *reinterpret_cast<const float4*>(qs + 8 * j);
         const float4 q1 = *reinterpret_cast<const float4*>(qs + 8 * j + 4);
         a0 = __fmaf_rn(q0.x, h2f_lo(w.x), a0); a1 = __fmaf_rn(q0.y, h2f_hi(w.x), a1);
@@ -973,8 +988,8 @@ __device__ __forceinline__ void attn_finish(MPtr M, int l, int pos, const AttnIt
             const __half v0 = __float2half(fin(kvp + kMaxKsQkv * HD, ip, bv0));
             const __half v1 = __float2half(fin(kvp + kMaxKsQkv * HD, ip + half, bv1));
             __half* kh = reinterpret_cast<__half*>(kls);      // position cur's K row into the swizzled tile
-            kh[((ip >> 3) * 64 + cur) * 8 + (ip & 7)] = y0;
-            kh[(((ip + half) >> 3) * 64 + cur) * 8 + ((ip + half) & 7)] = y1;
+            kh[kslot<HD>(cur, ip >> 3) * 8 + (ip & 7)] = y0;
+            kh[kslot<HD>(cur, (ip + half) >> 3) * 8 + ((ip + half) & 7)] = y1;
             vls[cur * HD + ip] = v0;
             vls[cur * HD + ip + half] = v1;
             if (h % M->G == 0) {                    // one of the kv head's G query heads appends to the cache
@@ -1709,8 +1724,8 @@ __global__ __launch_bounds__(kPThreads) void kT_attn(const DModel* Mp, int l, in
         if (mine && lane < half) {
             const int r = p - t0;
             __half* kh = reinterpret_cast<__half*>(kls);
-            kh[((ip >> 3) * 64 + r) * 8 + (ip & 7)] = y0;
-            kh[(((ip + half) >> 3) * 64 + r) * 8 + ((ip + half) & 7)] = y1;
+            kh[kslot<HD>(r, ip >> 3) * 8 + (ip & 7)] = y0;
+            kh[kslot<HD>(r, (ip + half) >> 3) * 8 + ((ip + half) & 7)] = y1;
             vls[r * HD + ip] = v0;
             vls[r * HD + ip + half] = v1;
             if (tb == T - 1) {                                     // one item per (kv head, chunk) appends
