@@ -1035,76 +1035,76 @@ __device__ __forceinline__ void attn_run(MPtr M, int l, int pos, int wg, int nwg
     }
 }
 
-// max-first merge of the chunk records [c0, c1) for dim d (cuda_infer.cu:688-702
-// attn_combine): M = max m_c, w_c = exp(m_c - M), den and acc as fma chains over the
-// chunks in order. Returns acc (not yet divided by den). UNROLL: c1 - c0 <=
-// kAttnSplit, all loads issued before the arithmetic.
-template <bool UNROLL>
-__device__ __forceinline__ float merge_recs(const float* r, int rec, int hd, int d, int c0, int c1, float& Mo,
-                                            float& deno) {
-    float M = -__builtin_inff(), den = 0.f, acc = 0.f;
-    if constexpr (UNROLL) {
-        float mv[kAttnSplit], lv[kAttnSplit], ov[kAttnSplit];
-#pragma unroll
-        for (int i = 0; i < kAttnSplit; i++) {
-            const int c = min(c0 + i, c1 - 1);
-            mv[i] = r[c * rec + hd];
-            lv[i] = r[c * rec + hd + 1];
-            ov[i] = r[c * rec + d];
-        }
-#pragma unroll
-        for (int i = 0; i < kAttnSplit; i++)
-            if (c0 + i < c1) M = fmaxf(M, mv[i]);
-#pragma unroll
-        for (int i = 0; i < kAttnSplit; i++)
-            if (c0 + i < c1) {
-                const float w = mi_expf(__fsub_rn(mv[i], M));
-                den = __fmaf_rn(lv[i], w, den);
-                acc = __fmaf_rn(ov[i], w, acc);
-            }
-    } else {
-        for (int c = c0; c < c1; c++) M = fmaxf(M, r[c * rec + hd]);
-        for (int c = c0; c < c1; c++) {
-            const float w = mi_expf(__fsub_rn(r[c * rec + hd], M));
-            den = __fmaf_rn(r[c * rec + hd + 1], w, den);
-            acc = __fmaf_rn(r[c * rec + d], w, acc);
-        }
-    }
-    Mo = M;
-    deno = den;
-    return acc;
-}
-// all nch records of one (head, dim) merged in one level
-__device__ __forceinline__ float combine_one(const float* recs, int rec, int hd, int d, int nch) {
-    float M, den;
-    const float acc = merge_recs<false>(recs, rec, hd, d, 0, nch, M, den);
-    return __fdiv_rn(acc, den);
-}
-// the canonical merge: one level up to kAttnSplit chunks, else each split of kAttnSplit
-// chunks merged (M_s, den_s, acc_s), then the splits in order the same way; the
-// global max equals the max over the split maxima
-__device__ __forceinline__ float combine_tree(const float* recs, int rec, int hd, int d, int nch) {
-    if (nch <= kAttnSplit) return combine_one(recs, rec, hd, d, nch);
+// The canonical merge of chunk records (o[HD], m, l) by max rescaling (cuda_infer.cu:
+// 688-702 attn_combine), as the oracle restates it: one wave merges the nch chunk
+// records of one head (records r[c * arec], lane = dims 64e + lane); the max over all
+// chunks first when there are
+// more than kAttnSplit; each split of kAttnSplit chunks with all its loads issued at
+// once (M_s = split max, w = exp(m - M_s), den and o as fma chains in chunk order),
+// then the splits in order scaled by exp(M_s - M). Returns o / den per lane and dim.
+template <int HD>
+__device__ __forceinline__ void comb_wave(const float* r, int arec, int nch, int lane, float (&out)[HD / 64]) {
+    constexpr int DPL = HD / 64;
     float Mx = -__builtin_inff();
-    for (int c = 0; c < nch; c++) Mx = fmaxf(Mx, recs[c * rec + hd]);
-    float den = 0.f, acc = 0.f;
-    for (int c0 = 0; c0 < nch; c0 += kAttnSplit) {
-        float Ms, ds;
-        const float as = merge_recs<false>(recs, rec, hd, d, c0, min(nch, c0 + kAttnSplit), Ms, ds);
-        const float w = mi_expf(__fsub_rn(Ms, Mx));
-        den = __fmaf_rn(ds, w, den);
-        acc = __fmaf_rn(as, w, acc);
+    if (nch > kAttnSplit) {
+        for (int c = lane; c < nch; c += 64) Mx = fmaxf(Mx, r[c * arec + HD]);
+        Mx = wave_max(Mx);
     }
-    return __fdiv_rn(acc, den);
+    float den = 0.f, acc[DPL];
+#pragma unroll
+    for (int e = 0; e < DPL; e++) acc[e] = 0.f;
+    for (int c0 = 0; c0 < nch; c0 += kAttnSplit) {
+        const int len = min(kAttnSplit, nch - c0);
+        const float* rs = r + (size_t)c0 * arec;
+        const float mv = lane < len ? rs[lane * arec + HD] : -__builtin_inff();
+        const float lv = lane < len ? rs[lane * arec + HD + 1] : 0.f;
+        float ov[kAttnSplit][DPL];
+#pragma unroll
+        for (int i = 0; i < kAttnSplit; i++)
+#pragma unroll
+            for (int e = 0; e < DPL; e++) ov[i][e] = i < len ? rs[i * arec + 64 * e + lane] : 0.f;
+        const float Ms = wave_max(mv);
+        const float wv = lane < len ? mi_expf(__fsub_rn(mv, Ms)) : 0.f;
+        float ds = 0.f, as[DPL];
+#pragma unroll
+        for (int e = 0; e < DPL; e++) as[e] = 0.f;
+#pragma unroll
+        for (int i = 0; i < kAttnSplit; i++)
+            if (i < len) {
+                const float wi = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wv), i));
+                const float li = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(lv), i));
+                ds = __fmaf_rn(li, wi, ds);
+#pragma unroll
+                for (int e = 0; e < DPL; e++) as[e] = __fmaf_rn(ov[i][e], wi, as[e]);
+            }
+        if (nch <= kAttnSplit) {
+            den = ds;
+#pragma unroll
+            for (int e = 0; e < DPL; e++) acc[e] = as[e];
+        } else {
+            const float ws = mi_expf(__fsub_rn(Ms, Mx));
+            den = __fmaf_rn(ds, ws, den);
+#pragma unroll
+            for (int e = 0; e < DPL; e++) acc[e] = __fmaf_rn(as[e], ws, acc[e]);
+        }
+    }
+#pragma unroll
+    for (int e = 0; e < DPL; e++) out[e] = __fdiv_rn(acc[e], den);
 }
 
-// chunk merge as its own phase (more than kInlineComb chunks): one thread per (head, dim)
-__device__ __forceinline__ void phase_comb(MPtr M, int l, int pos, int wg, int nwg) {
+// chunk merge as its own phase (more than kInlineComb chunks): head h on worker wave 1
+// of workgroup h (the heads spread over as many CUs), comb_wave's loads a split at a time
+template <int HD>
+__device__ __forceinline__ void phase_comb(MPtr M, int l, int pos, int wg, int wave, int lane) {
+    if (wave != 1 || wg >= M->NH) return;
+    // opaque lane: its addresses are not hoisted out of the phase loop
+    asm volatile("" : "+v"(lane));
     const int nch = (pos + 1 + kAttnChunk - 1) / kAttnChunk;
-    const float* att = att_rec(M, l);
-    float* out = M->att_out + (size_t)l * M->E;
-    for (int it = wg * blockDim.x + threadIdx.x; it < M->E; it += nwg * blockDim.x)
-        stc(out + it, combine_tree(att + (size_t)(it / M->HD) * M->maxch * M->arec, M->arec, M->HD, it % M->HD, nch));
+    float o[HD / 64];
+    comb_wave<HD>(att_rec(M, l) + (size_t)wg * M->maxch * M->arec, M->arec, nch, lane, o);
+    float* out = M->att_out + (size_t)l * M->E + (size_t)wg * HD;
+#pragma unroll
+    for (int e = 0; e < HD / 64; e++) stc(out + 64 * e + lane, o[e]);
 }
 
 // ------------------------------------------------------------------ the persistent step
@@ -1205,7 +1205,7 @@ __global__ __launch_bounds__(kPThreads) void k_step(const DModel* Mp, int pos, i
             __syncthreads();
             if (ctl) ctl_barrier(gb, M->err);
             __syncthreads();
-            phase_comb(M, l, pos, wg, nwg);
+            phase_comb<HD>(M, l, pos, wg, wave, lane);
         }
         __syncthreads();
         stamp(M, sb + 1, 64);
@@ -1304,9 +1304,10 @@ __global__ __launch_bounds__(kPThreads) void k_attn(const DModel* Mp, int l, int
     attn_prefetch<HD>(M, l, pos, blockIdx.x, gridDim.x, S.U, wave - 1, lane);
     attn_run<HD>(M, l, pos, blockIdx.x, gridDim.x, S.U, wave - 1, lane);
 }
+template <int HD>
 __global__ __launch_bounds__(kPThreads) void k_attn_comb(const DModel* Mp, int l, int pos) {
     const MPtr M = (MPtr)Mp;
-    phase_comb(M, l, pos, blockIdx.x, gridDim.x);
+    phase_comb<HD>(M, l, pos, blockIdx.x, threadIdx.x >> 6, threadIdx.x & 63);
 }
 __global__ __launch_bounds__(kPThreads) void k_o(const DModel* Mp, int l, int pos) {
     const MPtr M = (MPtr)Mp;
@@ -1756,9 +1757,8 @@ __global__ __launch_bounds__(kPThreads) void kT_attn(const DModel* Mp, int l, in
 }
 
 // chunk merge of token t's records for query head h (one wave per (t, h); lane = dims
-// lane + 64j) into the O phase's int8 records in xT. The merge is combine_tree's
-// arithmetic (cuda_infer.cu:688-702 attn_combine), with each split's 16 chunk maxima,
-// weights and sums taken lane-parallel and the fma chains run in chunk order.
+// lane + 64j) into the O phase's int8 records in xT. The merge is comb_wave's, the
+// step's merge phase uses the same function.
 template <int HD>
 __global__ __launch_bounds__(256) void kT_comb(const DModel* Mp, int l, int T) {
     const MPtr M = (MPtr)Mp;
@@ -1768,55 +1768,14 @@ __global__ __launch_bounds__(256) void kT_comb(const DModel* Mp, int l, int T) {
     if (item >= T * M->NH) return;
     const int t = item / M->NH, hh = item - t * M->NH, nch = (pos + t + kAttnChunk) / kAttnChunk, arec = M->arec;
     const float* r = attT_at(M, l, t) + (size_t)hh * M->maxch * arec;
-    float Mx = -__builtin_inff();
-    if (nch > kAttnSplit) {
-        for (int c = lane; c < nch; c += 64) Mx = fmaxf(Mx, r[c * arec + HD]);
-        Mx = wave_max(Mx);
-    }
-    float den = 0.f, acc[DPL];
-#pragma unroll
-    for (int e = 0; e < DPL; e++) acc[e] = 0.f;
-    for (int c0 = 0; c0 < nch; c0 += kAttnSplit) {
-        const int len = min(kAttnSplit, nch - c0);
-        const float* rs = r + (size_t)c0 * arec;
-        const float mv = lane < len ? rs[lane * arec + HD] : -__builtin_inff();
-        const float lv = lane < len ? rs[lane * arec + HD + 1] : 0.f;
-        float ov[kAttnSplit][DPL];
-#pragma unroll
-        for (int i = 0; i < kAttnSplit; i++)
-#pragma unroll
-            for (int e = 0; e < DPL; e++) ov[i][e] = i < len ? rs[i * arec + 64 * e + lane] : 0.f;
-        const float Ms = wave_max(mv);
-        const float wv = lane < len ? mi_expf(__fsub_rn(mv, Ms)) : 0.f;
-        float ds = 0.f, as[DPL];
-#pragma unroll
-        for (int e = 0; e < DPL; e++) as[e] = 0.f;
-#pragma unroll
-        for (int i = 0; i < kAttnSplit; i++)
-            if (i < len) {
-                const float wi = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wv), i));
-                const float li = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(lv), i));
-                ds = __fmaf_rn(li, wi, ds);
-#pragma unroll
-                for (int e = 0; e < DPL; e++) as[e] = __fmaf_rn(ov[i][e], wi, as[e]);
-            }
-        if (nch <= kAttnSplit) {
-            den = ds;
-#pragma unroll
-            for (int e = 0; e < DPL; e++) acc[e] = as[e];
-        } else {
-            const float ws = mi_expf(__fsub_rn(Ms, Mx));
-            den = __fmaf_rn(ds, ws, den);
-#pragma unroll
-            for (int e = 0; e < DPL; e++) acc[e] = __fmaf_rn(as[e], ws, acc[e]);
-        }
-    }
+    float o[DPL];
+    comb_wave<HD>(r, arec, nch, lane, o);
     const int nblk = M->E / 32;
 #pragma unroll
     for (int e = 0; e < DPL; e++) {
         int q, s8;
         float d;
-        quant32_vals(__fdiv_rn(acc[e], den), q, d, s8);
+        quant32_vals(o[e], q, d, s8);
         const int el = hh * HD + 64 * e + lane;
         uint8_t* rec = M->xT + ((size_t)t * nblk + (el >> 5)) * kTRec;
         rec[el & 31] = (uint8_t)(q & 0xFF);
@@ -2076,7 +2035,7 @@ __global__ __launch_bounds__(64) void k_isums(PMat W, const int8_t* xq, int32_t*
 // read once per item and never staged in LDS; the g heads then reuse them. Per head
 // the arithmetic is attn_core's: scores as four fma chains over d mod 4, the chunk
 // softmax with the 64-lane butterfly sum, p.v as an fma chain over positions.
-// The merge is combine_tree's, done by the last arrivals: after its chunk records
+// The merge is comb_wave's order, done by the last arrivals: after its chunk records
 // (o[hd], m, l) are stored and drained, an item bumps its split's counter; the wave
 // that completes a split merges its chunks (and writes the output if there is one
 // split), then bumps the head group's counter, whose last arrival merges the splits.
@@ -2173,7 +2132,7 @@ __device__ __forceinline__ void attn_item_heads(const __half* kr, const __half* 
 }
 
 // One wave merges the records [c0, c1) of one head (contiguous, REC floats each)
-// as merge_recs does, lane = dims DPL*lane + e: M = max over all records, w_i =
+// as comb_wave does, lane = dims DPL*lane + e: M = max over all records, w_i =
 // exp(m_i - M), then den and acc as fma chains in record order. The records come
 // into LDS 16 at a time by DMA (lds: 16 * REC floats); w_i and l_i reach every lane
 // by readlane. The loops stay rolled: this code runs once per split on a CU that
@@ -2430,7 +2389,10 @@ void launch_phase(const DModel& M, const DModel* dM, int nwg, int phase, int l, 
     switch (phase) {
         case 0: LAUNCH(k_qkv, nwg, kPThreads, s, dM, l, pos); break;
         case 1: with_hd(M.HD, [&](auto hd) { LAUNCH((k_attn<decltype(hd)::value>), nwg, kPThreads, s, dM, l, pos); }); break;
-        case 2: if (nch > kInlineComb) LAUNCH(k_attn_comb, nwg, kPThreads, s, dM, l, pos); break;
+        case 2:
+            if (nch > kInlineComb)
+                with_hd(M.HD, [&](auto hd) { LAUNCH((k_attn_comb<decltype(hd)::value>), nwg, kPThreads, s, dM, l, pos); });
+            break;
         case 3: LAUNCH(k_o, nwg, kPThreads, s, dM, l, pos); break;
         case 4: LAUNCH(k_gu, nwg, kPThreads, s, dM, l); break;
         case 5: LAUNCH(k_down, nwg, kPThreads, s, dM, l); break;
