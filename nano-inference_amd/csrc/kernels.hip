@@ -1092,19 +1092,48 @@ __device__ __forceinline__ void comb_wave(const float* r, int arec, int nch, int
     for (int e = 0; e < DPL; e++) out[e] = __fdiv_rn(acc[e], den);
 }
 
-// chunk merge as its own phase (more than kInlineComb chunks): head h on worker wave 1
-// of workgroup h (the heads spread over as many CUs), comb_wave's loads a split at a time
 template <int HD>
-__device__ __forceinline__ void phase_comb(MPtr M, int l, int pos, int wg, int wave, int lane) {
+__device__ __forceinline__ void lds_merge(const float* r, int c0, int c1, float* lds, int lane, float& Mo, float& deno,
+                                          float (&acc)[HD / 64]);
+// chunk merge as its own phase (more than kInlineComb chunks): head h on worker wave 1
+// of workgroup h (the heads spread over as many CUs), in comb_wave's order: the max over
+// all chunks (past kAttnSplit), then each split merged by lds_merge (its 16 records
+// DMA'd into `lds`, 16 * (HD + 32) floats, with rolled loops: an unrolled merge here made
+// the whole step ~6 us per token slower even when the phase does not run), then the
+// splits scaled by exp(M_s - M)
+template <int HD>
+__device__ __forceinline__ void phase_comb(MPtr M, int l, int pos, int wg, int wave, int lane, float* lds) {
     if (wave != 1 || wg >= M->NH) return;
     // opaque lane: its addresses are not hoisted out of the phase loop
     asm volatile("" : "+v"(lane));
+    constexpr int DPL = HD / 64;
     const int nch = (pos + 1 + kAttnChunk - 1) / kAttnChunk;
-    float o[HD / 64];
-    comb_wave<HD>(att_rec(M, l) + (size_t)wg * M->maxch * M->arec, M->arec, nch, lane, o);
+    const float* r = att_rec(M, l) + (size_t)wg * M->maxch * M->arec;
+    float Mx = -__builtin_inff();
+    if (nch > kAttnSplit) {
+        for (int c = lane; c < nch; c += 64) Mx = fmaxf(Mx, r[c * M->arec + HD]);
+        Mx = wave_max(Mx);
+    }
+    float den = 0.f, acc[DPL];
+#pragma unroll
+    for (int e = 0; e < DPL; e++) acc[e] = 0.f;
+    for (int c0 = 0; c0 < nch; c0 += kAttnSplit) {
+        float Ms, ds, as[DPL];
+        lds_merge<HD>(r, c0, min(nch, c0 + kAttnSplit), lds, lane, Ms, ds, as);
+        if (nch <= kAttnSplit) {
+            den = ds;
+#pragma unroll
+            for (int e = 0; e < DPL; e++) acc[e] = as[e];
+        } else {
+            const float ws = mi_expf(__fsub_rn(Ms, Mx));
+            den = __fmaf_rn(ds, ws, den);
+#pragma unroll
+            for (int e = 0; e < DPL; e++) acc[e] = __fmaf_rn(as[e], ws, acc[e]);
+        }
+    }
     float* out = M->att_out + (size_t)l * M->E + (size_t)wg * HD;
 #pragma unroll
-    for (int e = 0; e < HD / 64; e++) stc(out + 64 * e + lane, o[e]);
+    for (int e = 0; e < DPL; e++) stc(out + DPL * lane + e, __fdiv_rn(acc[e], den));
 }
 
 // ------------------------------------------------------------------ the persistent step
@@ -1205,7 +1234,7 @@ __global__ __launch_bounds__(kPThreads) void k_step(const DModel* Mp, int pos, i
             __syncthreads();
             if (ctl) ctl_barrier(gb, M->err);
             __syncthreads();
-            phase_comb<HD>(M, l, pos, wg, wave, lane);
+            phase_comb<HD>(M, l, pos, wg, wave, lane, reinterpret_cast<float*>(S.U));
         }
         __syncthreads();
         stamp(M, sb + 1, 64);
@@ -1307,7 +1336,8 @@ __global__ __launch_bounds__(kPThreads) void k_attn(const DModel* Mp, int l, int
 template <int HD>
 __global__ __launch_bounds__(kPThreads) void k_attn_comb(const DModel* Mp, int l, int pos) {
     const MPtr M = (MPtr)Mp;
-    phase_comb<HD>(M, l, pos, blockIdx.x, threadIdx.x >> 6, threadIdx.x & 63);
+    __shared__ __align__(16) float lds[kAttnSplit * (HD + 32)];
+    phase_comb<HD>(M, l, pos, blockIdx.x, threadIdx.x >> 6, threadIdx.x & 63, lds);
 }
 __global__ __launch_bounds__(kPThreads) void k_o(const DModel* Mp, int l, int pos) {
     const MPtr M = (MPtr)Mp;
