@@ -1,12 +1,14 @@
 """Headline benchmark: batch-1 greedy decode tok/s, Qwen2.5-1.5B-shape q4_0, tg128.
 
-    python bench.py [--gpus 1] [--steps 128] [--warmup 8]
+    python bench.py [--gpus 1] [--steps 5] [--warmup 1]
 
 Workload: random-init S15 GGUF (hidden 1536, 28 layers,
 12/2 heads, hd 128, FFN 8960, vocab 151936) written from a fixed seed, a 64-token
-seeded random prompt, then `--steps` decode steps (tg128 = 128). A step is one
-decode token (one pass over all weights). The timed region starts with the
-prompt's K/V and every weight resident in HBM.
+seeded random prompt, then greedy tg128. ONE STEP IS ONE WHOLE tg128: the prompt is
+prefilled (untimed, every weight resident in HBM), then 128 decode tokens are timed
+(positions 64..191). `--steps K` runs K such generations from the same prompt and
+`value` = 128*K / (their summed time); `ms_per_step` = the time of one tg128.
+`--warmup W` runs W untimed generations first.
 
 Prints ONE JSON line on stdout. Besides the contract keys it carries:
   roofline      the dominant kernel: the persistent step kernel k_step, one
@@ -20,6 +22,10 @@ Prints ONE JSON line on stdout. Besides the contract keys it carries:
                 With --persistent 0 the dominant kernel is the gate/up phase.
   step_roofline bytes/token x tok/s against the measured stream-read bandwidth
   stream_gbps   one-launch stream read of a 4 GiB buffer (> the 256 MB MALL)
+  phases        the in-kernel profile of one step (device clock stamps per workgroup
+                and phase, mi_profile_step): per GEMV phase, weight bytes / the
+                phase's time from the previous grid barrier's exit to its own exit,
+                against stream_gbps
   gemv          config 1 microbench: each S15 GEMV shape, rotated over copies
                 totalling > 512 MB so every launch reads from HBM
   attention_depth  config 3: S15 decode attention at L = 512..32768, 28 rotated
@@ -243,6 +249,18 @@ def attention_depth(torch, lengths=(512, 4096, 16384, 32768), layers=28, reps=3,
     return res
 
 
+def cpu_model():
+    """the host CPU's model name (lscpu's "Model name", from /proc/cpuinfo)"""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(path, prompt, n_prompt=64, n_gen=129):
     """oracle fp32 (cpu_infer semantics) on the host cores: the whole config2
     workload (64-token prompt, 128 decode steps), about 15 s on 16 threads"""
@@ -252,17 +270,59 @@ def cpu_baseline(path, prompt, n_prompt=64, n_gen=129):
     m = O.Model(path, O.MODE_FP32, max_seq=n_prompt + n_gen + 1, threads=threads)
     _, _, tp, td = m.generate(prompt[:n_prompt], n_gen)
     m.close()
-    return dict(value=round((n_gen - 1) / td, 3), unit="tok/s", cores=threads, kind="port",
+    return dict(value=round((n_gen - 1) / td, 3), unit="tok/s", cores=threads, kind="port", cpu=cpu_model(),
                 sample="S15 greedy decode: %d-token prompt (%.1f s) then %d tokens (%d decode steps in %.1f s), "
-                       "oracle fp32 = cpu_infer.cpp semantics, OpenMP %d threads" % (n_prompt, tp, n_gen, n_gen - 1,
-                                                                                       td, threads))
+                       "oracle fp32 = cpu_infer.cpp semantics, OpenMP %d threads on %s" % (
+                           n_prompt, tp, n_gen, n_gen - 1, td, threads, cpu_model()))
+
+
+# q4_0 weight bytes of one layer's GEMV of each phase kind (rows x blocks x 18)
+def phase_weight_bytes(info):
+    E, FF = info.n_embd, info.n_ff
+    qkv = info.n_head * info.head_dim + 2 * info.n_head_kv * info.head_dim
+    nbE, nbF = E // 32, FF // 32
+    return {"qkv": qkv * nbE * 18, "o": E * nbE * 18, "gate_up": 2 * FF * nbE * 18, "down": E * nbF * 18,
+            "lm_head": info.n_vocab * nbE * 18}
+
+
+def phase_profile(eng, stream_gbps):
+    """In-kernel phase times of one persistent step (mi_profile_step: device clock stamps
+    of every workgroup). A phase runs from the previous grid barrier's exit to its own
+    barrier's exit (the earliest exit over workgroups = when the barrier completed); per
+    GEMV kind, the weight bytes of all layers / the summed phase times, against the
+    measured stream bandwidth."""
+    t = eng.profile_step()
+    L = eng.info.n_layer
+    exits = [0.0]
+    kinds = []
+    for l in range(L):
+        for k, name in enumerate(("qkv", "attn", "o", "gate_up", "down")):
+            exits.append(float(t[:, 1 + l * 25 + 5 * k + 4].min()))
+            kinds.append(name)
+    exits.append(float(t[:, 1 + L * 25 + 4].min()))
+    kinds.append("lm_head")
+    wb = phase_weight_bytes(eng.info)
+    tot = {}
+    for i, name in enumerate(kinds):
+        tot[name] = tot.get(name, 0.0) + exits[i + 1] - exits[i]
+    out = []
+    for name in ("qkv", "attn", "o", "gate_up", "down", "lm_head"):
+        us = tot[name]
+        n = 1 if name == "lm_head" else L
+        d = dict(phase=name, us_per_layer=round(us / n, 2), us_total=round(us, 1))
+        if name in wb:
+            gbps = wb[name] * n / (us * 1e-6) / 1e9
+            d.update(weight_bytes=wb[name], gbps=round(gbps, 1), frac_of_stream=round(gbps / stream_gbps, 4))
+        out.append(d)
+    return out, round(exits[-1], 1)
 
 
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=128)
-    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--steps", type=int, default=5, help="timed tg128 generations")
+    ap.add_argument("--warmup", type=int, default=1, help="untimed tg128 generations before them")
+    ap.add_argument("--tg", type=int, default=128, help="decode tokens per step (the metric is tg128)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-micro", action="store_true")
     ap.add_argument("--persistent", type=int, default=1)
@@ -303,32 +363,49 @@ def main():
     path = ensure_gguf("config2")
     V = minfer.SHAPES[shape]["n_vocab"]
     prompt = minfer.prompt_ids(pseed, n_prompt, V)
+    tg = args.tg
     t = time.time()
-    eng = minfer.Engine(path, max_ctx=n_prompt + args.steps + args.warmup + 16, persistent=args.persistent)
+    eng = minfer.Engine(path, max_ctx=n_prompt + tg + 16, persistent=args.persistent)
     info = eng.info
     log("loaded in %.1f s: plan cb=%s ks=%s, %d CUs, weights %d B" % (time.time() - t, list(info.plan_cb),
                                                                      list(info.plan_ks), info.n_cu, info.weight_bytes))
-    # warmup: one short generation from the same prompt
-    eng.prefill(prompt)
-    eng.generate(args.warmup + 1)
-    # timed: prefill (untimed), then exactly `steps` decode steps
-    eng.prefill(prompt)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    toks, margins = eng.generate(args.steps + 1)
-    t1 = time.perf_counter()
-    st = eng.stats()
-    assert st["steps"] == args.steps
-    wall_ms = (t1 - t0) * 1000
-    ms_per_step = wall_ms / args.steps
-    tok_s = args.steps / (t1 - t0)
-    log("decode: %d steps in %.2f ms wall (%.2f ms device) = %.1f tok/s" % (args.steps, wall_ms, st["decode_ms"], tok_s))
-    mean_pos = n_prompt + (args.steps - 1) / 2.0
+
+    def one_tg():
+        """prefill the prompt (untimed), then one timed tg: 1 + tg tokens, the first
+        being the prefill's prediction, so exactly tg decode steps (positions 64..)"""
+        eng.prefill(prompt)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        toks, margins = eng.generate(tg + 1)
+        torch.cuda.synchronize()
+        dt = time.perf_counter() - t0
+        st = eng.stats()
+        assert st["steps"] == tg
+        return toks, dt, st["decode_ms"]
+
+    for _ in range(args.warmup):
+        one_tg()
+    wall = dev_ms = 0.0
+    toks = None
+    for k in range(args.steps):
+        tk, dt, dms = one_tg()
+        if toks is None:
+            toks = tk
+        assert tk == toks, "tg%d stream differs between steps" % tg
+        wall += dt
+        dev_ms += dms
+        log("step %d: tg%d in %.2f ms wall (%.2f ms device)" % (k, tg, dt * 1e3, dms))
+    ntok = tg * args.steps
+    ms_per_step = wall * 1e3 / args.steps
+    tok_s = ntok / wall
+    log("decode: %d x tg%d = %d tokens in %.2f ms wall (%.2f ms device) = %.1f tok/s" % (
+        args.steps, tg, ntok, wall * 1e3, dev_ms, tok_s))
+    mean_pos = n_prompt + (tg - 1) / 2.0
     bpt = bytes_per_token(info, mean_pos)
     if info.persistent:
         # dominant kernel: k_step, one launch per token; its mean duration comes
         # from the engine's HIP events around the timed launches on its stream
-        k_us = st["decode_ms"] * 1e3 / args.steps
+        k_us = dev_ms * 1e3 / ntok
         k_bytes = int(bpt)
         kname = "k_step (persistent decode step, 1 launch/token, %d workgroups)" % info.n_cu
     else:
@@ -338,10 +415,17 @@ def main():
         kname = "k_gu (gate/up GEMV phase, %d launches/token)" % info.n_layer
     k_gbps = k_bytes / (k_us * 1e-6) / 1e9
     log("%s: %.2f us per launch, %.1f GB/s" % (kname, k_us, k_gbps))
-    eng.close()
-    del eng
     stream = stream_bw(torch)
     log("stream read: %.1f GB/s" % stream)
+    phases, prof_total = (None, None)
+    if info.persistent:
+        phases, prof_total = phase_profile(eng, stream)
+        for ph in phases:
+            log("phase %-8s %7.2f us/layer%s" % (ph["phase"], ph["us_per_layer"],
+                                                 "  %7.1f GB/s = %.1f%% of stream" % (ph["gbps"], 100 * ph["frac_of_stream"])
+                                                 if "gbps" in ph else ""))
+    eng.close()
+    del eng
     micro = [] if args.no_micro else gemv_microbench(torch)
     for m in micro:
         log("gemv %-8s %6d x %5d: %8.2f us  %7.1f GB/s" % (m["shape"], m["rows"], m["k"], m["us"], m["gbps"]))
@@ -350,7 +434,7 @@ def main():
         log("attention L=%-6d %8.2f us/layer  %7.1f GB/s" % (a["L"], a["us_per_layer"], a["gbps"]))
     spec = verify = None
     if not args.no_extra:
-        stoks, spec = spec_decode(path, prompt, args.steps + 1)
+        stoks, spec = spec_decode(path, prompt, tg + 1)
         spec["identical_to_plain"] = stoks == toks
         log("speculative decode: %s" % spec)
         verify = verify_cost()
@@ -360,14 +444,17 @@ def main():
         log("cpu baseline: %s" % cpu)
     achieved_step = bpt * tok_s / 1e9
     rec = {
-        "metric": "batch-1 decode tok/s, Qwen2.5-1.5B q4_0 tg128; GEMV HBM GB/s vs peak",
+        "metric": "batch-1 decode tok/s, Qwen2.5-1.5B q4_0 tg%d; GEMV HBM GB/s vs peak" % tg,
         "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(ms_per_step, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "q4_0 weights x int8 activations, int32 dot, fp32 accumulate/softmax, fp16 KV",
         "data": "synthetic: seeded random-init GGUF (mi_synth_gguf seed %d), seeded random prompt" % mseed,
-        "config": {"workload": "config2: Qwen2.5-1.5B-architecture q4_0 batch-1 greedy decode, 64-token prompt, tg%d"
-                   % args.steps, "shape": "S15 E1536 L28 H12/2 hd128 FF8960 V151936", "global_batch": 1,
-                   "prompt": n_prompt, "step_mode": "persistent" if info.persistent else "one launch per phase",
+        "config": {"workload": "config2: Qwen2.5-1.5B-architecture q4_0 batch-1 greedy decode, 64-token prompt, "
+                               "tg%d; one step = one whole tg%d (%d decode tokens timed), %d steps" % (tg, tg, tg,
+                                                                                                     args.steps),
+                   "shape": "S15 E1536 L28 H12/2 hd128 FF8960 V151936", "global_batch": 1,
+                   "prompt": n_prompt, "tokens_per_step": tg,
+                   "step_mode": "persistent" if info.persistent else "one launch per phase",
                    "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "kernel": kname,
                      "achieved": round(k_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
@@ -378,9 +465,10 @@ def main():
                           "stream_gbps": round(stream, 1), "frac_of_stream": round(achieved_step / stream, 4),
                           "roofline_tok_s": round(stream * 1e9 / bpt, 1)},
         "stream_gbps": round(stream, 1),
+        "phases": phases, "profiled_step_us": prof_total,
         "gemv": micro,
         "attention_depth": attn,
-        "device_decode_ms": round(st["decode_ms"], 3),
+        "device_decode_ms": round(dev_ms, 3),
         "cpu_baseline": cpu,
         "speculative": spec,
         "verify_step": verify,

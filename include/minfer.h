@@ -201,12 +201,17 @@ typedef struct mi_synth_shape {
     int32_t head_type;     /* output.weight: 0 or 2 q4_0, 8 q8_0, 14 q6_K (real Qwen files carry q6_K) */
     int32_t down_type;     /* ffn_down.weight: 0 or 2 q4_0, 3 q4_1 (llama.cpp's q4_0 recipe) */
     int32_t tied;          /* 1: no output.weight, the embedding serves as lm_head */
+    float qk_bias_std;     /* > 0: attn_q/attn_k biases N(0, qk_bias_std) instead of N(0, 0.02) */
+    float norm_offset;     /* != 0: norm weights norm_offset + N(0, 0.02) (real models carry ~1) */
 } mi_synth_shape;
 /* Writes a seeded random-init qwen2 GGUF: q4_0 matrices (uniform nibbles, fp16
  * |N(0,0.002)| scales), fp32 N(0,0.02) norms/biases/embedding, a token list of
  * n_vocab entries. Same seed -> same bytes. Other matrix types, when asked for, have
- * random codes with scales of a similar weight range. No reference counterpart (the
- * reference runs downloaded Qwen files, README.md:58). */
+ * random codes with scales of a similar weight range. qk_bias_std and norm_offset
+ * (0: off) give attention scores of order 1 (parity tests of RoPE and the GQA head
+ * mapping need them; at the defaults the scores are ~1e-2 and attention is near
+ * uniform). No reference counterpart (the reference runs downloaded Qwen files,
+ * README.md:58). */
 int mi_synth_gguf(const char* path, const mi_synth_shape* shape, uint64_t seed);
 
 /* ---------------- kernel-level entry points (device pointers) ----------------

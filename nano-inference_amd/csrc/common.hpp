@@ -84,7 +84,8 @@ struct DModel {
     // its (token, margin bits) as one 64-bit word to ring[pos], pinned host memory the
     // host polls while later launches run (mega.cu:847-856, 1165-1178)
     uint64_t* ring;                // [maxseq] device address of the mapped host ring
-    int32_t eos;                   // the GGUF's eos token: a kGenRing launch whose input is eos does nothing
+    int32_t eos;                   // the GGUF's eos token when generation stops there, else -1: a kGenRing
+                                   // launch whose input is eos does nothing
     // multi-token steps (T <= kMaxT tokens at positions pos..pos+T-1, one launch per
     // phase): per-token copies of the exchange buffers, token index after the segment
     int32_t* posT;                 // [1] position of the step's first token (set before each launch sequence)

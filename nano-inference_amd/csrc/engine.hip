@@ -475,7 +475,10 @@ static int load_impl(mi_engine* e, const char* path) {
     HIPCHK(e, hipHostMalloc((void**)&e->h_ring, sizeof(uint64_t) * (size_t)e->maxseq,
                             hipHostMallocMapped | hipHostMallocCoherent));
     HIPCHK(e, hipHostGetDevicePointer((void**)&M.ring, e->h_ring, 0));
-    M.eos = e->eos;
+    // a kGenRing launch whose input token is M.eos does nothing: only when generation
+    // stops at eos; with stop_eos off an eos is an ordinary token and the steps go on
+    // (the reference's RAWIDS mode keeps generating past it, cuda_infer.cu:1192)
+    M.eos = e->opts.stop_eos ? e->eos : -1;
     e->M_logits = M;
     if ((rc = alloc_buf(e, &e->M_logits.logits, (size_t)e->V))) return rc;
     if ((rc = alloc_buf(e, &e->M_logits.logitsT, TM * e->V))) return rc;

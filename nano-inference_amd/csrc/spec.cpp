@@ -28,18 +28,27 @@ int32_t mi_ngram_draft(const int32_t* h, int32_t len, int32_t ngmax, int32_t kma
     return 0;
 }
 
-// Draft length K in 0..tmax-1 that maximises the expected tokens per unit of step
-// cost when each draft is accepted with probability alpha: E(K) = (1-alpha^(K+1)) /
-// (1-alpha) tokens for a step costing 1 + slope*K single-token steps. K = 0 scores 1.
+// Draft length for the next verify step. A step that carries k drafts costs 1 + slope*k
+// single-token steps and, when each draft survives with probability alpha independently,
+// yields (1 - alpha^(k+1)) / (1 - alpha) tokens on average (the accepted prefix plus the
+// correction). Returns the k in 0..tmax-1 with the highest yield per unit of cost; k = 0
+// (a plain step) yields exactly one token per unit, and a larger k must beat the best so
+// far strictly. alpha^(k+1) is built by repeated multiplication, so the choice matches
+// the reference's rule (mega.cu:581-589) float for float.
 int32_t mi_best_draft_len(float alpha, float slope, int32_t tmax) {
-    int kb = 0;
-    float vb = 1.f, pw = alpha;
-    for (int K = 1; K < tmax; K++) {
-        pw *= alpha;   // alpha^(K+1)
-        const float v = (1.f - pw) / (1.f - alpha) / (1.f + slope * K);
-        if (v > vb) { vb = v; kb = K; }
+    int32_t best_k = 0;
+    float best_rate = 1.f;
+    float all_accepted = alpha;                    // alpha^(k+1) once updated for k
+    for (int32_t k = 1; k < tmax; ++k) {
+        all_accepted *= alpha;
+        const float expected_tokens = (1.f - all_accepted) / (1.f - alpha);
+        const float rate = expected_tokens / (1.f + slope * k);
+        if (rate > best_rate) {
+            best_rate = rate;
+            best_k = k;
+        }
     }
-    return kb;
+    return best_k;
 }
 
 }  // extern "C"

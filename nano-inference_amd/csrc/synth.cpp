@@ -6,7 +6,10 @@
 // token_embd.weight, output_norm.weight, output.weight and the per-layer
 // attention/FFN tensors with q/k/v biases. Distributions:
 // q4_0 matrices with uniform nibbles 0..15 and fp16 |N(0, 0.002)| scales; norms,
-// biases and the embedding fp32 N(0, 0.02).
+// biases and the embedding fp32 N(0, 0.02). Two optional knobs (off in every BASELINE
+// config) make attention matter: q/k biases N(0, qk_bias_std) and norm weights
+// norm_offset + N(0, 0.02), which give O(1) attention scores that depend on the
+// relative position, so a RoPE or head-mapping mistake changes the output.
 //
 // Determinism: every tensor is cut into fixed segments, each filled from its own
 // splitmix64 stream keyed by (seed, tensor index, segment index), and normals come
@@ -271,7 +274,16 @@ extern "C" int mi_synth_gguf(const char* path, const mi_synth_shape* sh, uint64_
     for (size_t i = 0; i < ts.size() && w.ok; i++) {
         Out& t = ts[i];
         int64_t n = 1; for (auto e : t.ne) n *= e;
-        if (t.type == mi::GT_F32) fill_f32(t, seed, i, n, 0.02f);
+        if (t.type == mi::GT_F32) {
+            const bool qk_bias = t.name.find("attn_q.bias") != std::string::npos ||
+                                 t.name.find("attn_k.bias") != std::string::npos;
+            const bool norm = t.name.find("norm.weight") != std::string::npos;
+            fill_f32(t, seed, i, n, qk_bias && sh->qk_bias_std > 0.f ? sh->qk_bias_std : 0.02f);
+            if (norm && sh->norm_offset != 0.f) {
+                float* p = reinterpret_cast<float*>(t.bytes.data());
+                for (int64_t k = 0; k < n; k++) p[k] += sh->norm_offset;
+            }
+        }
         else if (t.type == mi::GT_Q4_0) fill_q4(t, seed, i, n / 32, 0.002f);
         else fill_blocks(t, seed, i, t.type == mi::GT_Q6_K ? n / 256 : n / 32, 0.002f);
         pos = ftell(f);

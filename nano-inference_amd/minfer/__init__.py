@@ -48,7 +48,8 @@ class Stats(C.Structure):
 class SynthShape(C.Structure):
     _fields_ = [("n_layer", C.c_int32), ("n_embd", C.c_int32), ("n_ff", C.c_int32), ("n_head", C.c_int32),
                 ("n_head_kv", C.c_int32), ("n_vocab", C.c_int32), ("rope_base", C.c_float), ("rms_eps", C.c_float),
-                ("emb_type", C.c_int32), ("head_type", C.c_int32), ("down_type", C.c_int32), ("tied", C.c_int32)]
+                ("emb_type", C.c_int32), ("head_type", C.c_int32), ("down_type", C.c_int32), ("tied", C.c_int32),
+                ("qk_bias_std", C.c_float), ("norm_offset", C.c_float)]
 
 
 TOKEN_CB = C.CFUNCTYPE(C.c_int, C.c_int32, C.c_void_p)
@@ -128,14 +129,15 @@ GT_Q4_0, GT_Q4_1, GT_Q8_0, GT_Q6_K = 2, 3, 8, 14
 
 
 def synth_gguf(path, shape, seed, rope_base=1e6, rms_eps=1e-6, emb_q4=False, emb_type=None, head_type=0,
-               down_type=0, tied=False):
+               down_type=0, tied=False, qk_bias_std=0.0, norm_offset=0.0):
     """Write a seeded random-init qwen2 GGUF (mi_synth_gguf). shape: name or dict.
     emb_type 0/2/8 (F32, q4_0, q8_0), head_type 2/8/14 (q4_0, q8_0, q6_K), down_type 2/3
-    (q4_0, q4_1), tied: no output.weight (0 means the default of each)."""
+    (q4_0, q4_1), tied: no output.weight (0 means the default of each). qk_bias_std /
+    norm_offset: attention scores of order 1 (0 = the BASELINE distributions)."""
     d = SHAPES[shape] if isinstance(shape, str) else shape
     et = emb_type if emb_type is not None else (2 if emb_q4 else 0)
     s = SynthShape(d["n_layer"], d["n_embd"], d["n_ff"], d["n_head"], d["n_head_kv"], d["n_vocab"],
-                   rope_base, rms_eps, et, head_type, down_type, 1 if tied else 0)
+                   rope_base, rms_eps, et, head_type, down_type, 1 if tied else 0, qk_bias_std, norm_offset)
     _check(lib().mi_synth_gguf(path.encode(), C.byref(s), C.c_uint64(seed)))
     return path
 

@@ -47,7 +47,7 @@ void orc_rope_cs(int pos, int i, int hd, float base, float* c, float* s) {
     *s = sinf(theta);
 }
 
-/* cpu_infer.cpp:49-61 */
+/* cpu_infer.cpp:49-61 (exported as orc_rope_fp32) */
 static void rope(float* v, int n_head, int hd, int pos, float base) {
     int half = hd / 2;
     for (int h = 0; h < n_head; h++) {
@@ -61,6 +61,8 @@ static void rope(float* v, int n_head, int hd, int pos, float base) {
         }
     }
 }
+
+void orc_rope_fp32(float* v, int n_head, int hd, int pos, float base) { rope(v, n_head, hd, pos, base); }
 
 /* cpu_infer.cpp:121-140 for one head */
 void orc_attention_fp32(const float* qh, const float* k, const float* v, int L, int hd,

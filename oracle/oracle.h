@@ -130,6 +130,11 @@ void orc_attention_fp32(const float* q, const float* k, const float* v, int L, i
                         int stride, float scale, float* out);
 /* RoPE cos/sin for (pos, i) exactly as cpu_infer computes them (cpu_infer.cpp:54-55) */
 void orc_rope_cs(int pos, int i, int hd, float base, float* c, float* s);
+/* NEOX RoPE in place over n_head heads of hd floats: pairs (i, i + hd/2) rotated by
+ * the angle with cos c[i], sin s[i] (the q8act mode's rotation, as the GPU computes it) */
+void orc_rope_rotate(float* v, int n_head, int hd, const float* c, const float* s);
+/* the fp32 mode's RoPE at position pos (cpu_infer.cpp:49-61, angle from powf/cosf/sinf) */
+void orc_rope_fp32(float* v, int n_head, int hd, int pos, float base);
 
 #ifdef __cplusplus
 }

@@ -226,6 +226,12 @@ static int rows_q8(const orc_tensor* W, const orc_plan* P, int kind, const struc
     return 0;
 }
 
+/* NEOX RoPE of n_head heads (cpu_infer.cpp:49-61): pair (i, i + hd/2) rotated by the
+ * angle whose cos/sin are c[i], s[i]: (x0, x1) -> (x0 c - x1 s, x0 s + x1 c), the four
+ * products rounded separately (no fma). Exported as orc_rope_rotate. Parity: known
+ * answers (a quarter turn maps (x, y) to (-y, x)) and a float64 rotation
+ * (tests/test_oracle_numerics.py), and the attention-sensitive golden model, where a
+ * flipped sign moves the logits by ~2x their range (tests/test_oracle_golden.py). */
 static void rope_q8(float* v, int n_head, int hd, const float* c, const float* s) {
     const int half = hd / 2;
     for (int h = 0; h < n_head; h++) {
@@ -238,6 +244,8 @@ static void rope_q8(float* v, int n_head, int hd, const float* c, const float* s
         }
     }
 }
+
+void orc_rope_rotate(float* v, int n_head, int hd, const float* c, const float* s) { rope_q8(v, n_head, hd, c, s); }
 
 /* one decode step in the GPU engine's numerics; see the table at the top */
 int32_t orc_forward_q8act(struct orc_model* m, int32_t token, int32_t pos) {

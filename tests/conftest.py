@@ -23,10 +23,11 @@ def tmpdir_mi():
 
 def synth_cached(name, shape, seed, expect_hash=None, **types):
     """Regenerate a synthetic GGUF (or reuse an identical one) under TMP. types:
-    emb_type / head_type / down_type / tied, as minfer.synth_gguf takes them."""
+    emb_type / head_type / down_type / tied / qk_bias_std / norm_offset, as
+    minfer.synth_gguf takes them."""
     import minfer
     os.makedirs(TMP, exist_ok=True)
-    tag = "".join("-%s%s" % (k, int(v)) for k, v in sorted(types.items()))
+    tag = "".join("-%s%s" % (k, "%g" % v) for k, v in sorted(types.items()))
     path = os.path.join(TMP, "%s-%d%s.gguf" % (name, seed, tag))
     marker = path + ".ok"
     if not (os.path.exists(path) and os.path.exists(marker)):

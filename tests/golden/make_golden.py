@@ -9,7 +9,12 @@ prove the regeneration.
     python tests/golden/make_golden.py [config0] [config2] [tiny] [mixed]
 
 `mixed` is the tiny shape with the tensor types of a real Qwen2.5 q4_0 file
-(q6_K output.weight, q4_1 ffn_down) and a q8_0 token embedding.
+(q6_K output.weight, q4_1 ffn_down) and a q8_0 token embedding. `attn` (head_dim
+128) and `attn64` (head_dim 64) are attention-sensitive models: q/k biases
+N(0, 2) and norm weights 1 + N(0, 0.02) give attention scores of order 1 that
+depend on the relative position, so the streams pin RoPE and the GQA head
+mapping (with the BASELINE distributions attention is near uniform and a
+RoPE sign flip leaves the greedy stream unchanged).
 """
 import json
 import os
@@ -27,6 +32,8 @@ REF = os.path.join(ROOT, "oracle", "_ref", "cpu_infer")
 TMP = os.environ.get("MI_TMP", "/tmp/mi")
 TINY = dict(n_layer=2, n_embd=256, n_ff=512, n_head=4, n_head_kv=2, n_vocab=4096)
 MIXED = dict(head_type=minfer.GT_Q6_K, down_type=minfer.GT_Q4_1, emb_type=minfer.GT_Q8_0)
+ATTN = dict(n_layer=2, n_embd=512, n_ff=1024, n_head=4, n_head_kv=2, n_vocab=4096)
+SHARP = dict(qk_bias_std=2.0, norm_offset=1.0)
 
 
 def file_hash(path):
@@ -66,6 +73,10 @@ if __name__ == "__main__":
             run("tiny", TINY, 7, 8, 8, 64)
         elif w == "mixed":
             run("mixed", TINY, 17, 18, 12, 64, types=MIXED)
+        elif w == "attn":
+            run("attn", ATTN, 31, 32, 12, 64, types=SHARP)
+        elif w == "attn64":
+            run("attn64", TINY, 33, 34, 12, 64, types=SHARP)
         else:
             shape, ms, ps, npr, ng = minfer.CONFIGS[w]
             run(w, shape, ms, ps, npr, ng)

@@ -68,6 +68,8 @@ def lib():
             "orc_attention_canon": (None, [_P, _P, _P, C.c_int, C.c_int, C.c_int, C.c_float, C.c_int, _P]),
             "orc_attention_fp32": (None, [_P, _P, _P, C.c_int, C.c_int, C.c_int, C.c_float, _P]),
             "orc_rope_cs": (None, [C.c_int, C.c_int, C.c_int, C.c_float, _F, _F]),
+            "orc_rope_rotate": (None, [_P, C.c_int, C.c_int, _P, _P]),
+            "orc_rope_fp32": (None, [_P, C.c_int, C.c_int, C.c_int, C.c_float]),
             "orc_dequant_row": (None, [_P, C.c_int64, _P]),
             "orc_dequant_row_fma": (None, [_P, C.c_int64, _P]),
             "orc_requant_q4_0_row": (None, [_P, C.c_int, _P]),
@@ -121,6 +123,33 @@ def attention_fp32(q, k, v, L, hd, stride, scale):
     out = np.zeros(hd, np.float32)
     lib().orc_attention_fp32(ptr(q), ptr(k), ptr(v), L, hd, stride, C.c_float(scale), ptr(out))
     return out
+
+
+def rope_rotate(v, n_head, hd, c, s):
+    """the q8act mode's NEOX rotation (orc_rope_rotate) of a copy of v [n_head*hd]"""
+    v = np.array(v, dtype=np.float32)
+    c = np.ascontiguousarray(c, dtype=np.float32)
+    s = np.ascontiguousarray(s, dtype=np.float32)
+    lib().orc_rope_rotate(ptr(v), n_head, hd, ptr(c), ptr(s))
+    return v
+
+
+def rope_fp32(v, n_head, hd, pos, base):
+    """the fp32 mode's RoPE (orc_rope_fp32, cpu_infer.cpp:49-61) of a copy of v"""
+    v = np.array(v, dtype=np.float32)
+    lib().orc_rope_fp32(ptr(v), n_head, hd, pos, C.c_float(base))
+    return v
+
+
+def rope_cs(pos, hd, base):
+    """cos/sin of every pair at position pos as cpu_infer computes them"""
+    c = np.zeros(hd // 2, np.float32)
+    s = np.zeros(hd // 2, np.float32)
+    for i in range(hd // 2):
+        cc, ss = C.c_float(), C.c_float()
+        lib().orc_rope_cs(pos, i, hd, C.c_float(base), C.byref(cc), C.byref(ss))
+        c[i], s[i] = cc.value, ss.value
+    return c, s
 
 
 class Model:

@@ -3,8 +3,9 @@ CPU oracle in q8act mode with the engine's own reduction plan.
 
 Bar: logits bit-identical at every position (hence within any 1e-3 tolerance),
 greedy token streams identical over 128 steps. Agreement with the fp32
-cpu_infer semantics is reported as tokens-to-first-divergence plus the margin
-there (the int8 activations make exact agreement with fp32 a matter of luck).
+cpu_infer semantics (the reference's own token streams, tests/golden) is asserted
+as far as int8 activations allow it: a stream may leave the reference's only
+where the fp32 top-2 margin is within twice the measured int8 logit error.
 """
 import json
 import os
@@ -48,10 +49,21 @@ def golden(name):
 MODES = [pytest.param(1, id="persistent"), pytest.param(0, id="per-phase")]
 
 
+def sharp_model(name):
+    """the attention-sensitive golden models (O(1) attention scores): attn = head_dim
+    128 (E 512, 4/2 heads), attn64 = head_dim 64"""
+    fx = golden(name)
+    return synth_cached(fx["config"], fx["shape"], fx["model_seed"], **fx["types"]), fx
+
+
 @pytest.mark.parametrize("persistent", MODES)
-@pytest.mark.parametrize("shape,seed", [(TINY, 7), (SMALL, 21)])
+@pytest.mark.parametrize("shape,seed", [(TINY, 7), (SMALL, 21), ("attn", 0), ("attn64", 0)])
 def test_step_logits_bit_exact(shape, seed, persistent):
-    path = synth_cached("eng-%d" % shape["n_embd"], shape, seed)
+    if isinstance(shape, str):
+        path, fx = sharp_model(shape)
+        shape, seed = fx["shape"], fx["prompt_seed"]
+    else:
+        path = synth_cached("eng-%d" % shape["n_embd"], shape, seed)
     say("step logits", path, "persistent" if persistent else "per-phase")
     eng = minfer.Engine(path, max_ctx=256, persistent=persistent)
     assert eng.info.persistent == persistent
@@ -113,6 +125,30 @@ def test_config_stream_128(name, persistent):
     d = first_divergence(toks, fx["tokens"])
     say("%s vs fp32 cpu_infer: first divergence at %d of 128 (margin there %.4f)"
         % (name, d, margins[d] if d < len(margins) else float("nan")))
+    if d < 128 and persistent:
+        # the int8 activations move logits by up to ~1% of their range against fp32
+        # (measured: config0 1.2%, config2 1.0% max-abs); a greedy stream may leave the
+        # reference's only where the fp32 top-2 gap is within twice that
+        fm, frel = fp32_margin_at(path, fx["prompt"], fx["tokens"], d)
+        say("%s: fp32 margin at the divergence %.6f = %.5f of the logit range" % (name, fm, frel))
+        assert frel < FP32_TIE_BOUND, "diverged from cpu_infer at %d where its margin is %.4f of the range" % (d, frel)
+
+
+# a divergence from the fp32 reference stream must fall on a near tie: fp32 margin below
+# this fraction of max |logit| (twice the measured int8-activation logit error)
+FP32_TIE_BOUND = 0.02
+
+
+def fp32_margin_at(path, prompt, ref_tokens, d):
+    """margin (and margin / max |logit|) of the fp32 oracle's prediction of reference
+    token d, teacher-forced on the prompt and ref_tokens[:d]"""
+    seq = list(prompt) + list(ref_tokens[:d])
+    m = O.Model(path, O.MODE_FP32, max_seq=len(seq) + 2)
+    for pos, tok in enumerate(seq):
+        t, mg, lg = m.forward(tok, pos, True)
+    m.close()
+    assert t == ref_tokens[d]
+    return mg, mg / float(np.abs(lg).max())
 
 
 def gguf_tensor_data(path):
@@ -257,6 +293,16 @@ def test_streaming_generate():
     _, _, lb = ref.step(want[first], pos, want_logits=True)
     ref.close()
     assert np.array_equal(la.view(np.uint32), lb.view(np.uint32))
+    # without stop_eos the eos is an ordinary token (the reference's RAWIDS mode generates
+    # past it): a callback (streamed through the ring) must give the whole batch stream
+    say("streaming: eos passed through without stop_eos")
+    eng = minfer.Engine(stop_path, max_ctx=256, stop_eos=0)
+    eng.prefill(ids)
+    seen = []
+    got, gm = eng.generate(40, callback=lambda t: seen.append(t) and False)
+    assert got == want and seen == want
+    assert np.array_equal(np.float32(gm).view(np.uint32), np.float32(wm).view(np.uint32))
+    eng.close()
 
 
 @pytest.mark.parametrize("mode", [dict(persistent=1), dict(persistent=0), dict(persistent=1, spec=1)],
@@ -372,6 +418,49 @@ def test_long_context_chunk_merge_phase():
         res[persistent] = (toks, np.float32(margins).view(np.uint32))
         eng.close()
     orc = O.Model(path, O.MODE_Q8ACT, plan=plan_of(minfer.Engine(path, max_ctx=1200)), max_seq=1200)
+    rt, rm, _, _ = orc.generate(ids, 12)
+    rm = np.float32(rm).view(np.uint32)
+    for persistent in (1, 0):
+        assert res[persistent][0] == rt, persistent
+        assert np.array_equal(res[persistent][1], rm), persistent
+
+
+@pytest.mark.parametrize("name", ["attn", "attn64"])
+def test_attention_sensitive_stream(name):
+    """the attention-sensitive golden models (RoPE and the head mapping decide the
+    tokens): greedy stream and margins bit-identical to q8act, and the stream equals
+    the reference cpu_infer's fixture"""
+    path, fx = sharp_model(name)
+    say("%s stream 64" % name)
+    toks, margins, plan = run_stream(path, fx["prompt"], 64, max_ctx=128)
+    orc = O.Model(path, O.MODE_Q8ACT, plan=plan, max_seq=len(fx["prompt"]) + 70)
+    rt, rm, _, _ = orc.generate(fx["prompt"], 64)
+    assert toks == rt, "first difference at %d" % first_divergence(toks, rt)
+    assert np.array_equal(np.float32(margins).view(np.uint32), np.float32(rm).view(np.uint32))
+    d = first_divergence(toks, fx["tokens"])
+    say("%s vs fp32 cpu_infer: first divergence at %d of 64" % (name, d))
+    if d < 64:
+        _, frel = fp32_margin_at(path, fx["prompt"], fx["tokens"], d)
+        assert frel < FP32_TIE_BOUND, (d, frel)
+
+
+def test_long_context_merge_phase_hd128():
+    """head_dim 128 past 16 chunks (the merge phase and its two-level tree, records laid
+    out DPL*lane + e) on the attention-sensitive model: 1090-token prompt + 12 tokens,
+    both step modes, tokens and margins vs the q8act oracle"""
+    path, fx = sharp_model("attn")
+    V = fx["shape"]["n_vocab"]
+    say("hd128 long context 1100 positions")
+    ids = minfer.prompt_ids(41, 1090, V)
+    res = {}
+    for persistent in (1, 0):
+        eng = minfer.Engine(path, max_ctx=1200, persistent=persistent)
+        eng.prefill(ids)
+        toks, margins = eng.generate(12)
+        res[persistent] = (toks, np.float32(margins).view(np.uint32))
+        plan = plan_of(eng)
+        eng.close()
+    orc = O.Model(path, O.MODE_Q8ACT, plan=plan, max_seq=1200)
     rt, rm, _, _ = orc.generate(ids, 12)
     rm = np.float32(rm).view(np.uint32)
     for persistent in (1, 0):

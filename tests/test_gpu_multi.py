@@ -115,6 +115,55 @@ def test_long_context_multi_merge_phase(pos, T):
     eng.close()
 
 
+def test_long_context_multi_hd128():
+    """head_dim 128 at context 1020 + 8 (16 and 17 chunks: the merge tree) on the
+    attention-sensitive model (O(1) scores): T = 8 against eight single steps"""
+    import json, os
+    with open(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "cpu_infer_attn.json")) as f:
+        fx = json.load(f)
+    path = synth_cached(fx["config"], fx["shape"], fx["model_seed"], **fx["types"])
+    V = fx["shape"]["n_vocab"]
+    say("hd128 long context pos 1020 T 8")
+    eng = minfer.Engine(path, max_ctx=1100)
+    prompt = minfer.prompt_ids(43, 1020, V)
+    multi_vs_single(eng, prompt, 1020, 8, 29, V)
+    eng.close()
+
+
+def test_config4_verify_step_bit_identical():
+    """BASELINE config 4 at its own workload: S3 (hidden 2048, 36 layers, 16/2 heads,
+    FF 11008), a 1024-token context, one 8-token verify step (the current token + 7
+    drafts, TMAX = 8, mega.cu:50) bit-identical to the 8 tokens stepped one at a time"""
+    name = "config4"
+    cfg = minfer.CONFIGS[name]
+    shape = minfer.SHAPES[cfg[0]]
+    path = synth_cached(name, shape, cfg[1])
+    say("config4 (S3) context 1024 T 8")
+    eng = minfer.Engine(path, max_ctx=cfg[3] + 16)
+    prompt = minfer.prompt_ids(cfg[2], cfg[3], shape["n_vocab"])
+    multi_vs_single(eng, prompt, cfg[3], 8, cfg[2] + 1, shape["n_vocab"])
+    eng.close()
+
+
+def test_config4_short_context_oracle():
+    """S3 against the q8act oracle at a short context: an 8-token prompt stepped one
+    at a time, then an 8-token step, every position's logits bit for bit"""
+    cfg = minfer.CONFIGS["config4"]
+    shape = minfer.SHAPES[cfg[0]]
+    path = synth_cached("config4", shape, cfg[1])
+    say("config4 (S3) pos 8 T 8 + oracle")
+    eng = minfer.Engine(path, max_ctx=64)
+    prompt = minfer.prompt_ids(cfg[2] + 2, 8, shape["n_vocab"])
+    toks, lg = multi_vs_single(eng, prompt, 8, 8, cfg[2] + 3, shape["n_vocab"])
+    p = eng.plan
+    eng.close()
+    orc = O.Model(path, O.MODE_Q8ACT, plan=O.Plan.make(p["cb"], p["ks"], p["attn_chunk"], p["kv_f16"]), max_seq=64)
+    for i, tok in enumerate(list(prompt) + list(toks)):
+        _, _, lo = orc.forward(tok, i, True)
+        if i >= 8:
+            assert np.array_equal(bits(lo), bits(lg[i - 8])), "oracle differs at pos %d" % i
+
+
 def test_graph_replays_equal_direct_launches():
     """The multi-token step replays one captured HIP graph per (T, logits) with the
     position read from device memory. Replays at several positions, with eager

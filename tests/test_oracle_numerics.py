@@ -206,6 +206,60 @@ def test_rope_cs_float_theta():
     assert c.value == 1.0 and s.value == 0.0
 
 
+@pytest.mark.parametrize("hd", [64, 128])
+def test_rope_rotate_known_answers(hd):
+    """NEOX RoPE (cpu_infer.cpp:49-61) rotates pair (i, i + hd/2) counter-clockwise:
+    a quarter turn (cos 0, sin 1) maps (x, y) to (-y, x), a half turn to (-x, -y), and
+    no other element moves. A flipped sign gives (y, -x); adjacent pairs (2i, 2i+1),
+    the GPT-J layout, move other elements."""
+    rng = np.random.default_rng(hd)
+    nh, half = 3, hd // 2
+    v = rng.standard_normal(nh * hd).astype(np.float32)
+    x, y = v.reshape(nh, hd)[:, :half], v.reshape(nh, hd)[:, half:]
+    quarter = O.rope_rotate(v, nh, hd, np.zeros(half), np.ones(half)).reshape(nh, hd)
+    assert np.array_equal(quarter[:, :half], -y) and np.array_equal(quarter[:, half:], x)
+    halfturn = O.rope_rotate(v, nh, hd, -np.ones(half), np.zeros(half)).reshape(nh, hd)
+    assert np.array_equal(halfturn, -v.reshape(nh, hd))
+    # one pair at a quarter turn, the rest at angle 0: only that pair changes
+    c, s = np.ones(half), np.zeros(half)
+    c[5], s[5] = 0.0, 1.0
+    one = O.rope_rotate(v, nh, hd, c, s).reshape(nh, hd)
+    moved = np.argwhere(one != v.reshape(nh, hd))[:, 1]
+    assert set(moved.tolist()) == {5, 5 + half}
+    assert np.array_equal(one[:, 5], -y[:, 5]) and np.array_equal(one[:, 5 + half], x[:, 5])
+
+
+@pytest.mark.parametrize("pos", [1, 7, 100, 1023, 32767])
+def test_rope_matches_float64_rotation(pos):
+    """both modes' RoPE against a float64 rotation by theta_i = pos * base^(-2i/hd):
+    norms of every pair are kept, and q.k of two rotated vectors depends only on the
+    position difference (the property attention relies on)"""
+    hd, nh, base, half = 128, 2, 1e6, 64
+    rng = np.random.default_rng(pos)
+    v = rng.standard_normal(nh * hd).astype(np.float32)
+    th = pos * base ** (-2.0 * np.arange(half) / hd)
+    vv = v.astype(np.float64).reshape(nh, hd)
+    ref = np.concatenate([vv[:, :half] * np.cos(th) - vv[:, half:] * np.sin(th),
+                          vv[:, :half] * np.sin(th) + vv[:, half:] * np.cos(th)], axis=1)
+    c, s = O.rope_cs(pos, hd, base)
+    # float32 theta: |theta| <= pos, so its rounding error is ~pos * 6e-8
+    tol = 1e-5 + pos * 2.4e-7
+    for got in (O.rope_rotate(v, nh, hd, c, s), O.rope_fp32(v, nh, hd, pos, base)):
+        got = got.astype(np.float64).reshape(nh, hd)
+        assert np.abs(got - ref).max() <= tol * np.abs(vv).max()
+        pn = lambda a: a[:, :half] ** 2 + a[:, half:] ** 2
+        assert np.allclose(pn(got), pn(vv), rtol=1e-5, atol=1e-6)
+    # relative position: rot(q, p+d) . rot(k, p) equals rot(q, d) . rot(k, 0)
+    q, k = v[:hd], v[hd:]
+    d = 5
+    cq, sq = O.rope_cs(pos + d, hd, base)
+    ck, sk = O.rope_cs(pos, hd, base)
+    c0, s0 = O.rope_cs(d, hd, base)
+    dot_far = float(np.dot(O.rope_rotate(q, 1, hd, cq, sq).astype(np.float64), O.rope_rotate(k, 1, hd, ck, sk)))
+    dot_near = float(np.dot(O.rope_rotate(q, 1, hd, c0, s0).astype(np.float64), k.astype(np.float64)))
+    assert abs(dot_far - dot_near) <= (1e-4 + pos * 5e-6) * np.linalg.norm(q) * np.linalg.norm(k)
+
+
 class _Tensor(__import__("ctypes").Structure):
     import ctypes as C
     _fields_ = [("type", C.c_uint32), ("nd", C.c_int32), ("ne", C.c_int64 * 4), ("data", C.c_void_p)]
