@@ -254,6 +254,19 @@ int mi_attn_decode(const float* q, const uint16_t* kc, const uint16_t* vc, int32
                    int32_t n_head_kv, int32_t hd, int32_t L, int32_t ctx, float scale,
                    float* scratch, float* out, void* stream);
 
+/* The same attention as mi_attn_decode without a workspace argument and without any
+ * allocation. No counterpart in the reference: it is for callers that cannot allocate
+ * (code under HIP graph capture, serving loops, harnesses that forbid hipMalloc). The
+ * scratch is a library-held device array of MI_ATTN_NOALLOC_SCRATCH_FLOATS floats (16 MiB,
+ * one per GPU, held until the process ends); a shape that needs more than
+ * mi_attn_scratch_floats() allows returns MI_ERR_SHAPE (message via mi_last_error(NULL)).
+ * The first call on a device looks the array up and zeroes its counters with a kernel on
+ * `stream`. All calls on one GPU share the array: calls that overlap on one GPU race. */
+#define MI_ATTN_NOALLOC_SCRATCH_FLOATS (4u << 20)
+int mi_attn_decode_noalloc(const float* q, const uint16_t* kc, const uint16_t* vc, int32_t n_head,
+                           int32_t n_head_kv, int32_t hd, int32_t L, int32_t ctx, float scale,
+                           float* out, void* stream);
+
 /* stream-read roofline (bench/roofline.cu:39-71 k_gridstride): one launch reading
  * `bytes` (multiple of 16) with several 16-byte loads in flight per thread */
 int mi_stream_read(const void* buf, size_t bytes, uint32_t* sink, void* stream);

@@ -1103,6 +1103,27 @@ int mi_attn_decode(const float* q, const uint16_t* kc, const uint16_t* vc, int32
     return hipGetLastError() == hipSuccess ? MI_OK : MI_ERR_DEVICE;
 }
 
+static_assert(kNoAllocScratchFloats == MI_ATTN_NOALLOC_SCRATCH_FLOATS, "scratch size in minfer.h and kernels.hpp");
+
+int mi_attn_decode_noalloc(const float* q, const uint16_t* kc, const uint16_t* vc, int32_t n_head, int32_t n_head_kv,
+                           int32_t hd, int32_t L, int32_t ctx, float scale, float* out, void* stream) {
+    if (!q || !kc || !vc || !out || n_head < 1 || n_head_kv < 1 || hd < 1 || L < 1 || L > ctx)
+        return set_err(nullptr, MI_ERR_ARG, "mi_attn_decode_noalloc: bad argument");
+    const size_t need = attn_scratch_floats(n_head, hd, L);
+    if (need > MI_ATTN_NOALLOC_SCRATCH_FLOATS)
+        return set_err(nullptr, MI_ERR_SHAPE,
+                       "mi_attn_decode_noalloc: %d heads of %d over %d positions need %zu scratch floats, more than "
+                       "the %u the library holds (use mi_attn_decode with a workspace)",
+                       n_head, hd, L, need, (unsigned)MI_ATTN_NOALLOC_SCRATCH_FLOATS);
+    float* scr = nullptr;
+    const hipError_t e = noalloc_scratch((hipStream_t)stream, &scr);
+    if (e != hipSuccess) return set_err(nullptr, MI_ERR_DEVICE, "mi_attn_decode_noalloc: %s", hipGetErrorString(e));
+    if (!launch_attn_decode(q, reinterpret_cast<const __half*>(kc), reinterpret_cast<const __half*>(vc), n_head,
+                            n_head_kv, hd, L, ctx, scale, scr, out, (hipStream_t)stream))
+        return set_err(nullptr, MI_ERR_SHAPE, "mi_attn_decode_noalloc: unsupported shape");
+    return hipGetLastError() == hipSuccess ? MI_OK : MI_ERR_DEVICE;
+}
+
 size_t mi_attn_scratch_floats(int32_t n_head, int32_t hd, int32_t L) {
     return n_head < 1 || hd < 1 || L < 1 ? 0 : attn_scratch_floats(n_head, hd, L);
 }

@@ -39,6 +39,7 @@
 
 #include <algorithm>
 #include <climits>
+#include <mutex>
 #include <type_traits>
 
 namespace mi {
@@ -2547,6 +2548,49 @@ bool launch_attn_decode(const float* q, const __half* kc, const __half* vc, int 
     });
     return true;
 }
+// ------------------------------------------------------------------ allocation-free attention
+// Scratch of mi_attn_decode_noalloc: a file-scope device array (each GPU the library
+// runs on holds its own copy until the process ends), laid out as the workspace of
+// launch_attn_decode: arrival counters, then chunk and split records. Host code never
+// passes the array's name to a kernel (on the host it is a stand-in, not a device
+// address): the per-device address comes from hipGetSymbolAddress at the first call
+// on each device. Calls on one device share the array, so calls that overlap on one
+// GPU race; each completed call leaves the counters zero.
+static __device__ __align__(256) float scratch[kNoAllocScratchFloats];
+
+__global__ void k_zero_words(uint32_t* p, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = 0u;
+}
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+float* g_scratch_ptr[kMaxDevices] = {};
+}  // namespace
+
+// the device address of the current device's scratch array; the first call on a device
+// looks it up and zeroes its arrival counters with a kernel on the caller's stream (no
+// memset node: callers may capture the stream into a graph)
+hipError_t noalloc_scratch(hipStream_t s, float** out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return e;
+        LAUNCH(k_zero_words, (kAttnCounters + 255) / 256, 256, s, static_cast<uint32_t*>(p), kAttnCounters);
+        e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        g_scratch_ptr[dev] = static_cast<float*>(p);
+    }
+    *out = g_scratch_ptr[dev];
+    return hipSuccess;
+}
+
 void launch_stream(const void* buf, size_t bytes, uint32_t* sink, int n_cu, hipStream_t s) {
     LAUNCH(k_stream, 8 * n_cu, kThreads, s, reinterpret_cast<const u32x4*>(buf), bytes / 16, sink);
 }

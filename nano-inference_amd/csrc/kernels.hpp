@@ -49,6 +49,11 @@ void launch_gemv(const PMat& W, const int8_t* xq, const float* xd, const int32_t
                  int n_cu, hipStream_t s);
 void launch_isums(const PMat& W, const int8_t* xq, int32_t* isum, hipStream_t s);
 size_t attn_scratch_floats(int nh, int hd, int L);
+// floats of the file-scope scratch array behind mi_attn_decode_noalloc (16 MiB per device)
+constexpr size_t kNoAllocScratchFloats = size_t(4) << 20;
+// device address of the current device's scratch array (looked up, and its counters
+// zeroed on stream s, at the first call on each device)
+hipError_t noalloc_scratch(hipStream_t s, float** out);
 bool launch_attn_decode(const float* q, const __half* kc, const __half* vc, int nh, int nkv, int hd, int L, int ctx,
                         float scale, float* scratch, float* out, hipStream_t s);
 void launch_stream(const void* buf, size_t bytes, uint32_t* sink, int n_cu, hipStream_t s);
