@@ -817,6 +817,29 @@ __device__ __forceinline__ int kswz(int t) { return HD == 128 ? (t & 15) : ((t >
 template <int HD>
 __device__ __forceinline__ int kslot(int t, int v) { return t * (HD / 8) + (v ^ kswz<HD>(t)); }
 
+// one wave's DMA of the K rows krows[0..64) of a chunk into the swizzled tile, and of its
+// V rows row-major (rows past n repeat row n-1), as attn_issue_kv below does both
+template <int HD>
+__device__ __forceinline__ void attn_issue_k(const __half* krows, int n, uint4* kls, int lane) {
+    constexpr int NV = HD / 8, RPI = 64 / NV;
+    const int u = lane % NV;
+#pragma unroll
+    for (int i = 0; i < NV; i++) {
+        const int t = i * RPI + lane / NV;
+        __builtin_amdgcn_global_load_lds(krows + (size_t)min(t, n - 1) * HD + 8 * (u ^ kswz<HD>(t)),
+                                         (lds_ptr)(kls + i * 64), 16, 0, 0);
+    }
+}
+template <int HD>
+__device__ __forceinline__ void attn_issue_v(const __half* vrows, int n, __half* vls, int lane) {
+    constexpr int NV = HD / 8, RPI = 64 / NV;
+    const int r = lane / NV, col = (lane % NV) * 8;
+#pragma unroll
+    for (int i = 0; i < 64 / RPI; i++)
+        __builtin_amdgcn_global_load_lds(vrows + (size_t)min(i * RPI + r, n - 1) * HD + col,
+                                         (lds_ptr)(vls + i * RPI * HD), 16, 0, 0);
+}
+
 // DMA the chunk's K rows (swizzled tile) and V rows; rows past n repeat row n-1. K load i
 // fills tile slots 64i..64i+63, i.e. rows (64/NV)i.. whole: lane l takes slot 64i + l =
 // (row t, place u) and fetches vector u ^ kswz(t) of row t, 1 KB of consecutive rows per
@@ -2060,107 +2083,19 @@ __global__ __launch_bounds__(64) void k_isums(PMat W, const int8_t* xq, int32_t*
 
 // ------------------------------------------------------------------ standalone attention
 // q[nh][hd] fp32 and an fp16 cache [nkv][ctx][hd]; one launch does the whole
-// attention. One item = (kv head, 64-position chunk, group of g query heads of that
-// kv head). The wave loads the chunk's K rows lane = position (16-byte pieces) and V
-// rows lane = dims (4 or 2 bytes per position) straight into registers, so K/V are
-// read once per item and never staged in LDS; the g heads then reuse them. Per head
-// the arithmetic is attn_core's: scores as four fma chains over d mod 4, the chunk
-// softmax with the 64-lane butterfly sum, p.v as an fma chain over positions.
-// The merge is comb_wave's order, done by the last arrivals: after its chunk records
-// (o[hd], m, l) are stored and drained, an item bumps its split's counter; the wave
-// that completes a split merges its chunks (and writes the output if there is one
-// split), then bumps the head group's counter, whose last arrival merges the splits.
-// Records are written with agent-coherent stores (through the per-XCD L2) and
-// drained before the arrival atomic; every record line has one writer and one
-// reader in a launch, and the merging wave reads it (by DMA) only after all its
-// writers arrived, so no L2 can hold an older copy. No wave ever waits on another.
-// Each last arrival puts its counter back to zero.
+// attention (k_attn_tile below). The merge is comb_wave's order, done by the last
+// arrivals: after its chunk records (o[hd], m, l) are stored and drained, a workgroup
+// bumps its split's counter; the one that completes a split merges its chunks (and
+// writes the output if there is one split), then bumps the kv head's counter, whose
+// last arrival merges the splits. Records are written with agent-coherent stores
+// (through the per-XCD L2) and drained before the arrival atomic; every record line
+// has one writer and one reader in a launch, and the merging wave reads it only after
+// all its writers arrived, so no L2 can hold an older copy. No wave ever waits on
+// another. Each last arrival puts its counter back to zero.
 // scratch: counters [kAttnCounters] (zero before the first call, left zero by each
 // call) | chunk records [nh][nch][hd + 32] | split records [nh][nsp][hd + 32].
-constexpr int kItemWaves = 4;       // waves per workgroup
-constexpr int kItemMaxG = 8;        // query heads one item can take
-constexpr int kItemWgsPerXcd = 64;  // two workgroups per CU
-constexpr int kItemTarget = 2048;   // items to aim for: two per SIMD
+constexpr int kAttnMaxG = 8;        // query heads per kv head
 constexpr int kAttnCounters = 1 << 16;
-
-template <int HD, bool FULL>
-__device__ __forceinline__ void attn_item_heads(const __half* kr, const __half* vr, int n, const float* qsrc, float* qg,
-                                                float* pg, int g, float scale, int lane, float* rec, size_t hstride) {
-    constexpr int NV = HD / 8, DPL = HD / 64;
-    using VT = typename std::conditional<DPL == 2, uint32_t, uint16_t>::type;
-    uint4 kw[NV];
-    VT vw[64];
-    const uint4* kp = reinterpret_cast<const uint4*>(kr + (size_t)(FULL ? lane : min(lane, n - 1)) * HD);
-#pragma unroll
-    for (int j = 0; j < NV; j++) kw[j] = kp[j];
-#pragma unroll
-    for (int t = 0; t < 64; t++)
-        vw[t] = *reinterpret_cast<const VT*>(vr + (size_t)(FULL ? t : min(t, n - 1)) * HD + DPL * lane);
-    for (int i = lane; i < g * HD; i += 64) qg[i] = qsrc[i];   // the g query rows, behind the K/V loads
-    wave_lds_sync();
-    float kf[HD];
-#pragma unroll
-    for (int j = 0; j < NV; j++) {
-        kf[8 * j + 0] = h2f_lo(kw[j].x); kf[8 * j + 1] = h2f_hi(kw[j].x);
-        kf[8 * j + 2] = h2f_lo(kw[j].y); kf[8 * j + 3] = h2f_hi(kw[j].y);
-        kf[8 * j + 4] = h2f_lo(kw[j].z); kf[8 * j + 5] = h2f_hi(kw[j].z);
-        kf[8 * j + 6] = h2f_lo(kw[j].w); kf[8 * j + 7] = h2f_hi(kw[j].w);
-    }
-    const bool valid = FULL || lane < n;
-    for (int hh = 0; hh < g; hh++) {
-        const float* qh = qg + hh * HD;
-        float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
-#pragma unroll
-        for (int j = 0; j < NV; j++) {
-            const float4 q0 = ld4(qh + 8 * j), q1 = ld4(qh + 8 * j + 4);
-            a0 = __fmaf_rn(q0.x, kf[8 * j + 0], a0); a1 = __fmaf_rn(q0.y, kf[8 * j + 1], a1);
-            a2 = __fmaf_rn(q0.z, kf[8 * j + 2], a2); a3 = __fmaf_rn(q0.w, kf[8 * j + 3], a3);
-            a0 = __fmaf_rn(q1.x, kf[8 * j + 4], a0); a1 = __fmaf_rn(q1.y, kf[8 * j + 5], a1);
-            a2 = __fmaf_rn(q1.z, kf[8 * j + 6], a2); a3 = __fmaf_rn(q1.w, kf[8 * j + 7], a3);
-        }
-        const float sc = __fmul_rn(__fadd_rn(__fadd_rn(a0, a1), __fadd_rn(a2, a3)), scale);
-        const float sv = valid ? sc : -__builtin_inff();
-        const float m = wave_max(sv);
-        const float p = valid ? mi_expf(__fsub_rn(sv, m)) : 0.f;
-        const float lsum = bfly_sum64(p);
-        pg[hh * 64 + lane] = p;
-        if (lane == 0) {
-            stc(rec + hh * hstride + HD, m);
-            stc(rec + hh * hstride + HD + 1, lsum);
-        }
-    }
-    wave_lds_sync();
-    float vf[64 * DPL];
-#pragma unroll
-    for (int t = 0; t < 64; t++) {
-        if constexpr (DPL == 2) {
-            vf[2 * t] = h2f_lo(vw[t]);
-            vf[2 * t + 1] = h2f_hi(vw[t]);
-        } else {
-            vf[t] = __half2float(__ushort_as_half(vw[t]));
-        }
-    }
-    for (int hh = 0; hh < g; hh++) {
-        const float* ph = pg + hh * 64;
-        float acc[DPL];
-#pragma unroll
-        for (int e = 0; e < DPL; e++) acc[e] = 0.f;
-#pragma unroll
-        for (int t4 = 0; t4 < 16; t4++) {
-            const float4 p4 = ld4(ph + 4 * t4);
-            const float pv[4] = {p4.x, p4.y, p4.z, p4.w};
-#pragma unroll
-            for (int u = 0; u < 4; u++)
-                if (FULL || 4 * t4 + u < n) {
-#pragma unroll
-                    for (int e = 0; e < DPL; e++) acc[e] = __fmaf_rn(pv[u], vf[(4 * t4 + u) * DPL + e], acc[e]);
-                }
-        }
-#pragma unroll
-        for (int e = 0; e < DPL; e++) stc(rec + hh * hstride + DPL * lane + e, acc[e]);
-    }
-    wave_lds_sync();   // the wave's q/p staging is reused by its next item
-}
 
 // One wave merges the records [c0, c1) of one head (contiguous, REC floats each)
 // as comb_wave does, lane = dims DPL*lane + e: M = max over all records, w_i =
@@ -2231,45 +2166,6 @@ __device__ __forceinline__ void rr_issue(RegRecs<HD, N>& b, const float* r, int 
         }
     }
 }
-template <int HD, int N>
-__device__ __forceinline__ void rr_merge(const RegRecs<HD, N>& b, int n, int lane, float& M, float& den,
-                                         float (&acc)[HD / 64]) {
-    constexpr int DPL = HD / 64;
-    M = wave_max(b.m);
-    const float w = lane < n ? mi_expf(__fsub_rn(b.m, M)) : 0.f;
-    const int wb = __float_as_int(w), lb = __float_as_int(b.l);
-    den = 0.f;
-#pragma unroll
-    for (int e = 0; e < DPL; e++) acc[e] = 0.f;
-#pragma unroll
-    for (int i = 0; i < N; i++) {
-        if (i < n) {
-            const float wi = __int_as_float(__builtin_amdgcn_readlane(wb, i));
-            den = __fmaf_rn(__int_as_float(__builtin_amdgcn_readlane(lb, i)), wi, den);
-#pragma unroll
-            for (int e = 0; e < DPL; e++) acc[e] = __fmaf_rn(b.o[i][e], wi, acc[e]);
-        }
-    }
-}
-// The merges of g heads (records of head hh at r0 + hh * hstride, n <= N of them),
-// two heads' records in flight at a time; done(hh, M, den, acc) takes each result.
-template <int HD, int N, class F>
-__device__ __forceinline__ void rr_heads(const float* r0, size_t hstride, int n, int g, int lane, F done) {
-    RegRecs<HD, N> a, b;
-    float M, den, acc[HD / 64];
-    rr_issue<HD, N>(a, r0, n, lane);
-    for (int hh = 0; hh < g; hh += 2) {
-        if (hh + 1 < g) rr_issue<HD, N>(b, r0 + (hh + 1) * hstride, n, lane);
-        rr_merge<HD, N>(a, n, lane, M, den, acc);
-        done(hh, M, den, acc);
-        if (hh + 1 < g) {
-            if (hh + 2 < g) rr_issue<HD, N>(a, r0 + (hh + 2) * hstride, n, lane);
-            rr_merge<HD, N>(b, n, lane, M, den, acc);
-            done(hh + 1, M, den, acc);
-        }
-    }
-}
-
 // the wave's arrival on a counter of `need` arrivals: true for the last one, which
 // puts the counter back to zero (every arrival of this launch is in by then)
 __device__ __forceinline__ bool last_arrival(uint32_t* cnt, uint32_t need, int lane) {
@@ -2282,80 +2178,258 @@ __device__ __forceinline__ bool last_arrival(uint32_t* cnt, uint32_t need, int l
     return true;
 }
 
-// Items of unit u = kvh * nch + c and head group hg go to XCD u % 8 (workgroups
-// x, x + 8, ... share XCD x), so the groups of one unit read its K/V through one L2.
-// Within XCD x the items k = (u / 8) * ngrp + hg are dealt to (workgroup, wave) in
-// turn; the grid is a multiple of 8.
-template <int HD, bool RR>
-__global__ __launch_bounds__(64 * kItemWaves) __attribute__((amdgpu_waves_per_eu(2))) void k_attn_fused(const float* q, const __half* kc, const __half* vc,
-                                                                int nh, int nkv, int L, int ctx, float scale, int g,
-                                                                float* scratch, float* out) {
-    constexpr int REC = HD + 32, DPL = HD / 64;
-    constexpr int WLDS = kItemMaxG * (HD + 64) > kAttnSplit * REC ? kItemMaxG * (HD + 64) : kAttnSplit * REC;
-    __shared__ __align__(16) float smem[kItemWaves * WLDS];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    float* qg = smem + wave * WLDS;
-    float* pg = qg + kItemMaxG * HD;
-    const int nch = (L + kAttnChunk - 1) / kAttnChunk, G = nh / nkv, ngrp = G / g, units = nkv * nch;
-    const int nsp = (nch + kAttnSplit - 1) / kAttnSplit;
-    uint32_t* scnt = reinterpret_cast<uint32_t*>(scratch);          // [nkv][nsp][ngrp]
-    uint32_t* hcnt = scnt + (size_t)nkv * nsp * ngrp;                // [nkv][ngrp]
-    float* recs = scratch + kAttnCounters;
-    float* srecs = recs + (size_t)nh * nch * REC;
-    const int per = gridDim.x / 8, x = blockIdx.x % 8;
-    for (int k = kItemWaves * (blockIdx.x / 8) + wave;; k += kItemWaves * per) {
-        const int u = 8 * (k / ngrp) + x, hg = k % ngrp;
-        if (u >= units) break;
-        const int kvh = u / nch, c = u % nch, h0 = kvh * G + hg * g, t0 = c * kAttnChunk, n = min(kAttnChunk, L - t0);
-        const size_t row = (size_t)kvh * ctx + t0;
-        float* rec = recs + ((size_t)h0 * nch + c) * REC;
-        if (n == kAttnChunk)
-            attn_item_heads<HD, true>(kc + row * HD, vc + row * HD, n, q + (size_t)h0 * HD, qg, pg, g, scale, lane, rec,
-                                      (size_t)nch * REC);
-        else
-            attn_item_heads<HD, false>(kc + row * HD, vc + row * HD, n, q + (size_t)h0 * HD, qg, pg, g, scale, lane,
-                                       rec, (size_t)nch * REC);
-        const int sp = c / kAttnSplit, c0 = sp * kAttnSplit, c1 = min(nch, c0 + kAttnSplit);
-        if (!last_arrival(scnt + ((size_t)kvh * nsp + sp) * ngrp + hg, c1 - c0, lane)) continue;
-        // level 1: the split's chunks -> the output or a split record
-        auto put1 = [&](int hh, float M, float den, const float (&acc)[DPL]) {
-            const int h = h0 + hh;
-            if (nsp == 1) {
+// attn_core for H query heads of one kv head at once (q rows at qs, qs + HD, ...; rows
+// past nq - 1 repeat row nq - 1): each head's arithmetic is attn_core's, the same chains
+// in the same order, so the results carry the same bits; the K and V values are read
+// from LDS once for the H heads and the heads' chains interleave (attn_core alone is a
+// chain of dependent fmas and LDS waits). The probabilities reach the p.v lanes through
+// the wave's LDS row pl[H][64] (one 16-byte broadcast read gives four positions; a
+// readlane per position and head cost more than the fmas it feeds).
+template <int HD, int H>
+__device__ __forceinline__ void attn_core_h(const uint4* kls, const float* qs, int nq, const __half* vls, int n,
+                                            float scale, int lane, float* pl, float (&m)[H], float (&lsum)[H],
+                                            float (&acc)[H][HD / 64]) {
+    constexpr int NV = HD / 8, DPL = HD / 64;
+    const float* qr[H];
 #pragma unroll
-                for (int e = 0; e < DPL; e++) out[(size_t)h * HD + DPL * lane + e] = __fdiv_rn(acc[e], den);
+    for (int h = 0; h < H; h++) qr[h] = qs + min(h, nq - 1) * HD;
+    float a[H][4];
+#pragma unroll
+    for (int h = 0; h < H; h++) a[h][0] = a[h][1] = a[h][2] = a[h][3] = 0.f;
+#pragma unroll 4
+    for (int j = 0; j < NV; j++) {
+        const uint4 w = kls[kslot<HD>(lane, j)];
+#pragma unroll
+        for (int h = 0; h < H; h++) {
+            const float4 q0 = *reinterpret_cast<const float4*>(qr[h] + 8 * j);
+            const float4 q1 = *reinterpret_cast<const float4*>(qr[h] + 8 * j + 4);
+            a[h][0] = __fmaf_rn(q0.x, h2f_lo(w.x), a[h][0]); a[h][1] = __fmaf_rn(q0.y, h2f_hi(w.x), a[h][1]);
+            a[h][2] = __fmaf_rn(q0.z, h2f_lo(w.y), a[h][2]); a[h][3] = __fmaf_rn(q0.w, h2f_hi(w.y), a[h][3]);
+            a[h][0] = __fmaf_rn(q1.x, h2f_lo(w.z), a[h][0]); a[h][1] = __fmaf_rn(q1.y, h2f_hi(w.z), a[h][1]);
+            a[h][2] = __fmaf_rn(q1.z, h2f_lo(w.w), a[h][2]); a[h][3] = __fmaf_rn(q1.w, h2f_hi(w.w), a[h][3]);
+        }
+    }
+    const bool valid = lane < n;
+#pragma unroll
+    for (int h = 0; h < H; h++) {
+        const float sc = __fmul_rn(__fadd_rn(__fadd_rn(a[h][0], a[h][1]), __fadd_rn(a[h][2], a[h][3])), scale);
+        const float s = valid ? sc : -__builtin_inff();
+        m[h] = wave_max(s);
+        const float p = valid ? mi_expf(__fsub_rn(s, m[h])) : 0.f;
+        lsum[h] = bfly_sum64(p);
+        pl[h * 64 + lane] = p;                       // positions past n hold 0
+#pragma unroll
+        for (int e = 0; e < DPL; e++) acc[h][e] = 0.f;
+    }
+    wave_lds_sync();
+    using VT = typename std::conditional<DPL == 2, uint32_t, uint16_t>::type;
+    const int ns = __builtin_amdgcn_readfirstlane(n);
+    auto step = [&](VT w, const float (&pt)[H]) {
+#pragma unroll
+        for (int h = 0; h < H; h++) {
+            if constexpr (DPL == 2) {
+                acc[h][0] = __fmaf_rn(pt[h], h2f_lo(w), acc[h][0]);
+                acc[h][1] = __fmaf_rn(pt[h], h2f_hi(w), acc[h][1]);
             } else {
-                float* sr = srecs + ((size_t)h * nsp + sp) * REC;
-#pragma unroll
-                for (int e = 0; e < DPL; e++) stc(sr + DPL * lane + e, acc[e]);
-                if (lane == 0) {
-                    stc(sr + HD, M);
-                    stc(sr + HD + 1, den);
-                }
-            }
-        };
-        if constexpr (RR) {
-            rr_heads<HD, kAttnSplit>(recs + ((size_t)h0 * nch + c0) * REC, (size_t)nch * REC, c1 - c0, g, lane, put1);
-        } else {
-            for (int hh = 0; hh < g; hh++) {
-                float M, den, acc[DPL];
-                lds_merge<HD>(recs + (size_t)(h0 + hh) * nch * REC, c0, c1, qg, lane, M, den, acc);
-                put1(hh, M, den, acc);
+                acc[h][0] = __fmaf_rn(pt[h], __half2float(__ushort_as_half(w)), acc[h][0]);
             }
         }
-        if (nsp == 1 || !last_arrival(hcnt + (size_t)kvh * ngrp + hg, nsp, lane)) continue;
-        // level 2: the splits -> the output
+    };
+    // batches of 8 positions: the V values and the p broadcasts of a batch are read
+    // together, then the chains run over the positions in order; past the last whole
+    // batch, one position at a time up to n
+    int t0 = 0;
+    for (; t0 + 8 <= ns; t0 += 8) {
+        VT w[8];
+        float4 pv[H][2];
+#pragma unroll
+        for (int u = 0; u < 8; u++) w[u] = *reinterpret_cast<const VT*>(vls + (t0 + u) * HD + DPL * lane);
+#pragma unroll
+        for (int h = 0; h < H; h++) {
+            pv[h][0] = *reinterpret_cast<const float4*>(pl + h * 64 + t0);
+            pv[h][1] = *reinterpret_cast<const float4*>(pl + h * 64 + t0 + 4);
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            float pt[H];
+#pragma unroll
+            for (int h = 0; h < H; h++) {
+                const float4& v4 = pv[h][u >> 2];
+                pt[h] = (u & 3) == 0 ? v4.x : (u & 3) == 1 ? v4.y : (u & 3) == 2 ? v4.z : v4.w;
+            }
+            step(w[u], pt);
+        }
+    }
+    for (; t0 < ns; t0++) {
+        const VT w = *reinterpret_cast<const VT*>(vls + t0 * HD + DPL * lane);
+        float pt[H];
+#pragma unroll
+        for (int h = 0; h < H; h++) pt[h] = pl[h * 64 + t0];
+        step(w, pt);
+    }
+}
+
+// The merge of the records in b (what lds_merge computes: M = max over the records,
+// w_i = exp(m_i - M), den and acc as fma chains in record order, so the two give the
+// same bits). The weights w_i and sums l_i reach every lane through the wave's LDS row
+// wl[0..64) (w at 0, l at 32; four records per 16-byte read): a readlane each cost
+// more than the fmas they feed.
+template <int HD, int N>
+__device__ __forceinline__ void rr_merge(const RegRecs<HD, N>& b, int n, int lane, float* wl, float& M, float& den,
+                                             float (&acc)[HD / 64]) {
+    static_assert(N <= 32 && N % 4 == 0, "records per merge");
+    constexpr int DPL = HD / 64;
+    M = wave_max(b.m);
+    const float w = lane < n ? mi_expf(__fsub_rn(b.m, M)) : 0.f;
+    if (lane < 32) {
+        wl[lane] = w;
+        wl[32 + lane] = b.l;
+    }
+    wave_lds_sync();
+    den = 0.f;
+#pragma unroll
+    for (int e = 0; e < DPL; e++) acc[e] = 0.f;
+#pragma unroll
+    for (int i4 = 0; i4 < N; i4 += 4) {
+        if (i4 < n) {
+            const float4 w4 = *reinterpret_cast<const float4*>(wl + i4);
+            const float4 l4 = *reinterpret_cast<const float4*>(wl + 32 + i4);
+            const float wv[4] = {w4.x, w4.y, w4.z, w4.w}, lv[4] = {l4.x, l4.y, l4.z, l4.w};
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                if (i4 + k < n) {
+                    den = __fmaf_rn(lv[k], wv[k], den);
+#pragma unroll
+                    for (int e = 0; e < DPL; e++) acc[e] = __fmaf_rn(b.o[i4 + k][e], wv[k], acc[e]);
+                }
+            }
+        }
+    }
+    wave_lds_sync();            // the row is free for the next merge
+}
+// The merges of g heads (records of head hh at r0 + hh * hstride, n <= N of them),
+// two heads' records in flight at a time (head hh merges in LDS row wl + 64 * (hh & 1));
+// done(hh, M, den, acc) takes each result.
+template <int HD, int N, class F>
+__device__ __forceinline__ void rr_heads(const float* r0, size_t hstride, int n, int g, int lane, float* wl, F done) {
+    RegRecs<HD, N> a, b;
+    float M, den, acc[HD / 64];
+    rr_issue<HD, N>(a, r0, n, lane);
+    for (int hh = 0; hh < g; hh += 2) {
+        if (hh + 1 < g) rr_issue<HD, N>(b, r0 + (hh + 1) * hstride, n, lane);
+        rr_merge<HD, N>(a, n, lane, wl, M, den, acc);
+        done(hh, M, den, acc);
+        if (hh + 1 < g) {
+            if (hh + 2 < g) rr_issue<HD, N>(a, r0 + (hh + 2) * hstride, n, lane);
+            rr_merge<HD, N>(b, n, lane, wl + 64, M, den, acc);
+            done(hh + 1, M, den, acc);
+        }
+    }
+}
+
+// Standalone attention, one workgroup per unit (kv head, 64-position chunk) and
+// ceil(G / H) waves. The chunk's K rows come into LDS by coalesced DMA (1 KB of
+// consecutive rows per instruction) in the step kernel's swizzled tile (kslot), its V
+// rows next to them, and the G query rows of the kv head beside; wave w then computes
+// heads wH .. wH + H - 1 together (attn_core_h), so the K/V of a chunk are read once
+// from memory for all G heads. Records (o[hd], m, l) are stored agent-coherent and
+// drained; the workgroup that completes a split of kAttnSplit chunks merges the split
+// for every head of the kv head (each wave its heads, records held in registers), and
+// the one that completes the kv head's last split merges the splits: the canonical
+// merge, the order of orc_attention_canon. Past kRegRecs splits wave 0 merges them through
+// LDS. Scratch: counters [nkv][nsp] then [nkv] (zero before the first call, left zero) |
+// chunk records [nh][nch] | split records [nh][nsp].
+constexpr int kTileHeads = 2;                  // query heads per wave
+template <int HD, int H>
+__global__ __launch_bounds__(64 * (kAttnMaxG / H)) void k_attn_tile(const float* q, const __half* kc, const __half* vc,
+                                                                   int nh, int nkv, int L, int ctx, float scale,
+                                                                   float* scratch, float* out) {
+    constexpr int REC = HD + 32, DPL = HD / 64;
+    static_assert(kAttnSplit * (HD + 32) * 4 <= 2 * 64 * HD * 2, "the LDS merge fits the K/V tile");
+    static_assert(H >= 2, "the merges of a wave's two heads use its LDS rows hb and hb + 1");
+    __shared__ __align__(16) uint8_t smem[2 * 64 * HD * 2 + kAttnMaxG * HD * 4 + kAttnMaxG * 64 * 4 + 16];
+    uint4* kls = reinterpret_cast<uint4*>(smem);
+    __half* vls = reinterpret_cast<__half*>(smem + 64 * HD * 2);
+    float* qs = reinterpret_cast<float*>(smem + 2 * 64 * HD * 2);
+    float* pls = qs + kAttnMaxG * HD;                                  // [G][64] probabilities
+    int* flag = reinterpret_cast<int*>(pls + kAttnMaxG * 64);
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int nw = blockDim.x >> 6;
+    const int nch = (L + kAttnChunk - 1) / kAttnChunk, G = nh / nkv, nsp = (nch + kAttnSplit - 1) / kAttnSplit;
+    const int u = blockIdx.x, kvh = u / nch, c = u - kvh * nch, t0 = c * kAttnChunk, n = min(kAttnChunk, L - t0);
+    const int h0 = kvh * G, hb = wave * H, hn = min(H, G - hb);    // the wave's heads h0 + hb .. + hn - 1
+    uint32_t* scnt = reinterpret_cast<uint32_t*>(scratch);           // [nkv][nsp]
+    uint32_t* hcnt = scnt + (size_t)nkv * nsp;                        // [nkv]
+    float* recs = scratch + kAttnCounters;
+    float* srecs = recs + (size_t)nh * nch * REC;
+    const __half* kr = kc + ((size_t)kvh * ctx + t0) * HD;
+    const __half* vr = vc + ((size_t)kvh * ctx + t0) * HD;
+    if (wave == 0) attn_issue_k<HD>(kr, n, kls, lane);
+    if (wave == (nw > 1 ? 1 : 0)) attn_issue_v<HD>(vr, n, vls, lane);
+    if (wave == (nw > 2 ? 2 : 0)) dma_wave(q + (size_t)h0 * HD, qs, G * HD * 4, lane);
+    drain_vm();
+    __syncthreads();
+    {
+        float m[H], ls[H], acc[H][DPL];
+        attn_core_h<HD, H>(kls, qs + hb * HD, hn, vls, n, scale, lane, pls + hb * 64, m, ls, acc);
+#pragma unroll
+        for (int h = 0; h < H; h++) {
+            if (h < hn) {
+                float* rec = recs + ((size_t)(h0 + hb + h) * nch + c) * REC;
+#pragma unroll
+                for (int e = 0; e < DPL; e++) stc(rec + DPL * lane + e, acc[h][e]);
+                if (lane == 0) { stc(rec + HD, m[h]); stc(rec + HD + 1, ls[h]); }
+            }
+        }
+    }
+    drain_vm();
+    __syncthreads();                                   // every record of the workgroup is written
+    const int sp = c / kAttnSplit, c0 = sp * kAttnSplit, c1 = min(nch, c0 + kAttnSplit);
+    if (wave == 0) {
+        const bool last = last_arrival(scnt + (size_t)kvh * nsp + sp, c1 - c0, lane);
+        if (lane == 0) *flag = last;
+    }
+    __syncthreads();
+    if (!*flag) return;
+    // level 1: the split's chunks of each head -> the output (one split) or a split record
+    auto put1 = [&](int hh, float M, float den, const float (&acc)[DPL]) {
+        const int h = h0 + hb + hh;
+        if (nsp == 1) {
+#pragma unroll
+            for (int e = 0; e < DPL; e++) out[(size_t)h * HD + DPL * lane + e] = __fdiv_rn(acc[e], den);
+        } else {
+            float* sr = srecs + ((size_t)h * nsp + sp) * REC;
+#pragma unroll
+            for (int e = 0; e < DPL; e++) stc(sr + DPL * lane + e, acc[e]);
+            if (lane == 0) { stc(sr + HD, M); stc(sr + HD + 1, den); }
+        }
+    };
+    rr_heads<HD, kAttnSplit>(recs + ((size_t)(h0 + hb) * nch + c0) * REC, (size_t)nch * REC, c1 - c0, hn, lane,
+                                 pls + hb * 64, put1);
+    if (nsp == 1) return;
+    drain_vm();
+    __syncthreads();
+    if (wave == 0) {
+        const bool last = last_arrival(hcnt + kvh, nsp, lane);
+        if (lane == 0) *flag = last;
+    }
+    __syncthreads();
+    if (!*flag) return;
+    // level 2: the splits -> the output
+    if (nsp <= kRegRecs) {
         auto put = [&](int hh, float M, float den, const float (&acc)[DPL]) {
 #pragma unroll
-            for (int e = 0; e < DPL; e++) out[(size_t)(h0 + hh) * HD + DPL * lane + e] = __fdiv_rn(acc[e], den);
+            for (int e = 0; e < DPL; e++) out[(size_t)(h0 + hb + hh) * HD + DPL * lane + e] = __fdiv_rn(acc[e], den);
         };
-        if (RR && nsp <= kRegRecs) {
-            rr_heads<HD, kRegRecs>(srecs + (size_t)h0 * nsp * REC, (size_t)nsp * REC, nsp, g, lane, put);
-        } else {
-            for (int hh = 0; hh < g; hh++) {
-                float M, den, acc[DPL];
-                lds_merge<HD>(srecs + (size_t)(h0 + hh) * nsp * REC, 0, nsp, qg, lane, M, den, acc);
-                put(hh, M, den, acc);
-            }
+        rr_heads<HD, kRegRecs>(srecs + (size_t)(h0 + hb) * nsp * REC, (size_t)nsp * REC, nsp, hn, lane, pls + hb * 64,
+                                   put);
+    } else if (wave == 0) {
+        for (int hh = 0; hh < G; hh++) {
+            float M, den, acc[DPL];
+            lds_merge<HD>(srecs + (size_t)(h0 + hh) * nsp * REC, 0, nsp, reinterpret_cast<float*>(smem), lane, M, den,
+                          acc);
+#pragma unroll
+            for (int e = 0; e < DPL; e++) out[(size_t)(h0 + hh) * HD + DPL * lane + e] = __fdiv_rn(acc[e], den);
         }
     }
 }
@@ -2524,27 +2598,15 @@ size_t attn_scratch_floats(int nh, int hd, int L) {
 }
 bool launch_attn_decode(const float* q, const __half* kc, const __half* vc, int nh, int nkv, int hd, int L, int ctx,
                         float scale, float* scratch, float* out, hipStream_t s) {
-    if (nh % nkv || !kernels_support(nh / nkv, hd) || nh / nkv > kItemMaxG) return false;
+    if (nh % nkv || !kernels_support(nh / nkv, hd) || nh / nkv > kAttnMaxG) return false;
     const int G = nh / nkv, nch = (L + kAttnChunk - 1) / kAttnChunk, units = nkv * nch;
     const int nsp = (nch + kAttnSplit - 1) / kAttnSplit;
-    // counters: nkv * nsp * ngrp + nkv * ngrp <= nh * (nsp + 1)
+    // counters: nkv * nsp + nkv <= nh * (nsp + 1)
     if ((size_t)nh * (nsp + 1) > (size_t)kAttnCounters) return false;
-    // head groups per unit: the fewest (largest g, K/V read by fewer items) that still
-    // give kItemTarget items
-    int ngrp = 1;
-    while (ngrp < G && units * ngrp < kItemTarget) {
-        do ngrp++; while (G % ngrp);
-    }
-    const int per = std::max(1, std::min(kItemWgsPerXcd, ((units + 7) / 8 * ngrp + kItemWaves - 1) / kItemWaves));
+    const int nw = (G + kTileHeads - 1) / kTileHeads;
     with_hd(hd, [&](auto h) {
-        // the register merges pay off when a merge takes several heads (their loads
-        // overlap); with one head the kernel without them runs faster
-        if (G / ngrp >= 2)
-            LAUNCH((k_attn_fused<decltype(h)::value, true>), 8 * per, 64 * kItemWaves, s, q, kc, vc, nh, nkv, L, ctx,
-                   scale, G / ngrp, scratch, out);
-        else
-            LAUNCH((k_attn_fused<decltype(h)::value, false>), 8 * per, 64 * kItemWaves, s, q, kc, vc, nh, nkv, L, ctx,
-                   scale, G / ngrp, scratch, out);
+        LAUNCH((k_attn_tile<decltype(h)::value, kTileHeads>), units, 64 * nw, s, q, kc, vc, nh, nkv, L, ctx, scale,
+               scratch, out);
     });
     return true;
 }
