@@ -922,6 +922,97 @@ __device__ __forceinline__ void attn_core(const uint4* kls, const float* qs, con
     }
 }
 
+// attn_core for H query heads of one kv head at once (q rows at qs, qs + HD, ...; rows
+// past nq - 1 repeat row nq - 1): each head's arithmetic is attn_core's, the same chains
+// in the same order, so the results carry the same bits; the K and V values are read
+// from LDS once for the H heads and the heads' chains interleave (attn_core alone is a
+// chain of dependent fmas and LDS waits). The probabilities reach the p.v lanes through
+// the wave's LDS row pl[H][64] (one 16-byte broadcast read gives four positions; a
+// readlane per position and head cost more than the fmas it feeds).
+template <int HD, int H>
+__device__ __forceinline__ void attn_core_h(const uint4* kls, const float* qs, int nq, const __half* vls, int n,
+                                            float scale, int lane, float* pl, float (&m)[H], float (&lsum)[H],
+                                            float (&acc)[H][HD / 64]) {
+    constexpr int NV = HD / 8, DPL = HD / 64;
+    const float* qr[H];
+#pragma unroll
+    for (int h = 0; h < H; h++) qr[h] = qs + min(h, nq - 1) * HD;
+    float a[H][4];
+#pragma unroll
+    for (int h = 0; h < H; h++) a[h][0] = a[h][1] = a[h][2] = a[h][3] = 0.f;
+#pragma unroll 4
+    for (int j = 0; j < NV; j++) {
+        const uint4 w = kls[kslot<HD>(lane, j)];
+#pragma unroll
+        for (int h = 0; h < H; h++) {
+            const float4 q0 = *reinterpret_cast<const float4*>(qr[h] + 8 * j);
+            const float4 q1 = *reinterpret_cast<const float4*>(qr[h] + 8 * j + 4);
+            a[h][0] = __fmaf_rn(q0.x, h2f_lo(w.x), a[h][0]); a[h][1] = __fmaf_rn(q0.y, h2f_hi(w.x), a[h][1]);
+            a[h][2] = __fmaf_rn(q0.z, h2f_lo(w.y), a[h][2]); a[h][3] = __fmaf_rn(q0.w, h2f_hi(w.y), a[h][3]);
+            a[h][0] = __fmaf_rn(q1.x, h2f_lo(w.z), a[h][0]); a[h][1] = __fmaf_rn(q1.y, h2f_hi(w.z), a[h][1]);
+            a[h][2] = __fmaf_rn(q1.z, h2f_lo(w.w), a[h][2]); a[h][3] = __fmaf_rn(q1.w, h2f_hi(w.w), a[h][3]);
+        }
+    }
+    const bool valid = lane < n;
+#pragma unroll
+    for (int h = 0; h < H; h++) {
+        const float sc = __fmul_rn(__fadd_rn(__fadd_rn(a[h][0], a[h][1]), __fadd_rn(a[h][2], a[h][3])), scale);
+        const float s = valid ? sc : -__builtin_inff();
+        m[h] = wave_max(s);
+        const float p = valid ? mi_expf(__fsub_rn(s, m[h])) : 0.f;
+        lsum[h] = bfly_sum64(p);
+        pl[h * 64 + lane] = p;                       // positions past n hold 0
+#pragma unroll
+        for (int e = 0; e < DPL; e++) acc[h][e] = 0.f;
+    }
+    wave_lds_sync();
+    using VT = typename std::conditional<DPL == 2, uint32_t, uint16_t>::type;
+    const int ns = __builtin_amdgcn_readfirstlane(n);
+    auto step = [&](VT w, const float (&pt)[H]) {
+#pragma unroll
+        for (int h = 0; h < H; h++) {
+            if constexpr (DPL == 2) {
+                acc[h][0] = __fmaf_rn(pt[h], h2f_lo(w), acc[h][0]);
+                acc[h][1] = __fmaf_rn(pt[h], h2f_hi(w), acc[h][1]);
+            } else {
+                acc[h][0] = __fmaf_rn(pt[h], __half2float(__ushort_as_half(w)), acc[h][0]);
+            }
+        }
+    };
+    // batches of 8 positions: the V values and the p broadcasts of a batch are read
+    // together, then the chains run over the positions in order; past the last whole
+    // batch, one position at a time up to n
+    int t0 = 0;
+    for (; t0 + 8 <= ns; t0 += 8) {
+        VT w[8];
+        float4 pv[H][2];
+#pragma unroll
+        for (int u = 0; u < 8; u++) w[u] = *reinterpret_cast<const VT*>(vls + (t0 + u) * HD + DPL * lane);
+#pragma unroll
+        for (int h = 0; h < H; h++) {
+            pv[h][0] = *reinterpret_cast<const float4*>(pl + h * 64 + t0);
+            pv[h][1] = *reinterpret_cast<const float4*>(pl + h * 64 + t0 + 4);
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            float pt[H];
+#pragma unroll
+            for (int h = 0; h < H; h++) {
+                const float4& v4 = pv[h][u >> 2];
+                pt[h] = (u & 3) == 0 ? v4.x : (u & 3) == 1 ? v4.y : (u & 3) == 2 ? v4.z : v4.w;
+            }
+            step(w[u], pt);
+        }
+    }
+    for (; t0 < ns; t0++) {
+        const VT w = *reinterpret_cast<const VT*>(vls + t0 * HD + DPL * lane);
+        float pt[H];
+#pragma unroll
+        for (int h = 0; h < H; h++) pt[h] = pl[h * 64 + t0];
+        step(w, pt);
+    }
+}
+
 // Attention items (query head h, 64-position chunk c) of positions 0..pos. The G
 // query heads of one (kv head, chunk) read the same K/V rows, so they are placed on
 // one XCD (workgroups w = x + 8k share XCD x): unit u = kvh*nch + c, item index
@@ -1025,12 +1116,12 @@ __device__ __forceinline__ void attn_finish(MPtr M, int l, int pos, const AttnIt
         }
     }
     wave_lds_sync();
-    float m, lsum, acc[DPL];
-    attn_core<HD>(kls, qs, vls, n, M->scale, lane, m, lsum, acc);
+    float m[1], lsum[1], acc[1][DPL];
+    attn_core_h<HD, 1>(kls, qs, 1, vls, n, M->scale, lane, qs + HD, m, lsum, acc);
     float* rec = att_rec(M, l) + ((size_t)h * M->maxch + c) * M->arec;
 #pragma unroll
-    for (int e = 0; e < DPL; e++) stc(rec + DPL * lane + e, acc[e]);
-    if (lane == 0) { stc(rec + HD, m); stc(rec + HD + 1, lsum); }
+    for (int e = 0; e < DPL; e++) stc(rec + DPL * lane + e, acc[0][e]);
+    if (lane == 0) { stc(rec + HD, m[0]); stc(rec + HD + 1, lsum[0]); }
     wave_lds_sync();                           // LDS is reused by the wave's next item
 }
 
@@ -2176,97 +2267,6 @@ __device__ __forceinline__ bool last_arrival(uint32_t* cnt, uint32_t need, int l
     if (old + 1 != need) return false;
     if (lane == 0) stc(cnt, 0u);
     return true;
-}
-
-// attn_core for H query heads of one kv head at once (q rows at qs, qs + HD, ...; rows
-// past nq - 1 repeat row nq - 1): each head's arithmetic is attn_core's, the same chains
-// in the same order, so the results carry the same bits; the K and V values are read
-// from LDS once for the H heads and the heads' chains interleave (attn_core alone is a
-// chain of dependent fmas and LDS waits). The probabilities reach the p.v lanes through
-// the wave's LDS row pl[H][64] (one 16-byte broadcast read gives four positions; a
-// readlane per position and head cost more than the fmas it feeds).
-template <int HD, int H>
-__device__ __forceinline__ void attn_core_h(const uint4* kls, const float* qs, int nq, const __half* vls, int n,
-                                            float scale, int lane, float* pl, float (&m)[H], float (&lsum)[H],
-                                            float (&acc)[H][HD / 64]) {
-    constexpr int NV = HD / 8, DPL = HD / 64;
-    const float* qr[H];
-#pragma unroll
-    for (int h = 0; h < H; h++) qr[h] = qs + min(h, nq - 1) * HD;
-    float a[H][4];
-#pragma unroll
-    for (int h = 0; h < H; h++) a[h][0] = a[h][1] = a[h][2] = a[h][3] = 0.f;
-#pragma unroll 4
-    for (int j = 0; j < NV; j++) {
-        const uint4 w = kls[kslot<HD>(lane, j)];
-#pragma unroll
-        for (int h = 0; h < H; h++) {
-            const float4 q0 = *reinterpret_cast<const float4*>(qr[h] + 8 * j);
-            const float4 q1 = *reinterpret_cast<const float4*>(qr[h] + 8 * j + 4);
-            a[h][0] = __fmaf_rn(q0.x, h2f_lo(w.x), a[h][0]); a[h][1] = __fmaf_rn(q0.y, h2f_hi(w.x), a[h][1]);
-            a[h][2] = __fmaf_rn(q0.z, h2f_lo(w.y), a[h][2]); a[h][3] = __fmaf_rn(q0.w, h2f_hi(w.y), a[h][3]);
-            a[h][0] = __fmaf_rn(q1.x, h2f_lo(w.z), a[h][0]); a[h][1] = __fmaf_rn(q1.y, h2f_hi(w.z), a[h][1]);
-            a[h][2] = __fmaf_rn(q1.z, h2f_lo(w.w), a[h][2]); a[h][3] = __fmaf_rn(q1.w, h2f_hi(w.w), a[h][3]);
-        }
-    }
-    const bool valid = lane < n;
-#pragma unroll
-    for (int h = 0; h < H; h++) {
-        const float sc = __fmul_rn(__fadd_rn(__fadd_rn(a[h][0], a[h][1]), __fadd_rn(a[h][2], a[h][3])), scale);
-        const float s = valid ? sc : -__builtin_inff();
-        m[h] = wave_max(s);
-        const float p = valid ? mi_expf(__fsub_rn(s, m[h])) : 0.f;
-        lsum[h] = bfly_sum64(p);
-        pl[h * 64 + lane] = p;                       // positions past n hold 0
-#pragma unroll
-        for (int e = 0; e < DPL; e++) acc[h][e] = 0.f;
-    }
-    wave_lds_sync();
-    using VT = typename std::conditional<DPL == 2, uint32_t, uint16_t>::type;
-    const int ns = __builtin_amdgcn_readfirstlane(n);
-    auto step = [&](VT w, const float (&pt)[H]) {
-#pragma unroll
-        for (int h = 0; h < H; h++) {
-            if constexpr (DPL == 2) {
-                acc[h][0] = __fmaf_rn(pt[h], h2f_lo(w), acc[h][0]);
-                acc[h][1] = __fmaf_rn(pt[h], h2f_hi(w), acc[h][1]);
-            } else {
-                acc[h][0] = __fmaf_rn(pt[h], __half2float(__ushort_as_half(w)), acc[h][0]);
-            }
-        }
-    };
-    // batches of 8 positions: the V values and the p broadcasts of a batch are read
-    // together, then the chains run over the positions in order; past the last whole
-    // batch, one position at a time up to n
-    int t0 = 0;
-    for (; t0 + 8 <= ns; t0 += 8) {
-        VT w[8];
-        float4 pv[H][2];
-#pragma unroll
-        for (int u = 0; u < 8; u++) w[u] = *reinterpret_cast<const VT*>(vls + (t0 + u) * HD + DPL * lane);
-#pragma unroll
-        for (int h = 0; h < H; h++) {
-            pv[h][0] = *reinterpret_cast<const float4*>(pl + h * 64 + t0);
-            pv[h][1] = *reinterpret_cast<const float4*>(pl + h * 64 + t0 + 4);
-        }
-#pragma unroll
-        for (int u = 0; u < 8; u++) {
-            float pt[H];
-#pragma unroll
-            for (int h = 0; h < H; h++) {
-                const float4& v4 = pv[h][u >> 2];
-                pt[h] = (u & 3) == 0 ? v4.x : (u & 3) == 1 ? v4.y : (u & 3) == 2 ? v4.z : v4.w;
-            }
-            step(w[u], pt);
-        }
-    }
-    for (; t0 < ns; t0++) {
-        const VT w = *reinterpret_cast<const VT*>(vls + t0 * HD + DPL * lane);
-        float pt[H];
-#pragma unroll
-        for (int h = 0; h < H; h++) pt[h] = pl[h * 64 + t0];
-        step(w, pt);
-    }
 }
 
 // The merge of the records in b (what lds_merge computes: M = max over the records,
