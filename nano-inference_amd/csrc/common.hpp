@@ -94,7 +94,8 @@ struct DModel {
     float* attT;                   // [NL][kMaxT][NH][maxch][arec]
     float* oT;                     // [NL][ks_o][kMaxT][E]
     uint8_t* actT;                 // [NL][kMaxT][FF/32][kActRec]
-    uint8_t* xT;                   // [kMaxT][E/32][kTRec] int8 records of the current GEMM input
+    uint8_t* xT;                   // [3*NL+1][kMaxT][E/32][kTRec] int8 records of the GEMM inputs: per
+                                   // layer the qkv, o and gate/up inputs, then lm_head's (xT_slots)
     float* dT;                     // [NL][ks_d][kMaxT][E]
     float* candT;                  // [workgroups][kMaxT][4]
     float* logitsT;                // [kMaxT][V] (written when non-null)

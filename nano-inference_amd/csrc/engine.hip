@@ -49,6 +49,7 @@ struct mi_engine {
     hipEvent_t ev0 = nullptr, ev1 = nullptr;
     int nwg_persistent = 0;       // workgroups of the persistent step kernel (0: per-phase launches)
     bool coop = false;            // launch it cooperatively (after a plain launch's barrier failed)
+    bool multi_persistent = false;   // multi-token steps as one persistent launch too (kT_step)
     int32_t* h_iota = nullptr;    // pinned host memory, h_iota[p] = p: the source of posT
     uint64_t* h_ring = nullptr;   // pinned, device-mapped host memory [maxseq]: streamed tokens (DModel::ring)
     hipGraphExec_t gexec[2][kMaxT + 1] = {};   // multi-token step per (logits, T), captured on first use
@@ -439,6 +440,7 @@ static int load_impl(mi_engine* e, const char* path) {
             return set_err(e, MI_ERR_DEVICE, "persistent step kernel cannot be co-resident (cooperative %d, %d per CU)",
                            coop, per_cu);
         e->nwg_persistent = e->n_cu;      // one workgroup per CU
+        e->multi_persistent = e->opts.persistent >= 2 && multi_persistent_max_grid(e->HD) >= 1;
     }
     M.arec = attn_record_floats(e->HD);
     const size_t NL = (size_t)e->NL;
@@ -461,7 +463,7 @@ static int load_impl(mi_engine* e, const char* path) {
     if ((rc = alloc_buf(e, &M.posT, 1)) || (rc = alloc_buf(e, &M.hT, (size_t)(2 * e->NL + 1) * TM * e->E)) ||
         (rc = alloc_buf(e, &M.qkvT, NL * e->ks[0] * TM * e->QKV)) ||
         (rc = alloc_buf(e, &M.attT, NL * TM * e->NH * e->maxch * M.arec)) ||
-        (rc = alloc_buf(e, &M.xT, TM * (e->E / 32) * kTRec)) ||
+        (rc = alloc_buf(e, &M.xT, (3 * NL + 1) * TM * (e->E / 32) * kTRec)) ||
         (rc = alloc_buf(e, &M.oT, NL * e->ks[1] * TM * e->E)) ||
         (rc = alloc_buf(e, &M.actT, NL * TM * (e->FF / 32) * kActRec)) ||
         (rc = alloc_buf(e, &M.dT, NL * e->ks[3] * TM * e->E)) ||
@@ -501,7 +503,7 @@ int mi_load(const char* gguf_path, const mi_opts* opts, mi_engine** out) {
     *out = nullptr;
     std::unique_ptr<mi_engine> e(new mi_engine());
     if (opts) e->opts = *opts; else mi_default_opts(&e->opts);
-    if (e->opts.tchunk < 1 || e->opts.tchunk > 8 || e->opts.max_ctx < 0)
+    if (e->opts.tchunk < 1 || e->opts.tchunk > 8 || e->opts.max_ctx < 0 || e->opts.persistent < 0 || e->opts.persistent > 2)
         return set_err(nullptr, MI_ERR_ARG, "bad options");
     const int rc = load_impl(e.get(), gguf_path);
     if (rc) { g_load_error = e->err; return rc; }
@@ -537,24 +539,35 @@ int mi_debug_flag_barrier(mi_engine* e) {
 
 }  // extern "C"
 
-// One multi-token step (T > 1) at positions pos..pos+T-1. The kernels read the
-// position from posT, so the launch sequence of each (logits, T) is captured once into
-// a HIP graph and replayed at any position: ~300 launches cost one graph launch.
+// One multi-token step (T > 1) at positions pos..pos+T-1: with the persistent step, one
+// persistent launch (kT_step), otherwise one launch per phase. The kernels read the
+// position from posT, so the launch sequence of each (logits, T) can be captured once
+// into a HIP graph and replayed at any position.
 static int run_multi(mi_engine* e, int pos, int T, bool want_logits) {
     const DModel& M = want_logits ? e->M_logits : e->M;
     const DModel* dM = e->dM + (want_logits ? 1 : 0);
     HIPCHK(e, hipMemcpyAsync(e->M.posT, e->h_iota + pos, sizeof(int32_t), hipMemcpyHostToDevice, e->stream));
-    if (!e->opts.graphs) {
+    auto launch = [&]() -> hipError_t {
+        if (e->nwg_persistent && e->multi_persistent) {
+            const hipError_t err = launch_step_multi_persistent(M, dM, e->nwg_persistent, T, e->coop, e->stream);
+            if (err != hipErrorIllegalState && err != hipErrorCooperativeLaunchTooLarge) return err;
+            // the runtime refused the cooperative launch itself (nothing ran): the per-phase
+            // launches compute the same values
+            (void)hipGetLastError();
+            e->multi_persistent = false;
+        }
         launch_step_multi(M, dM, e->n_cu, T, e->stream);
-        HIPCHK(e, hipGetLastError());
+        return hipGetLastError();
+    };
+    if (!e->opts.graphs) {
+        HIPCHK(e, launch());
         return MI_OK;
     }
     hipGraphExec_t& g = e->gexec[want_logits ? 1 : 0][T];
     if (!g) {
         hipGraph_t graph = nullptr;
         HIPCHK(e, hipStreamBeginCapture(e->stream, hipStreamCaptureModeThreadLocal));
-        launch_step_multi(M, dM, e->n_cu, T, e->stream);
-        const hipError_t launched = hipGetLastError();
+        const hipError_t launched = launch();
         const hipError_t ended = hipStreamEndCapture(e->stream, &graph);
         HIPCHK(e, launched);
         HIPCHK(e, ended);
@@ -764,8 +777,7 @@ int mi_step(mi_engine* e, const int32_t* toks, int32_t T, int32_t pos, int32_t* 
         HIPCHK(e, hipMemcpyAsync(logits, T == 1 ? e->M_logits.logits : e->M_logits.logitsT, sizeof(float) * e->V * T,
                                  hipMemcpyDeviceToHost, e->stream));
     HIPCHK(e, hipStreamSynchronize(e->stream));
-    if (T == 1 && (rc = check_barrier(e)))
-        return rc == kRetry ? mi_step(e, toks, T, pos, argmax, margin, logits) : rc;
+    if ((rc = check_barrier(e))) return rc == kRetry ? mi_step(e, toks, T, pos, argmax, margin, logits) : rc;
     for (int t = 0; t < T; t++) {
         if (argmax) argmax[t] = tok[t];
         if (margin) margin[t] = mg[t];
@@ -787,12 +799,10 @@ int mi_prefill(mi_engine* e, const int32_t* ids, int32_t n, int32_t* first, floa
     HIPCHK(e, hipEventRecord(e->ev0, e->stream));
     // chunks of tchunk tokens through the multi-token step (cuda_infer.cu:1133-1144,
     // mega.cu:622, 819-820); its results equal one step per token bit for bit
-    bool ran_single = false;
     for (int p = 0; p < n;) {
         const int T = std::min(e->opts.tchunk, n - p);
         if (T == 1) {
             if (int rc = run_step(e, p, p == n - 1, false)) return rc;
-            ran_single = true;
         } else {
             if (int rc = run_multi(e, p, T, false)) return rc;
             if (p + T == n)   // the next position's token is the last prediction
@@ -806,8 +816,7 @@ int mi_prefill(mi_engine* e, const int32_t* ids, int32_t n, int32_t* first, floa
     HIPCHK(e, hipMemcpyAsync(&tok, e->M.out_tok + n - 1, 4, hipMemcpyDeviceToHost, e->stream));
     HIPCHK(e, hipMemcpyAsync(&mg, e->M.out_margin + n - 1, 4, hipMemcpyDeviceToHost, e->stream));
     HIPCHK(e, hipStreamSynchronize(e->stream));
-    if (ran_single)
-        if (int rc = check_barrier(e)) return rc == kRetry ? mi_prefill(e, ids, n, first, margin) : rc;
+    if (int rc = check_barrier(e)) return rc == kRetry ? mi_prefill(e, ids, n, first, margin) : rc;
     float ms = 0.f;
     HIPCHK(e, hipEventElapsedTime(&ms, e->ev0, e->ev1));
     e->stats.prefill_ms = ms;
@@ -827,12 +836,10 @@ int mi_teacher(mi_engine* e, const int32_t* ids, int32_t n, int32_t* pred, float
     for (int i = 0; i < n; i++)
         if (ids[i] < 0 || ids[i] >= e->V) return set_err(e, MI_ERR_ARG, "teacher token %d out of range", ids[i]);
     HIPCHK(e, hipMemcpyAsync(e->M.tokbuf, ids, sizeof(int32_t) * n, hipMemcpyHostToDevice, e->stream));
-    bool ran_single = false;
     for (int p = 0; p < n;) {
         const int T = std::min(e->opts.tchunk, n - p);
         if (T == 1) {
             if (int rc = run_step(e, p, 0, false)) return rc;
-            ran_single = true;
         } else {
             if (int rc = run_multi(e, p, T, false)) return rc;
         }
@@ -841,8 +848,7 @@ int mi_teacher(mi_engine* e, const int32_t* ids, int32_t n, int32_t* pred, float
     HIPCHK(e, hipMemcpyAsync(pred, e->M.out_tok, sizeof(int32_t) * n, hipMemcpyDeviceToHost, e->stream));
     HIPCHK(e, hipMemcpyAsync(margin, e->M.out_margin, sizeof(float) * n, hipMemcpyDeviceToHost, e->stream));
     HIPCHK(e, hipStreamSynchronize(e->stream));
-    if (ran_single)
-        if (int rc = check_barrier(e)) return rc == kRetry ? mi_teacher(e, ids, n, pred, margin) : rc;
+    if (int rc = check_barrier(e)) return rc == kRetry ? mi_teacher(e, ids, n, pred, margin) : rc;
     e->cur_len = n;
     e->next_ready = false;
     return MI_OK;
@@ -860,7 +866,7 @@ static int run_tokens(mi_engine* e, int pos, int T, int32_t* tok, float* mg) {
     HIPCHK(e, hipMemcpyAsync(tok, e->M.out_tok + pos, 4 * T, hipMemcpyDeviceToHost, e->stream));
     HIPCHK(e, hipMemcpyAsync(mg, e->M.out_margin + pos, 4 * T, hipMemcpyDeviceToHost, e->stream));
     HIPCHK(e, hipStreamSynchronize(e->stream));
-    const int rc = T == 1 ? check_barrier(e) : MI_OK;
+    const int rc = check_barrier(e);
     return rc == kRetry ? run_tokens(e, pos, T, tok, mg) : rc;
 }
 

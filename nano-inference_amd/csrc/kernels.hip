@@ -197,6 +197,21 @@ __device__ __forceinline__ uint32_t ldc(const uint32_t* p) {
 __device__ __forceinline__ void stc(float* p, float v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
 __device__ __forceinline__ void stc(uint32_t* p, uint32_t v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
 __device__ __forceinline__ void drain_vm() { __builtin_amdgcn_s_waitcnt(0x0F70); }      // vmcnt(0)
+__device__ __forceinline__ uint64_t ldc64(const void* p) {
+    return __hip_atomic_load(reinterpret_cast<const uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// a store to memory that other workgroups of the same launch read (P: agent-coherent)
+// or that only later launches read (plain)
+template <bool P>
+__device__ __forceinline__ void st_x(float* p, float v) {
+    if constexpr (P) stc(p, v);
+    else *p = v;
+}
+template <bool P>
+__device__ __forceinline__ void st_x(uint32_t* p, uint32_t v) {
+    if constexpr (P) stc(p, v);
+    else *p = v;
+}
 
 typedef __attribute__((address_space(3))) void* lds_ptr;
 // one wave copies `bytes` (multiple of 16, both ends 16-byte aligned) from global
@@ -546,6 +561,8 @@ __device__ __forceinline__ void st4(float* p, int i, float4 v) { *reinterpret_ca
 
 // quantise slice j (already scaled) into block records X; a 32-element block is
 // 8 lanes x 4 elements
+// X is LDS (P false) or a global record array that P selects the stores for
+template <bool P = false>
 __device__ __forceinline__ void quant_slice(float4 y, bool own, int e0, uint8_t* X, int lane, int rs = kXRec) {
     if (!own) y = make_float4(0.f, 0.f, 0.f, 0.f);
     const float a = max8(fmaxf(fmaxf(fabsf(y.x), fabsf(y.y)), fmaxf(fabsf(y.z), fabsf(y.w))));
@@ -555,11 +572,11 @@ __device__ __forceinline__ void quant_slice(float4 y, bool own, int e0, uint8_t*
     const int s = sum8(q0 + q1 + q2 + q3);
     if (own) {
         uint8_t* rec = X + (e0 >> 5) * rs;
-        *reinterpret_cast<uint32_t*>(rec + (e0 & 31)) =
-            (uint32_t)(q0 & 0xFF) | ((uint32_t)(q1 & 0xFF) << 8) | ((uint32_t)(q2 & 0xFF) << 16) | ((uint32_t)q3 << 24);
+        st_x<P>(reinterpret_cast<uint32_t*>(rec + (e0 & 31)),
+                (uint32_t)(q0 & 0xFF) | ((uint32_t)(q1 & 0xFF) << 8) | ((uint32_t)(q2 & 0xFF) << 16) | ((uint32_t)q3 << 24));
         if ((lane & 7) == 0) {
-            *reinterpret_cast<float*>(rec + 32) = fp16_round(__fdiv_rn(a, 127.f));
-            *reinterpret_cast<int*>(rec + 36) = 8 * s;
+            st_x<P>(reinterpret_cast<float*>(rec + 32), fp16_round(__fdiv_rn(a, 127.f)));
+            st_x<P>(reinterpret_cast<uint32_t*>(rec + 36), (uint32_t)(8 * s));
         }
     }
 }
@@ -1713,23 +1730,35 @@ __device__ __forceinline__ void tgemm(const PMat W, int wg, int nwg, const uint8
     else tgemm_cb<4>(W, wg, nwg, XT, nblk, T, P, wave, lane, stage, out);
 }
 
-// T tokens' records of the E-wide phase input: xT -> LDS (all threads)
-__device__ __forceinline__ void tstage_x(MPtr M, int T, uint8_t* XT) {
+// The thread index is made opaque per phase body: inside kT_step's layer loop its derived
+// addresses would otherwise be hoisted out of the loop and stay live across every phase.
+__device__ __forceinline__ int opaque_tid() {
+    int t = threadIdx.x;
+    asm volatile("" : "+v"(t));
+    return t;
+}
+// The GEMM inputs' int8 records, one slot per (layer, input) so that every line is
+// written once per step (the persistent step reads them with plain loads): slot 3l is
+// layer l's qkv input, 3l + 1 its o input, 3l + 2 its gate/up input, 3 NL lm_head's.
+constexpr int kXtQkv = 0, kXtO = 1, kXtGu = 2;
+__device__ __forceinline__ int xt_slot(MPtr M, int l, int which) { return l < M->NL ? 3 * l + which : 3 * M->NL; }
+__device__ __forceinline__ uint8_t* xT_at(MPtr M, int slot) { return M->xT + (size_t)slot * kMaxT * (M->E / 32) * kTRec; }
+// T tokens' records of an E-wide GEMM input: its xT slot -> LDS (all threads)
+__device__ __forceinline__ void tstage_x(MPtr M, int slot, int T, uint8_t* XT) {
     const int n8 = T * (M->E / 32) * (kTRec / 8);
-    const uint2* src = reinterpret_cast<const uint2*>(M->xT);
+    const uint2* src = reinterpret_cast<const uint2*>(xT_at(M, slot));
     uint2* dst = reinterpret_cast<uint2*>(XT);
-    for (int i = threadIdx.x; i < n8; i += blockDim.x) dst[i] = src[i];
+    for (int i = opaque_tid(); i < n8; i += blockDim.x) dst[i] = src[i];
 }
 
-// phase input of token blockIdx.x for the qkv (kind PH_QKV), gate/up (PH_GU) and
+// phase input of token t for the qkv (kind PH_QKV), gate/up (PH_GU) and
 // lm_head (PH_LM) GEMMs: x = h + split-K partials in order (layer 0 of qkv: the
 // token's embedding row) -> hT -> RMSNorm -> int8 records in xT. The same arithmetic
 // as the single-token step's norm prologue (cuda_infer.cu:43-60 rmsnorm, 80-89 quant).
-__global__ __launch_bounds__(kPThreads) void kT_in(const DModel* Mp, int l, int kind) {
-    const MPtr M = (MPtr)Mp;
+template <bool P>
+__device__ __forceinline__ void kT_in_body(MPtr M, int l, int kind, int t, float* x) {
     const int pos = *M->posT;
-    __shared__ __align__(16) float x[kMaxE];
-    const int t = blockIdx.x, wave = threadIdx.x >> 6, lane = threadIdx.x & 63, n = M->E, nblk = n / 32;
+    const int wave = threadIdx.x >> 6, lane = opaque_tid() & 63, n = M->E, nblk = n / 32;
     const bool qkv = kind == PH_QKV, lm = kind == PH_LM, dsrc = kind != PH_GU;
     const int pl = qkv ? l - 1 : lm ? M->NL - 1 : l;
     float* hdst = M->hT + hT_at(M, qkv ? 2 * l : 2 * l + 1, t);
@@ -1752,12 +1781,18 @@ __global__ __launch_bounds__(kPThreads) void kT_in(const DModel* Mp, int l, int 
             v = f4add(ldg4(h + e0), sum);
         }
         st4(x, e0, v);
-        if (!lm) *reinterpret_cast<float4*>(hdst + e0) = v;
+        if (!lm) {
+            if constexpr (P) {
+                stc(hdst + e0, v.x); stc(hdst + e0 + 1, v.y); stc(hdst + e0 + 2, v.z); stc(hdst + e0 + 3, v.w);
+            } else {
+                *reinterpret_cast<float4*>(hdst + e0) = v;
+            }
+        }
     }
     __syncthreads();
     const float* w = lm ? M->out_norm : qkv ? LY(M, l)->an : LY(M, l)->fn;
     const float sc = rms_scale(x, n, M->eps, lane);
-    uint8_t* xr = M->xT + (size_t)t * nblk * kTRec;
+    uint8_t* xr = xT_at(M, lm ? xt_slot(M, M->NL, 0) : xt_slot(M, l, qkv ? kXtQkv : kXtGu)) + (size_t)t * nblk * kTRec;
     for (int j = wave; 256 * j < n; j += kPWaves) {
         const int e0 = 256 * j + 4 * lane;
         const bool own = e0 < n;
@@ -1767,8 +1802,12 @@ __global__ __launch_bounds__(kPThreads) void kT_in(const DModel* Mp, int l, int 
             y = make_float4(__fmul_rn(__fmul_rn(xv.x, sc), wv.x), __fmul_rn(__fmul_rn(xv.y, sc), wv.y),
                             __fmul_rn(__fmul_rn(xv.z, sc), wv.z), __fmul_rn(__fmul_rn(xv.w, sc), wv.w));
         }
-        quant_slice(y, own, e0, xr, lane, kTRec);
+        quant_slice<P>(y, own, e0, xr, lane, kTRec);
     }
+}
+__global__ __launch_bounds__(kPThreads) void kT_in(const DModel* Mp, int l, int kind) {
+    __shared__ __align__(16) float x[kMaxE];
+    kT_in_body<false>((MPtr)Mp, l, kind, blockIdx.x, x);
 }
 
 __device__ __forceinline__ float* qkvT_at(MPtr M, int l) { return M->qkvT + (size_t)l * LY(M, 0)->qkv.ks * kMaxT * M->QKV; }
@@ -1781,20 +1820,25 @@ __device__ __forceinline__ uint8_t* actT_at(MPtr M, int l, int t) {
     return M->actT + ((size_t)l * kMaxT + t) * (M->FF / 32) * kActRec;
 }
 
-#define TPRELUDE(BYTES)                                                                          \
-    const MPtr M = (MPtr)Mp;                                                                     \
+// The phase bodies take the workgroup's LDS, its index and the grid size; P selects the
+// stores (and xT loads) for phases that run inside one persistent launch (kT_step).
+#define TBODY const int wave = threadIdx.x >> 6, lane = opaque_tid() & 63;
+#define TWRAP(BYTES, CALL)                                                                       \
     __shared__ __align__(16) uint8_t smem[BYTES];                                                \
-    const int wg = blockIdx.x, nwg = gridDim.x, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    CALL;
 
-__global__ __launch_bounds__(kPThreads) void kT_qkv(const DModel* Mp, int l, int T) {
-    TPRELUDE(kTGemvLds)
+template <bool PS>
+__device__ __forceinline__ void kT_qkv_body(MPtr M, int l, int T, uint8_t* smem, int wg, int nwg) {
+    TBODY
     uint8_t* XT = smem;
     float* P = reinterpret_cast<float*>(smem + kTXeBytes);
     const PMat W = ldmat(&LY(M, l)->qkv);
     float* part = qkvT_at(M, l);
-    tgemm(W, wg, nwg, XT, M->E / 32, T, P, wave, lane, [&] { tstage_x(M, T, XT); }, [&](int g, int s, int t, float v) {
-        part[((size_t)s * kMaxT + t) * W.rows + g * 64 + lane] = v;
-    });
+    tgemm(W, wg, nwg, XT, M->E / 32, T, P, wave, lane, [&] { tstage_x(M, xt_slot(M, l, kXtQkv), T, XT); },
+          [&](int g, int s, int t, float v) { st_x<PS>(&part[((size_t)s * kMaxT + t) * W.rows + g * 64 + lane], v); });
+}
+__global__ __launch_bounds__(kPThreads) void kT_qkv(const DModel* Mp, int l, int T) {
+    TWRAP(kTGemvLds, kT_qkv_body<false>((MPtr)Mp, l, T, smem, blockIdx.x, gridDim.x))
 }
 
 // Multi-token attention. Item = (kv head, 64-position chunk c, group of tg consecutive
@@ -1807,9 +1851,9 @@ __global__ __launch_bounds__(kPThreads) void kT_qkv(const DModel* Mp, int l, int
 template <int HD>
 constexpr int kt_attn_lds() { return 2 * 64 * HD * 2 + kPWaves * HD * 4; }
 
-template <int HD>
-__global__ __launch_bounds__(kPThreads) void kT_attn(const DModel* Mp, int l, int T) {
-    TPRELUDE(kt_attn_lds<HD>())
+template <int HD, bool PS>
+__device__ __forceinline__ void kT_attn_body(MPtr M, int l, int T, uint8_t* smem, int wg, int nwg) {
+    TBODY
     constexpr int half = HD / 2, DPL = HD / 64;
     const int pos = *M->posT;
     uint4* kls = reinterpret_cast<uint4*>(smem);
@@ -1894,23 +1938,24 @@ __global__ __launch_bounds__(kPThreads) void kT_attn(const DModel* Mp, int l, in
             attn_core<HD>(kls, qs, vls, min(kAttnChunk, pos + t + 1 - t0), M->scale, lane, m, lsum, acc);
             float* rec = attT_at(M, l, t) + ((size_t)h * M->maxch + c) * M->arec;
 #pragma unroll
-            for (int e = 0; e < DPL; e++) rec[DPL * lane + e] = acc[e];
-            if (lane == 0) { rec[HD] = m; rec[HD + 1] = lsum; }
+            for (int e = 0; e < DPL; e++) st_x<PS>(rec + DPL * lane + e, acc[e]);
+            if (lane == 0) { st_x<PS>(rec + HD, m); st_x<PS>(rec + HD + 1, lsum); }
         }
         __syncthreads();                                           // LDS is reused by the next item
     }
+}
+template <int HD>
+__global__ __launch_bounds__(kPThreads) void kT_attn(const DModel* Mp, int l, int T) {
+    TWRAP(kt_attn_lds<HD>(), (kT_attn_body<HD, false>((MPtr)Mp, l, T, smem, blockIdx.x, gridDim.x)))
 }
 
 // chunk merge of token t's records for query head h (one wave per (t, h); lane = dims
 // lane + 64j) into the O phase's int8 records in xT. The merge is comb_wave's, the
 // step's merge phase uses the same function.
-template <int HD>
-__global__ __launch_bounds__(256) void kT_comb(const DModel* Mp, int l, int T) {
-    const MPtr M = (MPtr)Mp;
+template <int HD, bool PS>
+__device__ __forceinline__ void kT_comb_item(MPtr M, int l, int item, int lane) {
     const int pos = *M->posT;
     constexpr int DPL = HD / 64;
-    const int lane = threadIdx.x & 63, item = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (item >= T * M->NH) return;
     const int t = item / M->NH, hh = item - t * M->NH, nch = (pos + t + kAttnChunk) / kAttnChunk, arec = M->arec;
     const float* r = attT_at(M, l, t) + (size_t)hh * M->maxch * arec;
     float o[DPL];
@@ -1921,33 +1966,45 @@ __global__ __launch_bounds__(256) void kT_comb(const DModel* Mp, int l, int T) {
         int q, s8;
         float d;
         quant32_vals(o[e], q, d, s8);
-        const int el = hh * HD + 64 * e + lane;
-        uint8_t* rec = M->xT + ((size_t)t * nblk + (el >> 5)) * kTRec;
-        rec[el & 31] = (uint8_t)(q & 0xFF);
+        const int el = hh * HD + 64 * e + lane;       // lanes 4k..4k+3 fill code word k of the block
+        uint8_t* rec = xT_at(M, xt_slot(M, l, kXtO)) + ((size_t)t * nblk + (el >> 5)) * kTRec;
+        const uint32_t b = (uint32_t)(q & 0xFF);
+        const uint32_t wd = b | (__shfl_down(b, 1) << 8) | (__shfl_down(b, 2) << 16) | (__shfl_down(b, 3) << 24);
+        if ((lane & 3) == 0) st_x<PS>(reinterpret_cast<uint32_t*>(rec + (el & 31)), wd);
         if ((lane & 31) == 0) {
-            *reinterpret_cast<float*>(rec + 32) = d;
-            *reinterpret_cast<int*>(rec + 36) = s8;
+            st_x<PS>(reinterpret_cast<float*>(rec + 32), d);
+            st_x<PS>(reinterpret_cast<uint32_t*>(rec + 36), (uint32_t)s8);
         }
     }
 }
+template <int HD>
+__global__ __launch_bounds__(256) void kT_comb(const DModel* Mp, int l, int T) {
+    const MPtr M = (MPtr)Mp;
+    const int item = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (item < T * M->NH) kT_comb_item<HD, false>(M, l, item, threadIdx.x & 63);
+}
 
-__global__ __launch_bounds__(kPThreads) void kT_o(const DModel* Mp, int l, int T) {
-    TPRELUDE(kTGemvLds)
+template <bool PS>
+__device__ __forceinline__ void kT_o_body(MPtr M, int l, int T, uint8_t* smem, int wg, int nwg) {
+    TBODY
     uint8_t* XT = smem;
     float* P = reinterpret_cast<float*>(smem + kTXeBytes);
     const PMat W = ldmat(&LY(M, l)->o);
     float* part = oT_at(M, l);
-    tgemm(W, wg, nwg, XT, M->E / 32, T, P, wave, lane, [&] { tstage_x(M, T, XT); }, [&](int g, int s, int t, float v) {
-        part[((size_t)s * kMaxT + t) * W.rows + g * 64 + lane] = v;
-    });
+    tgemm(W, wg, nwg, XT, M->E / 32, T, P, wave, lane, [&] { tstage_x(M, xt_slot(M, l, kXtO), T, XT); },
+          [&](int g, int s, int t, float v) { st_x<PS>(&part[((size_t)s * kMaxT + t) * W.rows + g * 64 + lane], v); });
+}
+__global__ __launch_bounds__(kPThreads) void kT_o(const DModel* Mp, int l, int T) {
+    TWRAP(kTGemvLds, kT_o_body<false>((MPtr)Mp, l, T, smem, blockIdx.x, gridDim.x))
 }
 
-__global__ __launch_bounds__(kPThreads) void kT_gu(const DModel* Mp, int l, int T) {
-    TPRELUDE(kTGemvLds)
+template <bool PS>
+__device__ __forceinline__ void kT_gu_body(MPtr M, int l, int T, uint8_t* smem, int wg, int nwg) {
+    TBODY
     uint8_t* XT = smem;
     float* P = reinterpret_cast<float*>(smem + kTXeBytes);
     const PMat W = ldmat(&LY(M, l)->gu);
-    tgemm(W, wg, nwg, XT, M->E / 32, T, P, wave, lane, [&] { tstage_x(M, T, XT); }, [&](int g, int s, int t, float v) {
+    tgemm(W, wg, nwg, XT, M->E / 32, T, P, wave, lane, [&] { tstage_x(M, xt_slot(M, l, kXtGu), T, XT); }, [&](int g, int s, int t, float v) {
         (void)s;
         const float u = __shfl(v, (lane & 31) + 32);
         const float e = mi_expf(-v);
@@ -1959,14 +2016,18 @@ __global__ __launch_bounds__(kPThreads) void kT_gu(const DModel* Mp, int l, int 
         const uint32_t wd = b | (__shfl_down(b, 1) << 8) | (__shfl_down(b, 2) << 16) | (__shfl_down(b, 3) << 24);
         if (lane < 32) {
             uint32_t* r = reinterpret_cast<uint32_t*>(actT_at(M, l, t) + (size_t)g * kActRec);
-            if ((lane & 3) == 0) r[lane / 4] = wd;
-            if (lane == 0) { r[8] = __float_as_uint(d); r[9] = (uint32_t)s8; }
+            if ((lane & 3) == 0) st_x<PS>(r + lane / 4, wd);
+            if (lane == 0) { st_x<PS>(r + 8, __float_as_uint(d)); st_x<PS>(r + 9, (uint32_t)s8); }
         }
     });
 }
+__global__ __launch_bounds__(kPThreads) void kT_gu(const DModel* Mp, int l, int T) {
+    TWRAP(kTGemvLds, kT_gu_body<false>((MPtr)Mp, l, T, smem, blockIdx.x, gridDim.x))
+}
 
-__global__ __launch_bounds__(kPThreads) void kT_down(const DModel* Mp, int l, int T) {
-    TPRELUDE(kTDownLds)
+template <bool PS>
+__device__ __forceinline__ void kT_down_body(MPtr M, int l, int T, uint8_t* smem, int wg, int nwg) {
+    TBODY
     uint8_t* XT = smem;
     float* P = reinterpret_cast<float*>(smem + kTXfBytes);
     const int nblk = M->FF / 32;
@@ -1984,24 +2045,28 @@ __global__ __launch_bounds__(kPThreads) void kT_down(const DModel* Mp, int l, in
             bhi = max(bhi, c1 * W.cb);
         }
         const int nb = max(0, bhi - blo);
-        for (int i = threadIdx.x; i < T * nb * (kTRec / 8); i += blockDim.x) {
+        for (int i = opaque_tid(); i < T * nb * (kTRec / 8); i += blockDim.x) {
             const int rcd = i / (kTRec / 8), k = i - rcd * (kTRec / 8), t = rcd / max(nb, 1), b = blo + rcd - t * nb;
             reinterpret_cast<uint2*>(XT + ((size_t)t * nblk + b) * kTRec)[k] =
                 reinterpret_cast<const uint2*>(actT_at(M, l, t) + (size_t)b * kActRec)[k];
         }
     };
     tgemm(W, wg, nwg, XT, nblk, T, P, wave, lane, stage, [&](int g, int s, int t, float v) {
-        part[((size_t)s * kMaxT + t) * W.rows + g * 64 + lane] = v;
+        st_x<PS>(&part[((size_t)s * kMaxT + t) * W.rows + g * 64 + lane], v);
     });
 }
+__global__ __launch_bounds__(kPThreads) void kT_down(const DModel* Mp, int l, int T) {
+    TWRAP(kTDownLds, kT_down_body<false>((MPtr)Mp, l, T, smem, blockIdx.x, gridDim.x))
+}
 
-__global__ __launch_bounds__(kPThreads) void kT_lm(const DModel* Mp, int T) {
-    TPRELUDE(kTGemvLds)
+template <bool PS>
+__device__ __forceinline__ void kT_lm_body(MPtr M, int T, uint8_t* smem, int wg, int nwg) {
+    TBODY
     uint8_t* XT = smem;
     float* P = reinterpret_cast<float*>(smem + kTXeBytes);
     const PMat W = ldmat(&M->lm);
     Top2 tp{-__builtin_inff(), INT_MAX, -__builtin_inff()};
-    tgemm(W, wg, nwg, XT, M->E / 32, T, P, wave, lane, [&] { tstage_x(M, T, XT); }, [&](int g, int s, int t, float v) {
+    tgemm(W, wg, nwg, XT, M->E / 32, T, P, wave, lane, [&] { tstage_x(M, xt_slot(M, M->NL, 0), T, XT); }, [&](int g, int s, int t, float v) {
         (void)s;
         const int row = g * 64 + lane;
         if (M->logitsT) M->logitsT[(size_t)t * M->V + row] = v;
@@ -2011,15 +2076,17 @@ __global__ __launch_bounds__(kPThreads) void kT_lm(const DModel* Mp, int T) {
         top2_wave(tp);
         if (lane == 0) {
             float* cd = M->candT + ((size_t)wg * kMaxT + wave) * 4;
-            cd[0] = tp.best;
-            cd[1] = __int_as_float(tp.idx);
-            cd[2] = tp.second;
+            st_x<PS>(cd, tp.best);
+            st_x<PS>(reinterpret_cast<uint32_t*>(cd + 1), (uint32_t)tp.idx);
+            st_x<PS>(cd + 2, tp.second);
         }
     }
 }
+__global__ __launch_bounds__(kPThreads) void kT_lm(const DModel* Mp, int T) {
+    TWRAP(kTGemvLds, kT_lm_body<false>((MPtr)Mp, T, smem, blockIdx.x, gridDim.x))
+}
 
-__global__ __launch_bounds__(kPThreads) void kT_argmax(const DModel* Mp, int ncand, int T) {
-    const MPtr M = (MPtr)Mp;
+__device__ __forceinline__ void kT_argmax_body(MPtr M, int ncand, int T) {
     const int pos = *M->posT;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     if (wave >= T) return;
@@ -2033,6 +2100,58 @@ __global__ __launch_bounds__(kPThreads) void kT_argmax(const DModel* Mp, int nca
         M->out_tok[pos + wave] = top2_token(tp, M->V);
         M->out_margin[pos + wave] = __fsub_rn(tp.best, tp.second);
     }
+}
+__global__ __launch_bounds__(kPThreads) void kT_argmax(const DModel* Mp, int ncand, int T) {
+    kT_argmax_body((MPtr)Mp, ncand, T);
+}
+
+// The multi-token step as one persistent launch (mega.cu:621-623 runs prompt chunks and
+// verify steps inside its persistent loop): one workgroup per CU runs the phase bodies
+// above in order, the step kernel's grid barrier between them (each workgroup drains its
+// stores first; a barrier that gives up sets M.err, and the later ones do not wait).
+// Values that cross workgroups inside the launch are stored agent-coherent (P = true)
+// into buffers whose lines are each written once per launch before any workgroup reads
+// them (per-layer partials, records and xT slots), so plain loads never meet a stale
+// line. The same arithmetic as the per-phase launches, so the same bits.
+constexpr int kTStepLds = kTDownLds > kTGemvLds ? kTDownLds : kTGemvLds;
+static_assert(kTStepLds >= kt_attn_lds<128>() && kTStepLds >= 4 * kMaxE, "every phase's LDS fits");
+template <int HD>
+__global__ __launch_bounds__(kPThreads) void kT_step(const DModel* Mp, int T) {
+    const MPtr M = (MPtr)Mp;
+    __shared__ __align__(16) uint8_t smem[kTStepLds];
+    const int wg = blockIdx.x, nwg = gridDim.x, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    float* xs = reinterpret_cast<float*>(smem);
+    GridBar gb = bar_init(M->bar, M->err);
+    auto barrier = [&] {
+        drain_vm();
+        __syncthreads();
+        if (wave == 0) ctl_barrier(gb, M->err);
+        __syncthreads();
+    };
+    for (int l = 0; l < M->NL; l++) {
+        if (wg < T) kT_in_body<true>(M, l, PH_QKV, wg, xs);
+        barrier();
+        kT_qkv_body<true>(M, l, T, smem, wg, nwg);
+        barrier();
+        kT_attn_body<HD, true>(M, l, T, smem, wg, nwg);
+        barrier();
+        for (int it = wg * kPWaves + wave; it < T * M->NH; it += nwg * kPWaves) kT_comb_item<HD, true>(M, l, it, lane);
+        barrier();
+        kT_o_body<true>(M, l, T, smem, wg, nwg);
+        barrier();
+        if (wg < T) kT_in_body<true>(M, l, PH_GU, wg, xs);
+        barrier();
+        kT_gu_body<true>(M, l, T, smem, wg, nwg);
+        barrier();
+        kT_down_body<true>(M, l, T, smem, wg, nwg);
+        barrier();
+    }
+    if (wg < T) kT_in_body<true>(M, M->NL - 1, PH_LM, wg, xs);
+    barrier();
+    kT_lm_body<true>(M, T, smem, wg, nwg);
+    barrier();
+    if (wave == 0) ctl_exit(M->bar);
+    if (wg == 0) kT_argmax_body(M, nwg, T);
 }
 
 // ------------------------------------------------------------------ standalone kernels
@@ -2543,6 +2662,26 @@ void launch_step_multi(const DModel& M, const DModel* dM, int nwg, int T, hipStr
     LAUNCH(kT_in, T, kPThreads, s, dM, M.NL - 1, (int)PH_LM);
     LAUNCH(kT_lm, nwg, kPThreads, s, dM, T);
     LAUNCH(kT_argmax, 1, kPThreads, s, dM, nwg, T);
+}
+hipError_t launch_step_multi_persistent(const DModel& M, const DModel* dM, int nwg, int T, bool coop, hipStream_t s) {
+    hipError_t err = hipSuccess;
+    with_hd(M.HD, [&](auto hd) {
+        const DModel* m = dM;
+        void* args[] = {&m, &T};
+        const void* f = reinterpret_cast<const void*>(&kT_step<decltype(hd)::value>);
+        err = coop ? hipLaunchCooperativeKernel(f, dim3(nwg), dim3(kPThreads), args, 0, s)
+                   : hipLaunchKernel(f, dim3(nwg), dim3(kPThreads), args, 0, s);
+    });
+    return err;
+}
+int multi_persistent_max_grid(int HD) {
+    int per_cu = 0;
+    with_hd(HD, [&](auto hd) {
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(&kT_step<decltype(hd)::value>),
+                                                         kPThreads, 0) != hipSuccess)
+            per_cu = 0;
+    });
+    return per_cu;
 }
 int kernels_max_tokens() { return kMaxT; }
 int kernels_max_chunks_multi() { return kTChunks; }

@@ -29,6 +29,11 @@ hipError_t launch_step_persistent(const DModel& M, const DModel* dM, int nwg, in
 // replayed), in one pass over the weights (int8 MFMA tiles), one launch per phase;
 // the predictions land in out_tok/out_margin[p..p+T-1], logits in logitsT if set
 void launch_step_multi(const DModel& M, const DModel* dM, int nwg, int T, hipStream_t s);
+// the same multi-token step as one persistent launch of nwg workgroups, all resident at
+// once (grid barriers; coop and M.bar / M.err as for launch_step_persistent)
+hipError_t launch_step_multi_persistent(const DModel& M, const DModel* dM, int nwg, int T, bool coop, hipStream_t s);
+// co-resident workgroups per CU of the persistent multi-token kernel (0: cannot launch)
+int multi_persistent_max_grid(int HD);
 int kernels_max_tokens();
 int kernels_max_chunks_multi();   // chunks per K segment the multi-token kernels stage
 // co-resident workgroups per CU of the persistent kernel (0: cannot launch)

@@ -6,7 +6,9 @@ logits across T): every token's logits are bit-identical to running the same
 tokens one at a time with T = 1, which is itself bit-identical to the q8act
 oracle (test_gpu_engine.py); one case is also checked against the oracle directly.
 Cases cover both chunk sizes of the q4 tiles (cb 8 and cb 4), a step that crosses
-a 64-position attention chunk, and a context past the inline chunk merge.
+a 64-position attention chunk, and a context past the inline chunk merge. Each runs
+the multi-token step both ways: as one launch per phase (persistent=1, the default)
+and as one persistent launch with grid barriers between the phases (persistent=2).
 
 Speculative generation (n-gram drafts verified by these steps) must be lossless:
 its tokens and margins equal the plain greedy decode (tools/specbench.sh:36 checks
@@ -42,6 +44,9 @@ def bits(x):
     return np.asarray(x, np.float32).view(np.uint32)
 
 
+MULTI = pytest.mark.parametrize("persistent", [1, 2], ids=["multi-phases", "multi-persistent"])
+
+
 def multi_vs_single(eng, prompt, pos, T, seed, V):
     """prefill prompt[:pos], then one T-token step vs T single steps, same tokens"""
     eng.prefill(prompt[:pos])
@@ -54,21 +59,23 @@ def multi_vs_single(eng, prompt, pos, T, seed, V):
     return toks, lg
 
 
+@MULTI
 @pytest.mark.parametrize("pos,T", [(12, 2), (12, 5), (61, 8), (3, 8)])
-def test_tiny_multi_bit_identical(pos, T):
+def test_tiny_multi_bit_identical(pos, T, persistent):
     path = synth_cached("eng-256", TINY, 7)
-    say("tiny pos %d T %d" % (pos, T))
-    eng = minfer.Engine(path, max_ctx=256)
+    say("tiny pos %d T %d persistent %d" % (pos, T, persistent))
+    eng = minfer.Engine(path, max_ctx=256, persistent=persistent)
     prompt = minfer.prompt_ids(11, pos, TINY["n_vocab"])
     multi_vs_single(eng, prompt, pos, T, 100 + pos + T, TINY["n_vocab"])
     eng.close()
 
 
-def test_small_multi_bit_identical_and_oracle():
+@MULTI
+def test_small_multi_bit_identical_and_oracle(persistent):
     path = synth_cached("eng-512", SMALL, 21)
     pos, T = 70, 8
-    say("small pos %d T %d (+ oracle)" % (pos, T))
-    eng = minfer.Engine(path, max_ctx=256)
+    say("small pos %d T %d (+ oracle) persistent %d" % (pos, T, persistent))
+    eng = minfer.Engine(path, max_ctx=256, persistent=persistent)
     prompt = minfer.prompt_ids(12, pos, SMALL["n_vocab"])
     toks, lg = multi_vs_single(eng, prompt, pos, T, 5, SMALL["n_vocab"])
     p = eng.plan
@@ -80,42 +87,46 @@ def test_small_multi_bit_identical_and_oracle():
             assert np.array_equal(bits(lo), bits(lg[i - pos])), "oracle differs at pos %d" % i
 
 
-def test_config0_multi_cb4_bit_identical():
+@MULTI
+def test_config0_multi_cb4_bit_identical(persistent):
     """S05 (hidden 896): q4 chunks of 4 blocks in the E-row matrices, head_dim 64"""
     shape = minfer.SHAPES["S05"]
     path = synth_cached("config0", shape, minfer.CONFIGS["config0"][1])
-    say("config0 pos 16 T 8")
-    eng = minfer.Engine(path, max_ctx=64)
+    say("config0 pos 16 T 8 persistent %d" % persistent)
+    eng = minfer.Engine(path, max_ctx=64, persistent=persistent)
     assert eng.plan["cb"][0] == 4
     prompt = minfer.prompt_ids(minfer.CONFIGS["config0"][2], 16, shape["n_vocab"])
     multi_vs_single(eng, prompt, 16, 8, 17, shape["n_vocab"])
     eng.close()
 
 
-def test_config2_multi_bit_identical():
-    """S15: head_dim 128, the down matrix split into 7 K segments"""
+@MULTI
+def test_config2_multi_bit_identical(persistent):
+    """S15: head_dim 128, the down matrix split into 10 K segments"""
     shape = minfer.SHAPES["S15"]
     path = synth_cached("config2", shape, minfer.CONFIGS["config2"][1])
-    say("config2 pos 64 T 8")
-    eng = minfer.Engine(path, max_ctx=128)
+    say("config2 pos 64 T 8 persistent %d" % persistent)
+    eng = minfer.Engine(path, max_ctx=128, persistent=persistent)
     prompt = minfer.prompt_ids(minfer.CONFIGS["config2"][2], 64, shape["n_vocab"])
     multi_vs_single(eng, prompt, 64, 8, 19, shape["n_vocab"])
     eng.close()
 
 
+@MULTI
 @pytest.mark.parametrize("pos,T", [(1000, 6), (1020, 8)])
-def test_long_context_multi_merge_phase(pos, T):
+def test_long_context_multi_merge_phase(pos, T, persistent):
     """past 4 chunks the chunk records are merged by their own kernel, past 16 as a
     two-level tree (1020 + 8: the step's tokens see 16 and 17 chunks)"""
     path = synth_cached("eng-256", TINY, 7)
-    say("tiny long context pos %d T %d" % (pos, T))
-    eng = minfer.Engine(path, max_ctx=1100)
+    say("tiny long context pos %d T %d persistent %d" % (pos, T, persistent))
+    eng = minfer.Engine(path, max_ctx=1100, persistent=persistent)
     prompt = minfer.prompt_ids(13, pos, TINY["n_vocab"])
     multi_vs_single(eng, prompt, pos, T, 23, TINY["n_vocab"])
     eng.close()
 
 
-def test_long_context_multi_hd128():
+@MULTI
+def test_long_context_multi_hd128(persistent):
     """head_dim 128 at context 1020 + 8 (16 and 17 chunks: the merge tree) on the
     attention-sensitive model (O(1) scores): T = 8 against eight single steps"""
     import json, os
@@ -123,14 +134,15 @@ def test_long_context_multi_hd128():
         fx = json.load(f)
     path = synth_cached(fx["config"], fx["shape"], fx["model_seed"], **fx["types"])
     V = fx["shape"]["n_vocab"]
-    say("hd128 long context pos 1020 T 8")
-    eng = minfer.Engine(path, max_ctx=1100)
+    say("hd128 long context pos 1020 T 8 persistent %d" % persistent)
+    eng = minfer.Engine(path, max_ctx=1100, persistent=persistent)
     prompt = minfer.prompt_ids(43, 1020, V)
     multi_vs_single(eng, prompt, 1020, 8, 29, V)
     eng.close()
 
 
-def test_config4_verify_step_bit_identical():
+@MULTI
+def test_config4_verify_step_bit_identical(persistent):
     """BASELINE config 4 at its own workload: S3 (hidden 2048, 36 layers, 16/2 heads,
     FF 11008), a 1024-token context, one 8-token verify step (the current token + 7
     drafts, TMAX = 8, mega.cu:50) bit-identical to the 8 tokens stepped one at a time"""
@@ -138,8 +150,8 @@ def test_config4_verify_step_bit_identical():
     cfg = minfer.CONFIGS[name]
     shape = minfer.SHAPES[cfg[0]]
     path = synth_cached(name, shape, cfg[1])
-    say("config4 (S3) context 1024 T 8")
-    eng = minfer.Engine(path, max_ctx=cfg[3] + 16)
+    say("config4 (S3) context 1024 T 8 persistent %d" % persistent)
+    eng = minfer.Engine(path, max_ctx=cfg[3] + 16, persistent=persistent)
     prompt = minfer.prompt_ids(cfg[2], cfg[3], shape["n_vocab"])
     multi_vs_single(eng, prompt, cfg[3], 8, cfg[2] + 1, shape["n_vocab"])
     eng.close()
@@ -164,7 +176,8 @@ def test_config4_short_context_oracle():
             assert np.array_equal(bits(lo), bits(lg[i - 8])), "oracle differs at pos %d" % i
 
 
-def test_graph_replays_equal_direct_launches():
+@MULTI
+def test_graph_replays_equal_direct_launches(persistent):
     """The multi-token step replays one captured HIP graph per (T, logits) with the
     position read from device memory. Replays at several positions, with eager
     single-token steps and host synchronizations in between, equal the same steps
@@ -172,8 +185,8 @@ def test_graph_replays_equal_direct_launches():
     path = synth_cached("eng-512", SMALL, 21)
     V = SMALL["n_vocab"]
     prompt = minfer.prompt_ids(5, 100, V)
-    g = minfer.Engine(path, max_ctx=256, graphs=1)
-    d = minfer.Engine(path, max_ctx=256, graphs=0)
+    g = minfer.Engine(path, max_ctx=256, graphs=1, persistent=persistent)
+    d = minfer.Engine(path, max_ctx=256, graphs=0, persistent=1)
     for e in (g, d):
         e.prefill(prompt)            # 12 replays of the T=8 graph and one of T=4 in g
     cases = [(100, 8, True), (100, 8, False), (64, 5, True), (69, 8, True), (60, 8, False), (68, 2, True),
