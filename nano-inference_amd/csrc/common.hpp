@@ -99,6 +99,26 @@ struct DModel {
     float* dT;                     // [NL][ks_d][kMaxT][E]
     float* candT;                  // [workgroups][kMaxT][4]
     float* logitsT;                // [kMaxT][V] (written when non-null)
+    struct SpecDev* spec;          // [1] state of speculative generation driven on the device
+};
+
+// Speculative generation on the device (mega.cu:863-895): each persistent multi-token
+// launch verifies tokbuf[pos..pos+T-1] = [current token, drafts] at pos = *posT, then its
+// workgroup 0 commits the accepted prefix plus the correction, updates the acceptance
+// average, drafts the next step into tokbuf and sets T and *posT for the next launch.
+// The emitted tokens are out_tok[p0-1 ..] (p0: the first generated position).
+struct SpecDev {
+    int32_t T;                     // tokens of the next verify step (1 + drafts)
+    int32_t done;                  // 1: generation finished; later launches return at once
+    int32_t emitted;               // tokens emitted so far (the first is the prefill's prediction)
+    int32_t n_gen;                 // tokens to emit
+    int32_t eos;                   // stop after emitting this token (-1: no stop)
+    int32_t last_pos;              // position of the last emitted token (its K/V not computed)
+    int32_t steps, drafted, accepted;
+    int32_t ngmax, maxseq, tmax;
+    float acc_num, acc_den;        // EWMA of accepted / (accepted + rejections) (mega.cu:613)
+    float slope;                   // opts.spec_slope
+    int32_t pad;
 };
 
 inline __host__ __device__ size_t tile_bytes(int cb) { return (size_t)cb * 1152; }

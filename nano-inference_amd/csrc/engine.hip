@@ -467,7 +467,7 @@ static int load_impl(mi_engine* e, const char* path) {
         (rc = alloc_buf(e, &M.oT, NL * e->ks[1] * TM * e->E)) ||
         (rc = alloc_buf(e, &M.actT, NL * TM * (e->FF / 32) * kActRec)) ||
         (rc = alloc_buf(e, &M.dT, NL * e->ks[3] * TM * e->E)) ||
-        (rc = alloc_buf(e, &M.candT, (size_t)e->n_cu * TM * 4)))
+        (rc = alloc_buf(e, &M.candT, (size_t)e->n_cu * TM * 4)) || (rc = alloc_buf(e, &M.spec, 1)))
         return rc;
     M.logits = nullptr;
     M.logitsT = nullptr;
@@ -870,6 +870,64 @@ static int run_tokens(mi_engine* e, int pos, int T, int32_t* tok, float* mg) {
     return rc == kRetry ? run_tokens(e, pos, T, tok, mg) : rc;
 }
 
+// Speculative generation driven on the device (mega.cu:863-895: the reference drafts,
+// commits and adapts K inside its persistent loop): the same steps as generate_spec below,
+// in the same float arithmetic, but each verify launch reads its T and position from
+// M.spec / posT and commits on the device (spec_commit), so the host only drafts the first
+// step, queues launches and reads the result once. A launch after the generation finished
+// returns at once; at most n_gen - 1 steps are needed (each emits at least one token).
+static int generate_spec_device(mi_engine* e, int n_gen, int32_t* out, float* margins, int32_t* n_out) {
+    const int p0 = e->cur_len;
+    const int TM = kernels_max_tokens();
+    std::vector<int32_t> hist((size_t)p0 + TM + 1);
+    HIPCHK(e, hipMemcpy(hist.data(), e->M.tokbuf, sizeof(int32_t) * (p0 + 1), hipMemcpyDeviceToHost));
+    const int eos = e->opts.stop_eos ? e->eos : -1;
+    SpecDev sp{};
+    sp.emitted = n_gen > 0 ? 1 : 0;                  // the prefill's prediction, tokbuf[p0]
+    sp.n_gen = n_gen;
+    sp.eos = eos;
+    sp.last_pos = p0;
+    sp.ngmax = e->opts.ngmax;
+    sp.maxseq = e->maxseq;
+    sp.tmax = TM;
+    sp.acc_num = 0.6f;
+    sp.acc_den = 1.f;
+    sp.slope = e->opts.spec_slope;
+    sp.done = n_gen <= 1 || (eos >= 0 && hist[p0] == eos);
+    if (!sp.done) {
+        const float alpha = std::min(std::max(sp.acc_num / sp.acc_den, 0.01f), 0.99f);
+        const int kmax = std::min(mi_best_draft_len(alpha, sp.slope, TM), std::min(n_gen - 2, e->maxseq - 1 - p0));
+        const int K = kmax > 0 ? mi_ngram_draft(hist.data(), p0 + 1, sp.ngmax, kmax, hist.data() + p0 + 1) : 0;
+        sp.T = K + 1;                                // tokbuf[p0] already holds the current token
+        if (K > 0)
+            HIPCHK(e, hipMemcpyAsync(e->M.tokbuf + p0 + 1, hist.data() + p0 + 1, sizeof(int32_t) * K, hipMemcpyHostToDevice, e->stream));
+    }
+    HIPCHK(e, hipMemcpyAsync(e->M.spec, &sp, sizeof(SpecDev), hipMemcpyHostToDevice, e->stream));
+    HIPCHK(e, hipMemcpyAsync(e->M.posT, e->h_iota + p0, sizeof(int32_t), hipMemcpyHostToDevice, e->stream));
+    const auto t_start = std::chrono::steady_clock::now();
+    for (int s = 0; !sp.done && s < n_gen - 1; s++)
+        HIPCHK(e, launch_spec_step(e->M, e->dM, e->nwg_persistent, e->coop, e->stream));
+    HIPCHK(e, hipMemcpyAsync(&sp, e->M.spec, sizeof(SpecDev), hipMemcpyDeviceToHost, e->stream));
+    HIPCHK(e, hipStreamSynchronize(e->stream));
+    if (int rc = check_barrier(e)) return rc == kRetry ? generate_spec_device(e, n_gen, out, margins, n_out) : rc;
+    const double ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t_start).count();
+    const int emitted = sp.emitted;
+    if (emitted > 0) {
+        // emitted token k is the prediction after position p0 - 1 + k
+        if (out) HIPCHK(e, hipMemcpy(out, e->M.out_tok + p0 - 1, sizeof(int32_t) * emitted, hipMemcpyDeviceToHost));
+        if (margins) HIPCHK(e, hipMemcpy(margins, e->M.out_margin + p0 - 1, sizeof(float) * emitted, hipMemcpyDeviceToHost));
+    }
+    e->stats.decode_ms = ms;
+    e->stats.steps = sp.steps;
+    e->stats.tokens = emitted;
+    e->stats.drafted = sp.drafted;
+    e->stats.accepted = sp.accepted;
+    e->cur_len = sp.last_pos;                        // the last emitted token sits there (tokbuf), K/V not computed
+    e->next_ready = true;
+    if (n_out) *n_out = emitted;
+    return MI_OK;
+}
+
 // Lossless speculative generation (mega.cu:863-895): each step runs [cur, draft]
 // at positions pos..pos+K and commits the predictions up to and including the first
 // one that disagrees with its draft. A token's logits do not depend on how many
@@ -942,7 +1000,10 @@ int mi_generate(mi_engine* e, int32_t n_gen, int32_t* out, float* margins, int32
     if (!e || n_gen < 0) return MI_ERR_ARG;
     if (!e->next_ready || e->cur_len < 1) return set_err(e, MI_ERR_STATE, "mi_generate needs mi_prefill first");
     if (e->cur_len + n_gen > e->maxseq) return set_err(e, MI_ERR_ARG, "n_gen %d exceeds the context capacity", n_gen);
-    if (e->opts.spec) return generate_spec(e, n_gen, out, margins, n_out, cb, user);
+    if (e->opts.spec) {
+        if (e->nwg_persistent && e->multi_persistent && !cb) return generate_spec_device(e, n_gen, out, margins, n_out);
+        return generate_spec(e, n_gen, out, margins, n_out, cb, user);
+    }
     e->stats.drafted = e->stats.accepted = 0;
     const int p0 = e->cur_len;                   // position of the first generated token
     const bool sync_each = cb != nullptr || e->opts.stop_eos;

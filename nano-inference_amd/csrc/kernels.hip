@@ -2113,11 +2113,102 @@ __global__ __launch_bounds__(kPThreads) void kT_argmax(const DModel* Mp, int nca
 // into buffers whose lines are each written once per launch before any workgroup reads
 // them (per-layer partials, records and xT slots), so plain loads never meet a stale
 // line. The same arithmetic as the per-phase launches, so the same bits.
+// ---- speculative generation on the device (the host loop's steps, engine.hip
+// generate_spec, in the same float arithmetic)
+// mi_best_draft_len (spec.cpp; mega.cu:581-589): the k in 0..tmax-1 with the best expected
+// tokens per unit of step cost
+__device__ __forceinline__ int spec_best_k(float alpha, float slope, int tmax) {
+    int best_k = 0;
+    float best_rate = 1.f, all_accepted = alpha;
+    for (int k = 1; k < tmax; ++k) {
+        all_accepted = __fmul_rn(all_accepted, alpha);
+        const float expected = __fdiv_rn(__fsub_rn(1.f, all_accepted), __fsub_rn(1.f, alpha));
+        const float rate = __fdiv_rn(expected, __fadd_rn(1.f, __fmul_rn(slope, (float)k)));
+        if (rate > best_rate) {
+            best_rate = rate;
+            best_k = k;
+        }
+    }
+    return best_k;
+}
+// mi_ngram_draft (spec.cpp; mega.cu:561-578) by one wave: for n = ngmax..1 the latest
+// earlier j whose h[j..j+n) equals the last n tokens of h[0..len), lanes testing 64
+// candidates j at a time from the top; its following tokens go to out. Returns K. The
+// history is read with agent-coherent loads (this wave has just written its tail).
+__device__ __forceinline__ int spec_draft(int32_t* h, int len, int ngmax, int kmax, int32_t* out, int lane) {
+    if (kmax <= 0) return 0;
+    auto hv = [&](int i) { return (int32_t)ldc(reinterpret_cast<const uint32_t*>(h + i)); };
+    for (int n = ngmax; n >= 1; n--) {
+        if (len < n + 1) continue;
+        for (int base = len - n - 1; base >= 0; base -= 64) {
+            const int j = base - lane;
+            bool match = j >= 0;
+            for (int k = 0; k < n && match; k++) match = hv(j + k) == hv(len - n + k);
+            const uint64_t b = __builtin_amdgcn_ballot_w64(match);
+            if (b) {
+                const int jj = base - (int)__builtin_ctzll(b);      // the largest matching j
+                const int K = min(kmax, len - (jj + n));
+                if (lane < K) out[lane] = hv(jj + n + lane);
+                return K;
+            }
+        }
+    }
+    return 0;
+}
+// after the verify step of T tokens at pos: the commit and the next draft (one wave)
+__device__ __forceinline__ void spec_commit(MPtr M, SpecDev* sp, int lane) {
+    const int pos = *M->posT, K = sp->T - 1;
+    int32_t* h = M->tokbuf;
+    int a = 0;
+    while (a < K && h[pos + 1 + a] == M->out_tok[pos + a]) a++;
+    int emitted = sp->emitted, last = sp->last_pos;
+    bool done = false;
+    for (int i = 0; i <= a && !done; i++) {
+        const int32_t y = M->out_tok[pos + i];
+        if (lane == 0) h[pos + 1 + i] = y;
+        emitted++;
+        last = pos + 1 + i;
+        done = emitted >= sp->n_gen || (sp->eos >= 0 && y == sp->eos);
+    }
+    const int np = pos + a + 1;                              // h[np] = the new current token (written above)
+    float an = sp->acc_num, ad = sp->acc_den;
+    if (K > 0) {
+        an = __fadd_rn(__fmul_rn(0.85f, an), __fmul_rn(0.15f, (float)a));
+        ad = __fadd_rn(__fmul_rn(0.85f, ad), __fmul_rn(0.15f, (float)(a + (a < K ? 1 : 0))));
+    }
+    int T = 1;
+    if (!done) {
+        drain_vm();                                          // the history writes above, before the search reads them
+        const float alpha = fminf(fmaxf(__fdiv_rn(an, ad), 0.01f), 0.99f);
+        const int kmax = min(spec_best_k(alpha, sp->slope, sp->tmax), min(sp->n_gen - emitted - 1, sp->maxseq - 1 - np));
+        T = 1 + spec_draft(h, np + 1, sp->ngmax, kmax, h + np + 1, lane);
+    }
+    if (lane == 0) {
+        sp->T = T;
+        sp->done = done;
+        sp->emitted = emitted;
+        sp->last_pos = last;
+        sp->steps += 1;
+        sp->drafted += K;
+        sp->accepted += a;
+        sp->acc_num = an;
+        sp->acc_den = ad;
+        if (!done) *M->posT = np;
+    }
+}
+
 constexpr int kTStepLds = kTDownLds > kTGemvLds ? kTDownLds : kTGemvLds;
 static_assert(kTStepLds >= kt_attn_lds<128>() && kTStepLds >= 4 * kMaxE, "every phase's LDS fits");
-template <int HD>
+// SPEC: T comes from M->spec (a speculative generation driven on the device): a launch
+// after the generation finished returns at once, and workgroup 0 ends the step with
+// spec_commit.
+template <int HD, bool SPEC>
 __global__ __launch_bounds__(kPThreads) void kT_step(const DModel* Mp, int T) {
     const MPtr M = (MPtr)Mp;
+    if constexpr (SPEC) {
+        if (M->spec->done) return;                           // every workgroup reads the same word
+        T = M->spec->T;
+    }
     __shared__ __align__(16) uint8_t smem[kTStepLds];
     const int wg = blockIdx.x, nwg = gridDim.x, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     float* xs = reinterpret_cast<float*>(smem);
@@ -2151,7 +2242,13 @@ __global__ __launch_bounds__(kPThreads) void kT_step(const DModel* Mp, int T) {
     kT_lm_body<true>(M, T, smem, wg, nwg);
     barrier();
     if (wave == 0) ctl_exit(M->bar);
-    if (wg == 0) kT_argmax_body(M, nwg, T);
+    if (wg == 0) {
+        kT_argmax_body(M, nwg, T);
+        if constexpr (SPEC) {
+            __syncthreads();                                 // the step's out_tok / out_margin
+            if (wave == 0) spec_commit(M, M->spec, lane);
+        }
+    }
 }
 
 // ------------------------------------------------------------------ standalone kernels
@@ -2668,7 +2765,19 @@ hipError_t launch_step_multi_persistent(const DModel& M, const DModel* dM, int n
     with_hd(M.HD, [&](auto hd) {
         const DModel* m = dM;
         void* args[] = {&m, &T};
-        const void* f = reinterpret_cast<const void*>(&kT_step<decltype(hd)::value>);
+        const void* f = reinterpret_cast<const void*>(&kT_step<decltype(hd)::value, false>);
+        err = coop ? hipLaunchCooperativeKernel(f, dim3(nwg), dim3(kPThreads), args, 0, s)
+                   : hipLaunchKernel(f, dim3(nwg), dim3(kPThreads), args, 0, s);
+    });
+    return err;
+}
+hipError_t launch_spec_step(const DModel& M, const DModel* dM, int nwg, bool coop, hipStream_t s) {
+    hipError_t err = hipSuccess;
+    with_hd(M.HD, [&](auto hd) {
+        const DModel* m = dM;
+        int T = 0;
+        void* args[] = {&m, &T};
+        const void* f = reinterpret_cast<const void*>(&kT_step<decltype(hd)::value, true>);
         err = coop ? hipLaunchCooperativeKernel(f, dim3(nwg), dim3(kPThreads), args, 0, s)
                    : hipLaunchKernel(f, dim3(nwg), dim3(kPThreads), args, 0, s);
     });
@@ -2677,7 +2786,7 @@ hipError_t launch_step_multi_persistent(const DModel& M, const DModel* dM, int n
 int multi_persistent_max_grid(int HD) {
     int per_cu = 0;
     with_hd(HD, [&](auto hd) {
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(&kT_step<decltype(hd)::value>),
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(&kT_step<decltype(hd)::value, true>),
                                                          kPThreads, 0) != hipSuccess)
             per_cu = 0;
     });

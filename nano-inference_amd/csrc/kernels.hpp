@@ -32,7 +32,10 @@ void launch_step_multi(const DModel& M, const DModel* dM, int nwg, int T, hipStr
 // the same multi-token step as one persistent launch of nwg workgroups, all resident at
 // once (grid barriers; coop and M.bar / M.err as for launch_step_persistent)
 hipError_t launch_step_multi_persistent(const DModel& M, const DModel* dM, int nwg, int T, bool coop, hipStream_t s);
-// co-resident workgroups per CU of the persistent multi-token kernel (0: cannot launch)
+// one verify step of a speculative generation driven on the device (M.spec holds T, the
+// position is *M.posT; a launch after the generation finished does nothing)
+hipError_t launch_spec_step(const DModel& M, const DModel* dM, int nwg, bool coop, hipStream_t s);
+// co-resident workgroups per CU of the persistent multi-token kernels (0: cannot launch)
 int multi_persistent_max_grid(int HD);
 int kernels_max_tokens();
 int kernels_max_chunks_multi();   // chunks per K segment the multi-token kernels stage

@@ -252,3 +252,36 @@ def test_spec_generate_repetitive_prompt():
     say("repetitive prompt: %d verify steps for %d tokens, %d drafted, %d accepted" %
         (st["steps"], st["tokens"], st["drafted"], st["accepted"]))
     assert st["drafted"] > 0
+
+
+@pytest.mark.parametrize("case", ["config2", "repetitive"])
+def test_spec_driven_on_device_equals_host_loop(case):
+    """persistent = 2 and no callback: the speculative loop runs on the device (each
+    persistent verify launch commits and drafts the next step itself). Tokens and margins
+    equal the plain greedy decode, and the verify steps, drafts and acceptances equal the
+    host-driven loop's one for one (the same draft rule in the same float arithmetic)."""
+    if case == "config2":
+        cfg = minfer.CONFIGS["config2"]
+        shape = minfer.SHAPES[cfg[0]]
+        path = synth_cached("config2", shape, cfg[1])
+        prompt, n_gen, max_ctx = minfer.prompt_ids(cfg[2], cfg[3], shape["n_vocab"]), 128, cfg[3] + 160
+    else:
+        path = synth_cached("eng-512", SMALL, 21)
+        prompt, n_gen, max_ctx = minfer.prompt_ids(31, 12, SMALL["n_vocab"]) * 6, 96, 200
+    res = {}
+    for mode, opts in (("plain", dict(spec=0)), ("host", dict(spec=1, persistent=1)),
+                       ("device", dict(spec=1, persistent=2))):
+        say("%s: %s" % (case, mode))
+        eng = minfer.Engine(path, max_ctx=max_ctx, **opts)
+        eng.prefill(prompt)
+        toks, margins = eng.generate(n_gen)
+        res[mode] = (toks, margins, eng.stats())
+        eng.close()
+    for mode in ("host", "device"):
+        assert res[mode][0] == res["plain"][0], mode
+        assert np.array_equal(bits(res[mode][1]), bits(res["plain"][1])), mode
+    h, d = res["host"][2], res["device"][2]
+    say("%s: %d steps, %d drafted, %d accepted (device %.1f ms, host loop %.1f ms)" %
+        (case, d["steps"], d["drafted"], d["accepted"], d["decode_ms"], h["decode_ms"]))
+    for k in ("steps", "tokens", "drafted", "accepted"):
+        assert d[k] == h[k], (k, d[k], h[k])
