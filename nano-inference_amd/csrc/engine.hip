@@ -876,6 +876,7 @@ static int run_tokens(mi_engine* e, int pos, int T, int32_t* tok, float* mg) {
 // M.spec / posT and commits on the device (spec_commit), so the host only drafts the first
 // step, queues launches and reads the result once. A launch after the generation finished
 // returns at once; at most n_gen - 1 steps are needed (each emits at least one token).
+// (sp below is the host copy; it is read back from the device after each batch.)
 static int generate_spec_device(mi_engine* e, int n_gen, int32_t* out, float* margins, int32_t* n_out) {
     const int p0 = e->cur_len;
     const int TM = kernels_max_tokens();
@@ -905,10 +906,16 @@ static int generate_spec_device(mi_engine* e, int n_gen, int32_t* out, float* ma
     HIPCHK(e, hipMemcpyAsync(e->M.spec, &sp, sizeof(SpecDev), hipMemcpyHostToDevice, e->stream));
     HIPCHK(e, hipMemcpyAsync(e->M.posT, e->h_iota + p0, sizeof(int32_t), hipMemcpyHostToDevice, e->stream));
     const auto t_start = std::chrono::steady_clock::now();
-    for (int s = 0; !sp.done && s < n_gen - 1; s++)
-        HIPCHK(e, launch_spec_step(e->M, e->dM, e->nwg_persistent, e->coop, e->stream));
-    HIPCHK(e, hipMemcpyAsync(&sp, e->M.spec, sizeof(SpecDev), hipMemcpyDeviceToHost, e->stream));
-    HIPCHK(e, hipStreamSynchronize(e->stream));
+    // launches in batches of kSpecBatch, the state read back after each: a generation
+    // that finished early leaves at most kSpecBatch - 1 launches that return at once
+    constexpr int kSpecBatch = 16;
+    for (int queued = 0; !sp.done && queued < n_gen - 1;) {
+        const int nb = std::min(kSpecBatch, n_gen - 1 - queued);
+        for (int i = 0; i < nb; i++) HIPCHK(e, launch_spec_step(e->M, e->dM, e->nwg_persistent, e->coop, e->stream));
+        queued += nb;
+        HIPCHK(e, hipMemcpyAsync(&sp, e->M.spec, sizeof(SpecDev), hipMemcpyDeviceToHost, e->stream));
+        HIPCHK(e, hipStreamSynchronize(e->stream));
+    }
     if (int rc = check_barrier(e)) return rc == kRetry ? generate_spec_device(e, n_gen, out, margins, n_out) : rc;
     const double ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t_start).count();
     const int emitted = sp.emitted;
