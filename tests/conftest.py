@@ -34,3 +34,43 @@ def synth_cached(name, shape, seed, expect_hash=None, **types):
         minfer.synth_gguf(path, shape, seed, **types)
         open(marker, "w").close()
     return path
+
+
+def gguf_kv_u32_offset(path, key):
+    """file offset of a u32 metadata value of a GGUF v3 file"""
+    import struct
+    with open(path, "rb") as f:
+        b = f.read()
+    o = [4]
+
+    def rd(fmt):
+        v = struct.unpack_from("<" + fmt, b, o[0])[0]
+        o[0] += struct.calcsize("<" + fmt)
+        return v
+
+    def rstr():
+        n = rd("Q")
+        o[0] += n
+        return b[o[0] - n:o[0]].decode()
+
+    sizes = {0: 1, 1: 1, 2: 2, 3: 2, 4: 4, 5: 4, 6: 4, 7: 1, 10: 8, 11: 8, 12: 8}
+
+    def skip(t):
+        if t == 8:
+            rstr()
+        elif t == 9:
+            et, n = rd("I"), rd("Q")
+            for _ in range(n):
+                skip(et)
+        else:
+            o[0] += sizes[t]
+
+    assert b[:4] == b"GGUF" and rd("I") == 3
+    _, nkv = rd("Q"), rd("Q")
+    for _ in range(nkv):
+        k, t = rstr(), rd("I")
+        if k == key:
+            assert t == 4
+            return o[0]
+        skip(t)
+    raise KeyError(key)

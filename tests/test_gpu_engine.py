@@ -16,7 +16,7 @@ import pytest
 
 import minfer
 import oracle_lib as O
-from conftest import synth_cached
+from conftest import synth_cached, gguf_kv_u32_offset
 
 pytestmark = pytest.mark.gpu
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
@@ -195,46 +195,6 @@ def gguf_tensor_data(path):
         infos.append((name, rd("I"), dims, rd("Q")))
     base = (o[0] + align - 1) // align * align
     return {n: (base + off, t, dims) for n, t, dims, off in infos}
-
-
-def gguf_kv_u32_offset(path, key):
-    """file offset of a u32 metadata value of a GGUF v3 file"""
-    import struct
-    with open(path, "rb") as f:
-        b = f.read()
-    o = [4]
-
-    def rd(fmt):
-        v = struct.unpack_from("<" + fmt, b, o[0])[0]
-        o[0] += struct.calcsize("<" + fmt)
-        return v
-
-    def rstr():
-        n = rd("Q")
-        o[0] += n
-        return b[o[0] - n:o[0]].decode()
-
-    sizes = {0: 1, 1: 1, 2: 2, 3: 2, 4: 4, 5: 4, 6: 4, 7: 1, 10: 8, 11: 8, 12: 8}
-
-    def skip(t):
-        if t == 8:
-            rstr()
-        elif t == 9:
-            et, n = rd("I"), rd("Q")
-            for _ in range(n):
-                skip(et)
-        else:
-            o[0] += sizes[t]
-
-    assert b[:4] == b"GGUF" and rd("I") == 3
-    _, nkv = rd("Q"), rd("Q")
-    for _ in range(nkv):
-        k, t = rstr(), rd("I")
-        if k == key:
-            assert t == 4
-            return o[0]
-        skip(t)
-    raise KeyError(key)
 
 
 def test_streaming_generate():

@@ -285,3 +285,51 @@ def test_spec_driven_on_device_equals_host_loop(case):
         (case, d["steps"], d["drafted"], d["accepted"], d["decode_ms"], h["decode_ms"]))
     for k in ("steps", "tokens", "drafted", "accepted"):
         assert d[k] == h[k], (k, d[k], h[k])
+
+
+def test_spec_driven_on_device_stops_at_eos(tmp_path):
+    """An eos stop inside a verify step's accepted run, with the commit on the device:
+    the output ends at the eos exactly as the plain decode's does (mega.cu:1014-1017
+    stops at tokenizer.ggml.eos_token_id), and a step at the eos position afterwards
+    gives the plain engine's logits bit for bit (the drafts written past the stop left
+    no trace in the positions before it). The prompt ends with 40 tokens of the model's
+    own greedy stream, which has fallen into a cycle by then, so the drafter has
+    matches from the first step on."""
+    import shutil
+    from conftest import gguf_kv_u32_offset
+    path = synth_cached("eng-512", SMALL, 21)
+    V = SMALL["n_vocab"]
+    base = minfer.prompt_ids(31, 12, V) * 6
+    ref = minfer.Engine(path, max_ctx=200)
+    ref.prefill(base)
+    stream, _ = ref.generate(96)
+    ref.close()
+    prompt, want, n_gen = base + stream[:40], stream[40:], 56
+    # the eos: the continuation's token whose first occurrence in it is the latest
+    first = max(want.index(t) for t in set(want))
+    assert first >= 3
+    stop_path = str(tmp_path / "eos-stop.gguf")
+    shutil.copy(path, stop_path)
+    with open(stop_path, "r+b") as f:
+        f.seek(gguf_kv_u32_offset(stop_path, "tokenizer.ggml.eos_token_id"))
+        f.write(np.uint32(want[first]).tobytes())
+    res = {}
+    for mode, opts in (("plain", dict(spec=0)), ("host", dict(spec=1, persistent=1)),
+                       ("device", dict(spec=1, persistent=2))):
+        say("eos stop at output %d: %s" % (first, mode))
+        eng = minfer.Engine(stop_path, max_ctx=200, stop_eos=1, **opts)
+        eng.prefill(prompt)
+        toks, margins = eng.generate(n_gen)
+        st = eng.stats()
+        _, _, lg = eng.step(want[first], len(prompt) + first, want_logits=True)
+        res[mode] = (toks, margins, lg, st)
+        eng.close()
+        say("  %d tokens, %d steps, %d drafted, %d accepted" % (len(toks), st["steps"], st["drafted"], st["accepted"]))
+    assert res["plain"][0] == want[:first + 1]
+    for mode in ("host", "device"):
+        assert res[mode][0] == res["plain"][0], mode
+        assert np.array_equal(bits(res[mode][1]), bits(res["plain"][1])), mode
+        assert np.array_equal(bits(res[mode][2]), bits(res["plain"][2])), mode
+    assert res["device"][3]["accepted"] > 0
+    for key in ("steps", "drafted", "accepted"):
+        assert res["device"][3][key] == res["host"][3][key], key
