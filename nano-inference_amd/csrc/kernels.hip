@@ -197,9 +197,6 @@ __device__ __forceinline__ uint32_t ldc(const uint32_t* p) {
 __device__ __forceinline__ void stc(float* p, float v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
 __device__ __forceinline__ void stc(uint32_t* p, uint32_t v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
 __device__ __forceinline__ void drain_vm() { __builtin_amdgcn_s_waitcnt(0x0F70); }      // vmcnt(0)
-__device__ __forceinline__ uint64_t ldc64(const void* p) {
-    return __hip_atomic_load(reinterpret_cast<const uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
 // a store to memory that other workgroups of the same launch read (P: agent-coherent)
 // or that only later launches read (plain)
 template <bool P>
