@@ -244,13 +244,12 @@ int mi_q4_block_isums(const uint8_t* packed, int32_t rows, int32_t nb, int32_t c
                       const int8_t* xq, int32_t* isum, void* stream);
 
 /* single-query GQA attention over an fp16 cache (cuda_infer.cu:650-702 attn_partial +
- * attn_combine, mega.cu:414-521), one kernel launch: q[n_head][hd] fp32, kc/vc
- * [n_head_kv][ctx][hd] fp16, positions 0..L-1, out[n_head][hd]; n_head / n_head_kv
- * <= 8. scratch holds mi_attn_scratch_floats(n_head, hd, L) floats: 65536 words of
- * arrival counters, then a record per head and 64-position chunk and, past 16 chunks,
- * a record per head and split of 16 chunks. The counter words must be zero before
- * the first call (zero-fill the scratch once); every completed call leaves them
- * zero. Calls that share a scratch buffer must not overlap. */
+ * attn_combine, mega.cu:414-521), two kernel launches on `stream` (chunk records, then
+ * their merge): q[n_head][hd] fp32, kc/vc [n_head_kv][ctx][hd] fp16, positions 0..L-1,
+ * out[n_head][hd]; n_head / n_head_kv <= 8, at most 512 splits of 16 64-position chunks
+ * (L <= 524288). scratch holds mi_attn_scratch_floats(n_head, hd, L) floats: a record
+ * per head and 64-position chunk, written and read within the call (no initial
+ * contents needed). Calls that share a scratch buffer must not overlap. */
 size_t mi_attn_scratch_floats(int32_t n_head, int32_t hd, int32_t L);
 int mi_attn_decode(const float* q, const uint16_t* kc, const uint16_t* vc, int32_t n_head,
                    int32_t n_head_kv, int32_t hd, int32_t L, int32_t ctx, float scale,
@@ -262,8 +261,8 @@ int mi_attn_decode(const float* q, const uint16_t* kc, const uint16_t* vc, int32
  * scratch is a library-held device array of MI_ATTN_NOALLOC_SCRATCH_FLOATS floats (16 MiB,
  * one per GPU, held until the process ends); a shape that needs more than
  * mi_attn_scratch_floats() allows returns MI_ERR_SHAPE (message via mi_last_error(NULL)).
- * The first call on a device looks the array up and zeroes its counters with a kernel on
- * `stream`. All calls on one GPU share the array: calls that overlap on one GPU race. */
+ * The first call on a device looks the array's address up. All calls on one GPU share
+ * the array: calls that overlap on one GPU race. */
 #define MI_ATTN_NOALLOC_SCRATCH_FLOATS (4u << 20)
 int mi_attn_decode_noalloc(const float* q, const uint16_t* kc, const uint16_t* vc, int32_t n_head,
                            int32_t n_head_kv, int32_t hd, int32_t L, int32_t ctx, float scale,

@@ -2386,20 +2386,11 @@ __global__ __launch_bounds__(64) void k_isums(PMat W, const int8_t* xq, int32_t*
 }
 
 // ------------------------------------------------------------------ standalone attention
-// q[nh][hd] fp32 and an fp16 cache [nkv][ctx][hd]; one launch does the whole
-// attention (k_attn_tile below). The merge is comb_wave's order, done by the last
-// arrivals: after its chunk records (o[hd], m, l) are stored and drained, a workgroup
-// bumps its split's counter; the one that completes a split merges its chunks (and
-// writes the output if there is one split), then bumps the kv head's counter, whose
-// last arrival merges the splits. Records are written with agent-coherent stores
-// (through the per-XCD L2) and drained before the arrival atomic; every record line
-// has one writer and one reader in a launch, and the merging wave reads it only after
-// all its writers arrived, so no L2 can hold an older copy. No wave ever waits on
-// another. Each last arrival puts its counter back to zero.
-// scratch: counters [kAttnCounters] (zero before the first call, left zero by each
-// call) | chunk records [nh][nch][hd + 32] | split records [nh][nsp][hd + 32].
+// q[nh][hd] fp32 and an fp16 cache [nkv][ctx][hd]; two launches do the whole
+// attention: k_attn_rec writes a record (o[hd], m, l) per head and 64-position chunk,
+// k_attn_merge merges them in the canonical order. scratch: chunk records o
+// [nh][nch][hd], m [nh][nch], l [nh][nch].
 constexpr int kAttnMaxG = 8;        // query heads per kv head
-constexpr int kAttnCounters = 1 << 16;
 
 // One wave merges the records [c0, c1) of one head (contiguous, REC floats each)
 // as comb_wave does, lane = dims DPL*lane + e: M = max over all records, w_i =
@@ -2440,211 +2431,184 @@ __device__ __forceinline__ void lds_merge(const float* r, int c0, int c1, float*
     deno = den;
 }
 
-// Up to 32 records of one head held in registers: lane i < n holds m and l of record i,
-// every lane its DPL dims of each record. rr_issue starts the loads (all of them at
-// once: the merge costs one memory round trip, and the next head's loads can be in
-// flight while rr_merge works on this one); rr_merge computes what lds_merge does
-// (M = max over the records, w_i = exp(m_i - M), den and acc as fma chains in record
-// order), so the two give the same bits.
-constexpr int kRegRecs = 32;
-template <int HD, int N>
-struct RegRecs { float m, l; float o[N][HD / 64]; };
-template <int HD, int N>
-__device__ __forceinline__ void rr_issue(RegRecs<HD, N>& b, const float* r, int n, int lane) {
-    constexpr int REC = HD + 32, DPL = HD / 64;
-    // opaque copy of the lane index: keeps the lane-derived addresses from being hoisted
-    // out of the item loop, where they would stay live across the items' register peak
-    asm volatile("" : "+v"(lane));
-    b.m = lane < n ? r[lane * REC + HD] : -__builtin_inff();
-    b.l = lane < n ? r[lane * REC + HD + 1] : 0.f;
-#pragma unroll
-    for (int i = 0; i < N; i++) {
-        if (i < n) {
-            if constexpr (DPL == 2) {
-                const float2 v = *reinterpret_cast<const float2*>(r + i * REC + 2 * lane);
-                b.o[i][0] = v.x;
-                b.o[i][1] = v.y;
-            } else {
-                b.o[i][0] = r[i * REC + lane];
-            }
-        }
-    }
-}
-// the wave's arrival on a counter of `need` arrivals: true for the last one, which
-// puts the counter back to zero (every arrival of this launch is in by then)
-__device__ __forceinline__ bool last_arrival(uint32_t* cnt, uint32_t need, int lane) {
-    drain_vm();                                    // this wave's record stores are done
-    uint32_t old = 0;
-    if (lane == 0) old = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    old = __builtin_amdgcn_readfirstlane(old);
-    if (old + 1 != need) return false;
-    if (lane == 0) stc(cnt, 0u);
-    return true;
+// Standalone attention, part 1: the chunk records. A unit is (kv head, 64-position
+// chunk). A workgroup takes S units per round (units SP .. SP + S - 1 for P = w,
+// w + grid, ...) with W = ceil(G / H) compute waves per unit (H heads each) and one data
+// wave. The data wave DMAs a round's K rows (coalesced, 1 KB of consecutive rows per
+// instruction, into the step kernel's swizzled tile: kslot), V rows and the G query rows
+// of each unit's kv head into one of two sets of LDS buffers, and issues the next
+// round's DMA into the other set as soon as the compute waves start on this one, so
+// every CU keeps loads in flight while it computes (all units' DMA issued at once, as a
+// one-workgroup-per-unit launch does, lands everywhere at about the same time and
+// leaves the compute after it). A compute wave runs its H heads together
+// (attn_core_h: each head's arithmetic is attn_core's, so the records carry its bits).
+// Records go to recs as o[h][chunk][hd], then m[h][chunk], then l[h][chunk] (the merge
+// of 16 dims reads every m and l of a head: contiguous); the merge kernel reads them
+// after this launch ends (the kernel boundary orders the plain stores before it).
+template <int HD>
+constexpr int attn_rec_buf() { return 2 * 64 * HD * 2 + kAttnMaxG * HD * 4; }
+template <int H>
+constexpr int attn_rec_wmax() { return (kAttnMaxG + H - 1) / H; }          // compute waves per unit, at most
+template <int HD, int H, int S>
+constexpr int attn_rec_lds() { return 2 * S * attn_rec_buf<HD>() + S * attn_rec_wmax<H>() * H * 64 * 4; }
+
+// the DMA of unit u (kv head, chunk) into buffer B: K tile, V rows, the kv head's q rows
+template <int HD>
+__device__ __forceinline__ void attn_rec_issue(const float* q, const __half* kc, const __half* vc, int G, int nch, int L,
+                                               int ctx, int u, uint8_t* B, int lane) {
+    const int kvh = u / nch, t0 = (u - kvh * nch) * kAttnChunk, n = min(kAttnChunk, L - t0);
+    dma_wave(q + (size_t)kvh * G * HD, B + 2 * 64 * HD * 2, G * HD * 4, lane);
+    attn_issue_k<HD>(kc + ((size_t)kvh * ctx + t0) * HD, n, reinterpret_cast<uint4*>(B), lane);
+    attn_issue_v<HD>(vc + ((size_t)kvh * ctx + t0) * HD, n, reinterpret_cast<__half*>(B + 64 * HD * 2), lane);
 }
 
-// The merge of the records in b (what lds_merge computes: M = max over the records,
-// w_i = exp(m_i - M), den and acc as fma chains in record order, so the two give the
-// same bits). The weights w_i and sums l_i reach every lane through the wave's LDS row
-// wl[0..64) (w at 0, l at 32; four records per 16-byte read): a readlane each cost
-// more than the fmas they feed.
-template <int HD, int N>
-__device__ __forceinline__ void rr_merge(const RegRecs<HD, N>& b, int n, int lane, float* wl, float& M, float& den,
-                                             float (&acc)[HD / 64]) {
-    static_assert(N <= 32 && N % 4 == 0, "records per merge");
-    constexpr int DPL = HD / 64;
-    M = wave_max(b.m);
-    const float w = lane < n ? mi_expf(__fsub_rn(b.m, M)) : 0.f;
-    if (lane < 32) {
-        wl[lane] = w;
-        wl[32 + lane] = b.l;
+template <int HD, int H, int S>
+__global__ __launch_bounds__(64 * (S * ((kAttnMaxG + H - 1) / H) + 1)) void k_attn_rec(const float* q, const __half* kc,
+                                                                      const __half* vc, int nh, int nkv, int L, int ctx,
+                                                                      float scale, float* recs) {
+    constexpr int DPL = HD / 64, KV = 2 * 64 * HD * 2, BUF = attn_rec_buf<HD>();
+    __shared__ __align__(16) uint8_t smem[attn_rec_lds<HD, H, S>()];
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int G = nh / nkv, W = (G + H - 1) / H, dw = S * W;          // wave dw moves the data
+    const int nch = (L + kAttnChunk - 1) / kAttnChunk, units = nkv * nch;
+    float* pls = reinterpret_cast<float*>(smem + 2 * S * BUF) + wave * H * 64;   // the wave's [H][64] probabilities
+    int P = blockIdx.x;
+    if (wave == dw) {
+#pragma unroll
+        for (int j = 0; j < S; j++)
+            if (S * P + j < units) attn_rec_issue<HD>(q, kc, vc, G, nch, L, ctx, S * P + j, smem + j * BUF, lane);
     }
-    wave_lds_sync();
-    den = 0.f;
+    for (int k = 0; S * P < units; k++, P += gridDim.x) {
+        if (wave == dw) drain_vm();                     // round P is in buffer set k & 1
+        __syncthreads();                                // (and the compute waves are done with the other set)
+        if (wave == dw) {
+            const int Pn = P + gridDim.x;
+            uint8_t* Bn = smem + ((k + 1) & 1) * S * BUF;
 #pragma unroll
-    for (int e = 0; e < DPL; e++) acc[e] = 0.f;
+            for (int j = 0; j < S; j++)
+                if (S * Pn + j < units) attn_rec_issue<HD>(q, kc, vc, G, nch, L, ctx, S * Pn + j, Bn + j * BUF, lane);
+            continue;
+        }
+        const int j = wave / W, u = S * P + j;
+        const int hb = (wave - j * W) * H, hn = min(H, G - hb);
+        if (u >= units) continue;
+        const int kvh = u / nch, c = u - kvh * nch, n = min(kAttnChunk, L - c * kAttnChunk);
+        const uint8_t* B = smem + ((k & 1) * S + j) * BUF;
+        float m[H], ls[H], acc[H][DPL];
+        attn_core_h<HD, H>(reinterpret_cast<const uint4*>(B), reinterpret_cast<const float*>(B + KV) + hb * HD, hn,
+                           reinterpret_cast<const __half*>(B + 64 * HD * 2), n, scale, lane, pls, m, ls, acc);
 #pragma unroll
-    for (int i4 = 0; i4 < N; i4 += 4) {
-        if (i4 < n) {
-            const float4 w4 = *reinterpret_cast<const float4*>(wl + i4);
-            const float4 l4 = *reinterpret_cast<const float4*>(wl + 32 + i4);
-            const float wv[4] = {w4.x, w4.y, w4.z, w4.w}, lv[4] = {l4.x, l4.y, l4.z, l4.w};
+        for (int h = 0; h < H; h++) {
+            if (h < hn) {
+                const size_t hc = (size_t)(kvh * G + hb + h) * nch + c;
 #pragma unroll
-            for (int k = 0; k < 4; k++) {
-                if (i4 + k < n) {
-                    den = __fmaf_rn(lv[k], wv[k], den);
-#pragma unroll
-                    for (int e = 0; e < DPL; e++) acc[e] = __fmaf_rn(b.o[i4 + k][e], wv[k], acc[e]);
+                for (int e = 0; e < DPL; e++) recs[hc * HD + DPL * lane + e] = acc[h][e];
+                if (lane == 0) {
+                    recs[(size_t)nh * nch * HD + hc] = m[h];
+                    recs[(size_t)nh * nch * (HD + 1) + hc] = ls[h];
                 }
             }
         }
     }
-    wave_lds_sync();            // the row is free for the next merge
-}
-// The merges of g heads (records of head hh at r0 + hh * hstride, n <= N of them),
-// two heads' records in flight at a time (head hh merges in LDS row wl + 64 * (hh & 1));
-// done(hh, M, den, acc) takes each result.
-template <int HD, int N, class F>
-__device__ __forceinline__ void rr_heads(const float* r0, size_t hstride, int n, int g, int lane, float* wl, F done) {
-    RegRecs<HD, N> a, b;
-    float M, den, acc[HD / 64];
-    rr_issue<HD, N>(a, r0, n, lane);
-    for (int hh = 0; hh < g; hh += 2) {
-        if (hh + 1 < g) rr_issue<HD, N>(b, r0 + (hh + 1) * hstride, n, lane);
-        rr_merge<HD, N>(a, n, lane, wl, M, den, acc);
-        done(hh, M, den, acc);
-        if (hh + 1 < g) {
-            if (hh + 2 < g) rr_issue<HD, N>(a, r0 + (hh + 2) * hstride, n, lane);
-            rr_merge<HD, N>(b, n, lane, wl + 64, M, den, acc);
-            done(hh + 1, M, den, acc);
-        }
-    }
 }
 
-// Standalone attention, one workgroup per unit (kv head, 64-position chunk) and
-// ceil(G / H) waves. The chunk's K rows come into LDS by coalesced DMA (1 KB of
-// consecutive rows per instruction) in the step kernel's swizzled tile (kslot), its V
-// rows next to them, and the G query rows of the kv head beside; wave w then computes
-// heads wH .. wH + H - 1 together (attn_core_h), so the K/V of a chunk are read once
-// from memory for all G heads. Records (o[hd], m, l) are stored agent-coherent and
-// drained; the workgroup that completes a split of kAttnSplit chunks merges the split
-// for every head of the kv head (each wave its heads, records held in registers), and
-// the one that completes the kv head's last split merges the splits: the canonical
-// merge, the order of orc_attention_canon. Past kRegRecs splits wave 0 merges them through
-// LDS. Scratch: counters [nkv][nsp] then [nkv] (zero before the first call, left zero) |
-// chunk records [nh][nch] | split records [nh][nsp].
-constexpr int kTileHeads = 2;                  // query heads per wave
-template <int HD, int H>
-__global__ __launch_bounds__(64 * (kAttnMaxG / H)) void k_attn_tile(const float* q, const __half* kc, const __half* vc,
-                                                                   int nh, int nkv, int L, int ctx, float scale,
-                                                                   float* scratch, float* out) {
-    constexpr int REC = HD + 32, DPL = HD / 64;
-    static_assert(kAttnSplit * (HD + 32) * 4 <= 2 * 64 * HD * 2, "the LDS merge fits the K/V tile");
-    static_assert(H >= 2, "the merges of a wave's two heads use its LDS rows hb and hb + 1");
-    __shared__ __align__(16) uint8_t smem[2 * 64 * HD * 2 + kAttnMaxG * HD * 4 + kAttnMaxG * 64 * 4 + 16];
-    uint4* kls = reinterpret_cast<uint4*>(smem);
-    __half* vls = reinterpret_cast<__half*>(smem + 64 * HD * 2);
-    float* qs = reinterpret_cast<float*>(smem + 2 * 64 * HD * 2);
-    float* pls = qs + kAttnMaxG * HD;                                  // [G][64] probabilities
-    int* flag = reinterpret_cast<int*>(pls + kAttnMaxG * 64);
-    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int nw = blockDim.x >> 6;
-    const int nch = (L + kAttnChunk - 1) / kAttnChunk, G = nh / nkv, nsp = (nch + kAttnSplit - 1) / kAttnSplit;
-    const int u = blockIdx.x, kvh = u / nch, c = u - kvh * nch, t0 = c * kAttnChunk, n = min(kAttnChunk, L - t0);
-    const int h0 = kvh * G, hb = wave * H, hn = min(H, G - hb);    // the wave's heads h0 + hb .. + hn - 1
-    uint32_t* scnt = reinterpret_cast<uint32_t*>(scratch);           // [nkv][nsp]
-    uint32_t* hcnt = scnt + (size_t)nkv * nsp;                        // [nkv]
-    float* recs = scratch + kAttnCounters;
-    float* srecs = recs + (size_t)nh * nch * REC;
-    const __half* kr = kc + ((size_t)kvh * ctx + t0) * HD;
-    const __half* vr = vc + ((size_t)kvh * ctx + t0) * HD;
-    if (wave == 0) attn_issue_k<HD>(kr, n, kls, lane);
-    if (wave == (nw > 1 ? 1 : 0)) attn_issue_v<HD>(vr, n, vls, lane);
-    if (wave == (nw > 2 ? 2 : 0)) dma_wave(q + (size_t)h0 * HD, qs, G * HD * 4, lane);
-    drain_vm();
+// Standalone attention, part 2: the canonical merge (orc_attention_canon's order, the
+// step's merge phase's) of one head's chunk records, for 32 of its dims (one 128-byte
+// line of each o record) per workgroup. Wave w takes the split pairs (2g, 2g + 1) for
+// g = w, w + 16, ... (all of a pair's loads in one batch): lane 16j + c (j < 2) loads m and l of chunk c of split 2g + j,
+// takes M_s as the max over its 16 lanes and w_c = exp(m_c - M_s), both into LDS; lane
+// 32j + d then runs acc_s (and, for d = 0, den_s) as fma chains in chunk order over o of
+// dim d. The split results meet in LDS; wave 0 merges the splits the same way (lane s:
+// w_s; lane d: the chains in split order) and divides (one split: acc / den directly).
+constexpr int kAttnMaxSplits = 512;
+constexpr int kMergeWaves = 16;
+template <int HD>
+__global__ __launch_bounds__(64 * kMergeWaves) void k_attn_merge(const float* recs, int nh, int L, float* out) {
+    constexpr int SR = 34;
+    __shared__ float sres[kAttnMaxSplits * SR];                        // [split][M, den, acc[32]]
+    __shared__ float wls[kMergeWaves][2][2][16];                        // per wave: [split j][w | l][chunk]
+    const int h = blockIdx.x / (HD / 32), d0 = (blockIdx.x - h * (HD / 32)) * 32;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int nch = (L + kAttnChunk - 1) / kAttnChunk, nsp = (nch + kAttnSplit - 1) / kAttnSplit;
+    const float* ro = recs + (size_t)h * nch * HD;
+    const float* rm = recs + (size_t)nh * nch * HD + (size_t)h * nch;
+    const float* rl = rm + (size_t)nh * nch;
+    for (int g = wave; 2 * g < nsp; g += kMergeWaves) {
+        // the pair's o values (lane 32j + d) and chunk (m, l) (lane 16j + c) in one batch
+        const int j = lane >> 5, d = lane & 31, sp = 2 * g + j;
+        const int c0 = sp * kAttnSplit, n = sp < nsp ? min(kAttnSplit, nch - c0) : 1;
+        float oo[kAttnSplit];
+#pragma unroll
+        for (int i = 0; i < kAttnSplit; i++) oo[i] = sp < nsp ? ro[(size_t)(c0 + min(i, n - 1)) * HD + d0 + d] : 0.f;
+        const int wj = (lane >> 4) & 1, wc = lane & 15, wsp = 2 * g + wj, cc = wsp * kAttnSplit + wc;
+        const bool ok = lane < 32 && wsp < nsp && cc < nch;
+        const float m = ok ? rm[cc] : -__builtin_inff();
+        const float l = ok ? rl[cc] : 0.f;
+        // chunk weights: M_s = max over the split's 16 lanes, w_c = exp(m_c - M_s)
+        float M = fmaxf(m, dppf<kDppRor8>(m));
+        M = fmaxf(M, dppf<kDppRor4>(M));
+        M = fmaxf(M, dppf<kDppXor2>(M));
+        M = fmaxf(M, dppf<kDppXor1>(M));
+        if (lane < 32) {
+            wls[wave][wj][0][wc] = ok ? mi_expf(__fsub_rn(m, M)) : 0.f;
+            wls[wave][wj][1][wc] = l;
+            if (wc == 0 && wsp < nsp) sres[wsp * SR] = M;
+        }
+        wave_lds_sync();
+        if (sp < nsp) {
+            float den = 0.f, acc = 0.f;
+#pragma unroll
+            for (int i = 0; i < kAttnSplit; i++) {
+                if (i < n) {
+                    const float w = wls[wave][j][0][i];
+                    den = __fmaf_rn(wls[wave][j][1][i], w, den);
+                    acc = __fmaf_rn(oo[i], w, acc);
+                }
+            }
+            float* sr = sres + sp * SR;
+            if (d == 0) sr[1] = den;
+            sr[2 + d] = acc;
+        }
+        wave_lds_sync();                                                // wls is reused by the wave's next pair
+    }
     __syncthreads();
-    {
-        float m[H], ls[H], acc[H][DPL];
-        attn_core_h<HD, H>(kls, qs + hb * HD, hn, vls, n, scale, lane, pls + hb * 64, m, ls, acc);
+    if (wave != 0) return;
+    const int d = lane & 31;
+    float den, acc;
+    if (nsp == 1) {
+        den = sres[1];
+        acc = sres[2 + d];
+    } else {
+        // M over the splits, then lane s computes w_s = exp(M_s - M) (splits s, s + 64, ...
+        // into sres's M column), then the lanes run the chains in split order
+        float M = -__builtin_inff();
+        for (int sp = lane; sp < nsp; sp += 64) M = fmaxf(M, sres[sp * SR]);
+        M = wave_max(M);
+        for (int sp = lane; sp < nsp; sp += 64) sres[sp * SR] = mi_expf(__fsub_rn(sres[sp * SR], M));
+        wave_lds_sync();
+        den = 0.f;
+        acc = 0.f;
+        int sp = 0;
+        for (; sp + 4 <= nsp; sp += 4) {
+            float w[4], dn[4], ac[4];
 #pragma unroll
-        for (int h = 0; h < H; h++) {
-            if (h < hn) {
-                float* rec = recs + ((size_t)(h0 + hb + h) * nch + c) * REC;
+            for (int i = 0; i < 4; i++) {
+                w[i] = sres[(sp + i) * SR];
+                dn[i] = sres[(sp + i) * SR + 1];
+                ac[i] = sres[(sp + i) * SR + 2 + d];
+            }
 #pragma unroll
-                for (int e = 0; e < DPL; e++) stc(rec + DPL * lane + e, acc[h][e]);
-                if (lane == 0) { stc(rec + HD, m[h]); stc(rec + HD + 1, ls[h]); }
+            for (int i = 0; i < 4; i++) {
+                den = __fmaf_rn(dn[i], w[i], den);
+                acc = __fmaf_rn(ac[i], w[i], acc);
             }
         }
-    }
-    drain_vm();
-    __syncthreads();                                   // every record of the workgroup is written
-    const int sp = c / kAttnSplit, c0 = sp * kAttnSplit, c1 = min(nch, c0 + kAttnSplit);
-    if (wave == 0) {
-        const bool last = last_arrival(scnt + (size_t)kvh * nsp + sp, c1 - c0, lane);
-        if (lane == 0) *flag = last;
-    }
-    __syncthreads();
-    if (!*flag) return;
-    // level 1: the split's chunks of each head -> the output (one split) or a split record
-    auto put1 = [&](int hh, float M, float den, const float (&acc)[DPL]) {
-        const int h = h0 + hb + hh;
-        if (nsp == 1) {
-#pragma unroll
-            for (int e = 0; e < DPL; e++) out[(size_t)h * HD + DPL * lane + e] = __fdiv_rn(acc[e], den);
-        } else {
-            float* sr = srecs + ((size_t)h * nsp + sp) * REC;
-#pragma unroll
-            for (int e = 0; e < DPL; e++) stc(sr + DPL * lane + e, acc[e]);
-            if (lane == 0) { stc(sr + HD, M); stc(sr + HD + 1, den); }
-        }
-    };
-    rr_heads<HD, kAttnSplit>(recs + ((size_t)(h0 + hb) * nch + c0) * REC, (size_t)nch * REC, c1 - c0, hn, lane,
-                                 pls + hb * 64, put1);
-    if (nsp == 1) return;
-    drain_vm();
-    __syncthreads();
-    if (wave == 0) {
-        const bool last = last_arrival(hcnt + kvh, nsp, lane);
-        if (lane == 0) *flag = last;
-    }
-    __syncthreads();
-    if (!*flag) return;
-    // level 2: the splits -> the output
-    if (nsp <= kRegRecs) {
-        auto put = [&](int hh, float M, float den, const float (&acc)[DPL]) {
-#pragma unroll
-            for (int e = 0; e < DPL; e++) out[(size_t)(h0 + hb + hh) * HD + DPL * lane + e] = __fdiv_rn(acc[e], den);
-        };
-        rr_heads<HD, kRegRecs>(srecs + (size_t)(h0 + hb) * nsp * REC, (size_t)nsp * REC, nsp, hn, lane, pls + hb * 64,
-                                   put);
-    } else if (wave == 0) {
-        for (int hh = 0; hh < G; hh++) {
-            float M, den, acc[DPL];
-            lds_merge<HD>(srecs + (size_t)(h0 + hh) * nsp * REC, 0, nsp, reinterpret_cast<float*>(smem), lane, M, den,
-                          acc);
-#pragma unroll
-            for (int e = 0; e < DPL; e++) out[(size_t)(h0 + hh) * HD + DPL * lane + e] = __fdiv_rn(acc[e], den);
+        for (; sp < nsp; sp++) {
+            den = __fmaf_rn(sres[sp * SR + 1], sres[sp * SR], den);
+            acc = __fmaf_rn(sres[sp * SR + 2 + d], sres[sp * SR], acc);
         }
     }
+    if (lane < 32) out[(size_t)h * HD + d0 + lane] = __fdiv_rn(acc, den);
 }
 
 __global__ __launch_bounds__(kThreads) void k_stream(const u32x4* __restrict__ p, size_t n4, uint32_t* sink) {
@@ -2838,37 +2802,50 @@ void launch_isums(const PMat& W, const int8_t* xq, int32_t* isum, hipStream_t s)
     hipLaunchKernelGGL(k_isums, dim3(W.rows / 64, W.nb), dim3(64), 0, s, W, xq, isum);
 }
 size_t attn_scratch_floats(int nh, int hd, int L) {
-    const int nch = (L + kAttnChunk - 1) / kAttnChunk, nsp = (nch + kAttnSplit - 1) / kAttnSplit;
-    return kAttnCounters + (size_t)nh * (nch + (nsp > 1 ? nsp : 0)) * (hd + 32);
+    const int nch = (L + kAttnChunk - 1) / kAttnChunk;
+    return (size_t)nh * nch * (hd + 2);
+}
+static int device_cus() {
+    static int n_cu = 0;
+    if (!n_cu) {
+        int dev = 0, n = 0;
+        if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 1)
+            n = 256;
+        n_cu = n;
+    }
+    return n_cu;
+}
+template <int HD, int H, int S>
+static void launch_attn_rec(const float* q, const __half* kc, const __half* vc, int nh, int nkv, int L, int ctx,
+                            float scale, float* recs, hipStream_t s) {
+    const int G = nh / nkv, units = nkv * ((L + kAttnChunk - 1) / kAttnChunk);
+    const int per_cu = max(1, (160 * 1024) / attn_rec_lds<HD, H, S>());
+    const int grid = min((units + S - 1) / S, device_cus() * per_cu);
+    LAUNCH((k_attn_rec<HD, H, S>), grid, 64 * (S * ((G + H - 1) / H) + 1), s, q, kc, vc, nh, nkv, L, ctx, scale, recs);
 }
 bool launch_attn_decode(const float* q, const __half* kc, const __half* vc, int nh, int nkv, int hd, int L, int ctx,
                         float scale, float* scratch, float* out, hipStream_t s) {
-    if (nh % nkv || !kernels_support(nh / nkv, hd) || nh / nkv > kAttnMaxG) return false;
-    const int G = nh / nkv, nch = (L + kAttnChunk - 1) / kAttnChunk, units = nkv * nch;
-    const int nsp = (nch + kAttnSplit - 1) / kAttnSplit;
-    // counters: nkv * nsp + nkv <= nh * (nsp + 1)
-    if ((size_t)nh * (nsp + 1) > (size_t)kAttnCounters) return false;
-    const int nw = (G + kTileHeads - 1) / kTileHeads;
+    if (nh % nkv || !kernels_support(nh / nkv, hd) || nh / nkv > kAttnMaxG || L < 1) return false;
+    const int nch = (L + kAttnChunk - 1) / kAttnChunk, nsp = (nch + kAttnSplit - 1) / kAttnSplit;
+    if (nsp > kAttnMaxSplits) return false;
     with_hd(hd, [&](auto h) {
-        LAUNCH((k_attn_tile<decltype(h)::value, kTileHeads>), units, 64 * nw, s, q, kc, vc, nh, nkv, L, ctx, scale,
-               scratch, out);
+        constexpr int HD = decltype(h)::value;
+        // one head per compute wave, one unit per round (two workgroups per CU at hd 128):
+        // the fastest of H = 1..3, S = 1..2 at L = 512..32768 on the box
+        launch_attn_rec<HD, 1, 1>(q, kc, vc, nh, nkv, L, ctx, scale, scratch, s);
+        LAUNCH((k_attn_merge<HD>), nh * (HD / 32), 64 * kMergeWaves, s, scratch, nh, L, out);
     });
     return true;
 }
 // ------------------------------------------------------------------ allocation-free attention
 // Scratch of mi_attn_decode_noalloc: a file-scope device array (each GPU the library
 // runs on holds its own copy until the process ends), laid out as the workspace of
-// launch_attn_decode: arrival counters, then chunk and split records. Host code never
-// passes the array's name to a kernel (on the host it is a stand-in, not a device
-// address): the per-device address comes from hipGetSymbolAddress at the first call
-// on each device. Calls on one device share the array, so calls that overlap on one
-// GPU race; each completed call leaves the counters zero.
+// launch_attn_decode: the chunk records, every one written before it is read in each
+// call, so nothing needs clearing. Host code never passes the array's name to a kernel
+// (on the host it is a stand-in, not a device address): the per-device address comes
+// from hipGetSymbolAddress at the first call on each device. Calls on one device share
+// the array, so calls that overlap on one GPU race.
 static __device__ __align__(256) float scratch[kNoAllocScratchFloats];
-
-__global__ void k_zero_words(uint32_t* p, int n) {
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < n) p[i] = 0u;
-}
 
 namespace {
 constexpr int kMaxDevices = 64;
@@ -2876,10 +2853,10 @@ std::mutex g_scratch_mu;
 float* g_scratch_ptr[kMaxDevices] = {};
 }  // namespace
 
-// the device address of the current device's scratch array; the first call on a device
-// looks it up and zeroes its arrival counters with a kernel on the caller's stream (no
-// memset node: callers may capture the stream into a graph)
+// the device address of the current device's scratch array (looked up at the first
+// call on a device)
 hipError_t noalloc_scratch(hipStream_t s, float** out) {
+    (void)s;
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return e;
@@ -2888,9 +2865,6 @@ hipError_t noalloc_scratch(hipStream_t s, float** out) {
     if (!g_scratch_ptr[dev]) {
         void* p = nullptr;
         e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
-        if (e != hipSuccess) return e;
-        LAUNCH(k_zero_words, (kAttnCounters + 255) / 256, 256, s, static_cast<uint32_t*>(p), kAttnCounters);
-        e = hipGetLastError();
         if (e != hipSuccess) return e;
         g_scratch_ptr[dev] = static_cast<float*>(p);
     }

@@ -159,15 +159,15 @@ def attention_case(torch, nh, nkv, hd, L, scratch, rng):
 
 
 def test_attention_scratch_reuse(torch):
-    """one scratch buffer, zero-filled once, through calls of different shapes: each
-    call leaves its arrival counters at zero, so the next one merges correctly"""
+    """one scratch buffer, NaN-filled once, through calls of different shapes: every
+    record a call reads it wrote itself, so neither the initial contents nor an earlier
+    call's records change the result"""
     rng = np.random.default_rng(5)
-    scratch = torch.zeros(minfer.attn_scratch_floats(16, 128, 5000), device="cuda")
+    scratch = torch.full((minfer.attn_scratch_floats(16, 128, 5000),), float("nan"), device="cuda")
     for nh, nkv, hd, L in [(12, 2, 128, 3000), (4, 2, 64, 100), (12, 2, 128, 3000), (16, 2, 128, 5000),
                            (14, 2, 64, 1100), (12, 2, 128, 64)]:
         say("scratch reuse nh=%d hd=%d L=%d" % (nh, hd, L))
         attention_case(torch, nh, nkv, hd, L, scratch, rng)
-        assert int(torch.count_nonzero(scratch[:65536])) == 0
 
 
 def rope_rows(x, pos0, base=1e6):
