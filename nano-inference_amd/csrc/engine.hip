@@ -312,6 +312,9 @@ static int load_impl(mi_engine* e, const char* path) {
                        e->NKV, e->HD, e->V);
     e->maxseq = e->opts.max_ctx > 0 ? e->opts.max_ctx : 4096;
     e->maxch = (e->maxseq + kAttnChunk - 1) / kAttnChunk;
+    if (e->maxch > kernels_max_ctx_chunks(e->HD))
+        return set_err(e, MI_ERR_SHAPE, "max_ctx %d exceeds the %d positions the attention merge holds", e->maxseq,
+                       kernels_max_ctx_chunks(e->HD) * kAttnChunk);
 
     // reduction plan (the float summation order; depends on the shape only)
     const int nbE = e->E / 32, nbF = e->FF / 32;

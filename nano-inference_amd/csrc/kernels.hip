@@ -1221,48 +1221,105 @@ __device__ __forceinline__ void comb_wave(const float* r, int arec, int nch, int
     for (int e = 0; e < DPL; e++) out[e] = __fdiv_rn(acc[e], den);
 }
 
+// The canonical merge (the oracle's, the standalone k_attn_merge's) of one head's chunk
+// records for 32 of its dims (one 128-byte line of each record): records r[c * arec]
+// (o[hd], m, l), nch of them, out[0..32) = the merged o / den for dims d0 .. d0 + 31.
+// All eight waves of the workgroup take part (it synchronizes the workgroup): wave w takes
+// the split pairs (2g, 2g + 1) for g = w, w + 8, ...: the pair's 32 o lines come into the
+// wave's LDS by DMA (8 records per instruction), lane 16j + c loads m, l of chunk c of
+// split 2g + j meanwhile, M_s is the max over its 16 lanes and w_c = exp(m_c - M_s) goes
+// to LDS; lane 32j + d then runs den_s (d = 0) and acc_s as fma chains in chunk order.
+// Wave 0 merges the splits the same way in split order (lane s: w_s; lane d: the chains)
+// and writes out with agent-coherent stores. The loops stay rolled (the step kernel's
+// phase loop holds this code; an unrolled register version cost ~1% at short contexts,
+// where the phase never runs). lds: 8 * (1024 + 64) + nsp * 34 floats.
+constexpr int kCombSR = 34;
+constexpr int kCombMaxSplits = 512;           // splits of 16 chunks the per-phase merge kernel holds in LDS
+constexpr int kCombWaveFloats = 1024 + 64;      // per wave: o lines [2][16][32], weights [2][w | l][16]
 template <int HD>
-__device__ __forceinline__ void lds_merge(const float* r, int c0, int c1, float* lds, int lane, float& Mo, float& deno,
-                                          float (&acc)[HD / 64]);
-// chunk merge as its own phase (more than kInlineComb chunks): head h on worker wave 1
-// of workgroup h (the heads spread over as many CUs), in comb_wave's order: the max over
-// all chunks (past kAttnSplit), then each split merged by lds_merge (its 16 records
-// DMA'd into `lds`, 16 * (HD + 32) floats, with rolled loops: an unrolled merge here made
-// the whole step ~6 us per token slower even when the phase does not run), then the
-// splits scaled by exp(M_s - M)
-template <int HD>
-__device__ __forceinline__ void phase_comb(MPtr M, int l, int pos, int wg, int wave, int lane, float* lds) {
-    if (wave != 1 || wg >= M->NH) return;
-    // opaque lane: its addresses are not hoisted out of the phase loop
+__device__ __forceinline__ void comb_slice(const float* r, int arec, int nch, int d0, int wave, int lane, float* lds,
+                                           float* out) {
+    // opaque lane and wave: their addresses are not hoisted out of the step's phase loop
     asm volatile("" : "+v"(lane));
-    constexpr int DPL = HD / 64;
-    const int nch = (pos + 1 + kAttnChunk - 1) / kAttnChunk;
-    const float* r = att_rec(M, l) + (size_t)wg * M->maxch * M->arec;
-    float Mx = -__builtin_inff();
-    if (nch > kAttnSplit) {
-        for (int c = lane; c < nch; c += 64) Mx = fmaxf(Mx, r[c * M->arec + HD]);
-        Mx = wave_max(Mx);
-    }
-    float den = 0.f, acc[DPL];
-#pragma unroll
-    for (int e = 0; e < DPL; e++) acc[e] = 0.f;
-    for (int c0 = 0; c0 < nch; c0 += kAttnSplit) {
-        float Ms, ds, as[DPL];
-        lds_merge<HD>(r, c0, min(nch, c0 + kAttnSplit), lds, lane, Ms, ds, as);
-        if (nch <= kAttnSplit) {
-            den = ds;
-#pragma unroll
-            for (int e = 0; e < DPL; e++) acc[e] = as[e];
-        } else {
-            const float ws = mi_expf(__fsub_rn(Ms, Mx));
-            den = __fmaf_rn(ds, ws, den);
-#pragma unroll
-            for (int e = 0; e < DPL; e++) acc[e] = __fmaf_rn(as[e], ws, acc[e]);
+    asm volatile("" : "+v"(wave));
+    const int nsp = (nch + kAttnSplit - 1) / kAttnSplit;
+    float* ol = lds + wave * kCombWaveFloats;
+    float* wls = ol + 1024;
+    float* sres = lds + 8 * kCombWaveFloats;                            // [split][M, den, acc[32]]
+    for (int g = wave; 2 * g < nsp; g += 8) {
+#pragma unroll 1
+        for (int k = 0; k < 4; k++) {                                   // o lines of chunks 8(k&1) .. +7 of split 2g + k/2
+            const int sp = min(2 * g + (k >> 1), nsp - 1);
+            const int c = min(sp * kAttnSplit + (k & 1) * 8 + (lane >> 3), nch - 1);
+            __builtin_amdgcn_global_load_lds(r + (size_t)c * arec + d0 + 4 * (lane & 7),
+                                             (lds_ptr)(ol + ((k >> 1) * 16 + (k & 1) * 8) * 32), 16, 0, 0);
         }
+        const int wj = (lane >> 4) & 1, wc = lane & 15, wsp = 2 * g + wj, cc = wsp * kAttnSplit + wc;
+        const bool ok = lane < 32 && wsp < nsp && cc < nch;
+        const float m = ok ? r[(size_t)cc * arec + HD] : -__builtin_inff();
+        const float l = ok ? r[(size_t)cc * arec + HD + 1] : 0.f;
+        float M = fmaxf(m, dppf<kDppRor8>(m));                          // max over the 16 lanes of the row
+        M = fmaxf(M, dppf<kDppRor4>(M));
+        M = fmaxf(M, dppf<kDppXor2>(M));
+        M = fmaxf(M, dppf<kDppXor1>(M));
+        if (lane < 32) {
+            wls[wj * 32 + wc] = ok ? mi_expf(__fsub_rn(m, M)) : 0.f;
+            wls[wj * 32 + 16 + wc] = l;
+            if (wc == 0 && wsp < nsp) sres[wsp * kCombSR] = M;
+        }
+        drain_vm();
+        wave_lds_sync();
+        const int j = lane >> 5, d = lane & 31, sp = 2 * g + j;
+        if (sp < nsp) {
+            const int n = min(kAttnSplit, nch - sp * kAttnSplit);
+            float den = 0.f, acc = 0.f;
+#pragma unroll 4
+            for (int i = 0; i < n; i++) {
+                const float w = wls[j * 32 + i];
+                den = __fmaf_rn(wls[j * 32 + 16 + i], w, den);
+                acc = __fmaf_rn(ol[(j * 16 + i) * 32 + d], w, acc);
+            }
+            float* sr = sres + sp * kCombSR;
+            if (d == 0) sr[1] = den;
+            sr[2 + d] = acc;
+        }
+        wave_lds_sync();                                                // ol and wls are reused by the next pair
     }
-    float* out = M->att_out + (size_t)l * M->E + (size_t)wg * HD;
-#pragma unroll
-    for (int e = 0; e < DPL; e++) stc(out + DPL * lane + e, __fdiv_rn(acc[e], den));
+    __syncthreads();
+    if (wave == 0) {
+        const int d = lane & 31;
+        float den, acc;
+        if (nsp == 1) {
+            den = sres[1];
+            acc = sres[2 + d];
+        } else {
+            float M = -__builtin_inff();
+            for (int sp = lane; sp < nsp; sp += 64) M = fmaxf(M, sres[sp * kCombSR]);
+            M = wave_max(M);
+            for (int sp = lane; sp < nsp; sp += 64) sres[sp * kCombSR] = mi_expf(__fsub_rn(sres[sp * kCombSR], M));
+            wave_lds_sync();
+            den = 0.f;
+            acc = 0.f;
+            for (int sp = 0; sp < nsp; sp++) {
+                den = __fmaf_rn(sres[sp * kCombSR + 1], sres[sp * kCombSR], den);
+                acc = __fmaf_rn(sres[sp * kCombSR + 2 + d], sres[sp * kCombSR], acc);
+            }
+        }
+        if (lane < 32) stc(out + d0 + lane, __fdiv_rn(acc, den));
+    }
+    __syncthreads();                                                    // lds is free again
+}
+// chunk merge as its own phase (more than kInlineComb chunks): workgroup t < NH * HD/32
+// merges head t / (HD/32) for 32 dims (comb_slice), all of the workgroup's waves taking
+// part; the merged vectors go to att_out for the O prologue
+template <int HD>
+__device__ __forceinline__ void phase_comb(MPtr M, int l, int pos, int wg, int nwg, int wave, int lane, float* lds) {
+    const int nch = (pos + 1 + kAttnChunk - 1) / kAttnChunk;
+    for (int t = wg; t < M->NH * (HD / 32); t += nwg) {
+        const int h = t / (HD / 32), d0 = (t - h * (HD / 32)) * 32;
+        comb_slice<HD>(att_rec(M, l) + (size_t)h * M->maxch * M->arec, M->arec, nch, d0, wave, lane, lds,
+                       M->att_out + (size_t)l * M->E + (size_t)h * HD);
+    }
 }
 
 // ------------------------------------------------------------------ the persistent step
@@ -1363,7 +1420,7 @@ __global__ __launch_bounds__(kPThreads) void k_step(const DModel* Mp, int pos, i
             __syncthreads();
             if (ctl) ctl_barrier(gb, M->err);
             __syncthreads();
-            phase_comb<HD>(M, l, pos, wg, wave, lane, reinterpret_cast<float*>(S.U));
+            phase_comb<HD>(M, l, pos, wg, nwg, wave, lane, reinterpret_cast<float*>(S.U));
         }
         __syncthreads();
         stamp(M, sb + 1, 64);
@@ -1465,8 +1522,8 @@ __global__ __launch_bounds__(kPThreads) void k_attn(const DModel* Mp, int l, int
 template <int HD>
 __global__ __launch_bounds__(kPThreads) void k_attn_comb(const DModel* Mp, int l, int pos) {
     const MPtr M = (MPtr)Mp;
-    __shared__ __align__(16) float lds[kAttnSplit * (HD + 32)];
-    phase_comb<HD>(M, l, pos, blockIdx.x, threadIdx.x >> 6, threadIdx.x & 63, lds);
+    __shared__ __align__(16) float lds[8 * kCombWaveFloats + kCombMaxSplits * kCombSR];
+    phase_comb<HD>(M, l, pos, blockIdx.x, gridDim.x, threadIdx.x >> 6, threadIdx.x & 63, lds);
 }
 __global__ __launch_bounds__(kPThreads) void k_o(const DModel* Mp, int l, int pos) {
     const MPtr M = (MPtr)Mp;
@@ -2392,45 +2449,6 @@ __global__ __launch_bounds__(64) void k_isums(PMat W, const int8_t* xq, int32_t*
 // [nh][nch][hd], m [nh][nch], l [nh][nch].
 constexpr int kAttnMaxG = 8;        // query heads per kv head
 
-// One wave merges the records [c0, c1) of one head (contiguous, REC floats each)
-// as comb_wave does, lane = dims DPL*lane + e: M = max over all records, w_i =
-// exp(m_i - M), then den and acc as fma chains in record order. The records come
-// into LDS 16 at a time by DMA (lds: 16 * REC floats); w_i and l_i reach every lane
-// by readlane. The loops stay rolled: this code runs once per split on a CU that
-// has not run it before, so its size is paid in instruction fetches.
-template <int HD>
-__device__ __forceinline__ void lds_merge(const float* r, int c0, int c1, float* lds, int lane, float& Mo, float& deno,
-                                          float (&acc)[HD / 64]) {
-    constexpr int REC = HD + 32, DPL = HD / 64;
-    float M = -__builtin_inff();
-    if (c1 - c0 > kAttnSplit) {                       // the max first when it spans batches
-        for (int b = c0; b < c1; b += 64) M = fmaxf(M, b + lane < c1 ? r[(size_t)(b + lane) * REC + HD] : -__builtin_inff());
-        M = wave_max(M);
-    }
-    float den = 0.f;
-#pragma unroll
-    for (int e = 0; e < DPL; e++) acc[e] = 0.f;
-    for (int b = c0; b < c1; b += kAttnSplit) {
-        const int n = min(kAttnSplit, c1 - b);
-        dma_wave(r + (size_t)b * REC, lds, n * REC * 4, lane);
-        drain_vm();
-        wave_lds_sync();
-        const float m = lane < n ? lds[lane * REC + HD] : -__builtin_inff();
-        if (c1 - c0 <= kAttnSplit) M = wave_max(m);
-        const float w = lane < n ? mi_expf(__fsub_rn(m, M)) : 0.f;
-        const int wb = __float_as_int(w), lb = __float_as_int(lane < n ? lds[lane * REC + HD + 1] : 0.f);
-        for (int i = 0; i < n; i++) {
-            const float wi = __int_as_float(__builtin_amdgcn_readlane(wb, i));
-            den = __fmaf_rn(__int_as_float(__builtin_amdgcn_readlane(lb, i)), wi, den);
-#pragma unroll
-            for (int e = 0; e < DPL; e++) acc[e] = __fmaf_rn(lds[i * REC + DPL * lane + e], wi, acc[e]);
-        }
-        wave_lds_sync();
-    }
-    Mo = M;
-    deno = den;
-}
-
 // Standalone attention, part 1: the chunk records. A unit is (kv head, 64-position
 // chunk). A workgroup takes S units per round (units SP .. SP + S - 1 for P = w,
 // w + grid, ...) with W = ceil(G / H) compute waves per unit (H heads each) and one data
@@ -2631,6 +2649,11 @@ __global__ __launch_bounds__(kThreads) void k_stream(const u32x4* __restrict__ p
 #define LAUNCH(kern, grid, block, stream, ...) hipLaunchKernelGGL(kern, dim3(grid), dim3(block), 0, stream, __VA_ARGS__)
 
 bool kernels_support(int G, int HD) { return (HD == 64 || HD == 128) && G >= 1; }
+// 64-position chunks the merge phase holds (its split results live in the step's LDS union)
+int kernels_max_ctx_chunks(int HD) {
+    const int ub = HD == 128 ? union_bytes<128>() : union_bytes<64>();
+    return min(kCombMaxSplits, (ub / 4 - 8 * kCombWaveFloats) / kCombSR) * kAttnSplit;
+}
 int attn_record_floats(int HD) { return HD + 32; }
 
 template <class F>

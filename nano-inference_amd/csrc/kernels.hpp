@@ -8,6 +8,7 @@ namespace mi {
 // host DModel M: a kernel-argument struct would be treated as invariant and kept in
 // scalar registers for the whole persistent step, which runs out of them.
 bool kernels_support(int G, int HD);
+int kernels_max_ctx_chunks(int HD);   // attention chunks (64 positions) a context may hold
 // reduction plan (blocks per chunk, K segments) of qkv, o, gate/up, down, lm_head;
 // false when the shape does not fit the kernels' LDS staging
 bool kernels_plan(int E, int FF, int cb[5], int ks[5]);
