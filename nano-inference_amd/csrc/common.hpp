@@ -28,7 +28,6 @@ constexpr int kThreads = kGroupRows * kWaves;
 constexpr int kPWaves = 8;         // waves per workgroup of the persistent step kernel
 constexpr int kPThreads = kGroupRows * kPWaves;
 constexpr int kMaxWaves = 8;
-constexpr int kAttnWaves = 2;      // waves per workgroup that take attention items (LDS bound)
 constexpr int kAttnChunk = 64;     // positions per attention partial
 constexpr int kInlineComb = 4;     // up to this many chunks the O phase merges them itself
 constexpr int kAttnSplit = 16;     // past this many chunks the records merge as a two-level tree

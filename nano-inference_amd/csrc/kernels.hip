@@ -394,10 +394,14 @@ __device__ __forceinline__ void seg_store(const PMat W, int wg, int nwg, int kw,
 }
 
 // ------------------------------------------------------------------ LDS layout
+// attention unit (kv head, chunk): the K and V tiles, shared by the unit's head waves,
+// then one area per wave: q / k / v split-K partials, q, and the wave's probability row
 template <int HD>
-constexpr int attn_wave_lds() { return 2 * 64 * HD * 2 + 3 * kMaxKsQkv * HD * 4 + 2 * HD * 4 + 64 * 4; }
+constexpr int attn_head_lds() { return 3 * kMaxKsQkv * HD * 4 + 2 * HD * 4 + 64 * 4; }
 template <int HD>
-constexpr int union_bytes() { return kAttnWaves * attn_wave_lds<HD>() > kCtlBytes ? kAttnWaves * attn_wave_lds<HD>() : kCtlBytes; }
+constexpr int attn_unit_lds() { return 2 * 64 * HD * 2 + kPWaves * attn_head_lds<HD>(); }
+template <int HD>
+constexpr int union_bytes() { return attn_unit_lds<HD>() > kCtlBytes ? attn_unit_lds<HD>() : kCtlBytes; }
 constexpr int kFixedLds = 8 * kMaxE + (kMaxE / 32) * kXRec + kPartTiles * 256 + 1024;
 template <int HD>
 constexpr int step_lds() { return kFixedLds + union_bytes<HD>(); }
@@ -647,7 +651,7 @@ __device__ __forceinline__ void stage(MPtr M, int l, int kind, int pos, const Ld
                       (dsrc ? LY(M, pl)->d.ks : LY(M, pl)->o.ks) * n * 4, d, lane);
         }
     }
-    if (kind != PH_ATTN) drain_vm();     // (attention stages nothing; its waves' K/V prefetch stays in flight)
+    drain_vm();     // (attention stages nothing; this completes the unit's K/V tile its waves prefetched)
 }
 // the control wave alone (the per-phase kernels, whose workers prefetch meanwhile)
 __device__ __forceinline__ void ctl_stage(MPtr M, int l, int kind, int pos, const Lds& S, int lane, bool resident) {
@@ -1027,56 +1031,41 @@ __device__ __forceinline__ void attn_core_h(const uint4* kls, const float* qs, i
     }
 }
 
-// Attention items (query head h, 64-position chunk c) of positions 0..pos. The G
-// query heads of one (kv head, chunk) read the same K/V rows, so they are placed on
-// one XCD (workgroups w = x + 8k share XCD x): unit u = kvh*nch + c, item index
-// iv = (u % 8) + 8*(hh + G*(u / 8)) for the unit's hh-th head; iv -> workgroup
-// iv % nwg, attention wave (iv / nwg) % kAttnWaves. Index values with u out of range
-// are skipped.
-struct AttnItem { int h, c; };
-__device__ __forceinline__ int attn_nvi(MPtr M, int nch) {
-    const int units = M->NKV * nch;
-    return 8 * M->G * ((units + 7) / 8);
-}
-__device__ __forceinline__ bool attn_decode(MPtr M, int nch, int iv, AttnItem& it) {
-    const int ux = iv % 8, rest = iv / 8, hh = rest % M->G, u = (rest / M->G) * 8 + ux;
-    if (u >= M->NKV * nch) return false;
-    it.h = (u / nch) * M->G + hh;
-    it.c = u % nch;
-    return true;
-}
-// the wave's first valid item index at or after iv (stride nwg * kAttnWaves); -1 if none
-__device__ __forceinline__ int attn_next(MPtr M, int nch, int iv, int nwg) {
-    const int nvi = attn_nvi(M, nch);
-    AttnItem it;
-    for (; iv < nvi; iv += nwg * kAttnWaves)
-        if (attn_decode(M, nch, iv, it)) return iv;
-    return -1;
+// Attention units (kv head kvh, 64-position chunk c) of positions 0..pos, unit u =
+// kvh * nch + c on workgroup u % nwg, u + nwg, ... . The unit's K and V rows come into
+// one LDS tile (workers 0 and 1 DMA them during the grid barrier before the phase); wave
+// hh of the workgroup (the control wave included) then computes query head kvh * G + hh
+// against it, so the tile is read from memory once for the G heads.
+template <int HD>
+__device__ __forceinline__ void attn_issue_unit(MPtr M, int l, int pos, int u, int nch, uint8_t* U, int wave, int lane) {
+    const int kvh = u / nch, t0 = (u - kvh * nch) * kAttnChunk, n = min(kAttnChunk, pos + 1 - t0);
+    const size_t rowbase = ((size_t)l * M->NKV + kvh) * M->maxseq + t0;
+    // the tile address through a VGPR: with a uniform (SGPR) generic pointer, the LDS
+    // cast's aperture check hits an instruction-selection error in this compiler; and an
+    // opaque lane, so the DMA addresses are not hoisted out of the step's phase loop
+    int zero = 0;
+    asm volatile("" : "+v"(zero));
+    asm volatile("" : "+v"(lane));
+    uint8_t* Uv = U + zero;
+    if (wave == 1) attn_issue_k<HD>(M->kc + rowbase * HD, n, reinterpret_cast<uint4*>(Uv), lane);
+    if (wave == 2) attn_issue_v<HD>(M->vc + rowbase * HD, n, reinterpret_cast<__half*>(Uv + 64 * HD * 2), lane);
 }
 
+// One head of a unit whose K/V tile is in LDS: the QKV partials of the head's q rows and,
+// in the chunk that holds position pos, of its kv head's k and v rows; q = segments +
+// bias + NEOX RoPE (cpu_infer.cpp:49-61); the last chunk finishes k/v of pos, rounds them
+// to fp16, writes them into the tile's row for pos (every head wave of the unit writes the
+// same values; each reads the row only after its own write) and head 0 appends them to
+// the cache. The record o[HD], max, sum goes to att[l][h][c] (agent-coherent stores).
 template <int HD>
-__device__ __forceinline__ void attn_issue_item(MPtr M, int l, int pos, const AttnItem& it, uint8_t* lds, int lane) {
-    const int kvh = it.h / M->G, t0 = it.c * kAttnChunk, n = min(kAttnChunk, pos + 1 - t0);
-    const size_t rowbase = ((size_t)l * M->NKV + kvh) * M->maxseq;
-    attn_issue_kv<HD>(M->kc + rowbase * HD, M->vc + rowbase * HD, t0, n, reinterpret_cast<uint4*>(lds),
-                      reinterpret_cast<__half*>(lds + 64 * HD * 2), lane);
-}
-
-// One item after its K/V DMA was issued: the QKV partials of the head's q rows and,
-// in the chunk that holds position pos, of its kv head's k and v rows; q = segments
-// + bias + NEOX RoPE (cpu_infer.cpp:49-61); the last chunk finishes k/v of pos,
-// rounds them to fp16, appends them to the cache and uses them for its own row.
-// The record o[HD], max, sum goes to att[l][h][c] (agent-coherent stores).
-template <int HD>
-__device__ __forceinline__ void attn_finish(MPtr M, int l, int pos, const AttnItem& it, uint8_t* lds, int lane) {
+__device__ __forceinline__ void attn_finish(MPtr M, int l, int pos, int h, int c, uint8_t* U, uint8_t* area, int lane) {
     constexpr int half = HD / 2, DPL = HD / 64;
-    uint4* kls = reinterpret_cast<uint4*>(lds);
-    __half* vls = reinterpret_cast<__half*>(lds + 64 * HD * 2);
-    float* qp = reinterpret_cast<float*>(lds + 2 * 64 * HD * 2);                 // [ks][HD]
+    uint4* kls = reinterpret_cast<uint4*>(U);
+    __half* vls = reinterpret_cast<__half*>(U + 64 * HD * 2);
+    float* qp = reinterpret_cast<float*>(area);                                   // [ks][HD]
     float* kvp = qp + kMaxKsQkv * HD;                                            // [ks][HD] k then [ks][HD] v
     float* qs = qp + 3 * kMaxKsQkv * HD;
     const LPtr Ly = LY(M, l);
-    const int h = it.h, c = it.c;
     const int ks = Ly->qkv.ks, kvh = h / M->G;
     const int L = pos + 1, nch = (L + kAttnChunk - 1) / kAttnChunk, t0 = c * kAttnChunk;
     const int n = min(kAttnChunk, L - t0);
@@ -1136,31 +1125,33 @@ __device__ __forceinline__ void attn_finish(MPtr M, int l, int pos, const AttnIt
 #pragma unroll
     for (int e = 0; e < DPL; e++) stc(rec + DPL * lane + e, acc[0][e]);
     if (lane == 0) { stc(rec + HD, m[0]); stc(rec + HD + 1, lsum[0]); }
-    wave_lds_sync();                           // LDS is reused by the wave's next item
 }
 
-// the attention wave kw's first item: K/V DMA only (issued before the grid barrier)
+// the workgroup's first unit: K/V DMA only, by workers 0 and 1 (issued before the grid
+// barrier; the phase's staging step drains it)
 template <int HD>
-__device__ __forceinline__ void attn_prefetch(MPtr M, int l, int pos, int wg, int nwg, uint8_t* U, int kw, int lane) {
-    if (kw >= kAttnWaves) return;
+__device__ __forceinline__ void attn_prefetch(MPtr M, int l, int pos, int wg, int nwg, uint8_t* U, int wave, int lane) {
     const int nch = (pos + 1 + kAttnChunk - 1) / kAttnChunk;
-    const int iv = attn_next(M, nch, wg + nwg * kw, nwg);
-    AttnItem it;
-    if (iv >= 0 && attn_decode(M, nch, iv, it)) attn_issue_item<HD>(M, l, pos, it, U + kw * attn_wave_lds<HD>(), lane);
+    if (wg < M->NKV * nch) attn_issue_unit<HD>(M, l, pos, wg, nch, U, wave, lane);
+    (void)nwg;
 }
-// all of the wave's items; the first one's K/V are already in flight
+// all of the workgroup's units, every wave taking part (the first unit's tile is in LDS;
+// later units reload it between workgroup barriers)
 template <int HD>
-__device__ __forceinline__ void attn_run(MPtr M, int l, int pos, int wg, int nwg, uint8_t* U, int kw, int lane) {
-    if (kw >= kAttnWaves) return;
-    const int nch = (pos + 1 + kAttnChunk - 1) / kAttnChunk;
-    uint8_t* lds = U + kw * attn_wave_lds<HD>();
-    bool first = true;
-    for (int iv = attn_next(M, nch, wg + nwg * kw, nwg); iv >= 0; iv = attn_next(M, nch, iv + nwg * kAttnWaves, nwg)) {
-        AttnItem it;
-        attn_decode(M, nch, iv, it);
-        if (!first) attn_issue_item<HD>(M, l, pos, it, lds, lane);
-        first = false;
-        attn_finish<HD>(M, l, pos, it, lds, lane);
+__device__ __forceinline__ void attn_run(MPtr M, int l, int pos, int wg, int nwg, uint8_t* U, int wave, int lane) {
+    // opaque lane: its addresses are not hoisted out of the step's phase loop
+    asm volatile("" : "+v"(lane));
+    const int nch = (pos + 1 + kAttnChunk - 1) / kAttnChunk, units = M->NKV * nch;
+    uint8_t* area = U + 2 * 64 * HD * 2 + wave * attn_head_lds<HD>();
+    for (int u = wg; u < units; u += nwg) {
+        if (u != wg) {
+            __syncthreads();                        // every head is done with the tile
+            attn_issue_unit<HD>(M, l, pos, u, nch, U, wave, lane);
+            drain_vm();
+            __syncthreads();
+        }
+        const int kvh = u / nch;
+        if (wave < M->G) attn_finish<HD>(M, l, pos, kvh * M->G + wave, u - kvh * nch, U, area, lane);
     }
 }
 
@@ -1347,16 +1338,12 @@ __device__ __forceinline__ void phase_next(MPtr M, int l, int kind, int& nl, int
     if (kind == PH_DOWN) { nl = l + 1; nk = nl < M->NL ? PH_QKV : PH_LM; }
     else { nl = l; nk = kind + 1; }
 }
-// workers: the tiles of phase (l, kind), or its attention items
+// workers: the tiles of GEMV phase (l, kind)
 template <int HD>
 __device__ __forceinline__ void phase_work(MPtr M, int l, int kind, int pos, int wg, int nwg, const Lds& S,
                                            int kw, Tile (&tl)[2], int lane) {
-    if (kind == PH_ATTN) {
-        attn_run<HD>(M, l, pos, wg, nwg, S.U, kw, lane);
-    } else {
-        const bool down = kind == PH_DOWN;
-        gemv_tiles(phase_mat(M, l, kind), wg, nwg, kw, tl, down ? S.U : S.X, down ? kActRec : kXRec, S.P, lane);
-    }
+    const bool down = kind == PH_DOWN;
+    gemv_tiles(phase_mat(M, l, kind), wg, nwg, kw, tl, down ? S.U : S.X, down ? kActRec : kXRec, S.P, lane);
 }
 // workers: the stores of phase (l, kind) (lm_head has its own epilogue)
 __device__ __forceinline__ void phase_store(MPtr M, int l, int kind, int wg, int nwg, const Lds& S, int kw, int lane) {
@@ -1410,11 +1397,13 @@ __global__ __launch_bounds__(kPThreads) void k_step(const DModel* Mp, int pos, i
         wg_prologue(M, l, kind, pos, wg, S, wave, lane, true);
         __syncthreads();
         stamp(M, sb);
-        if (!ctl) {
+        if (kind == PH_ATTN) {
+            attn_run<HD>(M, l, pos, wg, nwg, S.U, wave, lane);      // every wave: one query head each
+        } else if (!ctl) {
             phase_work<HD>(M, l, kind, pos, wg, nwg, S, kw, tl, lane);
-            tl[0] = Tile{};        // consumed: dead (and not in registers) until the next prefetch
-            tl[1] = Tile{};
         }
+        tl[0] = Tile{};            // consumed: dead (and not in registers) until the next prefetch
+        tl[1] = Tile{};
         if (kind == PH_ATTN && nch > kInlineComb) {           // the chunk merge as a phase of its own
             drain_vm();
             __syncthreads();
@@ -1462,7 +1451,7 @@ __global__ __launch_bounds__(kPThreads) void k_step(const DModel* Mp, int pos, i
             // the QKV prologue is done); attn_finish waits for them
             tl[0] = Tile{};
             tl[1] = Tile{};
-            attn_prefetch<HD>(M, nl, pos, wg, nwg, S.U, kw, lane);
+            attn_prefetch<HD>(M, nl, pos, wg, nwg, S.U, wave, lane);
         } else {
             // the next phase's first tiles, issued while the control wave waits at the
             // grid barrier (issuing ~60-120 KB per CU takes the texture unit ~1 us)
@@ -1515,9 +1504,10 @@ __global__ __launch_bounds__(kPThreads) void k_attn(const DModel* Mp, int l, int
     __shared__ __align__(16) uint8_t smem[step_lds<HD>()];
     const Lds S(smem);
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    if (wave == 0) return;
-    attn_prefetch<HD>(M, l, pos, blockIdx.x, gridDim.x, S.U, wave - 1, lane);
-    attn_run<HD>(M, l, pos, blockIdx.x, gridDim.x, S.U, wave - 1, lane);
+    attn_prefetch<HD>(M, l, pos, blockIdx.x, gridDim.x, S.U, wave, lane);
+    drain_vm();
+    __syncthreads();
+    attn_run<HD>(M, l, pos, blockIdx.x, gridDim.x, S.U, wave, lane);
 }
 template <int HD>
 __global__ __launch_bounds__(kPThreads) void k_attn_comb(const DModel* Mp, int l, int pos) {
@@ -2476,8 +2466,8 @@ __device__ __forceinline__ void attn_rec_issue(const float* q, const __half* kc,
                                                int ctx, int u, uint8_t* B, int lane) {
     const int kvh = u / nch, t0 = (u - kvh * nch) * kAttnChunk, n = min(kAttnChunk, L - t0);
     dma_wave(q + (size_t)kvh * G * HD, B + 2 * 64 * HD * 2, G * HD * 4, lane);
-    attn_issue_k<HD>(kc + ((size_t)kvh * ctx + t0) * HD, n, reinterpret_cast<uint4*>(B), lane);
-    attn_issue_v<HD>(vc + ((size_t)kvh * ctx + t0) * HD, n, reinterpret_cast<__half*>(B + 64 * HD * 2), lane);
+    attn_issue_kv<HD>(kc + (size_t)kvh * ctx * HD, vc + (size_t)kvh * ctx * HD, t0, n, reinterpret_cast<uint4*>(B),
+                      reinterpret_cast<__half*>(B + 64 * HD * 2), lane);
 }
 
 template <int HD, int H, int S>
@@ -2648,7 +2638,7 @@ __global__ __launch_bounds__(kThreads) void k_stream(const u32x4* __restrict__ p
 // ------------------------------------------------------------------ host side
 #define LAUNCH(kern, grid, block, stream, ...) hipLaunchKernelGGL(kern, dim3(grid), dim3(block), 0, stream, __VA_ARGS__)
 
-bool kernels_support(int G, int HD) { return (HD == 64 || HD == 128) && G >= 1; }
+bool kernels_support(int G, int HD) { return (HD == 64 || HD == 128) && G >= 1 && G <= kPWaves; }
 // 64-position chunks the merge phase holds (its split results live in the step's LDS union)
 int kernels_max_ctx_chunks(int HD) {
     const int ub = HD == 128 ? union_bytes<128>() : union_bytes<64>();
