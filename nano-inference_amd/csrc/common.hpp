@@ -40,6 +40,7 @@ constexpr int kMaxT = 8;           // tokens of one multi-token step (mega.cu:50
 struct PMat {                      // one q4_0 matrix in the tile layout
     const uint8_t* base;
     int32_t rows, nb, cb, nc, ks;
+    int32_t rot;                   // segment t of the work split runs on workgroup (t + rot) % grid
 };
 
 struct DLayer {

@@ -250,7 +250,14 @@ static int upload_mat(mi_engine* e, const uint8_t* rows_q4, int rows, int nb, in
     int rc = dev_alloc(e, &d, bytes);
     if (rc) return rc;
     HIPCHK(e, hipMemcpy(d, host.data(), bytes, hipMemcpyHostToDevice));
-    *out = PMat{reinterpret_cast<const uint8_t*>(d), rows, nb, cb, nb / cb, e->ks[kind]};
+    // placement of the work split (results do not depend on it): the QKV and O segments
+    // go to the last workgroups, which hold no down segment (the phase before QKV) and
+    // are not the gate/up phase's doubly loaded first ones (the phase after O); a
+    // workgroup busy in one phase prefetches the next one's tiles late
+    int rot = 0;
+    const int nseg = (rows / 64) * e->ks[kind];
+    if ((kind == 0 || kind == 1) && nseg < e->n_cu) rot = e->n_cu - nseg;
+    *out = PMat{reinterpret_cast<const uint8_t*>(d), rows, nb, cb, nb / cb, e->ks[kind], rot};
     e->weight_bytes += (uint64_t)rows * nb * 18;
     return MI_OK;
 }

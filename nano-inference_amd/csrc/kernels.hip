@@ -55,7 +55,7 @@ typedef const AS4 DLayer* LPtr;
 __device__ __forceinline__ LPtr LY(MPtr M, int l) { return (LPtr)M->layers + l; }
 __device__ __forceinline__ PMat ldmat(const AS4 PMat* m) {
     PMat r;
-    r.base = m->base; r.rows = m->rows; r.nb = m->nb; r.cb = m->cb; r.nc = m->nc; r.ks = m->ks;
+    r.base = m->base; r.rows = m->rows; r.nb = m->nb; r.cb = m->cb; r.nc = m->nc; r.ks = m->ks; r.rot = m->rot;
     return r;
 }
 
@@ -305,10 +305,16 @@ constexpr int kMaxKsQkv = 2;               // q/k/v partials an attention item s
 constexpr int kMaxKsRes = 12;              // split-K partials a residual add takes
 
 // Segments (64-row group g, K segment s; t = g*ks + s) go round-robin to
-// workgroups, t -> workgroup t % nwg. A workgroup's tiles are its segments'
+// workgroups, t -> workgroup (t + W.rot) % nwg. A workgroup's tiles are its segments'
 // chunks in order; tile k belongs to worker k % kWorkers, which holds it in
 // register slot (k / kWorkers) % 2.
 struct TileRef { const uint8_t* p; int b0; };
+// the workgroup's place in W's round-robin (W.rot < nwg); wg_tile and wg_segments take
+// the place, which their callers compute once
+__device__ __forceinline__ int wg_place(const PMat W, int wg, int nwg) {
+    const int v = wg - W.rot;
+    return v < 0 ? v + nwg : v;
+}
 __device__ __forceinline__ bool wg_tile(const PMat W, int wg, int nwg, int k, TileRef& r) {
     const int nseg = (W.rows >> 6) * W.ks;
     int t, c;
@@ -360,6 +366,7 @@ __device__ __forceinline__ void prefetch(const PMat W, int wg, int nwg, int kw, 
     TileRef r;
     tl[0] = Tile{};
     tl[1] = Tile{};
+    wg = wg_place(W, wg, nwg);
     if (wg_tile(W, wg, nwg, kw, r)) tile_load(tl[0], r.p, W.cb, lane);
     if (wg_tile(W, wg, nwg, kw + kWorkers, r)) tile_load(tl[1], r.p, W.cb, lane);
 }
@@ -371,6 +378,7 @@ template <int CB>
 __device__ __forceinline__ void gemv_tiles_cb(const PMat W, int wg, int nwg, int kw, Tile (&tl)[2], const uint8_t* x,
                                               int rs, float* P, int lane) {
     TileRef r;
+    wg = wg_place(W, wg, nwg);
     if (!wg_tile(W, wg, nwg, kw, r)) return;
     P[kw * 64 + lane] = chunk_dot<CB>(tl[0], x, rs, r.b0);
     if (!wg_tile(W, wg, nwg, kw + kWorkers, r)) return;
@@ -388,7 +396,7 @@ __device__ __forceinline__ void gemv_tiles(const PMat W, int wg, int nwg, int kw
 
 // worker epilogue: segment sums stored as split-K partials part[s][row]
 __device__ __forceinline__ void seg_store(const PMat W, int wg, int nwg, int kw, const float* P, float* part, int lane) {
-    wg_segments(W, wg, nwg, kw, [&](int g, int s, int k0, int k1) {
+    wg_segments(W, wg_place(W, wg, nwg), nwg, kw, [&](int g, int s, int k0, int k1) {
         stc(part + (size_t)s * W.rows + g * 64 + lane, seg_sum(P, k0, k1, lane));
     });
 }
@@ -585,14 +593,18 @@ __device__ __forceinline__ void quant_slice(float4 y, bool own, int e0, uint8_t*
 // 1/sqrt(mean(x^2) + eps) of the n-vector x in LDS, the same on every lane of every
 // wave: lane l sums x[256j + 4l + i]^2 over j, then i, by fma; xor butterfly
 __device__ __forceinline__ float rms_scale(const float* x, int n, float eps, int lane) {
+    // every load first (slices past n read as zeros: fma(0, 0, a) = a, a >= +0), then the chain
+    constexpr int NJ = kMaxE / 256;
+    float4 v[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; j++) v[j] = 256 * j + 4 * lane < n ? ld4(x + 256 * j + 4 * lane) : make_float4(0.f, 0.f, 0.f, 0.f);
     float a = 0.f;
-#pragma unroll 8
-    for (int e0 = 4 * lane; e0 < n; e0 += 256) {
-        const float4 v = ld4(x + e0);
-        a = __fmaf_rn(v.x, v.x, a);
-        a = __fmaf_rn(v.y, v.y, a);
-        a = __fmaf_rn(v.z, v.z, a);
-        a = __fmaf_rn(v.w, v.w, a);
+#pragma unroll
+    for (int j = 0; j < NJ; j++) {
+        a = __fmaf_rn(v[j].x, v[j].x, a);
+        a = __fmaf_rn(v[j].y, v[j].y, a);
+        a = __fmaf_rn(v[j].z, v[j].z, a);
+        a = __fmaf_rn(v[j].w, v[j].w, a);
     }
     a = bfly_sum64(a);
     return __fdiv_rn(1.0f, __builtin_sqrtf(__fadd_rn(__fdiv_rn(a, (float)n), eps)));   // correctly rounded sqrt
@@ -736,7 +748,7 @@ __device__ __forceinline__ void wg_prologue(MPtr M, int l, int kind, int pos, in
 // row): silu(g)*u = g/(1+exp(-g))*u (cpu_infer.cpp:144-147) on lanes 0..31, quantized
 // to one int8 act block record (32 codes, scale, 8*sum) on its own 128-byte line.
 __device__ __forceinline__ void gu_store(const PMat W, int wg, int nwg, int kw, const float* P, uint8_t* act, int lane) {
-    wg_segments(W, wg, nwg, kw, [&](int g, int s, int k0, int k1) {
+    wg_segments(W, wg_place(W, wg, nwg), nwg, kw, [&](int g, int s, int k0, int k1) {
         (void)s;
         const float v = seg_sum(P, k0, k1, lane);
         const float u = __shfl(v, (lane & 31) + 32);
@@ -764,7 +776,8 @@ __device__ __forceinline__ void lm_epilogue(MPtr M, int wg, int nwg, const Lds& 
                                             unsigned dead = 0) {
     if (wave > 0) {
         Top2 t{-__builtin_inff(), INT_MAX, -__builtin_inff()};
-        wg_segments(ldmat(&M->lm), wg, nwg, wave - 1, [&](int g, int s, int k0, int k1) {
+        const PMat Wl = ldmat(&M->lm);
+        wg_segments(Wl, wg_place(Wl, wg, nwg), nwg, wave - 1, [&](int g, int s, int k0, int k1) {
             (void)s;
             const float v = seg_sum(S.P, k0, k1, lane);
             const int row = g * 64 + lane;
