@@ -1380,6 +1380,14 @@ __device__ __forceinline__ void phase_prefetch(MPtr M, int l, int kind, int wg, 
     }
 }
 
+// a workgroup with no O segment skips the O phase's staging and prologue (the records'
+// merge and quantisation feed only the O GEMV; the residual is not touched there)
+__device__ __forceinline__ bool phase_idle(MPtr M, int l, int kind, int wg, int nwg) {
+    if (kind != PH_O) return false;
+    const PMat W = phase_mat(M, l, kind);
+    return wg_place(W, wg, nwg) >= (W.rows >> 6) * W.ks;
+}
+
 template <int HD>
 __global__ __launch_bounds__(kPThreads) void k_step(const DModel* Mp, int pos, int gen) {
     const MPtr M = (MPtr)Mp;
@@ -1407,7 +1415,7 @@ __global__ __launch_bounds__(kPThreads) void k_step(const DModel* Mp, int pos, i
     int l = 0, kind = PH_QKV;
     for (int sb = 1;; sb += 5) {
         __syncthreads();
-        wg_prologue(M, l, kind, pos, wg, S, wave, lane, true);
+        if (!phase_idle(M, l, kind, wg, nwg)) wg_prologue(M, l, kind, pos, wg, S, wave, lane, true);
         __syncthreads();
         stamp(M, sb);
         if (kind == PH_ATTN) {
@@ -1471,7 +1479,8 @@ __global__ __launch_bounds__(kPThreads) void k_step(const DModel* Mp, int pos, i
             phase_prefetch(M, nl, nk, wg, nwg, kw, tl, lane);
         }
         __syncthreads();
-        stage(M, nl, nk, pos, S, wave, kPWaves, lane, true);
+        if (!phase_idle(M, nl, nk, wg, nwg)) stage(M, nl, nk, pos, S, wave, kPWaves, lane, true);
+        else drain_vm();
         l = nl;
         kind = nk;
     }
