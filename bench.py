@@ -198,12 +198,14 @@ def verify_cost(reps=10):
                 note="T=8 = current token + 7 drafts (TMAX 8, mega.cu:50); the config's 8 drafts + 1 would be T=9")
 
 
-def attention_depth(torch, lengths=(512, 4096, 16384, 32768), layers=28, reps=3, graph=True):
+def attention_depth(torch, lengths=(512, 4096, 16384, 32768), layers=28, reps=3, graph=True, mfma=False):
     """config3: S15 split-KV decode attention (12/2 heads, hd 128), one query, fp16 K/V
     N(0,1) at context L, rotated over 28 layers' caches (28 x 32 MB at L = 32768 > the
     256 MB MALL), the 28 launches replayed from a graph. Algorithmic bytes per layer:
-    1024*L (K and V) + q/out."""
+    1024*L (K and V) + q/out. mfma: the matrix-core chunk records (mi_attn_decode_mfma)
+    instead of the canonical ones; its result is checked against the canonical one."""
     nh, nkv, hd = 12, 2, 128
+    attn = minfer.attn_decode_mfma if mfma else minfer.attn_decode
     res = []
     for L in lengths:
         kc = torch.randn(layers, nkv, L, hd, device="cuda").half()
@@ -213,21 +215,27 @@ def attention_depth(torch, lengths=(512, 4096, 16384, 32768), layers=28, reps=3,
         out = torch.empty(nh * hd, device="cuda")
         scale = 1.0 / hd ** 0.5
         for l in range(2):
-            minfer.attn_decode(q, kc[l], vc[l], nh, nkv, hd, L, L, scale, scratch, out)
+            attn(q, kc[l], vc[l], nh, nkv, hd, L, L, scale, scratch, out)
+        if mfma:
+            canon = torch.empty_like(out)
+            minfer.attn_decode(q, kc[1], vc[1], nh, nkv, hd, L, L, scale, scratch, canon)
+            torch.cuda.synchronize()
+            rel = float((out - canon).abs().max() / canon.abs().max())
+            assert rel <= 1e-5, "mfma attention off the canonical result by %g" % rel
         # the layers' launches replayed from a captured graph (ctypes launches from
         # Python would leave the GPU idle between the short kernels); the kernel's
         # counters return to zero by themselves, so replays need no reset. graph=False
         # (for kernel traces, which time each launch themselves): eager launches.
         def layer_loop():
             for l in range(layers):
-                minfer.attn_decode(q, kc[l], vc[l], nh, nkv, hd, L, L, scale, scratch, out)
+                attn(q, kc[l], vc[l], nh, nkv, hd, L, L, scale, scratch, out)
         g = None
         if graph:
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g):
                 layer_loop()
             ref = torch.empty_like(out)
-            minfer.attn_decode(q, kc[layers - 1], vc[layers - 1], nh, nkv, hd, L, L, scale, scratch, ref)
+            attn(q, kc[layers - 1], vc[layers - 1], nh, nkv, hd, L, L, scale, scratch, ref)
             g.replay()
             torch.cuda.synchronize()
             assert torch.equal(out.view(torch.int32), ref.view(torch.int32)), "graph replay differs from the eager launch"
@@ -333,13 +341,15 @@ def main():
     ap.add_argument("--attention-only", type=str, default="", metavar="L[,L...]",
                     help="only run the config3 attention-at-depth measurement at these context "
                          "lengths, print its JSON and exit")
+    ap.add_argument("--mfma", action="store_true",
+                    help="with --attention-only: the matrix-core chunk records (mi_attn_decode_mfma)")
     ap.add_argument("--eager", action="store_true",
                     help="with --attention-only: launch eagerly instead of replaying a graph (for kernel traces)")
     args = ap.parse_args()
     if args.attention_only:
         import torch
         lens = tuple(int(x) for x in args.attention_only.split(","))
-        res = attention_depth(torch, lengths=lens, graph=not args.eager)
+        res = attention_depth(torch, lengths=lens, graph=not args.eager, mfma=args.mfma)
         for a in res:
             log("attention L=%-6d %8.2f us/layer  %7.1f GB/s" % (a["L"], a["us_per_layer"], a["gbps"]))
         print(json.dumps({"attention_depth": res}), flush=True)
@@ -432,6 +442,9 @@ def main():
     attn = [] if args.no_micro else attention_depth(torch)
     for a in attn:
         log("attention L=%-6d %8.2f us/layer  %7.1f GB/s" % (a["L"], a["us_per_layer"], a["gbps"]))
+    attn_mx = [] if args.no_micro else attention_depth(torch, mfma=True)
+    for a in attn_mx:
+        log("attention (mfma records) L=%-6d %8.2f us/layer  %7.1f GB/s" % (a["L"], a["us_per_layer"], a["gbps"]))
     spec = verify = None
     if not args.no_extra:
         stoks, spec = spec_decode(path, prompt, tg + 1)
@@ -468,6 +481,7 @@ def main():
         "phases": phases, "profiled_step_us": prof_total,
         "gemv": micro,
         "attention_depth": attn,
+        "attention_depth_mfma": attn_mx,
         "device_decode_ms": round(dev_ms, 3),
         "cpu_baseline": cpu,
         "speculative": spec,

@@ -255,6 +255,17 @@ int mi_attn_decode(const float* q, const uint16_t* kc, const uint16_t* vc, int32
                    int32_t n_head_kv, int32_t hd, int32_t L, int32_t ctx, float scale,
                    float* scratch, float* out, void* stream);
 
+/* The same attention (same arguments, scratch and record layout, same merge) with each
+ * chunk's scores and p.v as fp16 matrix-core contractions: q and the probabilities are
+ * split into two fp16 parts each (~22 significant bits), K and V are used as stored, the
+ * products are exact and accumulate in fp32. Within ~1e-6 relative of mi_attn_decode,
+ * not bit-identical to it (the order of the sums inside a matrix instruction is the
+ * hardware's). Replaces the same reference kernels (cuda_infer.cu:650-702
+ * attn_partial + attn_combine); config-3 tolerance 1e-3 relative. */
+int mi_attn_decode_mfma(const float* q, const uint16_t* kc, const uint16_t* vc, int32_t n_head,
+                        int32_t n_head_kv, int32_t hd, int32_t L, int32_t ctx, float scale,
+                        float* scratch, float* out, void* stream);
+
 /* The same attention as mi_attn_decode without a workspace argument and without any
  * allocation. No counterpart in the reference: it is for callers that cannot allocate
  * (code under HIP graph capture, serving loops, harnesses that forbid hipMalloc). The

@@ -1187,6 +1187,15 @@ int mi_attn_decode(const float* q, const uint16_t* kc, const uint16_t* vc, int32
     return hipGetLastError() == hipSuccess ? MI_OK : MI_ERR_DEVICE;
 }
 
+int mi_attn_decode_mfma(const float* q, const uint16_t* kc, const uint16_t* vc, int32_t n_head, int32_t n_head_kv,
+                        int32_t hd, int32_t L, int32_t ctx, float scale, float* scratch, float* out, void* stream) {
+    if (!q || !kc || !vc || !scratch || !out || n_head < 1 || n_head_kv < 1 || L < 1 || L > ctx) return MI_ERR_ARG;
+    if (!launch_attn_decode_mfma(q, reinterpret_cast<const __half*>(kc), reinterpret_cast<const __half*>(vc), n_head,
+                                 n_head_kv, hd, L, ctx, scale, scratch, out, (hipStream_t)stream))
+        return MI_ERR_SHAPE;
+    return hipGetLastError() == hipSuccess ? MI_OK : MI_ERR_DEVICE;
+}
+
 static_assert(kNoAllocScratchFloats == MI_ATTN_NOALLOC_SCRATCH_FLOATS, "scratch size in minfer.h and kernels.hpp");
 
 int mi_attn_decode_noalloc(const float* q, const uint16_t* kc, const uint16_t* vc, int32_t n_head, int32_t n_head_kv,

@@ -2641,6 +2641,248 @@ __global__ __launch_bounds__(64 * kMergeWaves) void k_attn_merge(const float* re
     if (lane < 32) out[(size_t)h * HD + d0 + lane] = __fdiv_rn(acc, den);
 }
 
+// ------------------------------------------------------------------ standalone attention on MFMA
+// The chunk records of k_attn_rec (same units, same record layout, merged by the same
+// k_attn_merge), with a unit's scores and p.v as fp16 MFMA contractions instead of one
+// fp32 fma chain per head and lane. Per unit (kv head, 64-position chunk), one wave:
+//   S[pos][head] = K[pos][:] . q[head][:]   v_mfma_f32_16x16x32_f16, A = K rows (as
+//                                           stored, fp16, exact), B = q split in two
+//                                           fp16 parts q' = hi + lo (q' = q * 2^kq per
+//                                           kv head, so the parts stay in fp16 range)
+//   O^T[dim][head] = sum_pos V[pos][dim] p[head][pos]   A = V gathered from LDS, B = p
+//                                           split hi + lo the same way
+// The hi/lo split keeps ~22 significant bits of q and p, the products are exact and the
+// MFMA accumulates in fp32, so a record agrees with attn_core's to ~1e-6 relative, but
+// not bit for bit (the summation order inside an MFMA is the hardware's). The G <= 8
+// query heads of a kv head are the 16 MFMA columns (8 used). Lane l = 16g + c owns
+// column c (head c) and, in the D layout, rows 4g .. 4g + 3 of each tile: the scores of
+// positions 16mt + 4g + r, which are exactly the p values its B operand of the p.v
+// product needs (position 32ks + 16(e/4) + 4g + e%4 for element e of K step ks), so p
+// never leaves the registers; only V is gathered (8 halves per operand).
+// A workgroup is one compute wave and one data wave with NB unit buffers: with two, the
+// data wave DMAs the first two units at once, then each next unit as a buffer frees up;
+// with one (four workgroups per CU at hd 128), the next unit's DMA waits for the
+// compute and the CU's other workgroups fill the gap. The chunk probabilities use the
+// hardware exp2 (v_exp_f32, ~1 ulp) rather than mi_expf: the records are not
+// bit-canonical anyway, and the polynomial was a third of the wave's instructions.
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+constexpr int kVPad = 32;          // bytes after each 1-KB block of V rows (conflict-free gathers)
+template <int HD>
+constexpr int amx_vbytes() { return (64 * HD * 2 / 1024) * (1024 + kVPad); }
+template <int HD>
+constexpr int amx_buf() { return 64 * HD * 2 + amx_vbytes<HD>() + kAttnMaxG * HD * 4; }
+template <int HD>
+constexpr int amx_lds() { return amx_buf<HD>() + 64 * 4; }
+// s_waitcnt with vmcnt(n) and no wait on the other counters
+constexpr int waitcnt_vm(int n) { return 0x0F70 | (n & 15) | (((n >> 4) & 3) << 14); }
+
+// the DMA of unit u into buffer B: K rows (swizzled tile, kslot), V rows in 1-KB blocks
+// of RPI rows each followed by kVPad bytes, the kv head's G query rows; rows past n
+// repeat row n-1 (finite: their p is 0). 2 * HD / 8 + ceil(G * HD * 4 / 1024) loads.
+template <int HD>
+__device__ __forceinline__ void amx_issue(const float* q, const __half* kc, const __half* vc, int G, int nch, int L,
+                                          int ctx, int u, uint8_t* B, int lane) {
+    constexpr int NV = HD / 8, RPI = 64 / NV;
+    const int kvh = u / nch, t0 = (u - kvh * nch) * kAttnChunk, n = min(kAttnChunk, L - t0);
+    const __half* vr = vc + ((size_t)kvh * ctx + t0) * HD;
+    const __half* kr = kc + ((size_t)kvh * ctx + t0) * HD;
+    const int u8 = lane % NV;
+#pragma unroll
+    for (int i = 0; i < NV; i++) {         // K load i: tile slots 64i .. 64i + 63 (rows RPI*i ..)
+        const int t = i * RPI + lane / NV;
+        __builtin_amdgcn_global_load_lds(kr + (size_t)min(t, n - 1) * HD + 8 * (u8 ^ kswz<HD>(t)),
+                                         (lds_ptr)(B + i * 1024), 16, 0, 0);
+    }
+    const int r = lane / NV, col = (lane % NV) * 8;
+#pragma unroll
+    for (int i = 0; i < 64 / RPI; i++)
+        __builtin_amdgcn_global_load_lds(vr + (size_t)min(i * RPI + r, n - 1) * HD + col,
+                                         (lds_ptr)(B + 64 * HD * 2 + i * (1024 + kVPad)), 16, 0, 0);
+    dma_wave(q + (size_t)kvh * G * HD, B + 64 * HD * 2 + amx_vbytes<HD>(), G * HD * 4, lane);
+}
+
+__device__ __forceinline__ void split_f16(float x, _Float16& hi, _Float16& lo) {
+    hi = (_Float16)x;                                   // round to nearest even
+    lo = (_Float16)__fsub_rn(x, (float)hi);             // the remainder is exact in fp32
+}
+
+// both waves' halves of a lane value combined: max or sum over lanes l, l ^ 16, l ^ 32
+// and l ^ 48 (the lanes of one MFMA column)
+__device__ __forceinline__ float col_max(float v) {
+    float a, b;
+    pair16(v, a, b);
+    v = fmaxf(a, b);
+    pair32(v, a, b);
+    return fmaxf(a, b);
+}
+__device__ __forceinline__ float col_sum(float v) {
+    float a, b;
+    pair16(v, a, b);
+    v = __fadd_rn(a, b);
+    pair32(v, a, b);
+    return __fadd_rn(a, b);
+}
+
+template <int HD>
+__global__ __launch_bounds__(192) __attribute__((amdgpu_waves_per_eu(3))) void k_attn_mx(const float* q, const __half* kc, const __half* vc, int nh, int nkv,
+                                                 int L, int ctx, float scale, float* recs) {
+    constexpr int KS = HD / 32, NT = HD / 16, NV = HD / 8, RPI = 64 / NV, VB = 1024 + kVPad, BUF = amx_buf<HD>();
+    __shared__ __align__(16) uint8_t smem[amx_lds<HD>()];
+    const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);    // wave 2 moves data
+    const int G = nh / nkv, nch = (L + kAttnChunk - 1) / kAttnChunk, units = nkv * nch;
+    const int col = lane & 15, g = lane >> 4;
+    float* xch = reinterpret_cast<float*>(smem + BUF);              // [m w0 | m w1 | l w0 | l w1][16]
+    int P = blockIdx.x;
+    if (w == 2) amx_issue<HD>(q, kc, vc, G, nch, L, ctx, P, smem, lane);
+    int qkvh = -1;
+    f16x8 qh[KS], ql[KS];
+    float sc = 0.f;
+    // lane's part of a V gather address: row 4g + (e & 3) of a group of rows starting at a
+    // multiple of 16 lies in block (row / RPI), at (row % RPI) rows into it
+    const int vlane = (RPI == 4 ? g * VB : (g >> 1) * VB + (g & 1) * 4 * HD * 2) + 2 * col;
+    for (int k = 0; P < units; k++, P += gridDim.x) {
+        if (k > 0) {
+            __syncthreads();                            // the compute waves are done with the buffer
+            if (w == 2) amx_issue<HD>(q, kc, vc, G, nch, L, ctx, P, smem, lane);
+        }
+        if (w == 2) drain_vm();
+        __syncthreads();                                // unit P is in LDS
+        if (w == 2) {                                   // (the compute waves' three exchanges)
+            __syncthreads();
+            __syncthreads();
+            __syncthreads();
+            continue;
+        }
+        const int kvh = P / nch, c = P - kvh * nch, n = min(kAttnChunk, L - c * kAttnChunk);
+        if (kvh != qkvh) {
+            // q operands of the kv head's query heads: lane (g, col) holds head col,
+            // dims 32ks + 8g .. + 7, scaled by 2^kq (the largest |q| of the G heads
+            // just under 2^15) and split hi + lo
+            qkvh = kvh;
+            const float* qs = reinterpret_cast<const float*>(smem + 64 * HD * 2 + amx_vbytes<HD>());
+            float qv[KS][8];
+            float mx = 0.f;
+#pragma unroll
+            for (int ks = 0; ks < KS; ks++) {
+                float4 a = make_float4(0.f, 0.f, 0.f, 0.f), b = a;
+                if (col < G) {
+                    a = ld4(qs + col * HD + 32 * ks + 8 * g);
+                    b = ld4(qs + col * HD + 32 * ks + 8 * g + 4);
+                }
+                qv[ks][0] = a.x; qv[ks][1] = a.y; qv[ks][2] = a.z; qv[ks][3] = a.w;
+                qv[ks][4] = b.x; qv[ks][5] = b.y; qv[ks][6] = b.z; qv[ks][7] = b.w;
+#pragma unroll
+                for (int e = 0; e < 8; e++) mx = fmaxf(mx, fabsf(qv[ks][e]));
+            }
+            mx = wave_max(mx);
+            int ex = 0;
+            (void)frexpf(mx, &ex);
+            const int kq = mx > 0.f ? min(max(15 - ex, -100), 100) : 0;
+            sc = ldexpf(scale, -kq);
+#pragma unroll
+            for (int ks = 0; ks < KS; ks++)
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    _Float16 hi, lo;
+                    split_f16(ldexpf(qv[ks][e], kq), hi, lo);
+                    qh[ks][e] = hi;
+                    ql[ks][e] = lo;
+                }
+        }
+        // scores of this wave's positions 32w .. 32w + 31: tiles mt = 2w + j
+        const uint4* kls = reinterpret_cast<const uint4*>(smem);
+        f32x4 S[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+        for (int ks = 0; ks < KS; ks++)
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                const f16x8 a = __builtin_bit_cast(f16x8, kls[kslot<HD>(16 * (2 * w + j) + col, 4 * ks + g)]);
+                S[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qh[ks], S[j], 0, 0, 0);
+                S[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, ql[ks], S[j], 0, 0, 0);
+            }
+        // chunk softmax per head (column) over both waves' positions
+        float p[2][4];
+        float m = -__builtin_inff();
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const bool ok = col < G && 32 * w + 16 * j + 4 * g + r < n;
+                p[j][r] = ok ? __fmul_rn(S[j][r], sc) : -__builtin_inff();
+                m = fmaxf(m, p[j][r]);
+            }
+        m = col_max(m);
+        if (g == 0) xch[16 * w + col] = m;
+        __syncthreads();                                // (A) both maxima; K is no longer read
+        m = fmaxf(xch[col], xch[16 + col]);
+        float ls = 0.f;
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const bool ok = col < G && 32 * w + 16 * j + 4 * g + r < n;
+                p[j][r] = ok ? __builtin_amdgcn_exp2f(__fmul_rn(__fsub_rn(p[j][r], m), 0x1.715476p+0f)) : 0.f;
+                ls = __fadd_rn(ls, p[j][r]);
+            }
+        ls = col_sum(ls);
+        if (g == 0) xch[32 + 16 * w + col] = ls;
+        f16x8 ph, pl;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            _Float16 hi, lo;
+            split_f16(p[e / 4][e & 3], hi, lo);
+            ph[e] = hi;
+            pl[e] = lo;
+        }
+        // p.v over this wave's 32 positions (K step w of the unit); tile nt = dims
+        // 16nt .. 16nt + 15
+        const uint8_t* vb = smem + 64 * HD * 2 + vlane;
+        f32x4 O[NT];
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) {
+            f16x8 a;
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const int c0 = 32 * w + 16 * (e / 4) + (e & 3);             // row of lane group 0
+                a[e] = *reinterpret_cast<const _Float16*>(vb + (c0 / RPI) * VB + (c0 % 4) * HD * 2 + 32 * nt);
+            }
+            O[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, ph, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+            O[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pl, O[nt], 0, 0, 0);
+        }
+        // wave w finishes tiles [w NT/2, (w + 1) NT/2): the other half of its partials
+        // go through the (free) K tile
+        float4* xo = reinterpret_cast<float4*>(smem);
+#pragma unroll
+        for (int i = 0; i < NT / 2; i++) {
+            const f32x4 o = O[(1 - w) * (NT / 2) + i];
+            xo[(w * (NT / 2) + i) * 64 + lane] = make_float4(o[0], o[1], o[2], o[3]);
+        }
+        __syncthreads();                                // (B) the sums and the partials
+        ls = __fadd_rn(xch[32 + col], xch[48 + col]);
+        if (col < G) {
+            const size_t hc = (size_t)(kvh * G + col) * nch + c;
+#pragma unroll
+            for (int i = 0; i < NT / 2; i++) {
+                const int nt = w * (NT / 2) + i;
+                const float4 o = xo[((1 - w) * (NT / 2) + i) * 64 + lane];
+                const f32x4 mine = O[nt];
+                // wave 0's part + wave 1's part, the same order for both halves
+                const float4 s = w == 0 ? make_float4(__fadd_rn(mine[0], o.x), __fadd_rn(mine[1], o.y),
+                                                      __fadd_rn(mine[2], o.z), __fadd_rn(mine[3], o.w))
+                                        : make_float4(__fadd_rn(o.x, mine[0]), __fadd_rn(o.y, mine[1]),
+                                                      __fadd_rn(o.z, mine[2]), __fadd_rn(o.w, mine[3]));
+                st4(recs + hc * HD + 16 * nt + 4 * g, s);
+            }
+            if (w == 0 && g == 0) {
+                recs[(size_t)nh * nch * HD + hc] = m;
+                recs[(size_t)nh * nch * (HD + 1) + hc] = ls;
+            }
+        }
+        __syncthreads();                                // (C) the exchange area is read
+    }
+}
+
 __global__ __launch_bounds__(kThreads) void k_stream(const u32x4* __restrict__ p, size_t n4, uint32_t* sink) {
     const size_t nth = (size_t)gridDim.x * blockDim.x;
     size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -2868,6 +3110,23 @@ bool launch_attn_decode(const float* q, const __half* kc, const __half* vc, int 
         // one head per compute wave, one unit per round (two workgroups per CU at hd 128):
         // the fastest of H = 1..3, S = 1..2 at L = 512..32768 on the box
         launch_attn_rec<HD, 1, 1>(q, kc, vc, nh, nkv, L, ctx, scale, scratch, s);
+        LAUNCH((k_attn_merge<HD>), nh * (HD / 32), 64 * kMergeWaves, s, scratch, nh, L, out);
+    });
+    return true;
+}
+// the same two-launch attention with the chunk records from k_attn_mx (MFMA scores and
+// p.v): one compute and one data wave per workgroup, as many workgroups per CU as the
+// double-buffered LDS allows (two at hd 128)
+bool launch_attn_decode_mfma(const float* q, const __half* kc, const __half* vc, int nh, int nkv, int hd, int L,
+                             int ctx, float scale, float* scratch, float* out, hipStream_t s) {
+    if (nh % nkv || !kernels_support(nh / nkv, hd) || nh / nkv > kAttnMaxG || L < 1) return false;
+    const int nch = (L + kAttnChunk - 1) / kAttnChunk, nsp = (nch + kAttnSplit - 1) / kAttnSplit;
+    if (nsp > kAttnMaxSplits) return false;
+    with_hd(hd, [&](auto h) {
+        constexpr int HD = decltype(h)::value;
+        const int units = nkv * nch, per_cu = max(1, (160 * 1024) / amx_lds<HD>());
+        const int grid = min(units, device_cus() * per_cu);
+        LAUNCH((k_attn_mx<HD>), grid, 192, s, q, kc, vc, nh, nkv, L, ctx, scale, scratch);
         LAUNCH((k_attn_merge<HD>), nh * (HD / 32), 64 * kMergeWaves, s, scratch, nh, L, out);
     });
     return true;

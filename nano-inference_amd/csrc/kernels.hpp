@@ -65,6 +65,10 @@ constexpr size_t kNoAllocScratchFloats = size_t(4) << 20;
 hipError_t noalloc_scratch(hipStream_t s, float** out);
 bool launch_attn_decode(const float* q, const __half* kc, const __half* vc, int nh, int nkv, int hd, int L, int ctx,
                         float scale, float* scratch, float* out, hipStream_t s);
+// the same attention with MFMA chunk records (k_attn_mx): ~1e-6 relative of the
+// canonical records, not bit-identical
+bool launch_attn_decode_mfma(const float* q, const __half* kc, const __half* vc, int nh, int nkv, int hd, int L,
+                             int ctx, float scale, float* scratch, float* out, hipStream_t s);
 void launch_stream(const void* buf, size_t bytes, uint32_t* sink, int n_cu, hipStream_t s);
 
 }  // namespace mi

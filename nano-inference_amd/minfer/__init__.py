@@ -81,6 +81,8 @@ SIGNATURES = {
     "mi_attn_decode": (C.c_int, [_P, _P, _P, C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_float,
                                  _P, _P, _P]),
     "mi_attn_scratch_floats": (C.c_size_t, [C.c_int32, C.c_int32, C.c_int32]),
+    "mi_attn_decode_mfma": (C.c_int, [_P, _P, _P, C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_float,
+                                 _P, _P, _P]),
     "mi_attn_decode_noalloc": (C.c_int, [_P, _P, _P, C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_int32,
                                          C.c_float, _P, _P]),
     "mi_stream_read": (C.c_int, [_P, C.c_size_t, _P, _P]),
@@ -372,6 +374,12 @@ def attn_scratch_floats(n_head, hd, L):
 def attn_decode(q, kc, vc, n_head, n_head_kv, hd, L, ctx, scale, scratch, out, stream=None):
     _check(lib().mi_attn_decode(_ptr(q), _ptr(kc), _ptr(vc), n_head, n_head_kv, hd, L, ctx, C.c_float(scale),
                                 _ptr(scratch), _ptr(out), _stream(stream)))
+
+
+def attn_decode_mfma(q, kc, vc, n_head, n_head_kv, hd, L, ctx, scale, scratch, out, stream=None):
+    """attn_decode with MFMA chunk records (mi_attn_decode_mfma): ~1e-6 relative, not bit-identical"""
+    _check(lib().mi_attn_decode_mfma(_ptr(q), _ptr(kc), _ptr(vc), n_head, n_head_kv, hd, L, ctx, C.c_float(scale),
+                                     _ptr(scratch), _ptr(out), _stream(stream)))
 
 
 ATTN_NOALLOC_SCRATCH_FLOATS = 4 << 20   # MI_ATTN_NOALLOC_SCRATCH_FLOATS
