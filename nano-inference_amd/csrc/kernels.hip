@@ -2671,18 +2671,18 @@ constexpr int kVPad = 32;          // bytes after each 1-KB block of V rows (con
 template <int HD>
 constexpr int amx_vbytes() { return (64 * HD * 2 / 1024) * (1024 + kVPad); }
 template <int HD>
-constexpr int amx_buf() { return 64 * HD * 2 + amx_vbytes<HD>() + kAttnMaxG * HD * 4; }
+constexpr int amx_buf() { return 64 * HD * 2 + amx_vbytes<HD>(); }
 template <int HD>
 constexpr int amx_lds() { return amx_buf<HD>() + 64 * 4; }
 // s_waitcnt with vmcnt(n) and no wait on the other counters
 constexpr int waitcnt_vm(int n) { return 0x0F70 | (n & 15) | (((n >> 4) & 3) << 14); }
 
 // the DMA of unit u into buffer B: K rows (swizzled tile, kslot), V rows in 1-KB blocks
-// of RPI rows each followed by kVPad bytes, the kv head's G query rows; rows past n
-// repeat row n-1 (finite: their p is 0). 2 * HD / 8 + ceil(G * HD * 4 / 1024) loads.
+// of RPI rows each followed by kVPad bytes; rows past n repeat row n-1 (finite: their
+// p is 0)
 template <int HD>
-__device__ __forceinline__ void amx_issue(const float* q, const __half* kc, const __half* vc, int G, int nch, int L,
-                                          int ctx, int u, uint8_t* B, int lane) {
+__device__ __forceinline__ void amx_issue(const __half* kc, const __half* vc, int nch, int L, int ctx, int u,
+                                          uint8_t* B, int lane) {
     constexpr int NV = HD / 8, RPI = 64 / NV;
     const int kvh = u / nch, t0 = (u - kvh * nch) * kAttnChunk, n = min(kAttnChunk, L - t0);
     const __half* vr = vc + ((size_t)kvh * ctx + t0) * HD;
@@ -2699,7 +2699,6 @@ __device__ __forceinline__ void amx_issue(const float* q, const __half* kc, cons
     for (int i = 0; i < 64 / RPI; i++)
         __builtin_amdgcn_global_load_lds(vr + (size_t)min(i * RPI + r, n - 1) * HD + col,
                                          (lds_ptr)(B + 64 * HD * 2 + i * (1024 + kVPad)), 16, 0, 0);
-    dma_wave(q + (size_t)kvh * G * HD, B + 64 * HD * 2 + amx_vbytes<HD>(), G * HD * 4, lane);
 }
 
 __device__ __forceinline__ void split_f16(float x, _Float16& hi, _Float16& lo) {
@@ -2734,47 +2733,39 @@ __global__ __launch_bounds__(192) __attribute__((amdgpu_waves_per_eu(3))) void k
     const int col = lane & 15, g = lane >> 4;
     float* xch = reinterpret_cast<float*>(smem + BUF);              // [m w0 | m w1 | l w0 | l w1][16]
     int P = blockIdx.x;
-    if (w == 2) amx_issue<HD>(q, kc, vc, G, nch, L, ctx, P, smem, lane);
-    int qkvh = -1;
-    f16x8 qh[KS], ql[KS];
-    float sc = 0.f;
+    if (w == 2) amx_issue<HD>(kc, vc, nch, L, ctx, P, smem, lane);
     // lane's part of a V gather address: row 4g + (e & 3) of a group of rows starting at a
     // multiple of 16 lies in block (row / RPI), at (row % RPI) rows into it
     const int vlane = (RPI == 4 ? g * VB : (g >> 1) * VB + (g & 1) * 4 * HD * 2) + 2 * col;
     for (int k = 0; P < units; k++, P += gridDim.x) {
         if (k > 0) {
             __syncthreads();                            // the compute waves are done with the buffer
-            if (w == 2) amx_issue<HD>(q, kc, vc, G, nch, L, ctx, P, smem, lane);
-        }
-        if (w == 2) drain_vm();
-        __syncthreads();                                // unit P is in LDS
-        if (w == 2) {                                   // (the compute waves' three exchanges)
-            __syncthreads();
-            __syncthreads();
-            __syncthreads();
-            continue;
+            if (w == 2) amx_issue<HD>(kc, vc, nch, L, ctx, P, smem, lane);
         }
         const int kvh = P / nch, c = P - kvh * nch, n = min(kAttnChunk, L - c * kAttnChunk);
-        if (kvh != qkvh) {
-            // q operands of the kv head's query heads: lane (g, col) holds head col,
-            // dims 32ks + 8g .. + 7, scaled by 2^kq (the largest |q| of the G heads
-            // just under 2^15) and split hi + lo
-            qkvh = kvh;
-            const float* qs = reinterpret_cast<const float*>(smem + 64 * HD * 2 + amx_vbytes<HD>());
+        // the kv head's q operands, built while the unit's DMA is in flight: lane (g,
+        // col) holds head col, dims 32ks + 8g .. + 7, scaled by 2^kq (the largest |q| of
+        // the G heads just under 2^15) and split hi + lo
+        f16x8 qh[KS], ql[KS];
+        float sc = 0.f;
+        if (w < 2) {
             float qv[KS][8];
-            float mx = 0.f;
 #pragma unroll
             for (int ks = 0; ks < KS; ks++) {
                 float4 a = make_float4(0.f, 0.f, 0.f, 0.f), b = a;
                 if (col < G) {
-                    a = ld4(qs + col * HD + 32 * ks + 8 * g);
-                    b = ld4(qs + col * HD + 32 * ks + 8 * g + 4);
+                    const float* qr = q + (size_t)(kvh * G + col) * HD + 32 * ks + 8 * g;
+                    a = ld4(qr);
+                    b = ld4(qr + 4);
                 }
                 qv[ks][0] = a.x; qv[ks][1] = a.y; qv[ks][2] = a.z; qv[ks][3] = a.w;
                 qv[ks][4] = b.x; qv[ks][5] = b.y; qv[ks][6] = b.z; qv[ks][7] = b.w;
+            }
+            float mx = 0.f;
+#pragma unroll
+            for (int ks = 0; ks < KS; ks++)
 #pragma unroll
                 for (int e = 0; e < 8; e++) mx = fmaxf(mx, fabsf(qv[ks][e]));
-            }
             mx = wave_max(mx);
             int ex = 0;
             (void)frexpf(mx, &ex);
@@ -2789,6 +2780,17 @@ __global__ __launch_bounds__(192) __attribute__((amdgpu_waves_per_eu(3))) void k
                     qh[ks][e] = hi;
                     ql[ks][e] = lo;
                 }
+        }
+        // K is DMA'd before V: the scores start once K has landed, and V is waited for
+        // at the first exchange
+        if (w == 2) __builtin_amdgcn_s_waitcnt(waitcnt_vm(NV));
+        __syncthreads();                                // unit P's K tile is in LDS
+        if (w == 2) {
+            drain_vm();
+            __syncthreads();                            // (A) V too
+            __syncthreads();                            // (B)
+            __syncthreads();                            // (C)
+            continue;
         }
         // scores of this wave's positions 32w .. 32w + 31: tiles mt = 2w + j
         const uint4* kls = reinterpret_cast<const uint4*>(smem);
@@ -2814,7 +2816,7 @@ __global__ __launch_bounds__(192) __attribute__((amdgpu_waves_per_eu(3))) void k
             }
         m = col_max(m);
         if (g == 0) xch[16 * w + col] = m;
-        __syncthreads();                                // (A) both maxima; K is no longer read
+        __syncthreads();                                // (A) both maxima and V; K is no longer read
         m = fmaxf(xch[col], xch[16 + col]);
         float ls = 0.f;
 #pragma unroll
