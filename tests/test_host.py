@@ -166,3 +166,28 @@ def test_pred_hash_byte_layout():
     p2 = pred.copy()
     p2[[4, 5]] = p2[[5, 4]]
     assert minfer.pred_hash(list(p2), list(margin)) != h
+
+
+@pytest.mark.parametrize("name", ["mi_attn_decode", "mi_attn_decode_mfma"])
+def test_attention_rejects_bad_shapes_before_any_launch(name):
+    """the standalone attention entry points validate every argument before they
+    touch the device: bad pointers and positions give MI_ERR_ARG (-1), shapes the
+    kernels do not take give MI_ERR_SHAPE (-4); the pointers here are never
+    dereferenced because every case is rejected first"""
+    import ctypes as C
+    fn = getattr(minfer.lib(), name)
+    p = C.c_void_p(16)          # stand-in address: rejected calls never read it
+    cases = [
+        # (q, n_head, n_head_kv, hd, L, ctx, scratch, expected)
+        (None, 12, 2, 128, 64, 64, p, -1),        # no q
+        (p, 12, 2, 128, 64, 64, None, -1),        # no scratch
+        (p, 12, 2, 128, 65, 64, p, -1),           # L > ctx
+        (p, 12, 2, 128, 0, 64, p, -1),            # L < 1
+        (p, 12, 5, 128, 64, 64, p, -4),           # n_head not a multiple of n_head_kv
+        (p, 18, 2, 128, 64, 64, p, -4),           # 9 query heads per kv head
+        (p, 12, 2, 96, 64, 64, p, -4),            # head_dim 96
+        (p, 12, 2, 128, 600000, 600000, p, -4),   # more than 512 splits of 16 chunks
+    ]
+    for q, nh, nkv, hd, L, ctx, scr, want in cases:
+        rc = fn(q, p, p, nh, nkv, hd, L, ctx, C.c_float(0.1), scr, p, None)
+        assert rc == want, (name, nh, nkv, hd, L, ctx, rc)
