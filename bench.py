@@ -445,6 +445,8 @@ def main():
     attn_mx = [] if args.no_micro else attention_depth(torch, mfma=True)
     for a in attn_mx:
         log("attention (mfma records) L=%-6d %8.2f us/layer  %7.1f GB/s" % (a["L"], a["us_per_layer"], a["gbps"]))
+    for a in attn + attn_mx:          # against the stream roofline measured in this run
+        a["frac_of_stream"] = round(a["gbps"] / stream, 4)
     spec = verify = None
     if not args.no_extra:
         stoks, spec = spec_decode(path, prompt, tg + 1)
