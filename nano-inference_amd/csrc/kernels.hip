@@ -2644,7 +2644,7 @@ __global__ __launch_bounds__(64 * kMergeWaves) void k_attn_merge(const float* re
 // ------------------------------------------------------------------ standalone attention on MFMA
 // The chunk records of k_attn_rec (same units, same record layout, merged by the same
 // k_attn_merge), with a unit's scores and p.v as fp16 MFMA contractions instead of one
-// fp32 fma chain per head and lane. Per unit (kv head, 64-position chunk), one wave:
+// fp32 fma chain per head and lane. Per unit (kv head, 64-position chunk):
 //   S[pos][head] = K[pos][:] . q[head][:]   v_mfma_f32_16x16x32_f16, A = K rows (as
 //                                           stored, fp16, exact), B = q split in two
 //                                           fp16 parts q' = hi + lo (q' = q * 2^kq per
@@ -2659,12 +2659,15 @@ __global__ __launch_bounds__(64 * kMergeWaves) void k_attn_merge(const float* re
 // positions 16mt + 4g + r, which are exactly the p values its B operand of the p.v
 // product needs (position 32ks + 16(e/4) + 4g + e%4 for element e of K step ks), so p
 // never leaves the registers; only V is gathered (8 halves per operand).
-// A workgroup is one compute wave and one data wave with NB unit buffers: with two, the
-// data wave DMAs the first two units at once, then each next unit as a buffer frees up;
-// with one (four workgroups per CU at hd 128), the next unit's DMA waits for the
-// compute and the CU's other workgroups fill the gap. The chunk probabilities use the
-// hardware exp2 (v_exp_f32, ~1 ulp) rather than mi_expf: the records are not
-// bit-canonical anyway, and the polynomial was a third of the wave's instructions.
+// A workgroup is two compute waves and one data wave with one unit buffer (four
+// workgroups per CU at hd 128): the data wave DMAs the unit's K tile, then its V rows;
+// the compute waves meanwhile load q and build its operands, and compute wave w takes
+// positions 32w .. 32w + 31 (scores, its half of the chunk softmax, its half of p.v).
+// The maxima and sums of the two halves meet in LDS, and each wave adds the other's
+// partial tiles for half of the record. The next unit's DMA waits for the compute; the
+// CU's other workgroups fill the gap. The chunk probabilities use the hardware exp2
+// (v_exp_f32, ~1 ulp) rather than mi_expf: the records are not bit-canonical anyway,
+// and the polynomial was a third of a wave's instructions.
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 constexpr int kVPad = 32;          // bytes after each 1-KB block of V rows (conflict-free gathers)
