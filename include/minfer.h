@@ -272,8 +272,9 @@ int mi_attn_decode_mfma(const float* q, const uint16_t* kc, const uint16_t* vc, 
  * scratch is a library-held device array of MI_ATTN_NOALLOC_SCRATCH_FLOATS floats (16 MiB,
  * one per GPU, held until the process ends); a shape that needs more than
  * mi_attn_scratch_floats() allows returns MI_ERR_SHAPE (message via mi_last_error(NULL)).
- * The first call on a device looks the array's address up. All calls on one GPU share
- * the array: calls that overlap on one GPU race. */
+ * The first call on a device looks the array's address up on the host (no stream work):
+ * code that captures the call into a HIP graph makes one call on that device before the
+ * capture. All calls on one GPU share the array: calls that overlap on one GPU race. */
 #define MI_ATTN_NOALLOC_SCRATCH_FLOATS (4u << 20)
 int mi_attn_decode_noalloc(const float* q, const uint16_t* kc, const uint16_t* vc, int32_t n_head,
                            int32_t n_head_kv, int32_t hd, int32_t L, int32_t ctx, float scale,

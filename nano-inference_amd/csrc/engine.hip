@@ -98,21 +98,25 @@ int dev_alloc(mi_engine* e, void** p, size_t bytes) {
     return MI_OK;
 }
 
-// mega.cu:924-936 quant_row_q4_0: any non-q4_0 weight row -> q4_0 (amax/7, +8, clamp)
-void requant_row_q4_0(const float* y, int n, uint8_t* out) {
-    for (int b = 0; b < n / 32; b++, y += 32, out += 18) {
-        float amax = 0.f;
-        for (int j = 0; j < 32; j++) amax = std::max(amax, std::fabs(y[j]));
-        const float d = amax / 7.f, inv = d > 0.f ? 1.f / d : 0.f;
-        const uint16_t hd = f32_to_f16(d);
-        memcpy(out, &hd, 2);
-        for (int j = 0; j < 16; j++) {
-            int q0 = (int)lrintf(y[j] * inv) + 8, q1 = (int)lrintf(y[j + 16] * inv) + 8;
-            q0 = std::min(15, std::max(0, q0)); q1 = std::min(15, std::max(0, q1));
-            out[2 + j] = (uint8_t)(q0 | (q1 << 4));
-        }
+// Weights stored in another type are re-encoded as q4_0, the only format the kernels
+// read (mega.cu:924-936 is the recipe; the oracle restates the same steps, so the two
+// must agree bit for bit). For one block of 32 values:
+//   step  = (largest |value|) / 7, stored as fp16
+//   code  = lrintf(value * (1 / step)) + 8 (0 when step is 0), limited to 0..15
+//   byte j of the 16 holds the code of value j in its low nibble, value j + 16 in its high
+struct Q4Codec {
+    static uint8_t code(float v, float recip) { return (uint8_t)std::clamp((int)lrintf(v * recip) + 8, 0, 15); }
+    static void encode(const float* v, uint8_t* blk) {
+        float peak = 0.f;
+        for (int i = 0; i < 32; ++i) peak = std::max(peak, std::fabs(v[i]));
+        const float step = peak / 7.f;
+        const float recip = step > 0.f ? 1.f / step : 0.f;
+        const uint16_t h = f32_to_f16(step);
+        memcpy(blk, &h, sizeof h);
+        uint8_t* q = blk + 2;
+        for (int j = 0; j < 16; ++j) q[j] = (uint8_t)(code(v[j], recip) | (code(v[j + 16], recip) << 4));
     }
-}
+};
 
 void dequant_row(const GTensor& t, int64_t r, float* out) {
     const int64_t c = t.cols();
@@ -185,15 +189,32 @@ void dequant_row(const GTensor& t, int64_t r, float* out) {
     }
 }
 
-// a weight matrix as GGUF row-major q4_0 bytes (as stored, or requantized)
-const uint8_t* q4_rows(const GTensor& t, std::vector<uint8_t>& buf) {
-    if (t.type == GT_Q4_0) return t.data;
-    const int n = (int)t.cols(), rows = (int)t.rows();
-    buf.resize((size_t)rows * (n / 32) * 18);
-    std::vector<float> row(n);
-    for (int r = 0; r < rows; r++) { dequant_row(t, r, row.data()); requant_row_q4_0(row.data(), n, buf.data() + (size_t)r * (n / 32) * 18); }
-    return buf.data();
-}
+// The rows of a weight matrix as GGUF q4_0 bytes: a view of the mapped file when the
+// tensor is stored as q4_0, otherwise an owned copy with every row dequantized and
+// re-encoded block by block (Q4Codec).
+class Q4View {
+  public:
+    explicit Q4View(const GTensor& t) {
+        if (t.type == GT_Q4_0) {
+            bytes_ = t.data;
+            return;
+        }
+        const int64_t cols = t.cols(), nblk = cols / 32;
+        owned_.resize((size_t)t.rows() * nblk * 18);
+        std::vector<float> vals((size_t)cols);
+        uint8_t* dst = owned_.data();
+        for (int64_t r = 0; r < t.rows(); ++r) {
+            dequant_row(t, r, vals.data());
+            for (int64_t b = 0; b < nblk; ++b, dst += 18) Q4Codec::encode(vals.data() + 32 * b, dst);
+        }
+        bytes_ = owned_.data();
+    }
+    const uint8_t* data() const { return bytes_; }
+
+  private:
+    const uint8_t* bytes_ = nullptr;
+    std::vector<uint8_t> owned_;
+};
 
 }  // namespace
 
@@ -347,7 +368,7 @@ static int load_impl(mi_engine* e, const char* path) {
         return set_err(e, MI_ERR_FORMAT, "embedding/output shapes do not match the metadata");
 
     std::vector<DLayer> layers(e->NL);
-    std::vector<uint8_t> tmp, cat;
+    std::vector<uint8_t> cat;
     const size_t rbE = (size_t)nbE * 18, rbF = (size_t)nbF * 18;
     for (int l = 0; l < e->NL; l++) {
         const std::string p = "blk." + std::to_string(l) + ".";
@@ -366,18 +387,18 @@ static int load_impl(mi_engine* e, const char* path) {
             return set_err(e, MI_ERR_FORMAT, "layer %d tensor shapes do not match the metadata", l);
         // fused QKV rows [q; k; v]
         cat.resize((size_t)e->QKV * rbE);
-        memcpy(cat.data(), q4_rows(*t[1], tmp), (size_t)NQ * rbE);
-        memcpy(cat.data() + (size_t)NQ * rbE, q4_rows(*t[3], tmp), (size_t)e->KVD * rbE);
-        memcpy(cat.data() + (size_t)(NQ + e->KVD) * rbE, q4_rows(*t[5], tmp), (size_t)e->KVD * rbE);
+        memcpy(cat.data(), Q4View(*t[1]).data(), (size_t)NQ * rbE);
+        memcpy(cat.data() + (size_t)NQ * rbE, Q4View(*t[3]).data(), (size_t)e->KVD * rbE);
+        memcpy(cat.data() + (size_t)(NQ + e->KVD) * rbE, Q4View(*t[5]).data(), (size_t)e->KVD * rbE);
         int rc = upload_mat(e, cat.data(), e->QKV, nbE, 0, &layers[l].qkv);
         if (rc) return rc;
-        rc = upload_mat(e, q4_rows(*t[7], tmp), e->E, nbE, 1, &layers[l].o);
+        rc = upload_mat(e, Q4View(*t[7]).data(), e->E, nbE, 1, &layers[l].o);
         if (rc) return rc;
         // gate/up interleaved by 32-row groups
         {
-            std::vector<uint8_t> gb, ub;
-            const uint8_t* gr = q4_rows(*t[9], gb);
-            const uint8_t* ur = q4_rows(*t[10], ub);
+            const Q4View gv(*t[9]), uv(*t[10]);
+            const uint8_t* gr = gv.data();
+            const uint8_t* ur = uv.data();
             cat.resize((size_t)2 * e->FF * rbE);
             for (int G32 = 0; G32 < e->FF / 32; G32++) {
                 memcpy(cat.data() + (size_t)(64 * G32) * rbE, gr + (size_t)(32 * G32) * rbE, 32 * rbE);
@@ -386,7 +407,7 @@ static int load_impl(mi_engine* e, const char* path) {
             rc = upload_mat(e, cat.data(), 2 * e->FF, nbE, 2, &layers[l].gu);
             if (rc) return rc;
         }
-        rc = upload_mat(e, q4_rows(*t[11], tmp), e->E, nbF, 3, &layers[l].d);
+        rc = upload_mat(e, Q4View(*t[11]).data(), e->E, nbF, 3, &layers[l].d);
         if (rc) return rc;
         (void)rbF;
         rc = upload_f32(e, t[0], e->E, &layers[l].an);
@@ -414,7 +435,7 @@ static int load_impl(mi_engine* e, const char* path) {
     M.QKV = e->QKV; M.V = e->V; M.NL = e->NL; M.maxseq = e->maxseq; M.maxch = e->maxch;
     M.eps = e->eps;
     M.scale = 1.f / sqrtf((float)e->HD);
-    int rc = upload_mat(e, q4_rows(*tout, tmp), e->V, nbE, 4, &M.lm);
+    int rc = upload_mat(e, Q4View(*tout).data(), e->V, nbE, 4, &M.lm);
     if (rc) return rc;
     rc = upload_f32(e, te, (int64_t)e->V * e->E, &M.emb);
     if (rc) return rc;
@@ -569,7 +590,9 @@ static int run_multi(mi_engine* e, int pos, int T, bool want_logits) {
         launch_step_multi(M, dM, e->n_cu, T, e->stream);
         return hipGetLastError();
     };
-    if (!e->opts.graphs) {
+    // A cooperative launch is never captured: the fallback must reach the runtime as a
+    // cooperative dispatch every time (check_barrier drops the graphs when it switches).
+    if (!e->opts.graphs || (e->coop && e->nwg_persistent && e->multi_persistent)) {
         HIPCHK(e, launch());
         return MI_OK;
     }
@@ -628,6 +651,13 @@ static int check_barrier(mi_engine* e) {
         HIPCHK(e, hipMemset(e->M.err, 0, 4));
         if (!e->coop) {
             e->coop = true;
+            // graphs captured so far hold plain launches of the persistent kernel
+            for (auto& row : e->gexec)
+                for (hipGraphExec_t& g : row)
+                    if (g) {
+                        (void)hipGraphExecDestroy(g);
+                        g = nullptr;
+                    }
             return kRetry;
         }
         return set_err(e, MI_ERR_DEVICE, "grid barrier timed out under a cooperative launch");

@@ -1822,8 +1822,7 @@ __device__ __forceinline__ void tstage_x(MPtr M, int slot, int T, uint8_t* XT) {
 // token's embedding row) -> hT -> RMSNorm -> int8 records in xT. The same arithmetic
 // as the single-token step's norm prologue (cuda_infer.cu:43-60 rmsnorm, 80-89 quant).
 template <bool P>
-__device__ __forceinline__ void kT_in_body(MPtr M, int l, int kind, int t, float* x) {
-    const int pos = *M->posT;
+__device__ __forceinline__ void kT_in_body(MPtr M, int l, int kind, int t, float* x, int pos) {
     const int wave = threadIdx.x >> 6, lane = opaque_tid() & 63, n = M->E, nblk = n / 32;
     const bool qkv = kind == PH_QKV, lm = kind == PH_LM, dsrc = kind != PH_GU;
     const int pl = qkv ? l - 1 : lm ? M->NL - 1 : l;
@@ -1873,7 +1872,7 @@ __device__ __forceinline__ void kT_in_body(MPtr M, int l, int kind, int t, float
 }
 __global__ __launch_bounds__(kPThreads) void kT_in(const DModel* Mp, int l, int kind) {
     __shared__ __align__(16) float x[kMaxE];
-    kT_in_body<false>((MPtr)Mp, l, kind, blockIdx.x, x);
+    kT_in_body<false>((MPtr)Mp, l, kind, blockIdx.x, x, *((MPtr)Mp)->posT);
 }
 
 __device__ __forceinline__ float* qkvT_at(MPtr M, int l) { return M->qkvT + (size_t)l * LY(M, 0)->qkv.ks * kMaxT * M->QKV; }
@@ -1918,10 +1917,9 @@ template <int HD>
 constexpr int kt_attn_lds() { return 2 * 64 * HD * 2 + kPWaves * HD * 4; }
 
 template <int HD, bool PS>
-__device__ __forceinline__ void kT_attn_body(MPtr M, int l, int T, uint8_t* smem, int wg, int nwg) {
+__device__ __forceinline__ void kT_attn_body(MPtr M, int l, int T, uint8_t* smem, int wg, int nwg, int pos) {
     TBODY
     constexpr int half = HD / 2, DPL = HD / 64;
-    const int pos = *M->posT;
     uint4* kls = reinterpret_cast<uint4*>(smem);
     __half* vls = reinterpret_cast<__half*>(smem + 64 * HD * 2);
     float* qs = reinterpret_cast<float*>(smem + 2 * 64 * HD * 2) + wave * HD;
@@ -2012,15 +2010,14 @@ __device__ __forceinline__ void kT_attn_body(MPtr M, int l, int T, uint8_t* smem
 }
 template <int HD>
 __global__ __launch_bounds__(kPThreads) void kT_attn(const DModel* Mp, int l, int T) {
-    TWRAP(kt_attn_lds<HD>(), (kT_attn_body<HD, false>((MPtr)Mp, l, T, smem, blockIdx.x, gridDim.x)))
+    TWRAP(kt_attn_lds<HD>(), (kT_attn_body<HD, false>((MPtr)Mp, l, T, smem, blockIdx.x, gridDim.x, *((MPtr)Mp)->posT)))
 }
 
 // chunk merge of token t's records for query head h (one wave per (t, h); lane = dims
 // lane + 64j) into the O phase's int8 records in xT. The merge is comb_wave's, the
 // step's merge phase uses the same function.
 template <int HD, bool PS>
-__device__ __forceinline__ void kT_comb_item(MPtr M, int l, int item, int lane) {
-    const int pos = *M->posT;
+__device__ __forceinline__ void kT_comb_item(MPtr M, int l, int item, int lane, int pos) {
     constexpr int DPL = HD / 64;
     const int t = item / M->NH, hh = item - t * M->NH, nch = (pos + t + kAttnChunk) / kAttnChunk, arec = M->arec;
     const float* r = attT_at(M, l, t) + (size_t)hh * M->maxch * arec;
@@ -2047,7 +2044,7 @@ template <int HD>
 __global__ __launch_bounds__(256) void kT_comb(const DModel* Mp, int l, int T) {
     const MPtr M = (MPtr)Mp;
     const int item = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (item < T * M->NH) kT_comb_item<HD, false>(M, l, item, threadIdx.x & 63);
+    if (item < T * M->NH) kT_comb_item<HD, false>(M, l, item, threadIdx.x & 63, *M->posT);
 }
 
 template <bool PS>
@@ -2152,8 +2149,7 @@ __global__ __launch_bounds__(kPThreads) void kT_lm(const DModel* Mp, int T) {
     TWRAP(kTGemvLds, kT_lm_body<false>((MPtr)Mp, T, smem, blockIdx.x, gridDim.x))
 }
 
-__device__ __forceinline__ void kT_argmax_body(MPtr M, int ncand, int T) {
-    const int pos = *M->posT;
+__device__ __forceinline__ void kT_argmax_body(MPtr M, int ncand, int T, int pos) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     if (wave >= T) return;
     Top2 tp{-__builtin_inff(), INT_MAX, -__builtin_inff()};
@@ -2168,7 +2164,7 @@ __device__ __forceinline__ void kT_argmax_body(MPtr M, int ncand, int T) {
     }
 }
 __global__ __launch_bounds__(kPThreads) void kT_argmax(const DModel* Mp, int ncand, int T) {
-    kT_argmax_body((MPtr)Mp, ncand, T);
+    kT_argmax_body((MPtr)Mp, ncand, T, *((MPtr)Mp)->posT);
 }
 
 // The multi-token step as one persistent launch (mega.cu:621-623 runs prompt chunks and
@@ -2221,9 +2217,17 @@ __device__ __forceinline__ int spec_draft(int32_t* h, int len, int ngmax, int km
     }
     return 0;
 }
-// after the verify step of T tokens at pos: the commit and the next draft (one wave)
-__device__ __forceinline__ void spec_commit(MPtr M, SpecDev* sp, int lane) {
-    const int pos = *M->posT, K = sp->T - 1;
+// after the verify step of T tokens at pos: the commit and the next draft (one wave).
+// When a grid barrier of this launch gave up (*err set), workgroups may still be running
+// this step with its T and pos, and the step's outputs are not trustworthy: the state is
+// left as it was except done = 1, so the launches queued behind this one return at once
+// and the host recomputes the whole generation with cooperative launches.
+__device__ __forceinline__ void spec_commit(MPtr M, SpecDev* sp, int lane, int pos) {
+    if (ldc(reinterpret_cast<const uint32_t*>(M->err)) != 0) {
+        if (lane == 0) sp->done = 1;
+        return;
+    }
+    const int K = sp->T - 1;
     int32_t* h = M->tokbuf;
     int a = 0;
     while (a < K && h[pos + 1 + a] == M->out_tok[pos + a]) a++;
@@ -2275,6 +2279,9 @@ __global__ __launch_bounds__(kPThreads) void kT_step(const DModel* Mp, int T) {
         if (M->spec->done) return;                           // every workgroup reads the same word
         T = M->spec->T;
     }
+    // the step's position, read once: with SPEC, workgroup 0's spec_commit rewrites posT
+    // (and T) for the next launch at the end of this one
+    const int pos = *M->posT;
     __shared__ __align__(16) uint8_t smem[kTStepLds];
     const int wg = blockIdx.x, nwg = gridDim.x, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     float* xs = reinterpret_cast<float*>(smem);
@@ -2286,33 +2293,33 @@ __global__ __launch_bounds__(kPThreads) void kT_step(const DModel* Mp, int T) {
         __syncthreads();
     };
     for (int l = 0; l < M->NL; l++) {
-        if (wg < T) kT_in_body<true>(M, l, PH_QKV, wg, xs);
+        if (wg < T) kT_in_body<true>(M, l, PH_QKV, wg, xs, pos);
         barrier();
         kT_qkv_body<true>(M, l, T, smem, wg, nwg);
         barrier();
-        kT_attn_body<HD, true>(M, l, T, smem, wg, nwg);
+        kT_attn_body<HD, true>(M, l, T, smem, wg, nwg, pos);
         barrier();
-        for (int it = wg * kPWaves + wave; it < T * M->NH; it += nwg * kPWaves) kT_comb_item<HD, true>(M, l, it, lane);
+        for (int it = wg * kPWaves + wave; it < T * M->NH; it += nwg * kPWaves) kT_comb_item<HD, true>(M, l, it, lane, pos);
         barrier();
         kT_o_body<true>(M, l, T, smem, wg, nwg);
         barrier();
-        if (wg < T) kT_in_body<true>(M, l, PH_GU, wg, xs);
+        if (wg < T) kT_in_body<true>(M, l, PH_GU, wg, xs, pos);
         barrier();
         kT_gu_body<true>(M, l, T, smem, wg, nwg);
         barrier();
         kT_down_body<true>(M, l, T, smem, wg, nwg);
         barrier();
     }
-    if (wg < T) kT_in_body<true>(M, M->NL - 1, PH_LM, wg, xs);
+    if (wg < T) kT_in_body<true>(M, M->NL - 1, PH_LM, wg, xs, pos);
     barrier();
     kT_lm_body<true>(M, T, smem, wg, nwg);
     barrier();
     if (wave == 0) ctl_exit(M->bar);
     if (wg == 0) {
-        kT_argmax_body(M, nwg, T);
+        kT_argmax_body(M, nwg, T, pos);
         if constexpr (SPEC) {
             __syncthreads();                                 // the step's out_tok / out_margin
-            if (wave == 0) spec_commit(M, M->spec, lane);
+            if (wave == 0) spec_commit(M, M->spec, lane, pos);
         }
     }
 }

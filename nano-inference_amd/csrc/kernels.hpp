@@ -60,8 +60,8 @@ void launch_isums(const PMat& W, const int8_t* xq, int32_t* isum, hipStream_t s)
 size_t attn_scratch_floats(int nh, int hd, int L);
 // floats of the file-scope scratch array behind mi_attn_decode_noalloc (16 MiB per device)
 constexpr size_t kNoAllocScratchFloats = size_t(4) << 20;
-// device address of the current device's scratch array (looked up, and its counters
-// zeroed on stream s, at the first call on each device)
+// device address of the current device's scratch array (looked up on the host at the
+// first call on each device; s is not used)
 hipError_t noalloc_scratch(hipStream_t s, float** out);
 bool launch_attn_decode(const float* q, const __half* kc, const __half* vc, int nh, int nkv, int hd, int L, int ctx,
                         float scale, float* scratch, float* out, hipStream_t s);

@@ -157,3 +157,10 @@ def test_attention_mfma_scratch_reuse(torch):
         minfer.attn_decode(dev(torch, q), dev(torch, k16.view(np.int16)), dev(torch, v16.view(np.int16)), nh, nkv, hd,
                            L, ctx, float(scale), scratch, out)
         torch.cuda.synchronize()
+        canon = out.cpu().numpy().reshape(nh, hd)
+        G = nh // nkv
+        for h in range(nh):      # the canonical entry point on the same scratch: bit for bit
+            kf = np.ascontiguousarray(k16[h // G, :L].astype(np.float32))
+            vf = np.ascontiguousarray(v16[h // G, :L].astype(np.float32))
+            ref = O.attention_canon(np.ascontiguousarray(q[h]), kf.ravel(), vf.ravel(), L, hd, hd, float(scale))
+            assert np.array_equal(canon[h].view(np.uint32), ref.view(np.uint32)), (nh, hd, L, h)

@@ -479,3 +479,52 @@ def test_barrier_failure_recomputes_cooperatively(mode):
     assert np.array_equal(np.float32(gm).view(np.uint32), np.float32(wm).view(np.uint32))
     assert eng.refresh_info().coop == 1
     eng.close()
+
+
+@pytest.mark.parametrize("graphs", [0, 1], ids=["direct", "graphs"])
+@pytest.mark.parametrize("mode", ["multi_step", "prefill", "spec_device"])
+def test_barrier_failure_multi_token_persistent(mode, graphs):
+    """The same fallback for the persistent multi-token kernel (persistent=2), with its
+    launches direct or replayed from captured graphs: after the host raises the barrier
+    flag the engine switches to cooperative launches (graphs captured with plain
+    launches are dropped, cooperative launches are never captured) and recomputes, so
+    a multi-token step, a chunked prefill and a speculative generation driven on the
+    device all equal an undisturbed run's."""
+    path = synth_cached("eng-512", SMALL, 21)
+    V = SMALL["n_vocab"]
+    ids = minfer.prompt_ids(17, 20, V)
+    pat = minfer.prompt_ids(5, 6, V)
+    rep = (pat * 5)[:28]
+    opts = dict(max_ctx=128, persistent=2, graphs=graphs, spec=int(mode == "spec_device"))
+
+    def run(eng, flag):
+        if mode == "multi_step":
+            eng.prefill(ids)
+            toks = minfer.prompt_ids(3, 16, V)
+            eng.step(toks[:8], len(ids))             # the T = 8 graph is captured with a plain launch
+            if flag:
+                eng.debug_flag_barrier()
+            a, m = eng.step(toks[8:], len(ids) + 8)  # ... and replayed here
+            return a, m
+        if mode == "prefill":
+            if flag:
+                eng.prefill(ids[:9])                 # 8 + 1 tokens: captures the T = 8 launch
+                eng.debug_flag_barrier()
+            f, m = eng.prefill(ids)
+            return [f], [m]
+        eng.prefill(rep)
+        if flag:
+            eng.debug_flag_barrier()
+        return eng.generate(24)
+
+    ref = minfer.Engine(path, **opts)
+    want, wm = run(ref, False)
+    assert ref.refresh_info().coop == 0
+    ref.close()
+    say("multi-token barrier fallback via %s, graphs %d" % (mode, graphs))
+    eng = minfer.Engine(path, **opts)
+    got, gm = run(eng, True)
+    assert got == want
+    assert np.array_equal(np.float32(gm).view(np.uint32), np.float32(wm).view(np.uint32))
+    assert eng.refresh_info().coop == 1
+    eng.close()

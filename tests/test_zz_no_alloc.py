@@ -67,3 +67,37 @@ def test_noalloc_rejects_oversize(torch):
     with pytest.raises(minfer.MinferError) as ei:
         minfer.attn_decode_noalloc(q, kv, kv, nh, 4, hd, L, L, 0.1, out)
     assert ei.value.code == -4 and "scratch" in str(ei.value)
+
+
+def test_noalloc_graph_capture(torch):
+    """mi_attn_decode_noalloc captured into a HIP graph (after one eager call on the
+    device, which looks the scratch address up) and replayed three times, with other
+    eager work on the same scratch between the replays: every replay equals the eager
+    result bit for bit."""
+    rng = np.random.default_rng(5)
+    nh, nkv, hd, L = 12, 2, 128, 3000
+    ctx = L + 3
+    q = torch.from_numpy(rng.standard_normal((nh, hd)).astype(np.float32)).cuda()
+    kc = torch.from_numpy(rng.standard_normal((nkv, ctx, hd)).astype(np.float16).view(np.int16)).cuda()
+    vc = torch.from_numpy(rng.standard_normal((nkv, ctx, hd)).astype(np.float16).view(np.int16)).cuda()
+    scale = float(np.float32(1.0) / np.float32(math.sqrt(hd)))
+    eager = torch.full((nh * hd,), float("nan"), device="cuda")
+    minfer.attn_decode_noalloc(q, kc, vc, nh, nkv, hd, L, ctx, scale, eager)
+    torch.cuda.synchronize()
+    want = eager.cpu().numpy()
+    assert not np.isnan(want).any()
+    out = torch.full((nh * hd,), float("nan"), device="cuda")
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):                 # captured on torch's capture stream (the current one)
+        minfer.attn_decode_noalloc(q, kc, vc, nh, nkv, hd, L, ctx, scale, out)
+    other = torch.empty((nh * hd,), device="cuda")
+    for rep in range(3):
+        say("noalloc graph replay %d" % rep)
+        out.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        got = out.cpu().numpy()
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), rep
+        # eager work on the same scratch between replays (a smaller shape)
+        minfer.attn_decode_noalloc(q[:4].contiguous(), kc, vc, 4, nkv, hd, 500, ctx, scale, other[:4 * hd])
+        torch.cuda.synchronize()
