@@ -198,6 +198,37 @@ def verify_cost(reps=10):
                 note="T=8 = current token + 7 drafts (TMAX 8, mega.cu:50); the config's 8 drafts + 1 would be T=9")
 
 
+def verify_spec(n_gen=64):
+    """config4's drafter on its own shape: S3, a synthetic repetitive token stream of
+    1,000 tokens (a seeded 40-token pattern, 25 times) as the prompt, n_gen tokens by
+    speculative decoding (n-gram drafts verified by T <= 8 steps) driven by the host and
+    on the device, each checked token for token and margin for margin against plain
+    greedy decode. Reports verify steps, drafts, acceptances and tokens per step."""
+    shape, _, pseed, _, _ = minfer.CONFIGS["config4"]
+    path = ensure_gguf("config4")
+    V = minfer.SHAPES[shape]["n_vocab"]
+    import numpy as np
+    prompt = minfer.prompt_ids(pseed, 40, V) * 25
+    out = dict(workload="config4 drafter: S3, 1000-token repetitive prompt (40-token pattern x 25), %d generated" % n_gen)
+    ref = None
+    for mode, opts in (("plain", dict(spec=0)), ("host", dict(spec=1, persistent=1)), ("device", dict(spec=1, persistent=2))):
+        eng = minfer.Engine(path, max_ctx=len(prompt) + n_gen + 16, **opts)
+        eng.prefill(prompt)
+        toks, mg = eng.generate(n_gen)
+        st = eng.stats()
+        eng.close()
+        got = (toks, np.float32(mg).view(np.uint32).tolist())
+        if ref is None:
+            ref = got
+            out["plain_ms"] = round(st["decode_ms"], 3)
+            continue
+        assert got == ref, "speculative output differs from plain greedy decode (%s)" % mode
+        out[mode] = dict(ms=round(st["decode_ms"], 3), verify_steps=st["steps"], drafted=st["drafted"],
+                         accepted=st["accepted"], tokens_per_step=round(n_gen / max(st["steps"], 1), 3))
+    out["identical_to_plain"] = True
+    return out
+
+
 def attention_depth(torch, lengths=(512, 4096, 16384, 32768), layers=28, reps=3, graph=True, mfma=False):
     """config3: S15 split-KV decode attention (12/2 heads, hd 128), one query, fp16 K/V
     N(0,1) at context L, rotated over 28 layers' caches (28 x 32 MB at L = 32768 > the
@@ -305,9 +336,9 @@ def phase_profile(eng, stream_gbps):
     kinds = []
     for l in range(L):
         for k, name in enumerate(("qkv", "attn", "o", "gate_up", "down")):
-            exits.append(float(t[:, 1 + l * 25 + 5 * k + 4].min()))
+            exits.append(float(t[:, eng.prof_slot(l, k, 4)].min()))
             kinds.append(name)
-    exits.append(float(t[:, 1 + L * 25 + 4].min()))
+    exits.append(float(t[:, eng.prof_slot(L, 0, 4)].min()))
     kinds.append("lm_head")
     wb = phase_weight_bytes(eng.info)
     tot = {}
@@ -453,6 +484,7 @@ def main():
         spec["identical_to_plain"] = stoks == toks
         log("speculative decode: %s" % spec)
         verify = verify_cost()
+        verify["drafter"] = verify_spec()
         log("verify step: %s" % verify)
     cpu = None if args.no_cpu else cpu_baseline(path, prompt)
     if cpu:

@@ -175,14 +175,15 @@ int mi_time_phase(mi_engine* e, int32_t phase, int32_t layer, int32_t reps, doub
 
 /* In-kernel phase profile of one persistent step (the reference's PROFILE=1,
  * mega.cu:111-119, 1206-1224): reruns the last step once with every workgroup
- * stamping the device wall clock (100 MHz). With S = n_layer*25 + 6 slots and W =
- * the persistent grid (mi_model_info.n_cu workgroups), us[w*S + s] receives slot s
+ * stamping the device wall clock (100 MHz). With S = 1 + 8*(5*n_layer + 1) slots and
+ * W = the persistent grid (mi_model_info.n_cu workgroups), us[w*S + s] receives slot s
  * of workgroup w in microseconds since the earliest start, n >= W*S. Slots: 0 start;
- * then five per phase, for qkv, attention, o, gate/up and down of every layer and
+ * then eight per phase, for qkv, attention, o, gate/up and down of every layer and
  * finally lm_head: prologue end (inputs loaded, normalised and quantised), the
  * first worker wave's tiles done, its stores drained (lm_head: the workgroup's
- * argmax candidate written), phase end, barrier exit. Slots never stamped read as
- * 0 - earliest start. */
+ * argmax candidate written), phase end, barrier exit, the control wave's input
+ * staging landed, the first worker's staging landed (with its prefetched tiles), the
+ * residual add done (norm phases). Slots never stamped read as 0 - earliest start. */
 int mi_profile_step(mi_engine* e, double* us, int32_t n);
 
 /* Cost of a grid barrier of the persistent kernel: one cooperative launch of nwg
@@ -215,6 +216,15 @@ typedef struct mi_synth_shape {
  * uniform). No reference counterpart (the reference runs downloaded Qwen files,
  * README.md:58). */
 int mi_synth_gguf(const char* path, const mi_synth_shape* shape, uint64_t seed);
+
+/* Host-side bounds check of the step kernels' buffer indexing (no GPU needed). No
+ * counterpart in the reference: for a model shape, a context of max_ctx positions and a
+ * grid of n_cu workgroups, walks every index the single-token step (T = 1) or the
+ * multi-token phase bodies (T = 2..8) form for a step at pos, with each body's loop
+ * bounds, against the allocation sizes the engine uses. Returns MI_OK, MI_ERR_SHAPE with
+ * the buffer and index in err, or MI_ERR_ARG. */
+int mi_check_layout(const mi_synth_shape* shape, int32_t max_ctx, int32_t n_cu, int32_t T, int32_t pos, char* err,
+                    int32_t errlen);
 
 /* ---------------- kernel-level entry points (device pointers) ----------------
  * For the microbenchmarks and bit-exact parity tests. `stream` is a hipStream_t

@@ -10,6 +10,7 @@
 #include "common.hpp"
 #include "gguf.hpp"
 #include "kernels.hpp"
+#include "layout.hpp"
 #include "minfer.h"
 
 #include <algorithm>
@@ -306,6 +307,19 @@ static int alloc_buf(mi_engine* e, T** p, size_t count) {
     return rc;
 }
 
+// the buffer-layout facts of a model shape (layout.hpp)
+static Dims step_dims(int NL, int E, int FF, int NH, int NKV, int V, int maxseq, const int ks[5], int nwg) {
+    Dims d{};
+    d.NL = NL; d.E = E; d.FF = FF; d.NH = NH; d.NKV = NKV; d.HD = E / NH; d.V = V;
+    d.QKV = NH * d.HD + 2 * NKV * d.HD;
+    d.maxseq = maxseq;
+    d.maxch = (maxseq + kAttnChunk - 1) / kAttnChunk;
+    d.arec = attn_record_floats(d.HD);
+    d.ks_qkv = ks[0]; d.ks_o = ks[1]; d.ks_d = ks[3];
+    d.nwg = nwg;
+    return d;
+}
+
 static int load_impl(mi_engine* e, const char* path) {
     int ndev = 0;
     if (hipGetDeviceCount(&ndev) != hipSuccess || ndev <= e->opts.device)
@@ -462,7 +476,6 @@ static int load_impl(mi_engine* e, const char* path) {
     if (rc) return rc;
     HIPCHK(e, hipMemcpy(e->d_layers, layers.data(), layers.size() * sizeof(DLayer), hipMemcpyHostToDevice));
     M.layers = e->d_layers;
-    const size_t kvn = (size_t)e->NL * e->NKV * e->maxseq * e->HD;
     if (e->opts.persistent) {
         int coop = 0;
         HIPCHK(e, hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, e->opts.device));
@@ -475,30 +488,30 @@ static int load_impl(mi_engine* e, const char* path) {
     }
     M.arec = attn_record_floats(e->HD);
     const size_t NL = (size_t)e->NL;
-    if ((rc = alloc_buf(e, &M.kc, kvn)) || (rc = alloc_buf(e, &M.vc, kvn)) ||
+    const Dims D = step_dims(e->NL, e->E, e->FF, e->NH, e->NKV, e->V, e->maxseq, e->ks, e->n_cu);
+    if ((rc = alloc_buf(e, &M.kc, lay::kv_size(D))) || (rc = alloc_buf(e, &M.vc, lay::kv_size(D))) ||
         (rc = alloc_buf(e, &M.tokbuf, (size_t)e->maxseq + 1)) ||
-        (rc = alloc_buf(e, &M.hbuf, (size_t)(2 * e->NL + 1) * e->E)) ||
-        (rc = alloc_buf(e, &M.qkv_part, NL * e->ks[0] * e->QKV)) ||
-        (rc = alloc_buf(e, &M.att, NL * e->NH * e->maxch * M.arec)) ||
+        (rc = alloc_buf(e, &M.hbuf, lay::hbuf_size(D))) ||
+        (rc = alloc_buf(e, &M.qkv_part, lay::qkv_part_size(D))) ||
+        (rc = alloc_buf(e, &M.att, lay::att_size(D))) ||
         (rc = alloc_buf(e, &M.att_out, NL * e->E)) ||
-        (rc = alloc_buf(e, &M.o_part, NL * e->ks[1] * e->E)) ||
-        (rc = alloc_buf(e, &M.act, NL * (e->FF / 32) * kActRec)) ||
-        (rc = alloc_buf(e, &M.d_part, NL * e->ks[3] * e->E)) ||
+        (rc = alloc_buf(e, &M.o_part, lay::o_part_size(D))) ||
+        (rc = alloc_buf(e, &M.act, lay::act_size(D))) ||
+        (rc = alloc_buf(e, &M.d_part, lay::d_part_size(D))) ||
         (rc = alloc_buf(e, &M.cand, (size_t)e->n_cu * 32)) ||
         (rc = alloc_buf(e, &M.bar, (size_t)barrier_words())) || (rc = alloc_buf(e, &M.err, 64)) ||
         (rc = alloc_buf(e, &M.out_tok, (size_t)e->maxseq)) ||
         (rc = alloc_buf(e, &M.out_margin, (size_t)e->maxseq)))
         return rc;
     // multi-token step buffers (mi_step with T > 1)
-    const size_t TM = kMaxT;
-    if ((rc = alloc_buf(e, &M.posT, 1)) || (rc = alloc_buf(e, &M.hT, (size_t)(2 * e->NL + 1) * TM * e->E)) ||
-        (rc = alloc_buf(e, &M.qkvT, NL * e->ks[0] * TM * e->QKV)) ||
-        (rc = alloc_buf(e, &M.attT, NL * TM * e->NH * e->maxch * M.arec)) ||
-        (rc = alloc_buf(e, &M.xT, (3 * NL + 1) * TM * (e->E / 32) * kTRec)) ||
-        (rc = alloc_buf(e, &M.oT, NL * e->ks[1] * TM * e->E)) ||
-        (rc = alloc_buf(e, &M.actT, NL * TM * (e->FF / 32) * kActRec)) ||
-        (rc = alloc_buf(e, &M.dT, NL * e->ks[3] * TM * e->E)) ||
-        (rc = alloc_buf(e, &M.candT, (size_t)e->n_cu * TM * 4)) || (rc = alloc_buf(e, &M.spec, 1)))
+    if ((rc = alloc_buf(e, &M.posT, 1)) || (rc = alloc_buf(e, &M.hT, lay::hT_size(D))) ||
+        (rc = alloc_buf(e, &M.qkvT, lay::qkvT_size(D))) ||
+        (rc = alloc_buf(e, &M.attT, lay::attT_size(D))) ||
+        (rc = alloc_buf(e, &M.xT, lay::xT_size(D))) ||
+        (rc = alloc_buf(e, &M.oT, lay::oT_size(D))) ||
+        (rc = alloc_buf(e, &M.actT, lay::actT_size(D))) ||
+        (rc = alloc_buf(e, &M.dT, lay::dT_size(D))) ||
+        (rc = alloc_buf(e, &M.candT, lay::candT_size(D))) || (rc = alloc_buf(e, &M.spec, 1)))
         return rc;
     M.logits = nullptr;
     M.logitsT = nullptr;
@@ -514,7 +527,7 @@ static int load_impl(mi_engine* e, const char* path) {
     M.eos = e->opts.stop_eos ? e->eos : -1;
     e->M_logits = M;
     if ((rc = alloc_buf(e, &e->M_logits.logits, (size_t)e->V))) return rc;
-    if ((rc = alloc_buf(e, &e->M_logits.logitsT, TM * e->V))) return rc;
+    if ((rc = alloc_buf(e, &e->M_logits.logitsT, lay::logitsT_size(D)))) return rc;
     if ((rc = alloc_buf(e, &e->dM, 3))) return rc;
     HIPCHK(e, hipMemcpy(e->dM, &e->M, sizeof(DModel), hipMemcpyHostToDevice));
     HIPCHK(e, hipMemcpy(e->dM + 1, &e->M_logits, sizeof(DModel), hipMemcpyHostToDevice));
@@ -557,6 +570,112 @@ int mi_info(const mi_engine* e, mi_model_info* o) {
     o->persistent = e->nwg_persistent > 0;
     o->weight_bytes = e->weight_bytes;
     o->coop = e->coop ? 1 : 0;
+    return MI_OK;
+}
+
+// Host-side walk over every buffer index the step kernels form for one step of T
+// tokens at pos (T = 1: the single-token step; T > 1: the multi-token phase bodies),
+// with the loop bounds of each body, checked against the allocation sizes (layout.hpp).
+int mi_check_layout(const mi_synth_shape* sh, int32_t max_ctx, int32_t n_cu, int32_t T, int32_t pos, char* err,
+                    int32_t errlen) {
+    auto fail = [&](const char* fmt, ...) {
+        if (err && errlen > 0) {
+            va_list ap;
+            va_start(ap, fmt);
+            vsnprintf(err, (size_t)errlen, fmt, ap);
+            va_end(ap);
+        }
+        return MI_ERR_SHAPE;
+    };
+    if (!sh || max_ctx < 1 || n_cu < 1 || T < 1 || T > kMaxT || pos < 0) return MI_ERR_ARG;
+    const int NL = sh->n_layer, E = sh->n_embd, FF = sh->n_ff, NH = sh->n_head, NKV = sh->n_head_kv, V = sh->n_vocab;
+    if (NL < 1 || NH < 1 || NKV < 1 || E % NH || NH % NKV || E % 64 || FF % 64 || V % 64) return MI_ERR_ARG;
+    int cb[5], ks[5];
+    if (!kernels_plan(E, FF, cb, ks)) return fail("no plan for E=%d FF=%d", E, FF);
+    const Dims D = step_dims(NL, E, FF, NH, NKV, V, max_ctx, ks, n_cu);
+    const int HD = D.HD, G = NH / NKV, QKV = D.QKV, KVD = NKV * HD, nbE = E / 32, nbF = FF / 32;
+    if (pos + T > D.maxseq) return fail("positions %d..%d past the context %d (the engine rejects the step)", pos,
+                                        pos + T - 1, D.maxseq);
+    // every (buffer, element) formed below must lie inside the buffer
+    auto in = [&](const char* buf, size_t idx, size_t size) { return idx < size ? 0 : 1; };
+    int bad = 0;
+    const char* what = "";
+    size_t at = 0, lim = 0;
+    auto chk = [&](const char* buf, size_t idx, size_t size) {
+        if (!bad && in(buf, idx, size)) { bad = 1; what = buf; at = idx; lim = size; }
+    };
+    // GEMM outputs: segment t = g * ks + s (tseg), rows g * 64 + lane, tokens < T
+    auto gemm_out = [&](const char* buf, size_t base, int rows, int kseg, size_t size) {
+        for (int t = 0; t < (rows / 64) * kseg; t++) {
+            const int g = t / kseg, sg = t % kseg;
+            for (int tok = 0; tok < T; tok++)
+                chk(buf, base + ((size_t)sg * (T > 1 ? kMaxT : 1) + (T > 1 ? tok : 0)) * rows + g * 64 + 63, size);
+        }
+    };
+    const int nch = (pos + T - 1 + kAttnChunk) / kAttnChunk;      // chunks of the last token's context
+    if (nch > D.maxch) return fail("%d attention chunks > maxch %d", nch, D.maxch);
+    for (int l = 0; l < NL; l++) {
+        // K/V rows appended and read: positions 0 .. pos + T - 1 of every kv head
+        for (int kvh = 0; kvh < NKV; kvh++) chk("kc/vc", lay::kv(NKV, D.maxseq, HD, l, kvh, pos + T - 1) + HD - 1, lay::kv_size(D));
+        if (T == 1) {
+            gemm_out("qkv_part", lay::qkv_part(ks[0], QKV, l), QKV, ks[0], lay::qkv_part_size(D));
+            for (int h = 0; h < NH; h++)
+                for (int c = 0; c < nch; c++) chk("att", lay::att(NH, D.maxch, D.arec, l) + (size_t)(h * D.maxch + c) * D.arec + HD + 1, lay::att_size(D));
+            gemm_out("o_part", lay::o_part(ks[1], E, l), E, ks[1], lay::o_part_size(D));
+            for (int g = 0; g < FF / 32; g++) chk("act", lay::act(FF, l) + (size_t)g * kActRec + 39, lay::act_size(D));
+            gemm_out("d_part", lay::d_part(ks[3], E, l), E, ks[3], lay::d_part_size(D));
+            continue;
+        }
+        // kT_in (qkv and gate/up inputs): residual rows of hT, the int8 records in xT
+        for (int t = 0; t < T; t++) {
+            chk("hT", lay::hT(E, 2 * l, t) + E - 1, lay::hT_size(D));
+            chk("hT", lay::hT(E, 2 * l + 1, t) + E - 1, lay::hT_size(D));
+            for (int w : {lay::kXtQkv, lay::kXtO, lay::kXtGu})
+                chk("xT", lay::xT(E, lay::xt_slot(NL, l, w)) + ((size_t)t * nbE + nbE - 1) * kTRec + kTRec - 1, lay::xT_size(D));
+            for (int sg = 0; sg < ks[3]; sg++)
+                chk("dT", lay::dT(ks[3], E, l) + ((size_t)sg * kMaxT + t) * E + E - 1, lay::dT_size(D));
+            for (int sg = 0; sg < ks[1]; sg++)
+                chk("oT", lay::oT(ks[1], E, l) + ((size_t)sg * kMaxT + t) * E + E - 1, lay::oT_size(D));
+        }
+        gemm_out("qkvT", lay::qkvT(ks[0], QKV, l), QKV, ks[0], lay::qkvT_size(D));
+        // kT_attn items (kv head, chunk, token group) and the q/k/v rows they read
+        int tg = 1;
+        while (tg < T && NKV * nch * ((T + tg - 1) / tg) > n_cu) tg *= 2;
+        const int ngrp = (T + tg - 1) / tg;
+        for (int it = 0; it < NKV * nch * ngrp; it++) {
+            const int grp = it % ngrp, rest = it / ngrp, c = rest % nch, kvh = rest / nch;
+            const int ta = grp * tg, tb = std::min(T, ta + tg) - 1, t0 = c * kAttnChunk;
+            if (t0 > pos + tb) continue;
+            for (int t = ta; t <= tb; t++)
+                for (int hh = 0; hh < G; hh++) {
+                    const int h = kvh * G + hh;
+                    for (int sg = 0; sg < ks[0]; sg++)
+                        chk("qkvT", lay::qkvT(ks[0], QKV, l) + ((size_t)sg * kMaxT + t) * QKV + NH * HD + KVD + kvh * HD + HD - 1, lay::qkvT_size(D));
+                    if (t0 <= pos + t)
+                        chk("attT", lay::attT(NH, D.maxch, D.arec, l, t) + (size_t)(h * D.maxch + c) * D.arec + HD + 1, lay::attT_size(D));
+                }
+        }
+        // kT_comb: token t merges its chunks 0 .. (pos + t) / 64
+        for (int t = 0; t < T; t++)
+            for (int h = 0; h < NH; h++) {
+                const int nct = (pos + t + kAttnChunk) / kAttnChunk;
+                chk("attT", lay::attT(NH, D.maxch, D.arec, l, t) + (size_t)(h * D.maxch + nct - 1) * D.arec + HD + 1, lay::attT_size(D));
+            }
+        gemm_out("oT", lay::oT(ks[1], E, l), E, ks[1], lay::oT_size(D));
+        for (int t = 0; t < T; t++)
+            for (int g = 0; g < FF / 32; g++) chk("actT", lay::actT(FF, l, t) + (size_t)g * kActRec + 39, lay::actT_size(D));
+        for (int t = 0; t < T; t++) chk("actT", lay::actT(FF, l, t) + (size_t)(nbF - 1) * kActRec + kTRec - 1, lay::actT_size(D));
+        gemm_out("dT", lay::dT(ks[3], E, l), E, ks[3], lay::dT_size(D));
+    }
+    if (T > 1) {
+        for (int t = 0; t < T; t++) {
+            chk("hT", lay::hT(E, 2 * (NL - 1) + 1, t) + E - 1, lay::hT_size(D));
+            chk("xT", lay::xT(E, lay::xt_slot(NL, NL, 0)) + ((size_t)t * nbE + nbE - 1) * kTRec + kTRec - 1, lay::xT_size(D));
+            chk("logitsT", (size_t)t * V + V - 1, lay::logitsT_size(D));
+            for (int w = 0; w < n_cu; w++) chk("candT", lay::candT(w, t) + 3, lay::candT_size(D));
+        }
+    }
+    if (bad) return fail("%s index %zu outside its %zu elements (T=%d pos=%d)", what, at, lim, T, pos);
     return MI_OK;
 }
 

@@ -36,6 +36,7 @@
 // prologue loads in a wave that never prefetches is what lets them overlap.
 #include "common.hpp"
 #include "kernels.hpp"
+#include "layout.hpp"
 
 #include <algorithm>
 #include <climits>
@@ -533,11 +534,11 @@ __device__ __forceinline__ void ctl_exit(uint32_t* bar) {
 // ------------------------------------------------------------------ per-layer buffers
 __device__ __forceinline__ size_t hin(int l, int E) { return (size_t)(2 * l) * E; }
 __device__ __forceinline__ size_t hmid(int l, int E) { return (size_t)(2 * l + 1) * E; }
-__device__ __forceinline__ float* qkv_part(MPtr M, int l) { return M->qkv_part + (size_t)l * LY(M, 0)->qkv.ks * M->QKV; }
-__device__ __forceinline__ float* o_part(MPtr M, int l) { return M->o_part + (size_t)l * LY(M, 0)->o.ks * M->E; }
-__device__ __forceinline__ float* d_part(MPtr M, int l) { return M->d_part + (size_t)l * LY(M, 0)->d.ks * M->E; }
-__device__ __forceinline__ float* att_rec(MPtr M, int l) { return M->att + (size_t)l * M->NH * M->maxch * M->arec; }
-__device__ __forceinline__ uint8_t* act_rec(MPtr M, int l) { return M->act + (size_t)l * (M->FF / 32) * kActRec; }
+__device__ __forceinline__ float* qkv_part(MPtr M, int l) { return M->qkv_part + lay::qkv_part(LY(M, 0)->qkv.ks, M->QKV, l); }
+__device__ __forceinline__ float* o_part(MPtr M, int l) { return M->o_part + lay::o_part(LY(M, 0)->o.ks, M->E, l); }
+__device__ __forceinline__ float* d_part(MPtr M, int l) { return M->d_part + lay::d_part(LY(M, 0)->d.ks, M->E, l); }
+__device__ __forceinline__ float* att_rec(MPtr M, int l) { return M->att + lay::att(M->NH, M->maxch, M->arec, l); }
+__device__ __forceinline__ uint8_t* act_rec(MPtr M, int l) { return M->act + lay::act(M->FF, l); }
 
 // device wall clock (100 MHz) of one profile slot, one row per workgroup, written by
 // thread `who` (0: the control wave, 64: the first worker)
@@ -545,6 +546,14 @@ __device__ __forceinline__ void stamp(MPtr M, int slot, int who = 0) {
     if (threadIdx.x == who && M->prof)
         M->prof[(size_t)blockIdx.x * prof_slots(M->NL) + slot] = __builtin_amdgcn_s_memrealtime();
 }
+// Stamps inside a phase's prologue (profile slots 5-7 of a phase) cost the step ~2% even
+// when it is not profiled (code placement in the phase loop): built only with
+// -DMI_PROFILE_FINE; the default build leaves those slots at 0.
+#ifdef MI_PROFILE_FINE
+#define FINE_STAMP(...) stamp(__VA_ARGS__)
+#else
+#define FINE_STAMP(...) ((void)0)
+#endif
 
 // ------------------------------------------------------------------ control-wave prologues
 // the phases of a layer, then lm_head
@@ -672,7 +681,7 @@ __device__ __forceinline__ void ctl_stage(MPtr M, int l, int kind, int pos, cons
 
 // all waves: the phase input records X from the staged data (see ctl_stage)
 __device__ __forceinline__ void wg_prologue(MPtr M, int l, int kind, int pos, int wg, const Lds& S, int wave,
-                                            int lane, bool resident) {
+                                            int lane, bool resident, int slot = -1) {
     const int n = M->E, e0 = 256 * wave + 4 * lane;
     const bool has = 256 * wave < n, own = e0 < n;
     if (kind == PH_O) {
@@ -732,6 +741,7 @@ __device__ __forceinline__ void wg_prologue(MPtr M, int l, int kind, int pos, in
         stc(dst, x.x); stc(dst + 1, x.y); stc(dst + 2, x.z); stc(dst + 3, x.w);
     }
     __syncthreads();
+    if (slot >= 0) FINE_STAMP(M, slot);
     const float sc = rms_scale(h, n, M->eps, lane);
     if (!has) return;
     float4 y = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -1052,7 +1062,7 @@ __device__ __forceinline__ void attn_core_h(const uint4* kls, const float* qs, i
 template <int HD>
 __device__ __forceinline__ void attn_issue_unit(MPtr M, int l, int pos, int u, int nch, uint8_t* U, int wave, int lane) {
     const int kvh = u / nch, t0 = (u - kvh * nch) * kAttnChunk, n = min(kAttnChunk, pos + 1 - t0);
-    const size_t rowbase = ((size_t)l * M->NKV + kvh) * M->maxseq + t0;
+    const size_t rowbase = lay::kv(M->NKV, M->maxseq, 1, l, kvh, t0);
     // the tile address through a VGPR: with a uniform (SGPR) generic pointer, the LDS
     // cast's aperture check hits an instruction-selection error in this compiler; and an
     // opaque lane, so the DMA addresses are not hoisted out of the step's phase loop
@@ -1084,7 +1094,7 @@ __device__ __forceinline__ void attn_finish(MPtr M, int l, int pos, int h, int c
     const int n = min(kAttnChunk, L - t0);
     const bool last = c == nch - 1;
     const int cur = last ? pos - t0 : -1;
-    const size_t rowbase = ((size_t)l * M->NKV + kvh) * M->maxseq;
+    const size_t rowbase = lay::kv(M->NKV, M->maxseq, 1, l, kvh, 0);
     const float* part = qkv_part(M, l);
     const int rq = h * HD, rk = M->NH * HD + kvh * HD, rv = M->NH * HD + M->KVD + kvh * HD;
     // bias and RoPE table values are loaded in the same batch as the partials
@@ -1337,10 +1347,12 @@ __device__ __forceinline__ void phase_comb(MPtr M, int l, int pos, int wg, int n
 // Per phase: [all waves: staging DMA shares] sync [prologue] sync [workers: tiles]
 // sync [workers: segment sums, stores, store drain] sync [control: grid barrier |
 // workers: next phase's prefetch] sync.
-// Profile slots (every workgroup): 0 = start; then five per phase in the sequence
-// (qkv, attention, o, gate/up, down per layer, then lm_head): prologue end, first
-// worker's tiles done, its stores drained (lm: the control wave's candidate
-// written), phase end, barrier exit.
+// Profile slots (every workgroup): 0 = start; then kProfPerPhase per phase in the
+// sequence (qkv, attention, o, gate/up, down per layer, then lm_head): prologue end,
+// first worker's tiles done, its stores drained (lm: the control wave's candidate
+// written), phase end, barrier exit; with MI_PROFILE_FINE also the control wave's
+// staging landed, the first worker's staging landed (with its prefetched tiles), the
+// residual add done (norm phases).
 __device__ __forceinline__ PMat phase_mat(MPtr M, int l, int kind) {
     if (kind == PH_LM) return ldmat(&M->lm);
     const LPtr L = LY(M, l);
@@ -1411,11 +1423,16 @@ __global__ __launch_bounds__(kPThreads) void k_step(const DModel* Mp, int pos, i
     Tile tl[2];
     stamp(M, 0);
     stage(M, 0, PH_QKV, pos, S, wave, kPWaves, lane, true);
+    FINE_STAMP(M, 1 + 5);
     if (!ctl) phase_prefetch(M, 0, PH_QKV, wg, nwg, kw, tl, lane);
     int l = 0, kind = PH_QKV;
-    for (int sb = 1;; sb += 5) {
+    for (int sb = 1;; sb += kProfPerPhase) {
         __syncthreads();
+#ifdef MI_PROFILE_FINE
+        if (!phase_idle(M, l, kind, wg, nwg)) wg_prologue(M, l, kind, pos, wg, S, wave, lane, true, M->prof ? sb + 7 : -1);
+#else
         if (!phase_idle(M, l, kind, wg, nwg)) wg_prologue(M, l, kind, pos, wg, S, wave, lane, true);
+#endif
         __syncthreads();
         stamp(M, sb);
         if (kind == PH_ATTN) {
@@ -1481,6 +1498,8 @@ __global__ __launch_bounds__(kPThreads) void k_step(const DModel* Mp, int pos, i
         __syncthreads();
         if (!phase_idle(M, nl, nk, wg, nwg)) stage(M, nl, nk, pos, S, wave, kPWaves, lane, true);
         else drain_vm();
+        FINE_STAMP(M, sb + kProfPerPhase + 5);           // this wave's staging landed (control, first worker)
+        FINE_STAMP(M, sb + kProfPerPhase + 6, 64);
         l = nl;
         kind = nk;
     }
@@ -1613,7 +1632,7 @@ constexpr int kTDownLds = kTXfBytes + kTPBytes;    // down
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 
-__device__ __forceinline__ size_t hT_at(MPtr M, int slot, int t) { return ((size_t)slot * kMaxT + t) * M->E; }
+__device__ __forceinline__ size_t hT_at(MPtr M, int slot, int t) { return lay::hT(M->E, slot, t); }
 __device__ __forceinline__ float4 ldg4(const float* p) { return *reinterpret_cast<const float4*>(p); }
 __device__ __forceinline__ uint2 ntload8(const uint8_t* p) {
     const u32x2 v = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(p));
@@ -1804,11 +1823,12 @@ __device__ __forceinline__ int opaque_tid() {
     return t;
 }
 // The GEMM inputs' int8 records, one slot per (layer, input) so that every line is
-// written once per step (the persistent step reads them with plain loads): slot 3l is
-// layer l's qkv input, 3l + 1 its o input, 3l + 2 its gate/up input, 3 NL lm_head's.
-constexpr int kXtQkv = 0, kXtO = 1, kXtGu = 2;
-__device__ __forceinline__ int xt_slot(MPtr M, int l, int which) { return l < M->NL ? 3 * l + which : 3 * M->NL; }
-__device__ __forceinline__ uint8_t* xT_at(MPtr M, int slot) { return M->xT + (size_t)slot * kMaxT * (M->E / 32) * kTRec; }
+// written once per step (the persistent step reads them with plain loads; layout.hpp)
+using lay::kXtQkv;
+using lay::kXtO;
+using lay::kXtGu;
+__device__ __forceinline__ int xt_slot(MPtr M, int l, int which) { return lay::xt_slot(M->NL, l, which); }
+__device__ __forceinline__ uint8_t* xT_at(MPtr M, int slot) { return M->xT + lay::xT(M->E, slot); }
 // T tokens' records of an E-wide GEMM input: its xT slot -> LDS (all threads)
 __device__ __forceinline__ void tstage_x(MPtr M, int slot, int T, uint8_t* XT) {
     const int n8 = T * (M->E / 32) * (kTRec / 8);
@@ -1875,15 +1895,11 @@ __global__ __launch_bounds__(kPThreads) void kT_in(const DModel* Mp, int l, int 
     kT_in_body<false>((MPtr)Mp, l, kind, blockIdx.x, x, *((MPtr)Mp)->posT);
 }
 
-__device__ __forceinline__ float* qkvT_at(MPtr M, int l) { return M->qkvT + (size_t)l * LY(M, 0)->qkv.ks * kMaxT * M->QKV; }
-__device__ __forceinline__ float* oT_at(MPtr M, int l) { return M->oT + (size_t)l * LY(M, 0)->o.ks * kMaxT * M->E; }
-__device__ __forceinline__ float* dT_at(MPtr M, int l) { return M->dT + (size_t)l * LY(M, 0)->d.ks * kMaxT * M->E; }
-__device__ __forceinline__ float* attT_at(MPtr M, int l, int t) {
-    return M->attT + ((size_t)l * kMaxT + t) * M->NH * M->maxch * M->arec;
-}
-__device__ __forceinline__ uint8_t* actT_at(MPtr M, int l, int t) {
-    return M->actT + ((size_t)l * kMaxT + t) * (M->FF / 32) * kActRec;
-}
+__device__ __forceinline__ float* qkvT_at(MPtr M, int l) { return M->qkvT + lay::qkvT(LY(M, 0)->qkv.ks, M->QKV, l); }
+__device__ __forceinline__ float* oT_at(MPtr M, int l) { return M->oT + lay::oT(LY(M, 0)->o.ks, M->E, l); }
+__device__ __forceinline__ float* dT_at(MPtr M, int l) { return M->dT + lay::dT(LY(M, 0)->d.ks, M->E, l); }
+__device__ __forceinline__ float* attT_at(MPtr M, int l, int t) { return M->attT + lay::attT(M->NH, M->maxch, M->arec, l, t); }
+__device__ __forceinline__ uint8_t* actT_at(MPtr M, int l, int t) { return M->actT + lay::actT(M->FF, l, t); }
 
 // The phase bodies take the workgroup's LDS, its index and the grid size; P selects the
 // stores (and xT loads) for phases that run inside one persistent launch (kT_step).
@@ -1954,7 +1970,7 @@ __device__ __forceinline__ void kT_attn_body(MPtr M, int l, int T, uint8_t* smem
         const int ta = grp * tg, tb = min(T, ta + tg) - 1, t0 = c * kAttnChunk;
         if (t0 > pos + tb) continue;                               // uniform over the workgroup
         const int ncached = min(kAttnChunk, max(0, pos - t0));
-        const size_t rowbase = ((size_t)l * NKV + kvh) * M->maxseq;
+        const size_t rowbase = lay::kv(NKV, M->maxseq, 1, l, kvh, 0);     // row index of position 0
         if (wave == 0 && ncached > 0)
             attn_issue_kv<HD>(M->kc + rowbase * HD, M->vc + rowbase * HD, t0, ncached, kls, vls, lane);
         // this step's row pos + wave, if the chunk holds it and a token of the group sees it
@@ -2138,7 +2154,7 @@ __device__ __forceinline__ void kT_lm_body(MPtr M, int T, uint8_t* smem, int wg,
     if (wave < T) {
         top2_wave(tp);
         if (lane == 0) {
-            float* cd = M->candT + ((size_t)wg * kMaxT + wave) * 4;
+            float* cd = M->candT + lay::candT(wg, wave);
             st_x<PS>(cd, tp.best);
             st_x<PS>(reinterpret_cast<uint32_t*>(cd + 1), (uint32_t)tp.idx);
             st_x<PS>(cd + 2, tp.second);
@@ -2154,7 +2170,7 @@ __device__ __forceinline__ void kT_argmax_body(MPtr M, int ncand, int T, int pos
     if (wave >= T) return;
     Top2 tp{-__builtin_inff(), INT_MAX, -__builtin_inff()};
     for (int i = lane; i < ncand; i += 64) {
-        const float* cd = M->candT + ((size_t)i * kMaxT + wave) * 4;
+        const float* cd = M->candT + lay::candT(i, wave);
         top2_merge(tp, cd[0], __float_as_int(cd[1]), cd[2]);
     }
     top2_wave(tp);

@@ -45,9 +45,8 @@ int persistent_max_grid(int G, int HD);
 hipError_t launch_barriers(uint32_t* bar, int32_t* err, int nwg, int n, hipStream_t s);
 int barrier_words();        // uint32 words the grid barrier uses
 int attn_record_floats(int HD);   // floats per attention chunk record
-constexpr int kProfSlotsPerLayer = 25;
-// profile slots of one workgroup: start, 5 per phase (5 phases per layer, then lm_head)
-constexpr int prof_slots(int n_layer) { return n_layer * kProfSlotsPerLayer + 6; }
+constexpr int kProfPerPhase = 8;
+constexpr int prof_slots(int n_layer) { return 1 + (5 * n_layer + 1) * kProfPerPhase; }
 
 // one phase kernel of the step at pos: 0 qkv, 1 attention, 2 chunk merge (only
 // launched past kInlineComb chunks), 3 o, 4 gate/up+act, 5 down, 6 lm_head, 7 argmax

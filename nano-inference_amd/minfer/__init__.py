@@ -73,6 +73,8 @@ SIGNATURES = {
     "mi_barrier_cost": (C.c_int, [C.c_int32, C.c_int32, C.POINTER(C.c_double)]),
     "mi_debug_flag_barrier": (C.c_int, [_P]),
     "mi_synth_gguf": (C.c_int, [C.c_char_p, C.POINTER(SynthShape), C.c_uint64]),
+    "mi_check_layout": (C.c_int, [C.POINTER(SynthShape), C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_char_p,
+                                  C.c_int32]),
     "mi_q4_packed_bytes": (C.c_size_t, [C.c_int32, C.c_int32, C.c_int32]),
     "mi_q4_pack": (C.c_int, [_P, C.c_int32, C.c_int32, C.c_int32, _P]),
     "mi_quant_q8": (C.c_int, [_P, C.c_int32, _P, _P, _P, _P]),
@@ -144,6 +146,16 @@ def synth_gguf(path, shape, seed, rope_base=1e6, rms_eps=1e-6, emb_q4=False, emb
                    rope_base, rms_eps, et, head_type, down_type, 1 if tied else 0, qk_bias_std, norm_offset)
     _check(lib().mi_synth_gguf(path.encode(), C.byref(s), C.c_uint64(seed)))
     return path
+
+
+def check_layout(shape, max_ctx, n_cu, T, pos):
+    """mi_check_layout (host only): (status, message) of the bounds walk of one step"""
+    d = SHAPES[shape] if isinstance(shape, str) else shape
+    s = SynthShape(d["n_layer"], d["n_embd"], d["n_ff"], d["n_head"], d["n_head_kv"], d["n_vocab"],
+                   1e6, 1e-6, 0, 0, 0, 0, 0.0, 0.0)
+    buf = C.create_string_buffer(256)
+    rc = lib().mi_check_layout(C.byref(s), max_ctx, n_cu, T, pos, buf, 256)
+    return rc, buf.value.decode()
 
 
 def pred_hash(pred, margin):
@@ -259,12 +271,18 @@ class Engine:
         return ms.value
 
     PROFILE_PHASES = ["qkv", "attn", "o", "gate_up", "down"]
+    PROF_PER_PHASE = 8
+
+    @classmethod
+    def prof_slot(cls, layer, kind, j):
+        """column of stamp j of phase `kind` (0..4; kind 0 of layer n_layer = lm_head)"""
+        return 1 + (5 * layer + kind) * cls.PROF_PER_PHASE + j
 
     def profile_step(self):
-        """Stamps of one persistent step: an array [workgroups][n_layer*25 + 6] of
+        """Stamps of one persistent step: an array [workgroups][1 + 8*(5*n_layer + 1)] of
         microseconds since the earliest start (slot layout in mi_profile_step)."""
         import numpy as np
-        nslot = self.info.n_layer * 25 + 6
+        nslot = 1 + (5 * self.info.n_layer + 1) * self.PROF_PER_PHASE
         n = nslot * self.info.n_cu
         buf = (C.c_double * n)()
         _check(lib().mi_profile_step(self._h, buf, n), self._h)
@@ -284,14 +302,15 @@ class Engine:
             for j, part in enumerate(parts):
                 acc = np.zeros(t.shape[0])
                 for l in range(L):
-                    s = 1 + l * 25 + 5 * k + j
-                    acc += t[:, s] - t[:, s - 1]
+                    s = self.prof_slot(l, k, j)
+                    prev = s - 1 if j else self.prof_slot(l, k, 0) - self.PROF_PER_PHASE + 4
+                    acc += t[:, s] - t[:, prev] if (l, k) != (0, 0) or j else t[:, s] - t[:, 0]
                 out[ph + "_" + part] = (round(float(acc.mean()), 1), round(float(acc.max()), 1))
-            ends = [1 + l * 25 + 5 * k + 3 for l in range(L)]
+            ends = [self.prof_slot(l, k, 3) for l in range(L)]
             out[ph + "_barrier"] = round(float(sum(t[:, e + 1].min() - t[:, e].max() for e in ends)), 1)
-        s0 = 1 + L * 25
+        s0 = self.prof_slot(L, 0, 0)
         for j, part in enumerate(("lm_prep", "lm_tiles", "lm_cand", "lm_sync", "lm_wait")):
-            v = t[:, s0 + j] - t[:, s0 + j - 1]
+            v = t[:, s0 + j] - t[:, s0 + j - 1 if j else s0 - self.PROF_PER_PHASE + 4]
             out[part] = (round(float(v.mean()), 1), round(float(v.max()), 1))
         out["total"] = round(float(t[:, -1].max()), 1)
         return out

@@ -528,3 +528,42 @@ def test_barrier_failure_multi_token_persistent(mode, graphs):
     assert np.array_equal(np.float32(gm).view(np.uint32), np.float32(wm).view(np.uint32))
     assert eng.refresh_info().coop == 1
     eng.close()
+
+
+@pytest.mark.parametrize("kind", ["per_phase", "persistent", "multi_phases", "multi_persistent", "spec_host",
+                                  "spec_device"])
+def test_exact_argmax_ties_first_row(tmpdir_mi, kind):
+    """Exact logit ties in every step kind: output.weight rows i, j identical and k, m
+    their exact negation, every other row zero (conftest.tie_head_gguf), so each position's
+    top two logits are equal. The emitted token is the first row of the winning pair
+    (lowest index, cpu_infer.cpp:153-154; mega.cu:384-386) with margin 0, equal to the
+    q8act oracle's."""
+    from conftest import tie_head_gguf
+    shape = dict(n_layer=2, n_embd=256, n_ff=512, n_head=4, n_head_kv=2, n_vocab=4096)
+    src = synth_cached("tie-src", shape, 31)
+    path = tie_head_gguf(src, os.path.join(tmpdir_mi, "tie-31.gguf"), 100, 2000, 7, 3000)
+    prompt = minfer.prompt_ids(4, 6, shape["n_vocab"])
+    opts = dict(max_ctx=64)
+    opts.update({"per_phase": dict(persistent=0), "persistent": dict(persistent=1),
+                 "multi_phases": dict(persistent=1), "multi_persistent": dict(persistent=2),
+                 "spec_host": dict(spec=1, persistent=1), "spec_device": dict(spec=1, persistent=2)}[kind])
+    say("argmax ties via %s" % kind)
+    with minfer.Engine(path, **opts) as eng:
+        orc = O.Model(path, O.MODE_Q8ACT, plan=plan_of(eng), max_seq=64)
+        if kind.startswith("multi"):
+            eng.prefill(prompt[:2])
+            toks = prompt[2:6]
+            am, mg = eng.step(toks, 2)              # one T = 4 step at positions 2..5
+            for t in range(2):
+                orc.forward(prompt[t], t)
+            ref = [orc.forward(toks[t], 2 + t) for t in range(4)]
+            assert am == [r[0] for r in ref]
+            assert all(m == 0.0 for m in mg) and all(r[1] == 0.0 for r in ref)
+            assert set(am) <= {100, 7}
+        else:
+            first, m0 = eng.prefill(prompt)
+            got, gm = eng.generate(12)
+            ref, rm, _, _ = orc.generate(prompt, 12)
+            assert got == list(ref)
+            assert all(m == 0.0 for m in gm) and all(m == 0.0 for m in rm)
+            assert set(got) <= {100, 7}

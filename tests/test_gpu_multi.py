@@ -254,13 +254,22 @@ def test_spec_generate_repetitive_prompt():
     assert st["drafted"] > 0
 
 
-@pytest.mark.parametrize("case", ["config2", "repetitive"])
+@pytest.mark.parametrize("case", ["config2", "repetitive", "config4"])
 def test_spec_driven_on_device_equals_host_loop(case):
     """persistent = 2 and no callback: the speculative loop runs on the device (each
     persistent verify launch commits and drafts the next step itself). Tokens and margins
     equal the plain greedy decode, and the verify steps, drafts and acceptances equal the
-    host-driven loop's one for one (the same draft rule in the same float arithmetic)."""
-    if case == "config2":
+    host-driven loop's one for one (the same draft rule in the same float arithmetic).
+    config4: the drafter on its own shape (S3, the verify steps' int8 MFMA tiles at
+    context ~1000): a synthetic repetitive stream of 1,000 tokens (a seeded 40-token
+    pattern, 25 times) as the prompt, 64 generated."""
+    if case == "config4":
+        cfg = minfer.CONFIGS["config4"]
+        shape = minfer.SHAPES[cfg[0]]
+        path = synth_cached("config4", shape, cfg[1])
+        prompt, n_gen = minfer.prompt_ids(cfg[2], 40, shape["n_vocab"]) * 25, 64
+        max_ctx = len(prompt) + n_gen + 16
+    elif case == "config2":
         cfg = minfer.CONFIGS["config2"]
         shape = minfer.SHAPES[cfg[0]]
         path = synth_cached("config2", shape, cfg[1])

@@ -191,3 +191,33 @@ def test_attention_rejects_bad_shapes_before_any_launch(name):
     for q, nh, nkv, hd, L, ctx, scr, want in cases:
         rc = fn(q, p, p, nh, nkv, hd, L, ctx, C.c_float(0.1), scr, p, None)
         assert rc == want, (name, nh, nkv, hd, L, ctx, rc)
+
+
+LAYOUT_SHAPES = {
+    "TINY": dict(n_layer=2, n_embd=256, n_ff=512, n_head=4, n_head_kv=2, n_vocab=4096),
+    "SMALL": dict(n_layer=3, n_embd=512, n_ff=1536, n_head=8, n_head_kv=2, n_vocab=8192),
+    "S05": "S05", "S15": "S15", "S3": "S3",
+}
+
+
+@pytest.mark.parametrize("name,max_ctx", [("TINY", 64), ("SMALL", 104), ("SMALL", 1100), ("S05", 160), ("S15", 208),
+                                          ("S15", 4096), ("S3", 1040), ("S3", 1100)])
+def test_step_indices_stay_inside_their_buffers(name, max_ctx):
+    """Every index the single-token step and the multi-token phase bodies form (mi_check_layout,
+    a host-side walk with each body's loop bounds over the shared layout functions) lies inside
+    the buffer the engine allocates, for T = 1..8 at the first positions, across the first
+    chunk boundaries, and at the end of the context. Cases: the CLI's 40-token prefill with 48
+    generated (max_ctx 104), config 0/2 contexts, config 4 (S3 at context 1024), and a context
+    past the two-level merge."""
+    shape = LAYOUT_SHAPES[name]
+    for n_cu in (256, 80):
+        for T in range(1, 9):
+            for pos in sorted({0, 1, 7, 8, 40, 63, 64, 65, max_ctx // 2, max_ctx - T - 1, max_ctx - T}):
+                if pos < 0 or pos + T > max_ctx:
+                    continue
+                rc, msg = minfer.check_layout(shape, max_ctx, n_cu, T, pos)
+                assert rc == 0, (name, max_ctx, n_cu, T, pos, msg)
+    # a step past the context is refused, not walked
+    rc, msg = minfer.check_layout(shape, max_ctx, 256, 8, max_ctx - 7)
+    assert rc != 0 and "past the context" in msg
+

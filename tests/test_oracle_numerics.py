@@ -5,6 +5,7 @@ mode, swapped nibble order, dropped -8 term, wrong reduction, wrong exp range
 reduction) fails it. None of these call the GPU.
 """
 import math
+import os
 
 import numpy as np
 import pytest
@@ -345,3 +346,28 @@ def test_requant_q4_0_recipe():
     q = np.clip(np.rint(y[:32] * inv).astype(int) + 8, 0, 15)
     assert np.array_equal(out[2:18], (q[:16] | (q[16:] << 4)).astype(np.uint8))
     assert np.frombuffer(out[18:20].tobytes(), np.float16)[0] == 0 and np.all(out[20:36] == 0x88)
+
+
+def test_oracle_argmax_ties_take_the_first_row(tmpdir_mi):
+    """Exact logit ties (output.weight rows i, j identical and k, m their negation, every
+    other row zero, tests/conftest.py tie_head_gguf): at every position the greedy token
+    is the first row of the winning pair, i (v > 0) or k (v < 0), with margin 0, in both
+    oracle modes (cpu_infer.cpp:153-154 takes the first maximum)."""
+    import minfer
+    from conftest import synth_cached, tie_head_gguf
+    shape = dict(n_layer=2, n_embd=256, n_ff=512, n_head=4, n_head_kv=2, n_vocab=4096)
+    src = synth_cached("tie-src", shape, 31)
+    path = tie_head_gguf(src, os.path.join(tmpdir_mi, "tie-31.gguf"), 100, 2000, 7, 3000)
+    prompt = minfer.prompt_ids(4, 6, shape["n_vocab"])
+    for mode in (O.MODE_FP32, O.MODE_Q8ACT):
+        plan = O.Plan.make([8] * 5, [1, 1, 1, 2, 1]) if mode == O.MODE_Q8ACT else None
+        m = O.Model(path, mode, plan=plan, max_seq=64)
+        seen = set()
+        for p, t in enumerate(prompt):
+            a, mg, lg = m.forward(t, p, True)
+            v = float(lg[100])
+            assert lg[2000] == lg[100] and lg[7] == -lg[100] and lg[3000] == -lg[100]
+            want = 100 if v > 0 else 7 if v < 0 else 0
+            assert a == want and mg == 0.0, (mode, p, a, want, mg)
+            seen.add(want)
+        assert seen == {100, 7} or len(prompt) < 4, seen     # both signs occur over the prompt
