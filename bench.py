@@ -69,10 +69,10 @@ def gemv_microbench(torch, reps=40):
     import numpy as np
     out = []
     rng = np.random.default_rng(0)
-    # ks per shape: the fastest split of K up to 8 (the most partials the engine's residual
-    # add takes), from a sweep on the box
+    # ks per shape: the fastest split of K up to 12 (the most split-K partials the engine's
+    # residual add takes; down's is the engine's own plan), from a sweep on the box
     shapes = [("qkv", 2048, 1536, 6), ("o", 1536, 1536, 6), ("gate_up", 17920, 1536, 6),
-              ("down", 1536, 8960, 7), ("lm_head", 151936, 1536, 1)]
+              ("down", 1536, 8960, 10), ("lm_head", 151936, 1536, 2)]
     for name, rows, n_in, ks in shapes:
         nb, cb = n_in // 32, 8
         nbytes = minfer.packed_bytes(rows, nb, cb)
@@ -111,6 +111,20 @@ def gemv_microbench(torch, reps=40):
         del w
     torch.cuda.empty_cache()
     _ = rng
+    return out
+
+
+def gemv_kernel_us():
+    """config-1 kernel durations per shape from the committed rocprofv3 kernel-trace summary"""
+    out = {}
+    try:
+        with open(os.path.join(ROOT, "profiles", "k_gemv_config1.md")) as f:
+            for line in f:
+                if line.startswith("kernel_us_"):
+                    k, v = line[len("kernel_us_"):].split(":")
+                    out[k.strip()] = float(v)
+    except OSError:
+        pass
     return out
 
 
@@ -376,7 +390,16 @@ def main():
                     help="with --attention-only: the matrix-core chunk records (mi_attn_decode_mfma)")
     ap.add_argument("--eager", action="store_true",
                     help="with --attention-only: launch eagerly instead of replaying a graph (for kernel traces)")
+    ap.add_argument("--gemv-only", action="store_true",
+                    help="only run the config1 GEMV microbench, print its JSON and exit (for kernel traces)")
     args = ap.parse_args()
+    if args.gemv_only:
+        import torch
+        res = gemv_microbench(torch)
+        for m in res:
+            log("gemv %-8s %6d x %5d: %8.2f us  %7.1f GB/s" % (m["shape"], m["rows"], m["k"], m["us"], m["gbps"]))
+        print(json.dumps({"gemv": res}), flush=True)
+        return
     if args.attention_only:
         import torch
         lens = tuple(int(x) for x in args.attention_only.split(","))
@@ -468,7 +491,14 @@ def main():
     eng.close()
     del eng
     micro = [] if args.no_micro else gemv_microbench(torch)
+    ktr = gemv_kernel_us()
     for m in micro:
+        m["frac_of_stream"] = round(m["gbps"] / stream, 4)
+        if m["shape"] in ktr:          # kernel duration alone (rocprofv3 trace, profiles/k_gemv_config1.md)
+            alg = m["gbps"] * m["us"] * 1e3
+            m["kernel_us"] = ktr[m["shape"]]
+            m["kernel_gbps"] = round(alg / ktr[m["shape"]] / 1e3, 1)
+            m["kernel_frac_of_stream"] = round(m["kernel_gbps"] / stream, 4)
         log("gemv %-8s %6d x %5d: %8.2f us  %7.1f GB/s" % (m["shape"], m["rows"], m["k"], m["us"], m["gbps"]))
     attn = [] if args.no_micro else attention_depth(torch)
     for a in attn:

@@ -262,6 +262,18 @@ __device__ __forceinline__ void tile_load(Tile& t, const uint8_t* p, int cb, int
         t.s = make_uint4(v.x, v.y, 0u, 0u);
     }
 }
+// the same loads for a chunk size known at compile time (one straight-line sequence)
+template <int CB>
+__device__ __forceinline__ void tile_load_cb(Tile& t, const uint8_t* p, int lane) {
+#pragma unroll
+    for (int k = 0; k < CB; k++) t.q[k] = ntload16(p + k * 1024 + lane * 16);
+    if constexpr (CB == 8) {
+        t.s = ntload16(p + 8192 + lane * 16);
+    } else {
+        const uint2 v = *reinterpret_cast<const uint2*>(p + 4096 + lane * 8);
+        t.s = make_uint4(v.x, v.y, 0u, 0u);
+    }
+}
 __device__ __forceinline__ uint32_t u4_at(const uint4& v, int i) { return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w; }
 
 // sum of one chunk: an fma chain over its CB blocks, from 0
@@ -2459,6 +2471,52 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_seg(PMat W, const int8_t* xq, 
     }
 }
 
+// Wave-per-segment GEMV: grid wave w owns segment w (row group g, K segment s). Each
+// lane first loads its share of the segment's activation block records (codes, scale,
+// 8*sum) into registers, then the wave issues its first chunk's tile, then it writes the
+// records into its own LDS area: a wave's loads complete in issue order, so the records
+// land before the weights and no workgroup barrier waits on anyone's tiles. The chunks
+// follow with the next chunk's loads in flight while one is summed; chunk sums are added
+// left to right, the step's order, into one split-K partial.
+constexpr int kWaveMaxBlocks = 64;   // activation blocks of one wave's segment
+template <int NW, int CB>
+__global__ __launch_bounds__(64 * NW) void k_gemv_wave(PMat W, const int8_t* xq, const float* xd, const int32_t* xs8,
+                                                       float* part) {
+    __shared__ __align__(16) uint8_t X[NW][kWaveMaxBlocks * kXRec];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int task = blockIdx.x * NW + wave;
+    if (task >= (W.rows / 64) * W.ks) return;          // no workgroup barrier below
+    int g, s, c0, c1;
+    tseg(W, task, g, s, c0, c1);
+    const int b0 = c0 * CB, nblk = (c1 - c0) * CB;
+    // this lane's pieces of the records: code halves lane and lane + 64, block lane's scale and sum
+    uint4 q0 = make_uint4(0u, 0u, 0u, 0u), q1 = q0;
+    float d = 0.f;
+    int s8 = 0;
+    const uint4* xq4 = reinterpret_cast<const uint4*>(xq + 32 * b0);
+    if (lane < 2 * nblk) q0 = xq4[lane];
+    if (lane + 64 < 2 * nblk) q1 = xq4[lane + 64];
+    if (lane < nblk) { d = xd[b0 + lane]; s8 = xs8[b0 + lane]; }
+    Tile cur, nxt;
+    tile_load_cb<CB>(cur, tile_ptr(W, g, c0), lane);
+    uint8_t* x = X[wave];
+    if (lane < 2 * nblk) *reinterpret_cast<uint4*>(x + (lane >> 1) * kXRec + 16 * (lane & 1)) = q0;
+    if (lane + 64 < 2 * nblk) *reinterpret_cast<uint4*>(x + ((lane + 64) >> 1) * kXRec + 16 * (lane & 1)) = q1;
+    if (lane < nblk) {
+        *reinterpret_cast<float*>(x + lane * kXRec + 32) = d;
+        *reinterpret_cast<int32_t*>(x + lane * kXRec + 36) = s8;
+    }
+    wave_lds_sync();
+    float seg = 0.f;
+    for (int c = c0; c < c1; c++) {
+        if (c + 1 < c1) tile_load_cb<CB>(nxt, tile_ptr(W, g, c + 1), lane);
+        const float p = chunk_dot<CB>(cur, x, kXRec, (c - c0) * CB);
+        seg = c == c0 ? p : __fadd_rn(seg, p);
+        cur = nxt;
+    }
+    part[(size_t)s * W.rows + g * 64 + lane] = seg;
+}
+
 __global__ void k_seg_sum(const float* part, int rows, int ks, float* y) {
     const int r = blockIdx.x * blockDim.x + threadIdx.x;
     if (r >= rows) return;
@@ -3083,11 +3141,28 @@ int persistent_max_grid(int G, int HD) {
 void launch_quant(const float* x, int n, int8_t* xq, float* xd, int32_t* xs8, hipStream_t s) {
     LAUNCH(k_quant, (n + kThreads - 1) / kThreads, kThreads, s, x, n, xq, xd, xs8);
 }
+// Kernel choice by segment count and length (sweep on the box, config-1 shapes, µs per
+// launch from graph replay; every choice gives the same bits):
+// * one-chunk segments (qkv, o, gate/up at ks 6): one wave per segment, 1-wave workgroups
+//   (gate/up 5.38 -> 4.89, qkv 3.12 -> 2.88);
+// * many short segments (lm_head at ks 2: 4748 segments of 3 chunks): the same kernel, 4
+//   waves per workgroup (22.0 vs 24.4 for the dense loop at ks 1);
+// * few segments of several chunks (down): a workgroup per segment, a wave per chunk, so
+//   that all of a segment's loads go out at once (the wave kernel walks them in turn).
 void launch_gemv(const PMat& W, const int8_t* xq, const float* xd, const int32_t* xs8, float* part, float* y,
                  int n_cu, hipStream_t s) {
     const int tasks = (W.rows / 64) * W.ks;
     const int maxc = (W.nc + W.ks - 1) / W.ks;          // chunks of the longest segment
-    if (tasks <= kGemvWgsPerCu * n_cu && maxc >= 2 && maxc <= kSegMaxChunks) {
+    const bool wave1 = maxc == 1, wave4 = tasks > kGemvWgsPerCu * n_cu && maxc * W.cb <= kWaveMaxBlocks;
+    if (wave1 || wave4) {
+        auto go = [&](auto cbv) {
+            constexpr int CB = decltype(cbv)::value;
+            if (wave1) LAUNCH((k_gemv_wave<1, CB>), tasks, 64, s, W, xq, xd, xs8, part);
+            else LAUNCH((k_gemv_wave<4, CB>), (tasks + 3) / 4, 256, s, W, xq, xd, xs8, part);
+        };
+        if (W.cb == 8) go(std::integral_constant<int, 8>());
+        else go(std::integral_constant<int, 4>());
+    } else if (tasks <= kGemvWgsPerCu * n_cu && maxc >= 2 && maxc <= kSegMaxChunks) {
         switch (std::min(maxc, 8)) {
         case 2: LAUNCH(k_gemv_seg<2>, tasks, 128, s, W, xq, xd, xs8, part); break;
         case 3: LAUNCH(k_gemv_seg<3>, tasks, 192, s, W, xq, xd, xs8, part); break;

@@ -78,9 +78,11 @@ GEMV_SHAPES = [  # (rows, in, cb, ks): S15 QKV/O/gate-up/down, S05 cb=4, lm_head
     (1152, 896, 4, 7), (9728, 896, 4, 4), (896, 4864, 8, 8), (4096, 1536, 8, 1), (256, 2048, 8, 3),
     # launch shapes: waves looping over 18 chunks, 3 waves, a 70-chunk segment (one-wave loop)
     (1536, 8960, 8, 2), (640, 1536, 8, 2), (512, 8960, 4, 1),
-    # the config-1 microbench's own launch shapes (bench.py gemv_microbench): gate/up ks 6,
-    # down ks 7, the whole S15 lm_head at ks 1
-    (17920, 1536, 8, 6), (1536, 8960, 8, 7), (151936, 1536, 8, 1),
+    # the config-1 microbench's own launch shapes (bench.py gemv_microbench): one-chunk
+    # segments on one wave each (qkv, o, gate/up at ks 6), down ks 10, the whole S15 lm_head
+    # at ks 2 (4 waves per workgroup, 3-chunk segments) and at ks 1; cb 4 one-chunk segments
+    (17920, 1536, 8, 6), (1536, 8960, 8, 10), (151936, 1536, 8, 2), (151936, 1536, 8, 1),
+    (9728, 896, 4, 7),
 ]
 
 
