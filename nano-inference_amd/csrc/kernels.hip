@@ -1162,13 +1162,21 @@ __device__ __forceinline__ void attn_finish(MPtr M, int l, int pos, int h, int c
     if (lane == 0) { stc(rec + HD, m[0]); stc(rec + HD + 1, lsum[0]); }
 }
 
+// Workgroups per (kv head, chunk): the unit's G query heads go to S workgroups, S = 2
+// while the grid holds every such unit in one round. A unit's heads then run one per
+// SIMD (waves 0..2 for G = 6) instead of two on each of two SIMDs (waves w and w + 4
+// share one): the scores and p.v are VALU-bound chains, 1.86 us per unit at 64 positions
+// with six heads on four SIMDs. Each head's arithmetic is unchanged; only the chunk's K/V
+// tile is read twice. Unit u covers (kv head, chunk) u / S and head group u % S.
+__device__ __forceinline__ int attn_splits(MPtr M, int nch, int nwg) {
+    return M->G > 1 && 2 * M->NKV * nch <= nwg ? 2 : 1;
+}
 // the workgroup's first unit: K/V DMA only, by workers 0 and 1 (issued before the grid
 // barrier; the phase's staging step drains it)
 template <int HD>
 __device__ __forceinline__ void attn_prefetch(MPtr M, int l, int pos, int wg, int nwg, uint8_t* U, int wave, int lane) {
-    const int nch = (pos + 1 + kAttnChunk - 1) / kAttnChunk;
-    if (wg < M->NKV * nch) attn_issue_unit<HD>(M, l, pos, wg, nch, U, wave, lane);
-    (void)nwg;
+    const int nch = (pos + 1 + kAttnChunk - 1) / kAttnChunk, S = attn_splits(M, nch, nwg);
+    if (wg < M->NKV * nch * S) attn_issue_unit<HD>(M, l, pos, wg / S, nch, U, wave, lane);
 }
 // all of the workgroup's units, every wave taking part (the first unit's tile is in LDS;
 // later units reload it between workgroup barriers)
@@ -1176,17 +1184,19 @@ template <int HD>
 __device__ __forceinline__ void attn_run(MPtr M, int l, int pos, int wg, int nwg, uint8_t* U, int wave, int lane) {
     // opaque lane: its addresses are not hoisted out of the step's phase loop
     asm volatile("" : "+v"(lane));
-    const int nch = (pos + 1 + kAttnChunk - 1) / kAttnChunk, units = M->NKV * nch;
+    const int nch = (pos + 1 + kAttnChunk - 1) / kAttnChunk, S = attn_splits(M, nch, nwg), units = M->NKV * nch * S;
+    const int hpw = (M->G + S - 1) / S;                 // heads per workgroup
     uint8_t* area = U + 2 * 64 * HD * 2 + wave * attn_head_lds<HD>();
     for (int u = wg; u < units; u += nwg) {
+        const int uc = u / S, part = u - uc * S;
         if (u != wg) {
             __syncthreads();                        // every head is done with the tile
-            attn_issue_unit<HD>(M, l, pos, u, nch, U, wave, lane);
+            attn_issue_unit<HD>(M, l, pos, uc, nch, U, wave, lane);
             drain_vm();
             __syncthreads();
         }
-        const int kvh = u / nch;
-        if (wave < M->G) attn_finish<HD>(M, l, pos, kvh * M->G + wave, u - kvh * nch, U, area, lane);
+        const int kvh = uc / nch, hh = part * hpw + wave;
+        if (wave < hpw && hh < M->G) attn_finish<HD>(M, l, pos, kvh * M->G + hh, uc - kvh * nch, U, area, lane);
     }
 }
 
