@@ -614,18 +614,20 @@ __device__ __forceinline__ void quant_slice(float4 y, bool own, int e0, uint8_t*
 // 1/sqrt(mean(x^2) + eps) of the n-vector x in LDS, the same on every lane of every
 // wave: lane l sums x[256j + 4l + i]^2 over j, then i, by fma; xor butterfly
 __device__ __forceinline__ float rms_scale(const float* x, int n, float eps, int lane) {
-    // every load first (slices past n read as zeros: fma(0, 0, a) = a, a >= +0), then the chain
-    constexpr int NJ = kMaxE / 256;
-    float4 v[NJ];
-#pragma unroll
-    for (int j = 0; j < NJ; j++) v[j] = 256 * j + 4 * lane < n ? ld4(x + 256 * j + 4 * lane) : make_float4(0.f, 0.f, 0.f, 0.f);
+    // whole 256-element slices two at a time, both loads ahead of their part of the chain
+    // (n is uniform: a scalar loop), then a last partial slice read as zeros past n
+    // (fma(0, 0, a) = a for a >= +0)
     float a = 0.f;
-#pragma unroll
-    for (int j = 0; j < NJ; j++) {
-        a = __fmaf_rn(v[j].x, v[j].x, a);
-        a = __fmaf_rn(v[j].y, v[j].y, a);
-        a = __fmaf_rn(v[j].z, v[j].z, a);
-        a = __fmaf_rn(v[j].w, v[j].w, a);
+    const int nj = n >> 8;
+    int j = 0;
+    for (; j + 1 < nj; j += 2) {
+        const float4 u = ld4(x + 256 * j + 4 * lane), w = ld4(x + 256 * (j + 1) + 4 * lane);
+        a = __fmaf_rn(u.x, u.x, a); a = __fmaf_rn(u.y, u.y, a); a = __fmaf_rn(u.z, u.z, a); a = __fmaf_rn(u.w, u.w, a);
+        a = __fmaf_rn(w.x, w.x, a); a = __fmaf_rn(w.y, w.y, a); a = __fmaf_rn(w.z, w.z, a); a = __fmaf_rn(w.w, w.w, a);
+    }
+    for (; 256 * j < n; j++) {
+        const float4 u = 256 * j + 4 * lane < n ? ld4(x + 256 * j + 4 * lane) : make_float4(0.f, 0.f, 0.f, 0.f);
+        a = __fmaf_rn(u.x, u.x, a); a = __fmaf_rn(u.y, u.y, a); a = __fmaf_rn(u.z, u.z, a); a = __fmaf_rn(u.w, u.w, a);
     }
     a = bfly_sum64(a);
     return __fdiv_rn(1.0f, __builtin_sqrtf(__fadd_rn(__fdiv_rn(a, (float)n), eps)));   // correctly rounded sqrt
@@ -733,14 +735,17 @@ __device__ __forceinline__ void wg_prologue(MPtr M, int l, int kind, int pos, in
         const int ks = kind != PH_GU ? LY(M, pl)->d.ks : LY(M, pl)->o.ks;
         const float* hs = resident ? S.R : w + n;
         const float* ps = w + (resident ? n : 2 * n);
-        float4 p[kMaxKsRes];
-#pragma unroll
-        for (int s = 0; s < kMaxKsRes; s++)
-            if (s < ks) p[s] = ld4(ps + s * n + e0);
-        float4 v = p[0];
-#pragma unroll
-        for (int s = 1; s < kMaxKsRes; s++)
-            if (s < ks) v = f4add(v, p[s]);
+        // the partials in order, four loads ahead of their adds (ks is uniform: a scalar
+        // loop; an unrolled loop over kMaxKsRes with a condition per partial branched and
+        // reloaded spilled scalars around every load)
+        float4 v = ld4(ps + e0);
+        int s = 1;
+        for (; s + 3 < ks; s += 4) {
+            const float4 a = ld4(ps + s * n + e0), b = ld4(ps + (s + 1) * n + e0);
+            const float4 c = ld4(ps + (s + 2) * n + e0), d = ld4(ps + (s + 3) * n + e0);
+            v = f4add(f4add(f4add(f4add(v, a), b), c), d);
+        }
+        for (; s < ks; s++) v = f4add(v, ld4(ps + s * n + e0));
         const float4 x = f4add(ld4(hs + e0), v);
         st4(h, e0, x);
         if (!resident && wg == 0 && kind != PH_LM) {
