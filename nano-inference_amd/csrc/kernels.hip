@@ -708,17 +708,27 @@ __device__ __forceinline__ void wg_prologue(MPtr M, int l, int kind, int pos, in
             const int HD = M->HD, arec = M->arec, hb = nch * arec;
             const int hh = e0 / HD, d = e0 - hh * HD;        // 4 | HD: one head
             const float* r = reinterpret_cast<const float*>(S.U) + hh * hb;
+            // every record's (m, l, o) read first (nch is uniform), then the chains
+            float mc[kInlineComb], lc[kInlineComb];
+            float4 oc[kInlineComb];
+#pragma unroll
+            for (int c = 0; c < kInlineComb; c++)
+                if (c < nch) { mc[c] = r[c * arec + HD]; lc[c] = r[c * arec + HD + 1]; oc[c] = ld4(r + c * arec + d); }
             float mx = -__builtin_inff();
-            for (int c = 0; c < nch; c++) mx = fmaxf(mx, r[c * arec + HD]);
+#pragma unroll
+            for (int c = 0; c < kInlineComb; c++)
+                if (c < nch) mx = fmaxf(mx, mc[c]);
             float den = 0.f;
             float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-            for (int c = 0; c < nch; c++) {
-                const float wc = mi_expf(__fsub_rn(r[c * arec + HD], mx));
-                den = __fmaf_rn(r[c * arec + HD + 1], wc, den);
-                const float4 o = ld4(r + c * arec + d);
-                acc = make_float4(__fmaf_rn(o.x, wc, acc.x), __fmaf_rn(o.y, wc, acc.y), __fmaf_rn(o.z, wc, acc.z),
-                                  __fmaf_rn(o.w, wc, acc.w));
-            }
+#pragma unroll
+            for (int c = 0; c < kInlineComb; c++)
+                if (c < nch) {
+                    const float wc = mi_expf(__fsub_rn(mc[c], mx));
+                    den = __fmaf_rn(lc[c], wc, den);
+                    const float4 o = oc[c];
+                    acc = make_float4(__fmaf_rn(o.x, wc, acc.x), __fmaf_rn(o.y, wc, acc.y), __fmaf_rn(o.z, wc, acc.z),
+                                      __fmaf_rn(o.w, wc, acc.w));
+                }
             y = make_float4(__fdiv_rn(acc.x, den), __fdiv_rn(acc.y, den), __fdiv_rn(acc.z, den), __fdiv_rn(acc.w, den));
         } else if (own) {
             y = ld4(S.T + e0);
