@@ -1867,11 +1867,14 @@ using lay::kXtGu;
 __device__ __forceinline__ int xt_slot(MPtr M, int l, int which) { return lay::xt_slot(M->NL, l, which); }
 __device__ __forceinline__ uint8_t* xT_at(MPtr M, int slot) { return M->xT + lay::xT(M->E, slot); }
 // T tokens' records of an E-wide GEMM input: its xT slot -> LDS (all threads)
+// the T tokens' input records of a GEMM (contiguous, 1-KB units shared over the waves)
+// into LDS by DMA, all in flight at once (a thread-per-8-bytes copy loop waited for
+// each load before its store)
 __device__ __forceinline__ void tstage_x(MPtr M, int slot, int T, uint8_t* XT) {
-    const int n8 = T * (M->E / 32) * (kTRec / 8);
-    const uint2* src = reinterpret_cast<const uint2*>(xT_at(M, slot));
-    uint2* dst = reinterpret_cast<uint2*>(XT);
-    for (int i = opaque_tid(); i < n8; i += blockDim.x) dst[i] = src[i];
+    const int tid = opaque_tid();
+    DmaShare d{tid >> 6, (int)(blockDim.x >> 6), 0};
+    dma_share(xT_at(M, slot), XT, T * (M->E / 32) * kTRec, d, tid & 63);
+    drain_vm();
 }
 
 // phase input of token t for the qkv (kind PH_QKV), gate/up (PH_GU) and
@@ -2160,11 +2163,26 @@ __device__ __forceinline__ void kT_down_body(MPtr M, int l, int T, uint8_t* smem
             blo = min(blo, c0 * W.cb);
             bhi = max(bhi, c1 * W.cb);
         }
-        const int nb = max(0, bhi - blo);
-        for (int i = opaque_tid(); i < T * nb * (kTRec / 8); i += blockDim.x) {
-            const int rcd = i / (kTRec / 8), k = i - rcd * (kTRec / 8), t = rcd / max(nb, 1), b = blo + rcd - t * nb;
-            reinterpret_cast<uint2*>(XT + ((size_t)t * nblk + b) * kTRec)[k] =
-                reinterpret_cast<const uint2*>(actT_at(M, l, t) + (size_t)b * kActRec)[k];
+        const int nb = max(0, bhi - blo), n8 = T * nb * (kTRec / 8);
+        // every load of a round in flight before its stores
+        constexpr int U = 4;
+        for (int i0 = opaque_tid(); i0 < n8; i0 += U * (int)blockDim.x) {
+            uint2 v[U];
+            int at[U];
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                const int i = i0 + u * (int)blockDim.x;
+                at[u] = -1;
+                if (i < n8) {
+                    const int rcd = i / (kTRec / 8), k = i - rcd * (kTRec / 8), t = div_small(rcd, max(nb, 1));
+                    const int b = blo + rcd - t * nb;
+                    v[u] = reinterpret_cast<const uint2*>(actT_at(M, l, t) + (size_t)b * kActRec)[k];
+                    at[u] = (int)(((size_t)t * nblk + b) * kTRec) + 8 * k;
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < U; u++)
+                if (at[u] >= 0) *reinterpret_cast<uint2*>(XT + at[u]) = v[u];
         }
     };
     tgemm(W, wg, nwg, XT, nblk, T, P, wave, lane, stage, [&](int g, int s, int t, float v) {
