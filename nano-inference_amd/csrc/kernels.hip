@@ -840,14 +840,27 @@ __device__ __forceinline__ void lm_epilogue(MPtr M, int wg, int nwg, const Lds& 
 // merge of the workgroups' candidates by one wave (top-2 merging is associative and
 // commutative, so any order gives the same token and margin); result on every lane;
 // *failed: whether any workgroup reported a failed barrier
+// a lane's candidate records i = lane, lane + 64, ... (record i: 4 floats at cand + i *
+// stride, 16-byte aligned), four loads in flight at a time, merged in that order
+template <class F>
+__device__ __forceinline__ void merge_cand_recs(const float* cand, int stride, int n, int lane, F f) {
+    for (int i0 = lane; i0 < n; i0 += 256) {
+        float4 c[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++)
+            if (i0 + 64 * u < n) c[u] = *reinterpret_cast<const float4*>(cand + (size_t)(i0 + 64 * u) * stride);
+#pragma unroll
+        for (int u = 0; u < 4; u++)
+            if (i0 + 64 * u < n) f(c[u]);
+    }
+}
 __device__ __forceinline__ Top2 wave_merge_cands(const float* cand, int n, int lane, unsigned* failed = nullptr) {
     Top2 t{-__builtin_inff(), INT_MAX, -__builtin_inff()};
     unsigned f = 0;
-    for (int i = lane; i < n; i += 64) {
-        const float* cd = cand + (size_t)i * 32;
-        top2_merge(t, cd[0], __float_as_int(cd[1]), cd[2]);
-        f |= __float_as_uint(cd[3]);
-    }
+    merge_cand_recs(cand, 32, n, lane, [&](float4 c) {
+        top2_merge(t, c.x, __float_as_int(c.y), c.z);
+        f |= __float_as_uint(c.w);
+    });
     top2_wave(t);
     if (failed) *failed = __builtin_amdgcn_ballot_w64(f != 0) != 0;
     return t;
@@ -2224,10 +2237,8 @@ __device__ __forceinline__ void kT_argmax_body(MPtr M, int ncand, int T, int pos
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     if (wave >= T) return;
     Top2 tp{-__builtin_inff(), INT_MAX, -__builtin_inff()};
-    for (int i = lane; i < ncand; i += 64) {
-        const float* cd = M->candT + lay::candT(i, wave);
-        top2_merge(tp, cd[0], __float_as_int(cd[1]), cd[2]);
-    }
+    merge_cand_recs(M->candT + lay::candT(0, wave), (int)lay::candT(1, 0), ncand, lane,
+                    [&](float4 c) { top2_merge(tp, c.x, __float_as_int(c.y), c.z); });
     top2_wave(tp);
     if (lane == 0) {
         M->out_tok[pos + wave] = top2_token(tp, M->V);
