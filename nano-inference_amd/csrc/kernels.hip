@@ -566,6 +566,16 @@ __device__ __forceinline__ void stamp(MPtr M, int slot, int who = 0) {
 #else
 #define FINE_STAMP(...) ((void)0)
 #endif
+// inside k_step<HD, PROF>: stamps only in the profiling instance (the checks of M->prof
+// in every phase cost the production step ~2%)
+#define STAMP_IF(...)                        \
+    do {                                     \
+        if constexpr (PROF) stamp(M, __VA_ARGS__); \
+    } while (0)
+#define FINE_STAMP_IF(...)                        \
+    do {                                          \
+        if constexpr (PROF) FINE_STAMP(M, __VA_ARGS__); \
+    } while (0)
 
 // ------------------------------------------------------------------ control-wave prologues
 // the phases of a layer, then lm_head
@@ -1450,7 +1460,7 @@ __device__ __forceinline__ bool phase_idle(MPtr M, int l, int kind, int wg, int 
     return wg_place(W, wg, nwg) >= (W.rows >> 6) * W.ks;
 }
 
-template <int HD>
+template <int HD, bool PROF>
 __global__ __launch_bounds__(kPThreads) void k_step(const DModel* Mp, int pos, int gen) {
     const MPtr M = (MPtr)Mp;
     __shared__ __align__(16) uint8_t smem[step_lds<HD>()];
@@ -1471,20 +1481,20 @@ __global__ __launch_bounds__(kPThreads) void k_step(const DModel* Mp, int pos, i
     }
     GridBar gb = bar_init(M->bar, M->err);
     Tile tl[2];
-    stamp(M, 0);
+    STAMP_IF(0);
     stage(M, 0, PH_QKV, pos, S, wave, kPWaves, lane, true);
-    FINE_STAMP(M, 1 + 5);
+    FINE_STAMP_IF(1 + 5);
     if (!ctl) phase_prefetch(M, 0, PH_QKV, wg, nwg, kw, tl, lane);
     int l = 0, kind = PH_QKV;
     for (int sb = 1;; sb += kProfPerPhase) {
         __syncthreads();
 #ifdef MI_PROFILE_FINE
-        if (!phase_idle(M, l, kind, wg, nwg)) wg_prologue(M, l, kind, pos, wg, S, wave, lane, true, M->prof ? sb + 7 : -1);
+        if (!phase_idle(M, l, kind, wg, nwg)) wg_prologue(M, l, kind, pos, wg, S, wave, lane, true, PROF ? sb + 7 : -1);
 #else
         if (!phase_idle(M, l, kind, wg, nwg)) wg_prologue(M, l, kind, pos, wg, S, wave, lane, true);
 #endif
         __syncthreads();
-        stamp(M, sb);
+        STAMP_IF(sb);
         if (kind == PH_ATTN) {
             attn_run<HD>(M, l, pos, wg, nwg, S.U, wave, lane);      // every wave: one query head each
         } else if (!ctl) {
@@ -1500,16 +1510,16 @@ __global__ __launch_bounds__(kPThreads) void k_step(const DModel* Mp, int pos, i
             phase_comb<HD>(M, l, pos, wg, nwg, wave, lane, reinterpret_cast<float*>(S.U));
         }
         __syncthreads();
-        stamp(M, sb + 1, 64);
+        STAMP_IF(sb + 1, 64);
         if (kind == PH_LM) {
             lm_epilogue(M, wg, nwg, S, wave, lane, gb.dead);
-            stamp(M, sb + 2);
+            STAMP_IF(sb + 2);
             __syncthreads();
-            stamp(M, sb + 3);
+            STAMP_IF(sb + 3);
             if (ctl) {
                 ctl_barrier(gb, M->err);
                 ctl_exit(M->bar);
-                stamp(M, sb + 4);
+                STAMP_IF(sb + 4);
                 if (wg == 0) {
                     unsigned failed;
                     const Top2 a = wave_merge_cands(M->cand, nwg, lane, &failed);
@@ -1523,17 +1533,17 @@ __global__ __launch_bounds__(kPThreads) void k_step(const DModel* Mp, int pos, i
         if (!ctl) {
             phase_store(M, l, kind, wg, nwg, S, kw, lane);
             drain_vm();
-            stamp(M, sb + 2, 64);
+            STAMP_IF(sb + 2, 64);
         } else {
             drain_vm();
             tl[0] = Tile{};
             tl[1] = Tile{};
         }
         __syncthreads();
-        stamp(M, sb + 3);
+        STAMP_IF(sb + 3);
         if (ctl) {
             ctl_barrier(gb, M->err);
-            stamp(M, sb + 4);
+            STAMP_IF(sb + 4);
         } else if (nk == PH_ATTN) {
             // the attention waves' first items: their K/V rows into LDS (U is free once
             // the QKV prologue is done); attn_finish waits for them
@@ -1548,8 +1558,8 @@ __global__ __launch_bounds__(kPThreads) void k_step(const DModel* Mp, int pos, i
         __syncthreads();
         if (!phase_idle(M, nl, nk, wg, nwg)) stage(M, nl, nk, pos, S, wave, kPWaves, lane, true);
         else drain_vm();
-        FINE_STAMP(M, sb + kProfPerPhase + 5);           // this wave's staging landed (control, first worker)
-        FINE_STAMP(M, sb + kProfPerPhase + 6, 64);
+        FINE_STAMP_IF(sb + kProfPerPhase + 5);           // this wave's staging landed (control, first worker)
+        FINE_STAMP_IF(sb + kProfPerPhase + 6, 64);
         l = nl;
         kind = nk;
     }
@@ -3113,7 +3123,9 @@ hipError_t launch_step_persistent(const DModel& M, const DModel* dM, int nwg, in
     with_hd(M.HD, [&](auto hd) {
         const DModel* m = dM;
         void* args[] = {&m, &pos, &gen};
-        const void* f = reinterpret_cast<const void*>(&k_step<decltype(hd)::value>);
+        // the profiling instance only when the model description carries a stamp buffer
+        const void* f = M.prof ? reinterpret_cast<const void*>(&k_step<decltype(hd)::value, true>)
+                               : reinterpret_cast<const void*>(&k_step<decltype(hd)::value, false>);
         err = coop ? hipLaunchCooperativeKernel(f, dim3(nwg), dim3(kPThreads), args, 0, s)
                    : hipLaunchKernel(f, dim3(nwg), dim3(kPThreads), args, 0, s);
     });
@@ -3185,7 +3197,7 @@ int persistent_max_grid(int G, int HD) {
     (void)G;
     int per_cu = 0;
     with_hd(HD, [&](auto hd) {
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(&k_step<decltype(hd)::value>),
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(&k_step<decltype(hd)::value, false>),
                                                          kPThreads, 0) != hipSuccess)
             per_cu = 0;
     });
