@@ -1742,26 +1742,38 @@ __device__ __forceinline__ void ttile_load(TTile<CB>& t, const uint8_t* tile, in
 // fp32 scale, 8*sum) are in LDS at XT[token][block]. acc[j][i]: row 16(2*(kg/2) + j) +
 // l%16, token 4*(kg%2) + i. Per (row, token) the float work is the single-token
 // chain: acc = fma(dw*dx, float(dot - 8*sum), acc) over the CB blocks in order, from 0.
-// The MFMA leaves block 2p's dot in lanes kg < 2 and block 2p+1's in kg >= 2 for each
-// row group; v_permlane32_swap of groups (q, q+2) hands each lane both blocks of
-// one row group (q = 2*(kg/2) + j), so every lane runs two chains per token.
+// The MFMA's C operand subtracts 8*sum (exact int32): lane kg's output slots are tokens
+// 4*(kg%2) + i of block 2p + kg/2. It leaves block 2p's results in lanes kg < 2 and block
+// 2p+1's in kg >= 2 for each row group; v_permlane32_swap of groups (q, q+2) hands each
+// lane both blocks of one row group (q = 2*(kg/2) + j), so every lane runs two chains per
+// token. Token slots T..kMaxT-1 read whatever their LDS records hold (XT has room for
+// kMaxT tokens, so the reads stay in bounds); their sums are never read.
 template <int CB>
-__device__ __forceinline__ void ttile_sums(const TTile<CB>& W, const uint8_t* XT, int nblk, int b0, int T,
+__device__ __forceinline__ void ttile_sums(const TTile<CB>& W, const uint8_t* XT, int nblk, int b0,
                                            float (&acc)[2][4], int lane) {
-    const int col = lane & 15, kg = lane >> 4, h = kg & 1, atok = col & 7;
-    const bool aon = ((col < 8) == (kg < 2)) && atok < T;
-    const uint8_t* xa = XT + ((size_t)atok * nblk + b0 + (col >> 3)) * kTRec + 8 * h;
+    const int col = lane & 15, kg = lane >> 4, h = kg & 1, hb = kg >> 1;
+    const int am = ((col < 8) == (kg < 2)) ? -1 : 0;
+    const uint8_t* xa = XT + ((col & 7) * nblk + b0 + (col >> 3)) * kTRec + 8 * h;
+    const uint8_t* xr = XT + ((4 * h) * nblk + b0) * kTRec + 32;
+    const int rs = nblk * kTRec;
 #pragma unroll
     for (int j = 0; j < 2; j++)
 #pragma unroll
         for (int i = 0; i < 4; i++) acc[j][i] = 0.f;
 #pragma unroll
     for (int p = 0; p < CB / 2; p++) {
-        v4i a = v4i{0, 0, 0, 0};
-        if (aon) {
-            const uint2 lo = *reinterpret_cast<const uint2*>(xa + 2 * p * kTRec);
-            const uint2 hi = *reinterpret_cast<const uint2*>(xa + 2 * p * kTRec + 16);
-            a = v4i{(int)lo.x, (int)lo.y, (int)hi.x, (int)hi.y};
+        const uint2 lo = *reinterpret_cast<const uint2*>(xa + 2 * p * kTRec);
+        const uint2 hi = *reinterpret_cast<const uint2*>(xa + 2 * p * kTRec + 16);
+        const v4i a = v4i{(int)lo.x & am, (int)lo.y & am, (int)hi.x & am, (int)hi.y & am};
+        float dx0[4], dx1[4];
+        v4i c;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float2 e0 = *reinterpret_cast<const float2*>(xr + i * rs + 2 * p * kTRec);
+            const float2 e1 = *reinterpret_cast<const float2*>(xr + i * rs + (2 * p + 1) * kTRec);
+            dx0[i] = e0.x;
+            dx1[i] = e1.x;
+            c[i] = (int)(0u - (uint32_t)__float_as_int(hb ? e1.y : e0.y));
         }
         int d[4][4];
 #pragma unroll
@@ -1769,28 +1781,18 @@ __device__ __forceinline__ void ttile_sums(const TTile<CB>& W, const uint8_t* XT
             const uint2 w = W.w[q][p];
             const v4i b = v4i{(int)(w.x & 0x0F0F0F0Fu), (int)(w.y & 0x0F0F0F0Fu), (int)((w.x >> 4) & 0x0F0F0F0Fu),
                               (int)((w.y >> 4) & 0x0F0F0F0Fu)};
-            const v4i r = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, v4i{0, 0, 0, 0}, 0, 0, 0);
+            const v4i r = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
 #pragma unroll
             for (int i = 0; i < 4; i++) d[q][i] = r[i];
         }
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            const int tok = 4 * h + i;
-            float dx0 = 0.f, dx1 = 0.f;
-            int xs0 = 0, xs1 = 0;
-            if (tok < T) {
-                const uint8_t* xr = XT + ((size_t)tok * nblk + b0 + 2 * p) * kTRec;
-                const float2 e0 = *reinterpret_cast<const float2*>(xr + 32);
-                const float2 e1 = *reinterpret_cast<const float2*>(xr + kTRec + 32);
-                dx0 = e0.x; xs0 = __float_as_int(e0.y);
-                dx1 = e1.x; xs1 = __float_as_int(e1.y);
-            }
 #pragma unroll
             for (int j = 0; j < 2; j++) {
                 const auto r = __builtin_amdgcn_permlane32_swap((unsigned)d[j][i], (unsigned)d[j + 2][i], false, false);
                 const uint32_t sw = W.s[j][p];
-                acc[j][i] = __fmaf_rn(__fmul_rn(h2f_lo(sw), dx0), __int2float_rn((int)r[0] - xs0), acc[j][i]);
-                acc[j][i] = __fmaf_rn(__fmul_rn(h2f_hi(sw), dx1), __int2float_rn((int)r[1] - xs1), acc[j][i]);
+                acc[j][i] = __fmaf_rn(__fmul_rn(h2f_lo(sw), dx0[i]), __int2float_rn((int)r[0]), acc[j][i]);
+                acc[j][i] = __fmaf_rn(__fmul_rn(h2f_hi(sw), dx1[i]), __int2float_rn((int)r[1]), acc[j][i]);
             }
         }
     }
@@ -1836,28 +1838,34 @@ __device__ __forceinline__ void tgemm_cb(const PMat W, int wg, int nwg, const ui
     __syncthreads();
     int nt = t, nk = k;
     bool hn = have && tnext(W, nseg, nwg, wave, nt, nk);
+    bool odd = false;   // the current tile is in nx
     for (int ts = wg; ts < nseg; ts += nwg) {
         int g, s, c0, c1;
         tseg(W, ts, g, s, c0, c1);
-        while (have && t == ts) {
+        // the tiles alternate between cur and nx (no register copy per chunk)
+        auto chunk = [&](const TTile<CB>& a, TTile<CB>& b) {
             if (hn) {
                 int g2, s2, a0, a1;
                 tseg(W, nt, g2, s2, a0, a1);
-                ttile_load<CB>(nx, tile_ptr(W, g2, a0 + nk), lane);
+                ttile_load<CB>(b, tile_ptr(W, g2, a0 + nk), lane);
             }
             float acc[2][4];
-            ttile_sums<CB>(cur, XT, nblk, (c0 + k) * CB, T, acc, lane);
+            ttile_sums<CB>(a, XT, nblk, (c0 + k) * CB, acc, lane);
             const int col = lane & 15, kg = lane >> 4;
             float* pc = P + (size_t)k * kMaxT * 64;
 #pragma unroll
             for (int j = 0; j < 2; j++)
 #pragma unroll
                 for (int i = 0; i < 4; i++) pc[(4 * (kg & 1) + i) * 64 + (2 * (kg >> 1) + j) * 16 + col] = acc[j][i];
-            cur = nx;
             t = nt;
             k = nk;
             have = hn;
             if (hn) hn = tnext(W, nseg, nwg, wave, nt, nk);
+        };
+        while (have && t == ts) {
+            if (!odd) chunk(cur, nx);
+            else chunk(nx, cur);
+            odd = !odd;
         }
         __syncthreads();
         if (wave < T) {
