@@ -1817,23 +1817,44 @@ __device__ __forceinline__ bool tnext(const PMat W, int nseg, int nwg, int wave,
     return false;
 }
 
+// A wave's first chunk of a T-token GEMM: (segment t, chunk k) and its tile loads.
+// The GEMM issues it itself before staging its input, or kT_step issues it during the
+// grid barrier before the phase (issued = true).
+template <int CB>
+struct TFirst {
+    TTile<CB> tile;
+    int t, k;
+    bool have, issued;
+};
+template <int CB>
+__device__ __forceinline__ void tgemm_first(const PMat W, int wg, int nwg, int wave, int lane, TFirst<CB>& f) {
+    const int nseg = (W.rows >> 6) * W.ks;
+    f.t = wg;
+    f.k = wave - kPWaves;
+    f.have = tnext(W, nseg, nwg, wave, f.t, f.k);
+    if (f.have) {
+        int g, s, c0, c1;
+        tseg(W, f.t, g, s, c0, c1);
+        ttile_load<CB>(f.tile, tile_ptr(W, g, c0 + f.k), lane);
+    }
+    f.issued = true;
+}
+
 // T-token GEMM over this workgroup's segments (t = wg, wg + nwg, ...). Each wave takes
 // chunks wave, wave + 8, ... of every segment and holds the next chunk's loads in
-// flight while it computes one (the first is issued before `stage` fills XT). Chunk
-// sums go to P[chunk][token][row]; after a segment, wave t adds token t's chunk sums
-// left to right and hands out(g, s, t, value) the row g*64 + lane.
+// flight while it computes one (the first is issued before `stage` fills XT, unless
+// it already is). Chunk sums go to P[chunk][token][row]; after a segment, wave t adds
+// token t's chunk sums left to right and hands out(g, s, t, value) the row g*64 + lane.
 template <int CB, class S, class F>
 __device__ __forceinline__ void tgemm_cb(const PMat W, int wg, int nwg, const uint8_t* XT, int nblk, int T, float* P,
-                                         int wave, int lane, S stage, F out) {
+                                         int wave, int lane, S stage, F out, TFirst<CB>& f) {
     const int nseg = (W.rows >> 6) * W.ks;
-    int t = wg, k = wave - kPWaves;
-    bool have = tnext(W, nseg, nwg, wave, t, k);
-    TTile<CB> cur, nx;
-    if (have) {
-        int g, s, c0, c1;
-        tseg(W, t, g, s, c0, c1);
-        ttile_load<CB>(cur, tile_ptr(W, g, c0 + k), lane);
-    }
+    if (!f.issued) tgemm_first<CB>(W, wg, nwg, wave, lane, f);
+    f.issued = false;
+    int t = f.t, k = f.k;
+    bool have = f.have;
+    TTile<CB>& cur = f.tile;
+    TTile<CB> nx;
     stage();
     __syncthreads();
     int nt = t, nk = k;
@@ -1876,11 +1897,18 @@ __device__ __forceinline__ void tgemm_cb(const PMat W, int wg, int nwg, const ui
         __syncthreads();
     }
 }
+// pre: the first chunks of this GEMM when kT_step issued them ahead (cb = 8 only);
+// issued = false otherwise
 template <class S, class F>
 __device__ __forceinline__ void tgemm(const PMat W, int wg, int nwg, const uint8_t* XT, int nblk, int T, float* P, int wave,
-                                      int lane, S stage, F out) {
-    if (W.cb == 8) tgemm_cb<8>(W, wg, nwg, XT, nblk, T, P, wave, lane, stage, out);
-    else tgemm_cb<4>(W, wg, nwg, XT, nblk, T, P, wave, lane, stage, out);
+                                      int lane, S stage, F out, TFirst<8>& pre) {
+    if (W.cb == 8) {
+        tgemm_cb<8>(W, wg, nwg, XT, nblk, T, P, wave, lane, stage, out, pre);
+    } else {
+        TFirst<4> own;
+        own.issued = false;
+        tgemm_cb<4>(W, wg, nwg, XT, nblk, T, P, wave, lane, stage, out, own);
+    }
 }
 
 // The thread index is made opaque per phase body: inside kT_step's layer loop its derived
@@ -1978,19 +2006,25 @@ __device__ __forceinline__ uint8_t* actT_at(MPtr M, int l, int t) { return M->ac
 #define TWRAP(BYTES, CALL)                                                                       \
     __shared__ __align__(16) uint8_t smem[BYTES];                                                \
     CALL;
+// the GEMM kernels' wrapper: their first chunks issued by the GEMM itself
+#define TWRAP_G(BYTES, CALL)                                                                     \
+    __shared__ __align__(16) uint8_t smem[BYTES];                                                \
+    TFirst<8> pre;                                                                               \
+    pre.issued = false;                                                                          \
+    CALL;
 
 template <bool PS>
-__device__ __forceinline__ void kT_qkv_body(MPtr M, int l, int T, uint8_t* smem, int wg, int nwg) {
+__device__ __forceinline__ void kT_qkv_body(MPtr M, int l, int T, uint8_t* smem, int wg, int nwg, TFirst<8>& pre) {
     TBODY
     uint8_t* XT = smem;
     float* P = reinterpret_cast<float*>(smem + kTXeBytes);
     const PMat W = ldmat(&LY(M, l)->qkv);
     float* part = qkvT_at(M, l);
     tgemm(W, wg, nwg, XT, M->E / 32, T, P, wave, lane, [&] { tstage_x(M, xt_slot(M, l, kXtQkv), T, XT); },
-          [&](int g, int s, int t, float v) { st_x<PS>(&part[((size_t)s * kMaxT + t) * W.rows + g * 64 + lane], v); });
+          [&](int g, int s, int t, float v) { st_x<PS>(&part[((size_t)s * kMaxT + t) * W.rows + g * 64 + lane], v); }, pre);
 }
 __global__ __launch_bounds__(kPThreads) void kT_qkv(const DModel* Mp, int l, int T) {
-    TWRAP(kTGemvLds, kT_qkv_body<false>((MPtr)Mp, l, T, smem, blockIdx.x, gridDim.x))
+    TWRAP_G(kTGemvLds, kT_qkv_body<false>((MPtr)Mp, l, T, smem, blockIdx.x, gridDim.x, pre))
 }
 
 // Multi-token attention. Item = (kv head, 64-position chunk c, group of tg consecutive
@@ -2135,21 +2169,21 @@ __global__ __launch_bounds__(256) void kT_comb(const DModel* Mp, int l, int T) {
 }
 
 template <bool PS>
-__device__ __forceinline__ void kT_o_body(MPtr M, int l, int T, uint8_t* smem, int wg, int nwg) {
+__device__ __forceinline__ void kT_o_body(MPtr M, int l, int T, uint8_t* smem, int wg, int nwg, TFirst<8>& pre) {
     TBODY
     uint8_t* XT = smem;
     float* P = reinterpret_cast<float*>(smem + kTXeBytes);
     const PMat W = ldmat(&LY(M, l)->o);
     float* part = oT_at(M, l);
     tgemm(W, wg, nwg, XT, M->E / 32, T, P, wave, lane, [&] { tstage_x(M, xt_slot(M, l, kXtO), T, XT); },
-          [&](int g, int s, int t, float v) { st_x<PS>(&part[((size_t)s * kMaxT + t) * W.rows + g * 64 + lane], v); });
+          [&](int g, int s, int t, float v) { st_x<PS>(&part[((size_t)s * kMaxT + t) * W.rows + g * 64 + lane], v); }, pre);
 }
 __global__ __launch_bounds__(kPThreads) void kT_o(const DModel* Mp, int l, int T) {
-    TWRAP(kTGemvLds, kT_o_body<false>((MPtr)Mp, l, T, smem, blockIdx.x, gridDim.x))
+    TWRAP_G(kTGemvLds, kT_o_body<false>((MPtr)Mp, l, T, smem, blockIdx.x, gridDim.x, pre))
 }
 
 template <bool PS>
-__device__ __forceinline__ void kT_gu_body(MPtr M, int l, int T, uint8_t* smem, int wg, int nwg) {
+__device__ __forceinline__ void kT_gu_body(MPtr M, int l, int T, uint8_t* smem, int wg, int nwg, TFirst<8>& pre) {
     TBODY
     uint8_t* XT = smem;
     float* P = reinterpret_cast<float*>(smem + kTXeBytes);
@@ -2169,14 +2203,14 @@ __device__ __forceinline__ void kT_gu_body(MPtr M, int l, int T, uint8_t* smem, 
             if ((lane & 3) == 0) st_x<PS>(r + lane / 4, wd);
             if (lane == 0) { st_x<PS>(r + 8, __float_as_uint(d)); st_x<PS>(r + 9, (uint32_t)s8); }
         }
-    });
+    }, pre);
 }
 __global__ __launch_bounds__(kPThreads) void kT_gu(const DModel* Mp, int l, int T) {
-    TWRAP(kTGemvLds, kT_gu_body<false>((MPtr)Mp, l, T, smem, blockIdx.x, gridDim.x))
+    TWRAP_G(kTGemvLds, kT_gu_body<false>((MPtr)Mp, l, T, smem, blockIdx.x, gridDim.x, pre))
 }
 
 template <bool PS>
-__device__ __forceinline__ void kT_down_body(MPtr M, int l, int T, uint8_t* smem, int wg, int nwg) {
+__device__ __forceinline__ void kT_down_body(MPtr M, int l, int T, uint8_t* smem, int wg, int nwg, TFirst<8>& pre) {
     TBODY
     uint8_t* XT = smem;
     float* P = reinterpret_cast<float*>(smem + kTXfBytes);
@@ -2218,14 +2252,14 @@ __device__ __forceinline__ void kT_down_body(MPtr M, int l, int T, uint8_t* smem
     };
     tgemm(W, wg, nwg, XT, nblk, T, P, wave, lane, stage, [&](int g, int s, int t, float v) {
         st_x<PS>(&part[((size_t)s * kMaxT + t) * W.rows + g * 64 + lane], v);
-    });
+    }, pre);
 }
 __global__ __launch_bounds__(kPThreads) void kT_down(const DModel* Mp, int l, int T) {
-    TWRAP(kTDownLds, kT_down_body<false>((MPtr)Mp, l, T, smem, blockIdx.x, gridDim.x))
+    TWRAP_G(kTDownLds, kT_down_body<false>((MPtr)Mp, l, T, smem, blockIdx.x, gridDim.x, pre))
 }
 
 template <bool PS>
-__device__ __forceinline__ void kT_lm_body(MPtr M, int T, uint8_t* smem, int wg, int nwg) {
+__device__ __forceinline__ void kT_lm_body(MPtr M, int T, uint8_t* smem, int wg, int nwg, TFirst<8>& pre) {
     TBODY
     uint8_t* XT = smem;
     float* P = reinterpret_cast<float*>(smem + kTXeBytes);
@@ -2236,7 +2270,7 @@ __device__ __forceinline__ void kT_lm_body(MPtr M, int T, uint8_t* smem, int wg,
         const int row = g * 64 + lane;
         if (M->logitsT) M->logitsT[(size_t)t * M->V + row] = v;
         top2_push(tp, v, row);
-    });
+    }, pre);
     if (wave < T) {
         top2_wave(tp);
         if (lane == 0) {
@@ -2248,7 +2282,7 @@ __device__ __forceinline__ void kT_lm_body(MPtr M, int T, uint8_t* smem, int wg,
     }
 }
 __global__ __launch_bounds__(kPThreads) void kT_lm(const DModel* Mp, int T) {
-    TWRAP(kTGemvLds, kT_lm_body<false>((MPtr)Mp, T, smem, blockIdx.x, gridDim.x))
+    TWRAP_G(kTGemvLds, kT_lm_body<false>((MPtr)Mp, T, smem, blockIdx.x, gridDim.x, pre))
 }
 
 __device__ __forceinline__ void kT_argmax_body(MPtr M, int ncand, int T, int pos) {
@@ -2392,27 +2426,41 @@ __global__ __launch_bounds__(kPThreads) void kT_step(const DModel* Mp, int T) {
         if (wave == 0) ctl_barrier(gb, M->err);
         __syncthreads();
     };
+    // the barrier before a GEMM phase also issues the phase's first tile loads: waves
+    // 1-7 after this workgroup's stores have drained, wave 0 once it has passed the
+    // barrier (its arrival and polls would otherwise wait for them); they land while
+    // the grid waits
+    TFirst<8> pre;
+    pre.issued = false;
+    auto barrier_pre = [&](const AS4 PMat* Wp) {
+        const PMat W = ldmat(Wp);
+        drain_vm();
+        __syncthreads();
+        if (wave == 0) ctl_barrier(gb, M->err);
+        if (W.cb == 8) tgemm_first<8>(W, wg, nwg, wave, opaque_tid() & 63, pre);
+        __syncthreads();
+    };
     for (int l = 0; l < M->NL; l++) {
         if (wg < T) kT_in_body<true>(M, l, PH_QKV, wg, xs, pos);
-        barrier();
-        kT_qkv_body<true>(M, l, T, smem, wg, nwg);
+        barrier_pre(&LY(M, l)->qkv);
+        kT_qkv_body<true>(M, l, T, smem, wg, nwg, pre);
         barrier();
         kT_attn_body<HD, true>(M, l, T, smem, wg, nwg, pos);
         barrier();
         for (int it = wg * kPWaves + wave; it < T * M->NH; it += nwg * kPWaves) kT_comb_item<HD, true>(M, l, it, lane, pos);
-        barrier();
-        kT_o_body<true>(M, l, T, smem, wg, nwg);
+        barrier_pre(&LY(M, l)->o);
+        kT_o_body<true>(M, l, T, smem, wg, nwg, pre);
         barrier();
         if (wg < T) kT_in_body<true>(M, l, PH_GU, wg, xs, pos);
-        barrier();
-        kT_gu_body<true>(M, l, T, smem, wg, nwg);
-        barrier();
-        kT_down_body<true>(M, l, T, smem, wg, nwg);
+        barrier_pre(&LY(M, l)->gu);
+        kT_gu_body<true>(M, l, T, smem, wg, nwg, pre);
+        barrier_pre(&LY(M, l)->d);
+        kT_down_body<true>(M, l, T, smem, wg, nwg, pre);
         barrier();
     }
     if (wg < T) kT_in_body<true>(M, M->NL - 1, PH_LM, wg, xs, pos);
-    barrier();
-    kT_lm_body<true>(M, T, smem, wg, nwg);
+    barrier_pre(&M->lm);
+    kT_lm_body<true>(M, T, smem, wg, nwg, pre);
     barrier();
     if (wave == 0) ctl_exit(M->bar);
     if (wg == 0) {
