@@ -189,26 +189,30 @@ def spec_decode(path, prompt, n_gen=128):
 def verify_cost(reps=10):
     """config4: S3 (hidden 2048, 36 layers), context 1024; a T=8 verify step (the
     current token + 7 drafts, TMAX = 8) against a T=1 step at the same position.
-    Wall time per mi_step call (upload, step, copy-back), mean of reps."""
+    Wall time per mi_step call (upload, step, copy-back), mean of reps. The engine's
+    default runs the T=8 step as one persistent launch; t8_per_phase_ms is the same step
+    as one launch per phase (persistent=1, same bits)."""
     shape, _, pseed, ctx, _ = minfer.CONFIGS["config4"]
     path = ensure_gguf("config4")
     V = minfer.SHAPES[shape]["n_vocab"]
-    eng = minfer.Engine(path, max_ctx=ctx + 16)
     prompt = minfer.prompt_ids(pseed, ctx, V)
-    eng.prefill(prompt)
     toks = minfer.prompt_ids(pseed + 1, 8, V)
     out = {}
-    for T in (1, 8):
-        arg = toks[:T] if T > 1 else toks[0]
-        for _ in range(3):
-            eng.step(arg, ctx)
-        t0 = time.perf_counter()
-        for _ in range(reps):
-            eng.step(arg, ctx)
-        out[T] = (time.perf_counter() - t0) / reps * 1e3
-    eng.close()
-    return dict(workload="config4: S3 q4_0, context 1024, verify T=8 vs T=1", t1_ms=round(out[1], 3),
-                t8_ms=round(out[8], 3), ratio=round(out[8] / out[1], 3),
+    for mode in (2, 1):
+        eng = minfer.Engine(path, max_ctx=ctx + 16, persistent=mode)
+        eng.prefill(prompt)
+        for T in ((1, 8) if mode == 2 else (8,)):
+            arg = toks[:T] if T > 1 else toks[0]
+            for _ in range(3):
+                eng.step(arg, ctx)
+            t0 = time.perf_counter()
+            for _ in range(reps):
+                eng.step(arg, ctx)
+            out[(mode, T)] = (time.perf_counter() - t0) / reps * 1e3
+        eng.close()
+    return dict(workload="config4: S3 q4_0, context 1024, verify T=8 vs T=1", t1_ms=round(out[(2, 1)], 3),
+                t8_ms=round(out[(2, 8)], 3), ratio=round(out[(2, 8)] / out[(2, 1)], 3),
+                t8_per_phase_ms=round(out[(1, 8)], 3),
                 note="T=8 = current token + 7 drafts (TMAX 8, mega.cu:50); the config's 8 drafts + 1 would be T=9")
 
 
@@ -225,7 +229,8 @@ def verify_spec(n_gen=64):
     prompt = minfer.prompt_ids(pseed, 40, V) * 25
     out = dict(workload="config4 drafter: S3, 1000-token repetitive prompt (40-token pattern x 25), %d generated" % n_gen)
     ref = None
-    for mode, opts in (("plain", dict(spec=0)), ("host", dict(spec=1, persistent=1)), ("device", dict(spec=1, persistent=2))):
+    for mode, opts in (("plain", dict(spec=0)), ("host", dict(spec=1, persistent=1)),
+                       ("host_persistent", dict(spec=1, persistent=2)), ("device", dict(spec=2, persistent=2))):
         eng = minfer.Engine(path, max_ctx=len(prompt) + n_gen + 16, **opts)
         eng.prefill(prompt)
         toks, mg = eng.generate(n_gen)

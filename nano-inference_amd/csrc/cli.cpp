@@ -8,8 +8,9 @@
 // format the reference's correctness gates parse). A newline ends the output either way.
 // stderr: the stat lines the reference's tools parse ("... = X tok/s", and with SPEC=1
 // "N generation steps, X tokens/step | drafted D, accepted A (P%)").
-// Environment: RAWIDS, SPEC (n-gram speculative decode, output identical to greedy),
-// NG (longest n-gram drafted, default 3), PERSISTENT (0: one launch per phase), GRAPHS (1:
+// Environment: RAWIDS, SPEC (n-gram speculative decode, output identical to greedy; 2: the
+// loop on the device), NG (longest n-gram drafted, default 3), PERSISTENT (0: one launch per
+// phase; 1: multi-token steps per phase, single tokens persistent; default 2), GRAPHS (1:
 // multi-token steps replay a HIP graph instead of launching kernel by kernel), TCHUNK
 // (prompt tokens per step, 1..8), DEVICE, and TEACHER=<k> (mega.cu:28-29, 1192-1205): the
 // ids are a reference sequence whose first k are the prompt; every position is predicted
@@ -78,7 +79,7 @@ int main(int argc, char** argv) {
     mi_opts o;
     mi_default_opts(&o);
     o.max_ctx = (int32_t)ids.size() + n_gen + 16;     // verify steps write ahead of the committed tokens
-    o.spec = env_int("SPEC", 0) != 0;
+    o.spec = std::min(std::max(env_int("SPEC", 0), 0), 2);
     o.ngmax = env_int("NG", o.ngmax);
     o.persistent = env_int("PERSISTENT", o.persistent);
     o.device = env_int("DEVICE", o.device);

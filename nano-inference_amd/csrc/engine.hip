@@ -228,7 +228,7 @@ void mi_default_opts(mi_opts* o) {
     o->spec = 0;
     o->ngmax = 3;
     o->spec_slope = 0.074f;
-    o->persistent = 1;
+    o->persistent = 2;
     o->stop_eos = 0;
     o->device = 0;
     o->graphs = 0;
@@ -547,7 +547,8 @@ int mi_load(const char* gguf_path, const mi_opts* opts, mi_engine** out) {
     *out = nullptr;
     std::unique_ptr<mi_engine> e(new mi_engine());
     if (opts) e->opts = *opts; else mi_default_opts(&e->opts);
-    if (e->opts.tchunk < 1 || e->opts.tchunk > 8 || e->opts.max_ctx < 0 || e->opts.persistent < 0 || e->opts.persistent > 2)
+    if (e->opts.tchunk < 1 || e->opts.tchunk > 8 || e->opts.max_ctx < 0 || e->opts.persistent < 0 || e->opts.persistent > 2 ||
+        e->opts.spec < 0 || e->opts.spec > 2)
         return set_err(nullptr, MI_ERR_ARG, "bad options");
     const int rc = load_impl(e.get(), gguf_path);
     if (rc) { g_load_error = e->err; return rc; }
@@ -1167,7 +1168,8 @@ int mi_generate(mi_engine* e, int32_t n_gen, int32_t* out, float* margins, int32
     if (!e->next_ready || e->cur_len < 1) return set_err(e, MI_ERR_STATE, "mi_generate needs mi_prefill first");
     if (e->cur_len + n_gen > e->maxseq) return set_err(e, MI_ERR_ARG, "n_gen %d exceeds the context capacity", n_gen);
     if (e->opts.spec) {
-        if (e->nwg_persistent && e->multi_persistent && !cb) return generate_spec_device(e, n_gen, out, margins, n_out);
+        if (e->opts.spec == 2 && e->nwg_persistent && e->multi_persistent && !cb)
+            return generate_spec_device(e, n_gen, out, margins, n_out);
         return generate_spec(e, n_gen, out, margins, n_out, cb, user);
     }
     e->stats.drafted = e->stats.accepted = 0;

@@ -495,7 +495,7 @@ def test_barrier_failure_multi_token_persistent(mode, graphs):
     ids = minfer.prompt_ids(17, 20, V)
     pat = minfer.prompt_ids(5, 6, V)
     rep = (pat * 5)[:28]
-    opts = dict(max_ctx=128, persistent=2, graphs=graphs, spec=int(mode == "spec_device"))
+    opts = dict(max_ctx=128, persistent=2, graphs=graphs, spec=2 if mode == "spec_device" else 0)
 
     def run(eng, flag):
         if mode == "multi_step":
@@ -531,7 +531,7 @@ def test_barrier_failure_multi_token_persistent(mode, graphs):
 
 
 @pytest.mark.parametrize("kind", ["per_phase", "persistent", "multi_phases", "multi_persistent", "spec_host",
-                                  "spec_device"])
+                                  "spec_host_persistent", "spec_device"])
 def test_exact_argmax_ties_first_row(tmpdir_mi, kind):
     """Exact logit ties in every step kind: output.weight rows i, j identical and k, m
     their exact negation, every other row zero (conftest.tie_head_gguf), so each position's
@@ -546,7 +546,8 @@ def test_exact_argmax_ties_first_row(tmpdir_mi, kind):
     opts = dict(max_ctx=64)
     opts.update({"per_phase": dict(persistent=0), "persistent": dict(persistent=1),
                  "multi_phases": dict(persistent=1), "multi_persistent": dict(persistent=2),
-                 "spec_host": dict(spec=1, persistent=1), "spec_device": dict(spec=1, persistent=2)}[kind])
+                 "spec_host": dict(spec=1, persistent=1), "spec_host_persistent": dict(spec=1, persistent=2),
+                 "spec_device": dict(spec=2, persistent=2)}[kind])
     say("argmax ties via %s" % kind)
     with minfer.Engine(path, **opts) as eng:
         orc = O.Model(path, O.MODE_Q8ACT, plan=plan_of(eng), max_seq=64)

@@ -279,21 +279,21 @@ def test_spec_driven_on_device_equals_host_loop(case):
         prompt, n_gen, max_ctx = minfer.prompt_ids(31, 12, SMALL["n_vocab"]) * 6, 96, 200
     res = {}
     for mode, opts in (("plain", dict(spec=0)), ("host", dict(spec=1, persistent=1)),
-                       ("device", dict(spec=1, persistent=2))):
+                       ("host_persistent", dict(spec=1, persistent=2)), ("device", dict(spec=2, persistent=2))):
         say("%s: %s" % (case, mode))
         eng = minfer.Engine(path, max_ctx=max_ctx, **opts)
         eng.prefill(prompt)
         toks, margins = eng.generate(n_gen)
         res[mode] = (toks, margins, eng.stats())
         eng.close()
-    for mode in ("host", "device"):
+    for mode in ("host", "host_persistent", "device"):
         assert res[mode][0] == res["plain"][0], mode
         assert np.array_equal(bits(res[mode][1]), bits(res["plain"][1])), mode
     h, d = res["host"][2], res["device"][2]
     say("%s: %d steps, %d drafted, %d accepted (device %.1f ms, host loop %.1f ms)" %
         (case, d["steps"], d["drafted"], d["accepted"], d["decode_ms"], h["decode_ms"]))
     for k in ("steps", "tokens", "drafted", "accepted"):
-        assert d[k] == h[k], (k, d[k], h[k])
+        assert d[k] == h[k] == res["host_persistent"][2][k], (k, d[k], h[k])
 
 
 def test_spec_driven_on_device_stops_at_eos(tmp_path):
@@ -324,7 +324,7 @@ def test_spec_driven_on_device_stops_at_eos(tmp_path):
         f.write(np.uint32(want[first]).tobytes())
     res = {}
     for mode, opts in (("plain", dict(spec=0)), ("host", dict(spec=1, persistent=1)),
-                       ("device", dict(spec=1, persistent=2))):
+                       ("host_persistent", dict(spec=1, persistent=2)), ("device", dict(spec=2, persistent=2))):
         say("eos stop at output %d: %s" % (first, mode))
         eng = minfer.Engine(stop_path, max_ctx=200, stop_eos=1, **opts)
         eng.prefill(prompt)
@@ -335,7 +335,7 @@ def test_spec_driven_on_device_stops_at_eos(tmp_path):
         eng.close()
         say("  %d tokens, %d steps, %d drafted, %d accepted" % (len(toks), st["steps"], st["drafted"], st["accepted"]))
     assert res["plain"][0] == want[:first + 1]
-    for mode in ("host", "device"):
+    for mode in ("host", "host_persistent", "device"):
         assert res[mode][0] == res["plain"][0], mode
         assert np.array_equal(bits(res[mode][1]), bits(res["plain"][1])), mode
         assert np.array_equal(bits(res[mode][2]), bits(res["plain"][2])), mode
