@@ -631,8 +631,12 @@ int mi_check_layout(const mi_synth_shape* sh, int32_t max_ctx, int32_t n_cu, int
         for (int t = 0; t < T; t++) {
             chk("hT", lay::hT(E, 2 * l, t) + E - 1, lay::hT_size(D));
             chk("hT", lay::hT(E, 2 * l + 1, t) + E - 1, lay::hT_size(D));
-            for (int w : {lay::kXtQkv, lay::kXtO, lay::kXtGu})
-                chk("xT", lay::xT(E, lay::xt_slot(NL, l, w)) + ((size_t)t * nbE + nbE - 1) * kTRec + kTRec - 1, lay::xT_size(D));
+            for (int w : {lay::kXtQkv, lay::kXtO, lay::kXtGu}) {
+                // the writers' last byte, and the last byte of the GEMMs' copy of T tokens
+                chk("xT", lay::xT(E, lay::xt_slot(NL, l, w)) + t * lay::xT_tok(E) + (size_t)(nbE - 1) * kTRec + kTRec - 1,
+                    lay::xT_size(D));
+                chk("xT", lay::xT(E, lay::xt_slot(NL, l, w)) + (size_t)(t + 1) * lay::xT_tok(E) - 1, lay::xT_size(D));
+            }
             for (int sg = 0; sg < ks[3]; sg++)
                 chk("dT", lay::dT(ks[3], E, l) + ((size_t)sg * kMaxT + t) * E + E - 1, lay::dT_size(D));
             for (int sg = 0; sg < ks[1]; sg++)
@@ -671,7 +675,9 @@ int mi_check_layout(const mi_synth_shape* sh, int32_t max_ctx, int32_t n_cu, int
     if (T > 1) {
         for (int t = 0; t < T; t++) {
             chk("hT", lay::hT(E, 2 * (NL - 1) + 1, t) + E - 1, lay::hT_size(D));
-            chk("xT", lay::xT(E, lay::xt_slot(NL, NL, 0)) + ((size_t)t * nbE + nbE - 1) * kTRec + kTRec - 1, lay::xT_size(D));
+            chk("xT", lay::xT(E, lay::xt_slot(NL, NL, 0)) + t * lay::xT_tok(E) + (size_t)(nbE - 1) * kTRec + kTRec - 1,
+                lay::xT_size(D));
+            chk("xT", lay::xT(E, lay::xt_slot(NL, NL, 0)) + (size_t)(t + 1) * lay::xT_tok(E) - 1, lay::xT_size(D));
             chk("logitsT", (size_t)t * V + V - 1, lay::logitsT_size(D));
             for (int w = 0; w < n_cu; w++) chk("candT", lay::candT(w, t) + 3, lay::candT_size(D));
         }

@@ -1683,8 +1683,14 @@ __global__ __launch_bounds__(64) void k_argmax(const DModel* Mp, int ncand, int 
 // token by kT_in (residual + RMSNorm + quant, one workgroup per token) or kT_comb
 // (chunk merge + quant), so no workgroup repeats the per-token prologue.
 constexpr int kTChunks = 16;       // chunk sums of one segment held in LDS
-constexpr int kTXeBytes = kMaxT * (kMaxE / 32) * kTRec;
-constexpr int kTXfBytes = kMaxT * (kMaxFF / 32) * kTRec;
+// LDS stride of one token's records: nblk * kTRec rounded up to 16 mod 128, so that the
+// eight tokens' records of one block sit in different LDS banks (at a stride that is a
+// multiple of 128 bytes, the MFMA operand reads of the eight token slots all hit the same
+// bank group: an 8-way conflict). The xT slots in memory use the same stride
+// (lay::xT_tok), so a slot's T tokens come into LDS as one copy.
+__device__ __forceinline__ int xt_stride(int nblk) { return (int)lay::xT_tok(32 * nblk); }
+constexpr int kTXeBytes = kMaxT * ((kMaxE / 32) * kTRec + 128);
+constexpr int kTXfBytes = kMaxT * ((kMaxFF / 32) * kTRec + 128);
 constexpr int kTPBytes = kTChunks * kMaxT * 64 * 4;
 constexpr int kTGemvLds = kTXeBytes + kTPBytes;    // qkv, o, gate/up, lm_head
 constexpr int kTDownLds = kTXfBytes + kTPBytes;    // down
@@ -1739,9 +1745,10 @@ __device__ __forceinline__ void ttile_load(TTile<CB>& t, const uint8_t* tile, in
 }
 
 // chunk sums of one tile for the T tokens whose block records (kTRec bytes: 32 codes,
-// fp32 scale, 8*sum) are in LDS at XT[token][block]. acc[j][i]: row 16(2*(kg/2) + j) +
-// l%16, token 4*(kg%2) + i. Per (row, token) the float work is the single-token
-// chain: acc = fma(dw*dx, float(dot - 8*sum), acc) over the CB blocks in order, from 0.
+// fp32 scale, 8*sum) are in LDS at XT + token * rs + block * kTRec (rs = xt_stride).
+// acc[j][i]: row 16(2*(kg/2) + j) + l%16, token 4*(kg%2) + i. Per (row, token) the
+// float work is the single-token chain: acc = fma(dw*dx, float(dot - 8*sum), acc) over
+// the CB blocks in order, from 0.
 // The MFMA's C operand subtracts 8*sum (exact int32): lane kg's output slots are tokens
 // 4*(kg%2) + i of block 2p + kg/2. It leaves block 2p's results in lanes kg < 2 and block
 // 2p+1's in kg >= 2 for each row group; v_permlane32_swap of groups (q, q+2) hands each
@@ -1749,13 +1756,12 @@ __device__ __forceinline__ void ttile_load(TTile<CB>& t, const uint8_t* tile, in
 // token. Token slots T..kMaxT-1 read whatever their LDS records hold (XT has room for
 // kMaxT tokens, so the reads stay in bounds); their sums are never read.
 template <int CB>
-__device__ __forceinline__ void ttile_sums(const TTile<CB>& W, const uint8_t* XT, int nblk, int b0,
+__device__ __forceinline__ void ttile_sums(const TTile<CB>& W, const uint8_t* XT, int rs, int b0,
                                            float (&acc)[2][4], int lane) {
     const int col = lane & 15, kg = lane >> 4, h = kg & 1, hb = kg >> 1;
     const int am = ((col < 8) == (kg < 2)) ? -1 : 0;
-    const uint8_t* xa = XT + ((col & 7) * nblk + b0 + (col >> 3)) * kTRec + 8 * h;
-    const uint8_t* xr = XT + ((4 * h) * nblk + b0) * kTRec + 32;
-    const int rs = nblk * kTRec;
+    const uint8_t* xa = XT + (col & 7) * rs + (b0 + (col >> 3)) * kTRec + 8 * h;
+    const uint8_t* xr = XT + (4 * h) * rs + b0 * kTRec + 32;
 #pragma unroll
     for (int j = 0; j < 2; j++)
 #pragma unroll
@@ -1848,7 +1854,7 @@ __device__ __forceinline__ void tgemm_first(const PMat W, int wg, int nwg, int w
 template <int CB, class S, class F>
 __device__ __forceinline__ void tgemm_cb(const PMat W, int wg, int nwg, const uint8_t* XT, int nblk, int T, float* P,
                                          int wave, int lane, S stage, F out, TFirst<CB>& f) {
-    const int nseg = (W.rows >> 6) * W.ks;
+    const int nseg = (W.rows >> 6) * W.ks, rs = xt_stride(nblk);
     if (!f.issued) tgemm_first<CB>(W, wg, nwg, wave, lane, f);
     f.issued = false;
     int t = f.t, k = f.k;
@@ -1871,7 +1877,7 @@ __device__ __forceinline__ void tgemm_cb(const PMat W, int wg, int nwg, const ui
                 ttile_load<CB>(b, tile_ptr(W, g2, a0 + nk), lane);
             }
             float acc[2][4];
-            ttile_sums<CB>(a, XT, nblk, (c0 + k) * CB, acc, lane);
+            ttile_sums<CB>(a, XT, rs, (c0 + k) * CB, acc, lane);
             const int col = lane & 15, kg = lane >> 4;
             float* pc = P + (size_t)k * kMaxT * 64;
 #pragma unroll
@@ -1932,7 +1938,7 @@ __device__ __forceinline__ uint8_t* xT_at(MPtr M, int slot) { return M->xT + lay
 __device__ __forceinline__ void tstage_x(MPtr M, int slot, int T, uint8_t* XT) {
     const int tid = opaque_tid();
     DmaShare d{tid >> 6, (int)(blockDim.x >> 6), 0};
-    dma_share(xT_at(M, slot), XT, T * (M->E / 32) * kTRec, d, tid & 63);
+    dma_share(xT_at(M, slot), XT, T * xt_stride(M->E / 32), d, tid & 63);
     drain_vm();
 }
 
@@ -1976,7 +1982,7 @@ __device__ __forceinline__ void kT_in_body(MPtr M, int l, int kind, int t, float
     __syncthreads();
     const float* w = lm ? M->out_norm : qkv ? LY(M, l)->an : LY(M, l)->fn;
     const float sc = rms_scale(x, n, M->eps, lane);
-    uint8_t* xr = xT_at(M, lm ? xt_slot(M, M->NL, 0) : xt_slot(M, l, qkv ? kXtQkv : kXtGu)) + (size_t)t * nblk * kTRec;
+    uint8_t* xr = xT_at(M, lm ? xt_slot(M, M->NL, 0) : xt_slot(M, l, qkv ? kXtQkv : kXtGu)) + (size_t)t * xt_stride(nblk);
     for (int j = wave; 256 * j < n; j += kPWaves) {
         const int e0 = 256 * j + 4 * lane;
         const bool own = e0 < n;
@@ -2151,7 +2157,7 @@ __device__ __forceinline__ void kT_comb_item(MPtr M, int l, int item, int lane, 
         float d;
         quant32_vals(o[e], q, d, s8);
         const int el = hh * HD + 64 * e + lane;       // lanes 4k..4k+3 fill code word k of the block
-        uint8_t* rec = xT_at(M, xt_slot(M, l, kXtO)) + ((size_t)t * nblk + (el >> 5)) * kTRec;
+        uint8_t* rec = xT_at(M, xt_slot(M, l, kXtO)) + (size_t)t * xt_stride(nblk) + (el >> 5) * kTRec;
         const uint32_t b = (uint32_t)(q & 0xFF);
         const uint32_t wd = b | (__shfl_down(b, 1) << 8) | (__shfl_down(b, 2) << 16) | (__shfl_down(b, 3) << 24);
         if ((lane & 3) == 0) st_x<PS>(reinterpret_cast<uint32_t*>(rec + (el & 31)), wd);
@@ -2228,7 +2234,7 @@ __device__ __forceinline__ void kT_down_body(MPtr M, int l, int T, uint8_t* smem
             blo = min(blo, c0 * W.cb);
             bhi = max(bhi, c1 * W.cb);
         }
-        const int nb = max(0, bhi - blo), n8 = T * nb * (kTRec / 8);
+        const int nb = max(0, bhi - blo), n8 = T * nb * (kTRec / 8), rs = xt_stride(nblk);
         // every load of a round in flight before its stores
         constexpr int U = 4;
         for (int i0 = opaque_tid(); i0 < n8; i0 += U * (int)blockDim.x) {
@@ -2242,7 +2248,7 @@ __device__ __forceinline__ void kT_down_body(MPtr M, int l, int T, uint8_t* smem
                     const int rcd = i / (kTRec / 8), k = i - rcd * (kTRec / 8), t = div_small(rcd, max(nb, 1));
                     const int b = blo + rcd - t * nb;
                     v[u] = reinterpret_cast<const uint2*>(actT_at(M, l, t) + (size_t)b * kActRec)[k];
-                    at[u] = (int)(((size_t)t * nblk + b) * kTRec) + 8 * k;
+                    at[u] = t * rs + b * kTRec + 8 * k;
                 }
             }
 #pragma unroll

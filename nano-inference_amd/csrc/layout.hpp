@@ -49,8 +49,15 @@ LAYFN size_t attT_size(const Dims& d) { return (size_t)d.NL * kMaxT * d.NH * d.m
 // gate/up input, 3 NL the lm_head input
 constexpr int kXtQkv = 0, kXtO = 1, kXtGu = 2;
 LAYFN int xt_slot(int NL, int l, int which) { return l < NL ? 3 * l + which : 3 * NL; }
-LAYFN size_t xT(int E, int slot) { return (size_t)slot * kMaxT * (E / 32) * kTRec; }   // bytes; + (t * E/32 + b) * kTRec + byte
-LAYFN size_t xT_size(const Dims& d) { return (size_t)(3 * d.NL + 1) * kMaxT * (d.E / 32) * kTRec; }
+// bytes per token in an xT slot: E/32 records of kTRec bytes, rounded up to 16 mod 128.
+// The GEMMs copy a slot's tokens into LDS as they lie, and at a stride that is a multiple
+// of 128 bytes the eight tokens' records of one block would share LDS banks.
+LAYFN size_t xT_tok(int E) {
+    const size_t s = (size_t)(E / 32) * kTRec;
+    return s + ((16 - s) & 127);
+}
+LAYFN size_t xT(int E, int slot) { return (size_t)slot * kMaxT * xT_tok(E); }   // bytes; + t * xT_tok(E) + b * kTRec + byte
+LAYFN size_t xT_size(const Dims& d) { return (size_t)(3 * d.NL + 1) * kMaxT * xT_tok(d.E); }
 LAYFN size_t oT(int ks, int E, int l) { return (size_t)l * ks * kMaxT * E; }              // + (s * kMaxT + t) * E + row
 LAYFN size_t oT_size(const Dims& d) { return (size_t)d.NL * d.ks_o * kMaxT * d.E; }
 LAYFN size_t actT(int FF, int l, int t) { return ((size_t)l * kMaxT + t) * (FF / 32) * kActRec; }  // bytes
