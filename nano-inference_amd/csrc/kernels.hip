@@ -2040,8 +2040,9 @@ __global__ __launch_bounds__(kPThreads) void kT_qkv(const DModel* Mp, int l, int
 // head) pairs of the group against it, one attn_core each (the single-token chunk
 // arithmetic), writing record (t, h, c). Token t uses the chunk's rows up to pos + t.
 // The item holding token T-1 appends the step's rows of the chunk to the cache.
+// LDS: the chunk's K tile and V rows, then per wave two q rows and two probability rows
 template <int HD>
-constexpr int kt_attn_lds() { return 2 * 64 * HD * 2 + kPWaves * HD * 4; }
+constexpr int kt_attn_lds() { return 2 * 64 * HD * 2 + kPWaves * (2 * HD + 2 * 64) * 4; }
 
 template <int HD, bool PS>
 __device__ __forceinline__ void kT_attn_body(MPtr M, int l, int T, uint8_t* smem, int wg, int nwg, int pos) {
@@ -2049,7 +2050,8 @@ __device__ __forceinline__ void kT_attn_body(MPtr M, int l, int T, uint8_t* smem
     constexpr int half = HD / 2, DPL = HD / 64;
     uint4* kls = reinterpret_cast<uint4*>(smem);
     __half* vls = reinterpret_cast<__half*>(smem + 64 * HD * 2);
-    float* qs = reinterpret_cast<float*>(smem + 2 * 64 * HD * 2) + wave * HD;
+    float* qs = reinterpret_cast<float*>(smem + 2 * 64 * HD * 2) + wave * (2 * HD + 2 * 64);
+    float* pl = qs + 2 * HD;
     const LPtr Ly = LY(M, l);
     const int G = M->G, NKV = M->NKV, ks = Ly->qkv.ks, QKV = M->QKV;
     const int nchx = (pos + T - 1 + kAttnChunk) / kAttnChunk;
@@ -2066,14 +2068,14 @@ __device__ __forceinline__ void kT_attn_body(MPtr M, int l, int T, uint8_t* smem
         for (int s = 1; s < ks; s++) v = __fadd_rn(v, part[((size_t)s * kMaxT + tok) * QKV + row]);
         return __fadd_rn(v, bq[row]);
     };
-    // q of (token t, head h), rotated at position pos + t, into the wave's qs
-    auto load_q = [&](int t, int h) {
+    // q of (token t, head h), rotated at position pos + t, into the wave's q row j
+    auto load_q = [&](int t, int h, int j) {
         if (lane < half) {
             const int rq = h * HD;
             const float2 cz = M->rope[(size_t)(pos + t) * half + ip];
             const float x0 = fin(t, rq + ip), x1 = fin(t, rq + ip + half);
-            qs[ip] = __fsub_rn(__fmul_rn(x0, cz.x), __fmul_rn(x1, cz.y));
-            qs[ip + half] = __fadd_rn(__fmul_rn(x0, cz.y), __fmul_rn(x1, cz.x));
+            qs[j * HD + ip] = __fsub_rn(__fmul_rn(x0, cz.x), __fmul_rn(x1, cz.y));
+            qs[j * HD + ip + half] = __fadd_rn(__fmul_rn(x0, cz.y), __fmul_rn(x1, cz.x));
         }
     };
     for (int it = wg; it < total; it += nwg) {
@@ -2097,9 +2099,22 @@ __device__ __forceinline__ void kT_attn_body(MPtr M, int l, int T, uint8_t* smem
             v0 = __float2half(fin(wave, rv + ip));
             v1 = __float2half(fin(wave, rv + ip + half));
         }
-        // the wave's first (token, head) pair of the group
-        const int npair = (tb - ta + 1) * G;
-        if (wave < npair) load_q(ta + wave / G, kvh * G + wave % G);
+        // (token, head) pairs i = ta.., in token-major order: wave w takes pairs w*ppw ..
+        // w*ppw + ppw - 1, two at a time (the q rows of both loaded together, and two
+        // heads of one token run as one attn_core_h<HD, 2>: the same chains per head as
+        // attn_core, the K and V values read once for both). The first two q rows load
+        // while the chunk's rows come in.
+        const int npair = (tb - ta + 1) * G, ppw = (npair + kPWaves - 1) / kPWaves;
+        auto pair_th = [&](int i, int& t, int& h) {
+            t = ta + i / G;
+            h = kvh * G + i % G;
+        };
+        {
+            const int i0 = wave * ppw;
+            int t, h;
+            if (i0 < npair) { pair_th(i0, t, h); load_q(t, h, 0); }
+            if (ppw > 1 && i0 + 1 < npair) { pair_th(i0 + 1, t, h); load_q(t, h, 1); }
+        }
         if (wave == 0) drain_vm();
         __syncthreads();                                           // cached rows landed
         if (mine && lane < half) {
@@ -2117,20 +2132,42 @@ __device__ __forceinline__ void kT_attn_body(MPtr M, int l, int T, uint8_t* smem
             }
         }
         __syncthreads();                                           // the chunk's rows complete
-        for (int i = wave; i < npair; i += kPWaves) {
-            const int t = ta + i / G, h = kvh * G + i % G;
-            if (i != wave) {
-                wave_lds_sync();
-                load_q(t, h);
-            }
-            wave_lds_sync();
-            if (t0 > pos + t) continue;                            // the chunk is past this token
-            float m, lsum, acc[DPL];
-            attn_core<HD>(kls, qs, vls, min(kAttnChunk, pos + t + 1 - t0), M->scale, lane, m, lsum, acc);
+        auto store_rec = [&](int t, int h, float m, float lsum, const float (&acc)[DPL]) {
             float* rec = attT_at(M, l, t) + ((size_t)h * M->maxch + c) * M->arec;
 #pragma unroll
             for (int e = 0; e < DPL; e++) st_x<PS>(rec + DPL * lane + e, acc[e]);
             if (lane == 0) { st_x<PS>(rec + HD, m); st_x<PS>(rec + HD + 1, lsum); }
+        };
+        for (int j0 = 0; j0 < ppw; j0 += 2) {
+            const int i0 = wave * ppw + j0;
+            if (i0 >= npair) break;
+            const bool two = j0 + 1 < ppw && i0 + 1 < npair;
+            int ta0, ha, tb0 = -1, hb = 0;
+            pair_th(i0, ta0, ha);
+            if (two) pair_th(i0 + 1, tb0, hb);
+            if (j0 > 0) {
+                wave_lds_sync();                                   // the last round's q rows are read
+                load_q(ta0, ha, 0);
+                if (two) load_q(tb0, hb, 1);
+            }
+            wave_lds_sync();
+            if (two && tb0 == ta0) {
+                if (t0 > pos + ta0) continue;                      // the chunk is past this token
+                float m[2], lsum[2], acc[2][DPL];
+                attn_core_h<HD, 2>(kls, qs, 2, vls, min(kAttnChunk, pos + ta0 + 1 - t0), M->scale, lane, pl, m, lsum, acc);
+                store_rec(ta0, ha, m[0], lsum[0], acc[0]);
+                store_rec(ta0, hb, m[1], lsum[1], acc[1]);
+            } else {
+                for (int k = 0; k < (two ? 2 : 1); k++) {
+                    const int t = k ? tb0 : ta0, h = k ? hb : ha;
+                    if (t0 > pos + t) continue;                    // the chunk is past this token
+                    if (k) wave_lds_sync();                        // pl is reused
+                    float m[1], lsum[1], acc[1][DPL];
+                    attn_core_h<HD, 1>(kls, qs + k * HD, 1, vls, min(kAttnChunk, pos + t + 1 - t0), M->scale, lane, pl, m,
+                                       lsum, acc);
+                    store_rec(t, h, m[0], lsum[0], acc[0]);
+                }
+            }
         }
         __syncthreads();                                           // LDS is reused by the next item
     }
