@@ -1245,9 +1245,65 @@ __device__ __forceinline__ void attn_run(MPtr M, int l, int pos, int wg, int nwg
 // more than kAttnSplit; each split of kAttnSplit chunks with all its loads issued at
 // once (M_s = split max, w = exp(m - M_s), den and o as fma chains in chunk order),
 // then the splits in order scaled by exp(M_s - M). Returns o / den per lane and dim.
+// Up to two splits (nch <= 2 kAttnSplit) every record's loads go out before any of the
+// arithmetic (one memory round trip instead of three); the arithmetic is the same.
+template <int HD>
+__device__ __forceinline__ void comb_wave2(const float* r, int arec, int nch, int lane, float (&out)[HD / 64]) {
+    constexpr int DPL = HD / 64, NS = kAttnSplit;
+    // lane c holds chunk c's (m, l); ov[i][e] is chunk i's o at dim 64e + lane
+    const bool in = lane < nch;
+    const float mv = in ? r[lane * arec + HD] : -__builtin_inff();
+    const float lv = in ? r[lane * arec + HD + 1] : 0.f;
+    float ov[2 * NS][DPL];
+#pragma unroll
+    for (int i = 0; i < 2 * NS; i++)
+#pragma unroll
+        for (int e = 0; e < DPL; e++) ov[i][e] = i < nch ? r[i * arec + 64 * e + lane] : 0.f;
+    const int len0 = min(NS, nch), len1 = nch - len0;
+    const float Ms0 = wave_max(lane < len0 ? mv : -__builtin_inff());
+    const float Ms1 = wave_max(lane >= NS ? mv : -__builtin_inff());
+    // chunk c of split s: w = exp(m_c - M_s) (each lane's chunk is in one split)
+    const float wv = in ? mi_expf(__fsub_rn(mv, lane < NS ? Ms0 : Ms1)) : 0.f;
+    float ds0 = 0.f, ds1 = 0.f, as0[DPL], as1[DPL];
+#pragma unroll
+    for (int e = 0; e < DPL; e++) as0[e] = as1[e] = 0.f;
+#pragma unroll
+    for (int i = 0; i < NS; i++)
+        if (i < len0) {
+            const float wi = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wv), i));
+            const float li = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(lv), i));
+            ds0 = __fmaf_rn(li, wi, ds0);
+#pragma unroll
+            for (int e = 0; e < DPL; e++) as0[e] = __fmaf_rn(ov[i][e], wi, as0[e]);
+        }
+    if (len1 <= 0) {
+#pragma unroll
+        for (int e = 0; e < DPL; e++) out[e] = __fdiv_rn(as0[e], ds0);
+        return;
+    }
+#pragma unroll
+    for (int i = 0; i < NS; i++)
+        if (i < len1) {
+            const float wi = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wv), NS + i));
+            const float li = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(lv), NS + i));
+            ds1 = __fmaf_rn(li, wi, ds1);
+#pragma unroll
+            for (int e = 0; e < DPL; e++) as1[e] = __fmaf_rn(ov[NS + i][e], wi, as1[e]);
+        }
+    const float Mx = fmaxf(Ms0, Ms1);
+    const float w0 = mi_expf(__fsub_rn(Ms0, Mx)), w1 = mi_expf(__fsub_rn(Ms1, Mx));
+    float den = __fmaf_rn(ds0, w0, 0.f);
+    den = __fmaf_rn(ds1, w1, den);
+#pragma unroll
+    for (int e = 0; e < DPL; e++) out[e] = __fdiv_rn(__fmaf_rn(as1[e], w1, __fmaf_rn(as0[e], w0, 0.f)), den);
+}
 template <int HD>
 __device__ __forceinline__ void comb_wave(const float* r, int arec, int nch, int lane, float (&out)[HD / 64]) {
     constexpr int DPL = HD / 64;
+    if (nch <= 2 * kAttnSplit) {
+        comb_wave2<HD>(r, arec, nch, lane, out);
+        return;
+    }
     float Mx = -__builtin_inff();
     if (nch > kAttnSplit) {
         for (int c = lane; c < nch; c += 64) Mx = fmaxf(Mx, r[c * arec + HD]);
