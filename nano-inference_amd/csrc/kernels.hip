@@ -1917,7 +1917,7 @@ __device__ __forceinline__ void tgemm_cb(const PMat W, int wg, int nwg, const ui
     bool have = f.have;
     TTile<CB>& cur = f.tile;
     TTile<CB> nx;
-    stage();
+    if (wg < nseg) stage();                          // a workgroup with no segment stages nothing
     __syncthreads();
     int nt = t, nk = k;
     bool hn = have && tnext(W, nseg, nwg, wave, nt, nk);
@@ -2008,7 +2008,13 @@ __device__ __forceinline__ void kT_in_body(MPtr M, int l, int kind, int t, float
     const bool qkv = kind == PH_QKV, lm = kind == PH_LM, dsrc = kind != PH_GU;
     const int pl = qkv ? l - 1 : lm ? M->NL - 1 : l;
     float* hdst = M->hT + hT_at(M, qkv ? 2 * l : 2 * l + 1, t);
-    for (int e0 = 256 * wave + 4 * lane; e0 < n; e0 += 256 * kPWaves) {
+    // wave j quantizes slice j (n <= kMaxE: one slice per wave at most); its norm
+    // weights are loaded with the inputs, not after the sum of squares
+    static_assert(kMaxE <= 256 * kPWaves, "one 256-element slice per wave");
+    const float* w = lm ? M->out_norm : qkv ? LY(M, l)->an : LY(M, l)->fn;
+    const int ew = 256 * wave + 4 * lane;
+    const float4 wv = ew < n ? ldg4(w + ew) : make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int e0 = ew; e0 < n; e0 += 256 * kPWaves) {
         float4 v;
         if (qkv && l == 0) {
             v = ldg4(M->emb + (size_t)M->tokbuf[pos + t] * n + e0);
@@ -2036,19 +2042,17 @@ __device__ __forceinline__ void kT_in_body(MPtr M, int l, int kind, int t, float
         }
     }
     __syncthreads();
-    const float* w = lm ? M->out_norm : qkv ? LY(M, l)->an : LY(M, l)->fn;
     const float sc = rms_scale(x, n, M->eps, lane);
     uint8_t* xr = xT_at(M, lm ? xt_slot(M, M->NL, 0) : xt_slot(M, l, qkv ? kXtQkv : kXtGu)) + (size_t)t * xt_stride(nblk);
-    for (int j = wave; 256 * j < n; j += kPWaves) {
-        const int e0 = 256 * j + 4 * lane;
-        const bool own = e0 < n;
+    if (256 * wave < n) {
+        const bool own = ew < n;
         float4 y = make_float4(0.f, 0.f, 0.f, 0.f);
         if (own) {
-            const float4 xv = ld4(x + e0), wv = ldg4(w + e0);
+            const float4 xv = ld4(x + ew);
             y = make_float4(__fmul_rn(__fmul_rn(xv.x, sc), wv.x), __fmul_rn(__fmul_rn(xv.y, sc), wv.y),
                             __fmul_rn(__fmul_rn(xv.z, sc), wv.z), __fmul_rn(__fmul_rn(xv.w, sc), wv.w));
         }
-        quant_slice<P>(y, own, e0, xr, lane, kTRec);
+        quant_slice<P>(y, own, ew, xr, lane, kTRec);
     }
 }
 __global__ __launch_bounds__(kPThreads) void kT_in(const DModel* Mp, int l, int kind) {
@@ -2100,8 +2104,53 @@ __global__ __launch_bounds__(kPThreads) void kT_qkv(const DModel* Mp, int l, int
 template <int HD>
 constexpr int kt_attn_lds() { return 2 * 64 * HD * 2 + kPWaves * (2 * HD + 2 * 64) * 4; }
 
+// The items of a T-token attention phase: tokens per item tg is the smallest power of
+// two that keeps the items within one per workgroup (more tokens per item: fewer K/V
+// stagings, more pairs per wave). Item it runs on workgroup nwg - 1 - it (+ k nwg), so
+// that the first items sit on the last workgroups, which have no QKV rows.
+struct KtAttnPlan { int nchx, tg, ngrp, total; };
+__device__ __forceinline__ KtAttnPlan kt_attn_plan(int NKV, int pos, int T, int nwg) {
+    KtAttnPlan P;
+    P.nchx = (pos + T - 1 + kAttnChunk) / kAttnChunk;
+    P.tg = 1;
+    while (P.tg < T && NKV * P.nchx * ((T + P.tg - 1) / P.tg) > nwg) P.tg *= 2;
+    P.ngrp = (T + P.tg - 1) / P.tg;
+    P.total = NKV * P.nchx * P.ngrp;
+    return P;
+}
+// item it: kv head, chunk, its tokens ta..tb; false when the chunk starts past them
+__device__ __forceinline__ bool kt_attn_item(const KtAttnPlan& P, int it, int T, int pos, int& kvh, int& c, int& ta,
+                                             int& tb) {
+    const int grp = it % P.ngrp, rest = it / P.ngrp;
+    c = rest % P.nchx;
+    kvh = rest / P.nchx;
+    ta = grp * P.tg;
+    tb = min(T, ta + P.tg) - 1;
+    return c * kAttnChunk <= pos + tb;
+}
+// The cached K/V rows (positions before pos) of this workgroup's first attention item
+// into LDS, issued by wave 0 during the QKV phase by a workgroup without QKV rows: the
+// cache rows do not depend on this step. True (on every wave) when issued.
+template <int HD>
+__device__ __forceinline__ bool kt_attn_prefetch(MPtr M, int l, int T, int pos, int wg, int nwg, uint8_t* smem) {
+    const KtAttnPlan P = kt_attn_plan(M->NKV, pos, T, nwg);
+    const int it = nwg - 1 - wg;
+    int kvh, c, ta, tb;
+    if (it >= P.total || !kt_attn_item(P, it, T, pos, kvh, c, ta, tb)) return false;
+    const int t0 = c * kAttnChunk, ncached = min(kAttnChunk, max(0, pos - t0));
+    if (ncached <= 0) return false;
+    if ((threadIdx.x >> 6) == 0) {
+        const size_t rowbase = lay::kv(M->NKV, M->maxseq, 1, l, kvh, 0);
+        attn_issue_kv<HD>(M->kc + rowbase * HD, M->vc + rowbase * HD, t0, ncached, reinterpret_cast<uint4*>(smem),
+                          reinterpret_cast<__half*>(smem + 64 * HD * 2), opaque_tid() & 63);
+    }
+    return true;
+}
+
+// kv_pre: kt_attn_prefetch issued this workgroup's first item's cached rows
 template <int HD, bool PS>
-__device__ __forceinline__ void kT_attn_body(MPtr M, int l, int T, uint8_t* smem, int wg, int nwg, int pos) {
+__device__ __forceinline__ void kT_attn_body(MPtr M, int l, int T, uint8_t* smem, int wg, int nwg, int pos,
+                                             bool kv_pre = false) {
     TBODY
     constexpr int half = HD / 2, DPL = HD / 64;
     uint4* kls = reinterpret_cast<uint4*>(smem);
@@ -2110,13 +2159,8 @@ __device__ __forceinline__ void kT_attn_body(MPtr M, int l, int T, uint8_t* smem
     float* pl = qs + 2 * HD;
     const LPtr Ly = LY(M, l);
     const int G = M->G, NKV = M->NKV, ks = Ly->qkv.ks, QKV = M->QKV;
-    const int nchx = (pos + T - 1 + kAttnChunk) / kAttnChunk;
-    // tokens per item: the smallest power of two that keeps the items within one per
-    // workgroup (more tokens per item: fewer K/V stagings, more pairs per wave)
-    int tg = 1;
-    while (tg < T && NKV * nchx * ((T + tg - 1) / tg) > nwg) tg *= 2;
-    const int ngrp = (T + tg - 1) / tg;
-    const int total = NKV * nchx * ngrp, ip = lane % half;
+    const KtAttnPlan AP = kt_attn_plan(NKV, pos, T, nwg);
+    const int total = AP.total, ip = lane % half;
     const float* part = qkvT_at(M, l);
     const float* bq = Ly->bqkv;
     auto fin = [&](int tok, int row) {
@@ -2134,13 +2178,12 @@ __device__ __forceinline__ void kT_attn_body(MPtr M, int l, int T, uint8_t* smem
             qs[j * HD + ip + half] = __fadd_rn(__fmul_rn(x0, cz.y), __fmul_rn(x1, cz.x));
         }
     };
-    for (int it = wg; it < total; it += nwg) {
-        const int grp = it % ngrp, rest = it / ngrp, c = rest % nchx, kvh = rest / nchx;
-        const int ta = grp * tg, tb = min(T, ta + tg) - 1, t0 = c * kAttnChunk;
-        if (t0 > pos + tb) continue;                               // uniform over the workgroup
-        const int ncached = min(kAttnChunk, max(0, pos - t0));
+    for (int it = nwg - 1 - wg; it < total; it += nwg) {
+        int kvh, c, ta, tb;
+        if (!kt_attn_item(AP, it, T, pos, kvh, c, ta, tb)) continue;   // uniform over the workgroup
+        const int t0 = c * kAttnChunk, ncached = min(kAttnChunk, max(0, pos - t0));
         const size_t rowbase = lay::kv(NKV, M->maxseq, 1, l, kvh, 0);     // row index of position 0
-        if (wave == 0 && ncached > 0)
+        if (wave == 0 && ncached > 0 && !(kv_pre && it == nwg - 1 - wg))
             attn_issue_kv<HD>(M->kc + rowbase * HD, M->vc + rowbase * HD, t0, ncached, kls, vls, lane);
         // this step's row pos + wave, if the chunk holds it and a token of the group sees it
         const int p = pos + wave;
@@ -2542,9 +2585,11 @@ __global__ __launch_bounds__(kPThreads) void kT_step(const DModel* Mp, int T) {
     for (int l = 0; l < M->NL; l++) {
         if (wg < T) kT_in_body<true>(M, l, PH_QKV, wg, xs, pos);
         barrier_pre(&LY(M, l)->qkv);
+        const PMat Wq = ldmat(&LY(M, l)->qkv);
+        const bool kv_pre = wg >= (Wq.rows >> 6) * Wq.ks && kt_attn_prefetch<HD>(M, l, T, pos, wg, nwg, smem);
         kT_qkv_body<true>(M, l, T, smem, wg, nwg, pre);
         barrier();
-        kT_attn_body<HD, true>(M, l, T, smem, wg, nwg, pos);
+        kT_attn_body<HD, true>(M, l, T, smem, wg, nwg, pos, kv_pre);
         barrier();
         for (int it = wg * kPWaves + wave; it < T * M->NH; it += nwg * kPWaves) kT_comb_item<HD, true>(M, l, it, lane, pos);
         barrier_pre(&LY(M, l)->o);
