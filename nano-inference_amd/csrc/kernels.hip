@@ -2561,6 +2561,11 @@ __global__ __launch_bounds__(kPThreads) void kT_step(const DModel* Mp, int T) {
     __shared__ __align__(16) uint8_t smem[kTStepLds];
     const int wg = blockIdx.x, nwg = gridDim.x, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     float* xs = reinterpret_cast<float*>(smem);
+    // the light phases (kT_in: token t; the chunk merge items) run on the last
+    // workgroups, rw = nwg - 1 - wg: the GEMM segments start at workgroup 0, so these
+    // have the least GEMM work in the phase after (their first tiles are issued late,
+    // when they reach the barrier last)
+    const int rw = nwg - 1 - wg;
     GridBar gb = bar_init(M->bar, M->err);
     auto barrier = [&] {
         drain_vm();
@@ -2583,7 +2588,7 @@ __global__ __launch_bounds__(kPThreads) void kT_step(const DModel* Mp, int T) {
         __syncthreads();
     };
     for (int l = 0; l < M->NL; l++) {
-        if (wg < T) kT_in_body<true>(M, l, PH_QKV, wg, xs, pos);
+        if (rw < T) kT_in_body<true>(M, l, PH_QKV, rw, xs, pos);
         barrier_pre(&LY(M, l)->qkv);
         const PMat Wq = ldmat(&LY(M, l)->qkv);
         const bool kv_pre = wg >= (Wq.rows >> 6) * Wq.ks && kt_attn_prefetch<HD>(M, l, T, pos, wg, nwg, smem);
@@ -2591,18 +2596,18 @@ __global__ __launch_bounds__(kPThreads) void kT_step(const DModel* Mp, int T) {
         barrier();
         kT_attn_body<HD, true>(M, l, T, smem, wg, nwg, pos, kv_pre);
         barrier();
-        for (int it = wg * kPWaves + wave; it < T * M->NH; it += nwg * kPWaves) kT_comb_item<HD, true>(M, l, it, lane, pos);
+        for (int it = rw * kPWaves + wave; it < T * M->NH; it += nwg * kPWaves) kT_comb_item<HD, true>(M, l, it, lane, pos);
         barrier_pre(&LY(M, l)->o);
         kT_o_body<true>(M, l, T, smem, wg, nwg, pre);
         barrier();
-        if (wg < T) kT_in_body<true>(M, l, PH_GU, wg, xs, pos);
+        if (rw < T) kT_in_body<true>(M, l, PH_GU, rw, xs, pos);
         barrier_pre(&LY(M, l)->gu);
         kT_gu_body<true>(M, l, T, smem, wg, nwg, pre);
         barrier_pre(&LY(M, l)->d);
         kT_down_body<true>(M, l, T, smem, wg, nwg, pre);
         barrier();
     }
-    if (wg < T) kT_in_body<true>(M, M->NL - 1, PH_LM, wg, xs, pos);
+    if (rw < T) kT_in_body<true>(M, M->NL - 1, PH_LM, rw, xs, pos);
     barrier_pre(&M->lm);
     kT_lm_body<true>(M, T, smem, wg, nwg, pre);
     barrier();
