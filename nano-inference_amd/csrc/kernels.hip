@@ -508,12 +508,17 @@ __device__ __forceinline__ GridBar bar_init(uint32_t* bar, const int32_t* err) {
     b.dead = 0;
     return b;
 }
-__device__ __forceinline__ void ctl_barrier(GridBar& b, int32_t* err) {
+// after(): work issued right after this workgroup's arrival, before the polls (loads
+// issued there complete before the first poll's result: loads retire in order)
+struct NoWork { __device__ void operator()() const {} };
+template <class F = NoWork>
+__device__ __forceinline__ void ctl_barrier(GridBar& b, int32_t* err, F after = F{}) {
     drain_vm();
-    if (b.dead) return;
+    if (b.dead) { after(); return; }
     const int lane = threadIdx.x & 63;
     b.need += b.per;
     if (lane == 0) __hip_atomic_fetch_add(b.arrive, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    after();
     // every lane loads and the exit tests are ballots: the loop is scalar control flow.
     // Lane kErrLane reads *err in the same round trip: once any barrier of this launch
     // (or of an earlier launch in the stream) has failed, or the host raised the flag,
@@ -2583,8 +2588,11 @@ __global__ __launch_bounds__(kPThreads) void kT_step(const DModel* Mp, int T) {
         const PMat W = ldmat(Wp);
         drain_vm();
         __syncthreads();
-        if (wave == 0) ctl_barrier(gb, M->err);
-        if (W.cb == 8) tgemm_first<8>(W, wg, nwg, wave, opaque_tid() & 63, pre);
+        auto first = [&] {
+            if (W.cb == 8) tgemm_first<8>(W, wg, nwg, wave, opaque_tid() & 63, pre);
+        };
+        if (wave == 0) ctl_barrier(gb, M->err, first);
+        else first();
         __syncthreads();
     };
     for (int l = 0; l < M->NL; l++) {
