@@ -397,7 +397,15 @@ def main():
                     help="with --attention-only: launch eagerly instead of replaying a graph (for kernel traces)")
     ap.add_argument("--gemv-only", action="store_true",
                     help="only run the config1 GEMV microbench, print its JSON and exit (for kernel traces)")
+    ap.add_argument("--verify-only", action="store_true",
+                    help="only run the config4 verify-step cost (T=8 vs T=1), print its JSON and exit "
+                         "(for kernel traces)")
     args = ap.parse_args()
+    if args.verify_only:
+        res = verify_cost()
+        log("verify step: %s" % res)
+        print(json.dumps({"verify_step": res}), flush=True)
+        return
     if args.gemv_only:
         import torch
         res = gemv_microbench(torch)
