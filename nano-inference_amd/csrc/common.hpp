@@ -92,7 +92,7 @@ struct DModel {
     float* hT;                     // [2*NL+1][kMaxT][E]
     float* qkvT;                   // [NL][ks_qkv][kMaxT][QKV]
     float* attT;                   // [NL][kMaxT][NH][maxch][arec]
-    float* oT;                     // [NL][ks_o][kMaxT][E]
+    float* oT;                     // [NL][ks_oT = O's chunks per row][kMaxT][E]
     uint8_t* actT;                 // [NL][kMaxT][FF/32][kActRec]
     uint8_t* xT;                   // [3*NL+1][kMaxT][E/32][kTRec] int8 records of the GEMM inputs: per
                                    // layer the qkv, o and gate/up inputs, then lm_head's (xT_slots)

@@ -308,7 +308,8 @@ static int alloc_buf(mi_engine* e, T** p, size_t count) {
 }
 
 // the buffer-layout facts of a model shape (layout.hpp)
-static Dims step_dims(int NL, int E, int FF, int NH, int NKV, int V, int maxseq, const int ks[5], int nwg) {
+static Dims step_dims(int NL, int E, int FF, int NH, int NKV, int V, int maxseq, const int cb[5], const int ks[5],
+                      int nwg) {
     Dims d{};
     d.NL = NL; d.E = E; d.FF = FF; d.NH = NH; d.NKV = NKV; d.HD = E / NH; d.V = V;
     d.QKV = NH * d.HD + 2 * NKV * d.HD;
@@ -316,6 +317,7 @@ static Dims step_dims(int NL, int E, int FF, int NH, int NKV, int V, int maxseq,
     d.maxch = (maxseq + kAttnChunk - 1) / kAttnChunk;
     d.arec = attn_record_floats(d.HD);
     d.ks_qkv = ks[0]; d.ks_o = ks[1]; d.ks_d = ks[3];
+    d.ks_oT = (E / 32) / cb[1];
     d.nwg = nwg;
     return d;
 }
@@ -488,7 +490,7 @@ static int load_impl(mi_engine* e, const char* path) {
     }
     M.arec = attn_record_floats(e->HD);
     const size_t NL = (size_t)e->NL;
-    const Dims D = step_dims(e->NL, e->E, e->FF, e->NH, e->NKV, e->V, e->maxseq, e->ks, e->n_cu);
+    const Dims D = step_dims(e->NL, e->E, e->FF, e->NH, e->NKV, e->V, e->maxseq, e->cb, e->ks, e->n_cu);
     if ((rc = alloc_buf(e, &M.kc, lay::kv_size(D))) || (rc = alloc_buf(e, &M.vc, lay::kv_size(D))) ||
         (rc = alloc_buf(e, &M.tokbuf, (size_t)e->maxseq + 1)) ||
         (rc = alloc_buf(e, &M.hbuf, lay::hbuf_size(D))) ||
@@ -593,7 +595,7 @@ int mi_check_layout(const mi_synth_shape* sh, int32_t max_ctx, int32_t n_cu, int
     if (NL < 1 || NH < 1 || NKV < 1 || E % NH || NH % NKV || E % 64 || FF % 64 || V % 64) return MI_ERR_ARG;
     int cb[5], ks[5];
     if (!kernels_plan(E, FF, cb, ks)) return fail("no plan for E=%d FF=%d", E, FF);
-    const Dims D = step_dims(NL, E, FF, NH, NKV, V, max_ctx, ks, n_cu);
+    const Dims D = step_dims(NL, E, FF, NH, NKV, V, max_ctx, cb, ks, n_cu);
     const int HD = D.HD, G = NH / NKV, QKV = D.QKV, KVD = NKV * HD, nbE = E / 32, nbF = FF / 32;
     if (pos + T > D.maxseq) return fail("positions %d..%d past the context %d (the engine rejects the step)", pos,
                                         pos + T - 1, D.maxseq);
@@ -639,8 +641,8 @@ int mi_check_layout(const mi_synth_shape* sh, int32_t max_ctx, int32_t n_cu, int
             }
             for (int sg = 0; sg < ks[3]; sg++)
                 chk("dT", lay::dT(ks[3], E, l) + ((size_t)sg * kMaxT + t) * E + E - 1, lay::dT_size(D));
-            for (int sg = 0; sg < ks[1]; sg++)
-                chk("oT", lay::oT(ks[1], E, l) + ((size_t)sg * kMaxT + t) * E + E - 1, lay::oT_size(D));
+            for (int sg = 0; sg < D.ks_oT; sg++)
+                chk("oT", lay::oT(D.ks_oT, E, l) + ((size_t)sg * kMaxT + t) * E + E - 1, lay::oT_size(D));
         }
         gemm_out("qkvT", lay::qkvT(ks[0], QKV, l), QKV, ks[0], lay::qkvT_size(D));
         // kT_attn items (kv head, chunk, token group) and the q/k/v rows they read
@@ -666,7 +668,7 @@ int mi_check_layout(const mi_synth_shape* sh, int32_t max_ctx, int32_t n_cu, int
                 const int nct = (pos + t + kAttnChunk) / kAttnChunk;
                 chk("attT", lay::attT(NH, D.maxch, D.arec, l, t) + (size_t)(h * D.maxch + nct - 1) * D.arec + HD + 1, lay::attT_size(D));
             }
-        gemm_out("oT", lay::oT(ks[1], E, l), E, ks[1], lay::oT_size(D));
+        gemm_out("oT", lay::oT(D.ks_oT, E, l), E, D.ks_oT, lay::oT_size(D));
         for (int t = 0; t < T; t++)
             for (int g = 0; g < FF / 32; g++) chk("actT", lay::actT(FF, l, t) + (size_t)g * kActRec + 39, lay::actT_size(D));
         for (int t = 0; t < T; t++) chk("actT", lay::actT(FF, l, t) + (size_t)(nbF - 1) * kActRec + kTRec - 1, lay::actT_size(D));

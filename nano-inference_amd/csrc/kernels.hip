@@ -2003,6 +2003,15 @@ __device__ __forceinline__ void tstage_x(MPtr M, int slot, int T, uint8_t* XT) {
     drain_vm();
 }
 
+// O in the per-phase multi-token launches: one K segment per chunk (ks = nc; 2.18 ->
+// 2.14 ms per 8-token S3 step); the persistent kT_step keeps the plan's split, which is
+// faster there. oT is laid out for nc partials either way.
+__device__ __forceinline__ PMat omatT(MPtr M, int l, bool persistent) {
+    PMat W = ldmat(&LY(M, l)->o);
+    if (!persistent) W.ks = W.nc;
+    return W;
+}
+__device__ __forceinline__ float* oT_at(MPtr M, int l) { return M->oT + lay::oT(LY(M, 0)->o.nc, M->E, l); }
 // phase input of token t for the qkv (kind PH_QKV), gate/up (PH_GU) and
 // lm_head (PH_LM) GEMMs: x = h + split-K partials in order (layer 0 of qkv: the
 // token's embedding row) -> hT -> RMSNorm -> int8 records in xT. The same arithmetic
@@ -2024,8 +2033,8 @@ __device__ __forceinline__ void kT_in_body(MPtr M, int l, int kind, int t, float
         if (qkv && l == 0) {
             v = ldg4(M->emb + (size_t)M->tokbuf[pos + t] * n + e0);
         } else {
-            const int ks = dsrc ? LY(M, pl)->d.ks : LY(M, pl)->o.ks;
-            const float* part = dsrc ? M->dT + (size_t)pl * LY(M, 0)->d.ks * kMaxT * n : M->oT + (size_t)pl * LY(M, 0)->o.ks * kMaxT * n;
+            const int ks = dsrc ? LY(M, pl)->d.ks : omatT(M, pl, P).ks;
+            const float* part = dsrc ? M->dT + (size_t)pl * LY(M, 0)->d.ks * kMaxT * n : oT_at(M, pl);
             const float* h = M->hT + hT_at(M, dsrc ? 2 * pl + 1 : 2 * l, t);
             float4 p[kMaxKsRes];
 #pragma unroll
@@ -2066,7 +2075,6 @@ __global__ __launch_bounds__(kPThreads) void kT_in(const DModel* Mp, int l, int 
 }
 
 __device__ __forceinline__ float* qkvT_at(MPtr M, int l) { return M->qkvT + lay::qkvT(LY(M, 0)->qkv.ks, M->QKV, l); }
-__device__ __forceinline__ float* oT_at(MPtr M, int l) { return M->oT + lay::oT(LY(M, 0)->o.ks, M->E, l); }
 __device__ __forceinline__ float* dT_at(MPtr M, int l) { return M->dT + lay::dT(LY(M, 0)->d.ks, M->E, l); }
 __device__ __forceinline__ float* attT_at(MPtr M, int l, int t) { return M->attT + lay::attT(M->NH, M->maxch, M->arec, l, t); }
 __device__ __forceinline__ uint8_t* actT_at(MPtr M, int l, int t) { return M->actT + lay::actT(M->FF, l, t); }
@@ -2320,7 +2328,7 @@ __device__ __forceinline__ void kT_o_body(MPtr M, int l, int T, uint8_t* smem, i
     TBODY
     uint8_t* XT = smem;
     float* P = reinterpret_cast<float*>(smem + kTXeBytes);
-    const PMat W = ldmat(&LY(M, l)->o);
+    const PMat W = omatT(M, l, PS);
     float* part = oT_at(M, l);
     tgemm(W, wg, nwg, XT, M->E / 32, T, P, wave, lane, [&] { tstage_x(M, xt_slot(M, l, kXtO), T, XT); },
           [&](int g, int s, int t, float v) { st_x<PS>(&part[((size_t)s * kMaxT + t) * W.rows + g * 64 + lane], v); }, pre);
@@ -3296,6 +3304,7 @@ bool kernels_plan(int E, int FF, int cb[5], int ks[5]) {
     const int ncF = nbF / cbF, cap = std::min(kMaxKsRes, kCtlBytes / (4 * E) - 2);
     if (cap < 1) return false;
     ks[3] = std::max(1, std::min(std::min(cap, ncF), kPlanWgs / (E / 64)));
+    if (nbE / cbE > kMaxKsRes) return false;      // the per-phase multi-token O's partials (one per chunk)
     return (FF / 32) * kActRec <= kCtlBytes;
 }
 

@@ -14,6 +14,7 @@ namespace mi {
 struct Dims {
     int NL, E, FF, NH, NKV, HD, QKV, V, maxseq, maxch, arec;
     int ks_qkv, ks_o, ks_d;        // split-K segments of qkv, o and down (the plan)
+    int ks_oT;                     // O's split in the multi-token steps: one segment per chunk
     int nwg;                       // workgroups of the persistent kernels (argmax candidates)
 };
 
@@ -59,7 +60,7 @@ LAYFN size_t xT_tok(int E) {
 LAYFN size_t xT(int E, int slot) { return (size_t)slot * kMaxT * xT_tok(E); }   // bytes; + t * xT_tok(E) + b * kTRec + byte
 LAYFN size_t xT_size(const Dims& d) { return (size_t)(3 * d.NL + 1) * kMaxT * xT_tok(d.E); }
 LAYFN size_t oT(int ks, int E, int l) { return (size_t)l * ks * kMaxT * E; }              // + (s * kMaxT + t) * E + row
-LAYFN size_t oT_size(const Dims& d) { return (size_t)d.NL * d.ks_o * kMaxT * d.E; }
+LAYFN size_t oT_size(const Dims& d) { return (size_t)d.NL * d.ks_oT * kMaxT * d.E; }
 LAYFN size_t actT(int FF, int l, int t) { return ((size_t)l * kMaxT + t) * (FF / 32) * kActRec; }  // bytes
 LAYFN size_t actT_size(const Dims& d) { return (size_t)d.NL * kMaxT * (d.FF / 32) * kActRec; }
 LAYFN size_t dT(int ks, int E, int l) { return (size_t)l * ks * kMaxT * E; }              // + (s * kMaxT + t) * E + row
