@@ -106,22 +106,41 @@ def gemv_microbench(torch, reps=40):
         torch.cuda.synchronize()
         us = e0.elapsed_time(e1) * 1000 / reps
         del g
+        # a plain read of the same weight bytes, launched the same way (graph replay over the
+        # same rotated copies): the stream roofline at this launch's size, fixed costs
+        # (launch, first round trip, drain) included, which a 4 GiB stream amortises away
+        sink = torch.zeros(1024, dtype=torch.int32, device="cuda")
+        gs = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gs):
+            for i in range(reps):
+                minfer.stream_read(w[i % copies], nbytes, sink)
+        gs.replay()
+        torch.cuda.synchronize()
+        e0.record()
+        gs.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        us_s = e0.elapsed_time(e1) * 1000 / reps
+        del gs
         alg = rows * nb * 18 + n_in + nb * 4 + rows * 4
-        out.append(dict(shape=name, rows=rows, k=n_in, ks=ks, us=round(us, 2), gbps=round(alg / us / 1e3, 1)))
+        out.append(dict(shape=name, rows=rows, k=n_in, ks=ks, us=round(us, 2), gbps=round(alg / us / 1e3, 1),
+                        sized_stream_us=round(us_s, 2), sized_stream_gbps=round(nbytes / us_s / 1e3, 1),
+                        frac_of_sized_stream=round(us_s / us, 4)))
         del w
     torch.cuda.empty_cache()
     _ = rng
     return out
 
 
-def gemv_kernel_us():
-    """config-1 kernel durations per shape from the committed rocprofv3 kernel-trace summary"""
+def gemv_kernel_us(prefix="kernel_us_"):
+    """config-1 kernel durations per shape from the committed rocprofv3 kernel-trace summary
+    (prefix "stream_kernel_us_": the plain read of the same bytes)"""
     out = {}
     try:
         with open(os.path.join(ROOT, "profiles", "k_gemv_config1.md")) as f:
             for line in f:
-                if line.startswith("kernel_us_"):
-                    k, v = line[len("kernel_us_"):].split(":")
+                if line.startswith(prefix):
+                    k, v = line[len(prefix):].split(":")
                     out[k.strip()] = float(v)
     except OSError:
         pass
@@ -410,7 +429,8 @@ def main():
         import torch
         res = gemv_microbench(torch)
         for m in res:
-            log("gemv %-8s %6d x %5d: %8.2f us  %7.1f GB/s" % (m["shape"], m["rows"], m["k"], m["us"], m["gbps"]))
+            log("gemv %-8s %6d x %5d: %8.2f us  %7.1f GB/s  (a read of the same bytes: %.2f us)" % (
+                m["shape"], m["rows"], m["k"], m["us"], m["gbps"], m["sized_stream_us"]))
         print(json.dumps({"gemv": res}), flush=True)
         return
     if args.attention_only:
@@ -504,7 +524,7 @@ def main():
     eng.close()
     del eng
     micro = [] if args.no_micro else gemv_microbench(torch)
-    ktr = gemv_kernel_us()
+    ktr, kst = gemv_kernel_us(), gemv_kernel_us("stream_kernel_us_")
     for m in micro:
         m["frac_of_stream"] = round(m["gbps"] / stream, 4)
         if m["shape"] in ktr:          # kernel duration alone (rocprofv3 trace, profiles/k_gemv_config1.md)
@@ -512,7 +532,11 @@ def main():
             m["kernel_us"] = ktr[m["shape"]]
             m["kernel_gbps"] = round(alg / ktr[m["shape"]] / 1e3, 1)
             m["kernel_frac_of_stream"] = round(m["kernel_gbps"] / stream, 4)
-        log("gemv %-8s %6d x %5d: %8.2f us  %7.1f GB/s" % (m["shape"], m["rows"], m["k"], m["us"], m["gbps"]))
+            if m["shape"] in kst:      # against a read of the same bytes, both from the same trace
+                m["sized_stream_kernel_us"] = kst[m["shape"]]
+                m["kernel_frac_of_sized_stream"] = round(kst[m["shape"]] / ktr[m["shape"]], 4)
+        log("gemv %-8s %6d x %5d: %8.2f us  %7.1f GB/s  (a read of the same bytes: %.2f us)" % (
+            m["shape"], m["rows"], m["k"], m["us"], m["gbps"], m["sized_stream_us"]))
     attn = [] if args.no_micro else attention_depth(torch)
     for a in attn:
         log("attention L=%-6d %8.2f us/layer  %7.1f GB/s" % (a["L"], a["us_per_layer"], a["gbps"]))
