@@ -27,11 +27,18 @@ Prints ONE JSON line on stdout. Besides the contract keys it carries:
                 phase's time from the previous grid barrier's exit to its own exit,
                 against stream_gbps
   gemv          config 1 microbench: each S15 GEMV shape, rotated over copies
-                totalling > 512 MB so every launch reads from HBM
+                totalling > 512 MB so every launch reads from HBM; sized_stream_us:
+                the stream kernel reading the same bytes, launched the same way
   attention_depth  config 3: S15 decode attention at L = 512..32768, 28 rotated
                 layer caches, GB/s of K/V read per layer
+  speculative   config 2 by speculative decoding (n-gram drafts, T <= 8 verify steps)
+  verify_step   config 4: an S3 T = 8 verify step against a T = 1 step at context 1024,
+                and the drafter on S3 with a repetitive 1000-token prompt
   cpu_baseline  the oracle's fp32 mode (a restatement of cpu_infer.cpp whose
                 token streams equal the reference binary's) on this host's cores
+
+Single measurements for kernel traces: --gemv-only, --attention-only L[,L...] [--mfma],
+--verify-only, --copy-calib MIB (counter calibration).
 """
 import argparse
 import json
