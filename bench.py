@@ -212,7 +212,7 @@ def spec_decode(path, prompt, n_gen=128):
                       accepted=st["accepted"], tokens_per_step=round(n_gen / max(st["steps"], 1), 3))
 
 
-def verify_cost(reps=10):
+def verify_cost(reps=10, modes=(2, 1)):
     """config4: S3 (hidden 2048, 36 layers), context 1024; a T=8 verify step (the
     current token + 7 drafts, TMAX = 8) against a T=1 step at the same position.
     Wall time per mi_step call (upload, step, copy-back), mean of reps. The engine's
@@ -224,7 +224,7 @@ def verify_cost(reps=10):
     prompt = minfer.prompt_ids(pseed, ctx, V)
     toks = minfer.prompt_ids(pseed + 1, 8, V)
     out = {}
-    for mode in (2, 1):
+    for mode in modes:
         eng = minfer.Engine(path, max_ctx=ctx + 16, persistent=mode)
         eng.prefill(prompt)
         for T in ((1, 8) if mode == 2 else (8,)):
@@ -238,7 +238,7 @@ def verify_cost(reps=10):
         eng.close()
     return dict(workload="config4: S3 q4_0, context 1024, verify T=8 vs T=1", t1_ms=round(out[(2, 1)], 3),
                 t8_ms=round(out[(2, 8)], 3), ratio=round(out[(2, 8)] / out[(2, 1)], 3),
-                t8_per_phase_ms=round(out[(1, 8)], 3),
+                t8_per_phase_ms=round(out[(1, 8)], 3) if (1, 8) in out else None,
                 note="T=8 = current token + 7 drafts (TMAX 8, mega.cu:50); the config's 8 drafts + 1 would be T=9")
 
 
@@ -426,9 +426,11 @@ def main():
     ap.add_argument("--verify-only", action="store_true",
                     help="only run the config4 verify-step cost (T=8 vs T=1), print its JSON and exit "
                          "(for kernel traces)")
+    ap.add_argument("--verify-persistent-only", action="store_true",
+                    help="with --verify-only: skip the per-phase launches (for counter runs)")
     args = ap.parse_args()
     if args.verify_only:
-        res = verify_cost()
+        res = verify_cost(modes=(2,) if args.verify_persistent_only else (2, 1))
         log("verify step: %s" % res)
         print(json.dumps({"verify_step": res}), flush=True)
         return
