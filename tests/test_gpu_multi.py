@@ -126,6 +126,19 @@ def test_long_context_multi_merge_phase(pos, T, persistent):
 
 
 @MULTI
+def test_long_context_multi_merge_bounds(persistent):
+    """2044 + 8: tokens 0-3 see 32 chunks (the most the multi-token merge takes with
+    every record load issued first) and tokens 4-7 see 33 (past it, the split-by-split
+    merge); T = 8 against eight single steps"""
+    path = synth_cached("eng-256", TINY, 7)
+    say("tiny long context pos 2044 T 8 persistent %d" % persistent)
+    eng = minfer.Engine(path, max_ctx=2100, persistent=persistent)
+    prompt = minfer.prompt_ids(14, 2044, TINY["n_vocab"])
+    multi_vs_single(eng, prompt, 2044, 8, 31, TINY["n_vocab"])
+    eng.close()
+
+
+@MULTI
 def test_long_context_multi_hd128(persistent):
     """head_dim 128 at context 1020 + 8 (16 and 17 chunks: the merge tree) on the
     attention-sensitive model (O(1) scores): T = 8 against eight single steps"""
